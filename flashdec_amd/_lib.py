@@ -1,0 +1,209 @@
+"""ctypes binding of ``libflashdec_hip.so`` (declared in ``include/flashdec_hip.h``).
+
+The library is loaded lazily on first use and never replaced by a fallback:
+if it is missing or fails to load, every HIP entry point raises
+``RuntimeError`` with the reason.  Structures below mirror the C structs
+field for field; ``struct_size`` lets the library reject a layout mismatch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+LIB_NAME = "libflashdec_hip.so"
+LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
+
+FD_OK = 0
+FD_DTYPE_F16 = 0
+FD_DTYPE_BF16 = 1
+FD_DTYPE_F32 = 2
+FD_INDEX_I32 = 0
+FD_INDEX_I64 = 1
+ABI_VERSION = 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_vp = ctypes.c_void_p
+
+
+class PagedDecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("dtype", _i32),
+        ("num_seqs", _i64),
+        ("num_q_heads", _i64),
+        ("num_kv_heads", _i64),
+        ("head_dim", _i64),
+        ("block_size", _i64),
+        ("num_blocks", _i64),
+        ("max_blocks_per_seq", _i64),
+        ("q", _vp),
+        ("q_stride", _i64 * 3),
+        ("k_cache", _vp),
+        ("k_stride", _i64 * 4),
+        ("v_cache", _vp),
+        ("v_stride", _i64 * 4),
+        ("block_tables", _vp),
+        ("block_tables_dtype", _i32),
+        ("block_tables_stride", _i64 * 2),
+        ("seq_lens", _vp),
+        ("seq_lens_dtype", _i32),
+        ("seq_lens_stride", _i64),
+        ("out", _vp),
+        ("out_stride", _i64 * 3),
+        ("sm_scale", ctypes.c_float),
+        ("num_splits", _i32),
+        ("split_acc", _vp),
+        ("split_acc_stride", _i64 * 4),
+        ("split_max", _vp),
+        ("split_sum", _vp),
+        ("split_stats_stride", _i64 * 3),
+        ("append_k", _vp),
+        ("append_k_stride", _i64 * 3),
+        ("append_v", _vp),
+        ("append_v_stride", _i64 * 3),
+        ("slot_mapping", _vp),
+        ("slot_mapping_dtype", _i32),
+        ("slot_mapping_stride", _i64),
+    ]
+
+
+class RopeAppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("dtype", _i32),
+        ("batch", _i64),
+        ("num_q_heads", _i64),
+        ("num_kv_heads", _i64),
+        ("head_dim", _i64),
+        ("block_size", _i64),
+        ("num_blocks", _i64),
+        ("rotary_dim", _i64),
+        ("base", ctypes.c_double),
+        ("q_out", _vp),
+        ("q", _vp),
+        ("k", _vp),
+        ("v", _vp),
+        ("k_cache", _vp),
+        ("v_cache", _vp),
+        ("block_ids", _vp),
+        ("block_offsets", _vp),
+        ("positions", _vp),
+        ("index_dtype", _i32),
+    ]
+
+
+EXPORTED_SYMBOLS = (
+    "fd_paged_decode",
+    "fd_paged_decode_plan",
+    "fd_fused_rope_kv_append",
+    "fd_kv_append",
+    "fd_last_error",
+    "fd_abi_version",
+)
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path() -> Path:
+    override = os.environ.get("FLASHDEC_AMD_LIB")
+    return Path(override) if override else LIB_PATH
+
+
+def load_library():
+    """Load and type the C-ABI library once; raise RuntimeError if unusable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} is not built: the HIP path has no fallback. "
+                "Build it with `python -m flashdec_amd._build` (or __graft_entry__.build())."
+            )
+        try:
+            lib = ctypes.CDLL(str(path))
+        except OSError as exc:
+            raise RuntimeError(f"failed to load {path}: {exc}") from exc
+        lib.fd_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), _vp]
+        lib.fd_paged_decode.restype = ctypes.c_int
+        lib.fd_paged_decode_plan.argtypes = [_i64, _i64, _i64, _i64, _i64]
+        lib.fd_paged_decode_plan.restype = ctypes.c_int
+        lib.fd_fused_rope_kv_append.argtypes = [ctypes.POINTER(RopeAppendArgs), _vp]
+        lib.fd_fused_rope_kv_append.restype = ctypes.c_int
+        lib.fd_kv_append.argtypes = [ctypes.POINTER(RopeAppendArgs), _vp]
+        lib.fd_kv_append.restype = ctypes.c_int
+        lib.fd_last_error.argtypes = []
+        lib.fd_last_error.restype = ctypes.c_char_p
+        lib.fd_abi_version.argtypes = []
+        lib.fd_abi_version.restype = ctypes.c_int
+        version = lib.fd_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != FD_OK:
+        msg = load_library().fd_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    if dtype == torch.bfloat16:
+        return FD_DTYPE_BF16
+    if dtype == torch.float16:
+        return FD_DTYPE_F16
+    if dtype == torch.float32:
+        return FD_DTYPE_F32
+    raise ValueError(f"unsupported dtype {dtype}")
+
+
+def index_code(dtype) -> int:
+    import torch
+
+    if dtype == torch.int64:
+        return FD_INDEX_I64
+    if dtype == torch.int32:
+        return FD_INDEX_I32
+    raise ValueError(f"unsupported index dtype {dtype}")
+
+
+def current_stream_handle(device) -> int:
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def paged_decode(args: PagedDecodeArgs, stream: int) -> None:
+    lib = load_library()
+    args.struct_size = ctypes.sizeof(PagedDecodeArgs)
+    check(lib.fd_paged_decode(ctypes.byref(args), stream), "fd_paged_decode")
+
+
+def paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len) -> int:
+    lib = load_library()
+    rc = lib.fd_paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
+    if rc < 0:
+        check(rc, "fd_paged_decode_plan")
+    return rc
+
+
+def rope_append(args: RopeAppendArgs, stream: int, *, rotate: bool) -> None:
+    lib = load_library()
+    args.struct_size = ctypes.sizeof(RopeAppendArgs)
+    if rotate:
+        check(lib.fd_fused_rope_kv_append(ctypes.byref(args), stream), "fd_fused_rope_kv_append")
+    else:
+        check(lib.fd_kv_append(ctypes.byref(args), stream), "fd_kv_append")

@@ -1,0 +1,80 @@
+// Shared helpers for the gfx950 kernels and the C-ABI glue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/flashdec_hip.h"
+
+namespace fd {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------- errors --
+// Thread-local message for fd_last_error(); set by the host-side glue only.
+std::string& last_error_slot();
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// ------------------------------------------------------------ conversions --
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) {
+  return static_cast<float>(x);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  return static_cast<T>(x);  // RNE on gfx950 (v_cvt_pk_bf16_f32 / v_cvt_f16_f32)
+}
+
+// bf16 / f16 halves of a packed dword -> f32 (exact)
+template <typename T>
+__device__ __forceinline__ float lo_f32(uint32_t w);
+template <typename T>
+__device__ __forceinline__ float hi_f32(uint32_t w);
+
+template <>
+__device__ __forceinline__ float lo_f32<__bf16>(uint32_t w) {
+  return __builtin_bit_cast(float, w << 16);
+}
+template <>
+__device__ __forceinline__ float hi_f32<__bf16>(uint32_t w) {
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+template <>
+__device__ __forceinline__ float lo_f32<_Float16>(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+}
+template <>
+__device__ __forceinline__ float hi_f32<_Float16>(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
+// two f32 -> packed 16-bit pair (lo in bits 0..15), RNE
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const uint16_t a = __builtin_bit_cast(uint16_t, from_f32<T>(lo));
+  const uint16_t b = __builtin_bit_cast(uint16_t, from_f32<T>(hi));
+  return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+}
+
+// -------------------------------------------------------------- indices --
+__device__ __forceinline__ int64_t load_index(const void* base, int64_t elem, int is64) {
+  return is64 ? static_cast<const int64_t*>(base)[elem]
+              : static_cast<int64_t>(static_cast<const int32_t*>(base)[elem]);
+}
+
+// ----------------------------------------------------------- wave utils --
+__device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace fd

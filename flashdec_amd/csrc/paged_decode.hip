@@ -1,0 +1,779 @@
+// Paged single-token decode attention for gfx950 (MI355X).
+//
+// Work decomposition: one workgroup per (request, KV head, KV split).  The
+// split covers a contiguous range of 32-token tiles; the four waves of the
+// workgroup take its tiles round-robin, each keeping its own online-softmax
+// state for all query heads of the KV head (grouped GQA), and the waves are
+// merged in LDS so that one partial (or the final row) leaves the workgroup.
+//
+//  * decode_mfma_kernel  -- head_dim 128, <= 16 query heads per KV head,
+//    unit dim stride (token-major, vLLM NHD/HND views).  QK^T and PV run on
+//    v_mfma_f32_16x16x32_{bf16,f16}; V is transposed in registers.
+//  * decode_generic_kernel -- any strides (dim-major caches), head_dim 64,
+//    any group size; VALU only.
+//  * split_reduce_kernel -- LSE merge of the split partials.
+//
+// Reference semantics followed (cysong2025/flashdec):
+//   flashdec/kernels/paged_decode.py:124-327  grouped decode + fused append
+//   flashdec/kernels/paged_decode.py:330-543  split stage (uniform tile split,
+//                                             append owned by the last tile)
+//   flashdec/kernels/paged_decode.py:546-642  LSE merge; zero rows for
+//                                             seq_len == 0 / slot < 0
+#include "fd_common.h"
+
+namespace fd {
+
+struct DecodeParams {
+  const void* q;
+  int64_t qs0, qs1, qs2;
+  void* k;
+  int64_t ks0, ks1, ks2, ks3;
+  void* v;
+  int64_t vs0, vs1, vs2, vs3;
+  const void* bt;
+  int64_t bts0, bts1;
+  const void* sl;
+  int64_t sls;
+  void* out;
+  int64_t os0, os1, os2;
+  float* acc;
+  int64_t as0, as1, as2, as3;
+  float* mx;
+  float* sm;
+  int64_t ss0, ss1, ss2;
+  const void* ak;
+  int64_t aks0, aks1, aks2;
+  const void* av;
+  int64_t avs0, avs1, avs2;
+  const void* slot;
+  int64_t slots;
+  int bt_i64, sl_i64, slot_i64, fuse;
+  int num_seqs, hq, hkv, group, head_dim, block_size;
+  int64_t num_blocks, max_blocks_per_seq;
+  int splits;
+  float scale_log2;  // sm_scale * log2(e): scores live in the base-2 domain
+};
+
+// Row-level bookkeeping shared by both decode kernels.
+struct RowInfo {
+  int64_t eff_len;  // tokens attended (0 => zero output row)
+  int64_t app_tok;  // token taken from append_k/v (-1: none)
+  int64_t slot;     // cache slot receiving the appended token
+  int t_begin, t_end;  // tile range [t_begin, t_end) of this split (32-token tiles)
+};
+
+__device__ __forceinline__ RowInfo row_info(const DecodeParams& p, int b, int split) {
+  RowInfo r;
+  const int64_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
+  bool active = seq_len > 0;
+  r.slot = -1;
+  if (p.fuse) {
+    r.slot = load_index(p.slot, b * p.slots, p.slot_i64);
+    active = active && r.slot >= 0;
+  }
+  int64_t eff = active ? seq_len : 0;
+  // never walk past the block-table row, whatever seq_lens says
+  const int64_t cap = p.max_blocks_per_seq * p.block_size;
+  eff = eff < cap ? eff : cap;
+  r.eff_len = eff;
+  r.app_tok = (p.fuse && eff > 0) ? eff - 1 : -1;
+  const int num_tiles = static_cast<int>((eff + 31) / 32);
+  const int tps = (num_tiles + p.splits - 1) / p.splits;
+  r.t_begin = split * tps;
+  r.t_end = min(r.t_begin + tps, num_tiles);
+  return r;
+}
+
+// ===================================================== MFMA fast path ====
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<__bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<_Float16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Register footprint of one 32-token tile for one lane (lane = 16*g + c):
+//   kf[mt][s]: K row (token 16*mt + c), dims [32*s + 8*g, +8)   (QK A operand)
+//   vf[i]    : V row (token vtok(g, i)), dims [8*c, +8)          (PV, transposed)
+// vtok(g, i) = 4*g + i (i < 4) or 16 + 4*g + (i - 4): the same tokens whose
+// scores this lane holds after QK (MFMA D layout: rows 4*g + r of each
+// 16-row tile), so P needs no cross-lane movement.
+struct TileRegs {
+  u32x4 kf[2][4];
+  u32x4 vf[8];
+  uint32_t vmask;  // bit i: V row i is a real token
+};
+
+__device__ __forceinline__ int vtok(int g, int i) { return i < 4 ? 4 * g + i : 12 + 4 * g + i; }
+
+// Physical block of a token, read with the token clamped to the last attended
+// one so the block-table read stays inside the row.  A 32-token tile shares
+// one table entry for 32-token blocks and two for 16-token blocks.
+template <typename T, int BS>
+__device__ __forceinline__ void load_tile(const DecodeParams& p, int b, int kvh, const RowInfo& r,
+                                          int tile, int c, int g, TileRegs& t) {
+  const int64_t tok0 = static_cast<int64_t>(tile) * 32;
+  const int64_t last = r.eff_len - 1;  // >= tok0 for any tile in range
+  const T* kbase = static_cast<const T*>(p.k);
+  const T* vbase = static_cast<const T*>(p.v);
+  const int64_t btrow = b * p.bts0;
+  int64_t blk_a = 0, blk_b = 0;
+  if constexpr (BS == 32) {
+    blk_a = load_index(p.bt, btrow + tile * p.bts1, p.bt_i64);
+  } else if constexpr (BS == 16) {
+    const int64_t pa = 2 * static_cast<int64_t>(tile);
+    int64_t pb = pa + 1;
+    pb = pb <= last / 16 ? pb : pa;
+    blk_a = load_index(p.bt, btrow + pa * p.bts1, p.bt_i64);
+    blk_b = load_index(p.bt, btrow + pb * p.bts1, p.bt_i64);
+  }
+  auto block_of = [&](int64_t tok, int64_t tq) -> int64_t {
+    if constexpr (BS == 32) {
+      (void)tok;
+      (void)tq;
+      return blk_a;
+    } else if constexpr (BS == 16) {
+      (void)tq;
+      return (tok - tok0) < 16 ? blk_a : blk_b;
+    } else {
+      (void)tok;
+      return load_index(p.bt, btrow + (tq / BS) * p.bts1, p.bt_i64);
+    }
+  };
+  // K: rows 16*mt + c
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int64_t tok = tok0 + 16 * mt + c;
+    const int64_t tq = tok < last ? tok : last;
+    const int64_t blk = block_of(tok, tq);
+    const bool ok = tok <= last && blk >= 0 && blk < p.num_blocks;
+    const T* row;
+    if (tok == r.app_tok) {
+      row = static_cast<const T*>(p.ak) + b * p.aks0 + kvh * p.aks1;
+    } else {
+      row = ok ? kbase + blk * p.ks0 + kvh * p.ks1 + (tq % BS) * p.ks2 : kbase;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      t.kf[mt][s] = *reinterpret_cast<const u32x4*>(row + 32 * s + 8 * g);
+  }
+  // V: rows vtok(g, i)
+  uint32_t vm = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t tok = tok0 + vtok(g, i);
+    const int64_t tq = tok < last ? tok : last;
+    const int64_t blk = block_of(tok, tq);
+    const bool ok = tok <= last && blk >= 0 && blk < p.num_blocks;
+    const T* row;
+    if (tok == r.app_tok) {
+      row = static_cast<const T*>(p.av) + b * p.avs0 + kvh * p.avs1;
+      vm |= 1u << i;
+    } else {
+      row = ok ? vbase + blk * p.vs0 + kvh * p.vs1 + (tq % BS) * p.vs2 : vbase;
+      vm |= ok ? (1u << i) : 0u;
+    }
+    t.vf[i] = *reinterpret_cast<const u32x4*>(row + 8 * c);
+  }
+  t.vmask = vm;
+}
+
+// Fused append: the lanes holding the newest token's K/V pieces store them at
+// the request's slot (the same bytes they feed to QK/PV from registers).
+template <typename T, int BS>
+__device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, const RowInfo& r, int tile,
+                                             int c, int g, const TileRegs& t) {
+  const int64_t blk = r.slot / BS, off = r.slot % BS;
+  if (blk >= p.num_blocks) return;
+  const int at = static_cast<int>(r.app_tok - static_cast<int64_t>(tile) * 32);
+  if ((at & 15) == c) {
+    T* dst = static_cast<T*>(p.k) + blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      *reinterpret_cast<u32x4*>(dst + 32 * s + 8 * g) = (at >> 4) ? t.kf[1][s] : t.kf[0][s];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (vtok(g, i) == at) {
+      T* dst = static_cast<T*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
+      *reinterpret_cast<u32x4*>(dst + 8 * c) = t.vf[i];
+    }
+  }
+}
+
+// Online-softmax state of one lane: query head c, dims 32*g + 8*r + n.
+struct WaveState {
+  f32x4 acc[8];  // acc[n][r]
+  float m;       // running max (base-2 domain), uniform over g
+  float l;       // partial denominator of this lane's tokens
+};
+
+template <typename T>
+__device__ __forceinline__ void process_tile(const TileRegs& t, const u32x4 (&qf)[4], float scale_log2,
+                                             WaveState& st) {
+  // S^T[token][head] = K . Q^T  (two 16-token row tiles)
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    s0 = mfma16x16x32<T>(t.kf[0][s], qf[s], s0);
+    s1 = mfma16x16x32<T>(t.kf[1][s], qf[s], s1);
+  }
+  float sc[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    sc[r] = s0[r] * scale_log2;
+    sc[4 + r] = s1[r] * scale_log2;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    sc[i] = (t.vmask >> i) & 1u ? sc[i] : -INFINITY;
+    mx = fmaxf(mx, sc[i]);
+  }
+  mx = fmaxf(mx, shfl_xor_f32(mx, 16));
+  mx = fmaxf(mx, shfl_xor_f32(mx, 32));
+  const float m_new = fmaxf(st.m, mx);
+  const float m_use = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = exp2f(st.m - m_use);
+  float pr[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pr[i] = exp2f(sc[i] - m_use);
+    psum += pr[i];
+  }
+  st.l = st.l * alpha + psum;
+  st.m = m_new;
+  // P^T operand, split into a 16-bit head and a 16-bit tail so the PV
+  // product keeps ~16 mantissa bits of the fp32 probabilities.
+  u32x4 ph, pl;
+  {
+    float lo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t hb = pack2<T>(pr[i], 0.f) & 0xffffu;
+      lo[i] = pr[i] - lo_f32<T>(hb);
+    }
+    ph[0] = pack2<T>(pr[0], pr[1]);
+    ph[1] = pack2<T>(pr[2], pr[3]);
+    ph[2] = pack2<T>(pr[4], pr[5]);
+    ph[3] = pack2<T>(pr[6], pr[7]);
+    pl[0] = pack2<T>(lo[0], lo[1]);
+    pl[1] = pack2<T>(lo[2], lo[3]);
+    pl[2] = pack2<T>(lo[4], lo[5]);
+    pl[3] = pack2<T>(lo[6], lo[7]);
+  }
+  // V^T operands: vt_n holds dim 8*c + n of the lane's eight tokens.  Rows of
+  // masked tokens are zeroed first (their memory may hold NaN/Inf).
+  u32x4 vz[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool keep = (t.vmask >> i) & 1u;
+    vz[i][0] = keep ? t.vf[i][0] : 0u;
+    vz[i][1] = keep ? t.vf[i][1] : 0u;
+    vz[i][2] = keep ? t.vf[i][2] : 0u;
+    vz[i][3] = keep ? t.vf[i][3] : 0u;
+  }
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int w = n >> 1;
+    const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 vt;
+    vt[0] = __builtin_amdgcn_perm(vz[1][w], vz[0][w], sel);
+    vt[1] = __builtin_amdgcn_perm(vz[3][w], vz[2][w], sel);
+    vt[2] = __builtin_amdgcn_perm(vz[5][w], vz[4][w], sel);
+    vt[3] = __builtin_amdgcn_perm(vz[7][w], vz[6][w], sel);
+    f32x4 a = st.acc[n] * alpha;
+    a = mfma16x16x32<T>(vt, ph, a);
+    st.acc[n] = mfma16x16x32<T>(vt, pl, a);
+  }
+}
+
+constexpr int kWaves = 4;
+constexpr int kAccPitch = 132;  // floats per head row in LDS (bank spread)
+
+template <typename T, int BS>
+__global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
+  __shared__ float s_acc[kWaves][16][kAccPitch];
+  __shared__ float s_m[kWaves][16];
+  __shared__ float s_l[kWaves][16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int split = blockIdx.x % p.splits;
+  const int pair = blockIdx.x / p.splits;
+  const int b = pair / p.hkv;
+  const int kvh = pair % p.hkv;
+  const int G = p.group;
+
+  // Q^T operand: query head kvh*G + c, dims [32*s + 8*g, +8)
+  u32x4 qf[4];
+  {
+    const bool hv = c < G;
+    const T* qrow = static_cast<const T*>(p.q) + b * p.qs0 + (kvh * G + (hv ? c : 0)) * p.qs1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * g);
+      qf[s] = hv ? x : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const RowInfo r = row_info(p, b, split);
+
+  WaveState st;
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.f;
+
+  int tile = r.t_begin + wave;
+  if (tile < r.t_end) {
+    TileRegs cur;
+    load_tile<T, BS>(p, b, kvh, r, tile, c, g, cur);
+    for (;;) {
+      // issue the next tile's loads before consuming the current one
+      const int next = tile + kWaves;
+      const bool more = next < r.t_end;
+      TileRegs nxt;
+      if (more) load_tile<T, BS>(p, b, kvh, r, next, c, g, nxt);
+      if (r.app_tok >= 0 && r.app_tok / 32 == tile) store_append<T, BS>(p, kvh, r, tile, c, g, cur);
+      process_tile<T>(cur, qf, p.scale_log2, st);
+      if (!more) break;
+      cur = nxt;
+      tile = next;
+    }
+  }
+  // denominator over the four lanes (g) that share query head c
+  float lt = st.l;
+  lt += shfl_xor_f32(lt, 16);
+  lt += shfl_xor_f32(lt, 32);
+  if (g == 0) {
+    s_m[wave][c] = st.m;
+    s_l[wave][c] = lt;
+  }
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    float* dst = &s_acc[wave][c][32 * g + 8 * rr];
+    *reinterpret_cast<f32x4*>(dst) = f32x4{st.acc[0][rr], st.acc[1][rr], st.acc[2][rr], st.acc[3][rr]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
+  }
+  __syncthreads();
+
+  // merge the four waves: thread -> (head h, dims [d0, d0 + 8))
+  const int h = threadIdx.x >> 4;
+  const int d0 = (threadIdx.x & 15) * 8;
+  if (h >= G) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float wt = exp2f(s_m[w][h] - Mu);
+    L += wt * s_l[w][h];
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(&s_acc[w][h][d0]);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(&s_acc[w][h][d0 + 4]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[j] += wt * a0[j];
+      o[4 + j] += wt * a1[j];
+    }
+  }
+  const int qh = kvh * G + h;
+  if (p.splits == 1) {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1 + d0 * p.os2;
+    if (p.os2 == 1) {
+      u32x4 w;
+      w[0] = pack2<T>(o[0] * inv, o[1] * inv);
+      w[1] = pack2<T>(o[2] * inv, o[3] * inv);
+      w[2] = pack2<T>(o[4] * inv, o[5] * inv);
+      w[3] = pack2<T>(o[6] * inv, o[7] * inv);
+      *reinterpret_cast<u32x4*>(dst) = w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[j * p.os2] = from_f32<T>(o[j] * inv);
+    }
+  } else {
+    float* a = p.acc + b * p.as0 + qh * p.as1 + split * p.as2 + d0 * p.as3;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j * p.as3] = o[j];
+    if (d0 == 0) {
+      const int64_t so = b * p.ss0 + qh * p.ss1 + split * p.ss2;
+      p.mx[so] = M;
+      p.sm[so] = L;
+    }
+  }
+}
+
+// ====================================================== generic path ====
+// One wave per (request, KV head, head group of <= 8 query heads, split).
+// Lane = token within a 64-token tile for QK; lane = dim for PV.
+constexpr int kGenHeads = 8;
+
+template <typename T, int D>
+__global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p, int head_groups) {
+  __shared__ float s_q[kGenHeads][D];
+  __shared__ float s_p[kGenHeads][64];
+  __shared__ int64_t s_vrow[64];  // element offset of the V row, -1 = masked, -2 = append
+
+  const int lane = threadIdx.x;
+  const int split = blockIdx.y;
+  const int hg = blockIdx.x % head_groups;
+  const int pair = blockIdx.x / head_groups;
+  const int b = pair / p.hkv;
+  const int kvh = pair % p.hkv;
+  const int G = p.group;
+  const int h0 = kvh * G + hg * kGenHeads;
+  const int nh = min(kGenHeads, G - hg * kGenHeads);
+
+  const T* qb = static_cast<const T*>(p.q) + b * p.qs0;
+  for (int i = lane; i < kGenHeads * D; i += 64) {
+    const int j = i / D, d = i % D;
+    s_q[j][d] = j < nh ? to_f32(qb[(h0 + j) * p.qs1 + d * p.qs2]) : 0.f;
+  }
+  const RowInfo r = row_info(p, b, split);
+  const T* kbase = static_cast<const T*>(p.k);
+  const T* vbase = static_cast<const T*>(p.v);
+  const T* akrow = p.fuse ? static_cast<const T*>(p.ak) + b * p.aks0 + kvh * p.aks1 : nullptr;
+  const T* avrow = p.fuse ? static_cast<const T*>(p.av) + b * p.avs0 + kvh * p.avs1 : nullptr;
+
+  // the split owning the appended token stores it (head group 0 only)
+  if (r.app_tok >= 0 && hg == 0 && r.app_tok / 32 >= r.t_begin && r.app_tok / 32 < r.t_end) {
+    const int64_t blk = r.slot / p.block_size, off = r.slot % p.block_size;
+    if (blk < p.num_blocks) {
+      T* kd = static_cast<T*>(p.k) + blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
+      T* vd = static_cast<T*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
+      for (int d = lane; d < D; d += 64) {
+        kd[d * p.ks3] = akrow[d * p.aks2];
+        vd[d * p.vs3] = avrow[d * p.avs2];
+      }
+    }
+  }
+
+  float m[kGenHeads], l[kGenHeads];
+  float acc[kGenHeads][D / 64];
+#pragma unroll
+  for (int j = 0; j < kGenHeads; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < D / 64; ++e) acc[j][e] = 0.f;
+  }
+  __syncthreads();
+
+  // 64-token tiles = two 32-token split tiles
+  const int64_t tok_begin = static_cast<int64_t>(r.t_begin) * 32;
+  const int64_t tok_end = min(static_cast<int64_t>(r.t_end) * 32, r.eff_len);
+  for (int64_t tok0 = tok_begin; tok0 < tok_end; tok0 += 64) {
+    const int64_t tok = tok0 + lane;
+    bool ok = tok < tok_end;
+    int64_t krow = 0, vrow = -1;
+    const bool is_app = ok && tok == r.app_tok;
+    if (ok && !is_app) {
+      const int64_t blk = load_index(p.bt, b * p.bts0 + (tok / p.block_size) * p.bts1, p.bt_i64);
+      ok = blk >= 0 && blk < p.num_blocks;
+      const int64_t off = tok % p.block_size;
+      krow = blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
+      vrow = ok ? blk * p.vs0 + kvh * p.vs1 + off * p.vs2 : -1;
+    }
+    if (is_app) vrow = -2;
+    float sc[kGenHeads];
+#pragma unroll
+    for (int j = 0; j < kGenHeads; ++j) sc[j] = 0.f;
+    if (ok) {
+      for (int d = 0; d < D; ++d) {
+        const float kv = is_app ? to_f32(akrow[d * p.aks2]) : to_f32(kbase[krow + d * p.ks3]);
+#pragma unroll
+        for (int j = 0; j < kGenHeads; ++j) sc[j] += s_q[j][d] * kv;
+      }
+    }
+    s_vrow[lane] = vrow;
+#pragma unroll
+    for (int j = 0; j < kGenHeads; ++j) {
+      const float s = ok ? sc[j] * p.scale_log2 : -INFINITY;
+      float mx = s;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, shfl_xor_f32(mx, o));
+      const float m_new = fmaxf(m[j], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m[j] - m_use);
+      const float pj = exp2f(s - m_use);
+      float ps = pj;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ps += shfl_xor_f32(ps, o);
+      l[j] = l[j] * alpha + ps;
+      m[j] = m_new;
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) acc[j][e] *= alpha;
+      s_p[j][lane] = pj;
+    }
+    __syncthreads();
+    const int n = static_cast<int>(min<int64_t>(64, tok_end - tok0));
+    for (int t = 0; t < n; ++t) {
+      const int64_t vr = s_vrow[t];
+      if (vr == -1) continue;
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) {
+        const int d = lane + 64 * e;
+        const float vv = vr == -2 ? to_f32(avrow[d * p.avs2]) : to_f32(vbase[vr + d * p.vs3]);
+#pragma unroll
+        for (int j = 0; j < kGenHeads; ++j) acc[j][e] += s_p[j][t] * vv;
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < kGenHeads; ++j) {
+    if (j >= nh) break;
+    const int qh = h0 + j;
+    if (p.splits == 1) {
+      const float inv = l[j] > 0.f ? 1.f / l[j] : 0.f;
+      T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1;
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) dst[(lane + 64 * e) * p.os2] = from_f32<T>(acc[j][e] * inv);
+    } else {
+      float* a = p.acc + b * p.as0 + qh * p.as1 + split * p.as2;
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) a[(lane + 64 * e) * p.as3] = acc[j][e];
+      if (lane == 0) {
+        const int64_t so = b * p.ss0 + qh * p.ss1 + split * p.ss2;
+        p.mx[so] = m[j];
+        p.sm[so] = l[j];
+      }
+    }
+  }
+}
+
+// ===================================================== split reducer ====
+// One wave per (request, query head): out = sum_s w_s acc_s / sum_s w_s l_s,
+// w_s = 2^(m_s - max_s m_s).
+template <typename T>
+__global__ __launch_bounds__(64) void split_reduce_kernel(DecodeParams p) {
+  const int b = blockIdx.x / p.hq;
+  const int qh = blockIdx.x % p.hq;
+  const int lane = threadIdx.x;
+  const int D = p.head_dim;
+  const int64_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
+  bool has = seq_len > 0;
+  if (p.fuse) has = has && load_index(p.slot, b * p.slots, p.slot_i64) >= 0;
+  const int64_t sb = b * p.ss0 + qh * p.ss1;
+  float M = -INFINITY;
+  if (has)
+    for (int s = 0; s < p.splits; ++s) M = fmaxf(M, p.mx[sb + s * p.ss2]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  float o0 = 0.f, o1 = 0.f;
+  const float* ab = p.acc + b * p.as0 + qh * p.as1;
+  if (has) {
+    for (int s = 0; s < p.splits; ++s) {
+      const float ms = p.mx[sb + s * p.ss2];
+      if (ms == -INFINITY) continue;
+      const float w = exp2f(ms - Mu);
+      L += w * p.sm[sb + s * p.ss2];
+      const float* a = ab + s * p.as2;
+      o0 += w * a[lane * p.as3];
+      if (D > 64) o1 += w * a[(lane + 64) * p.as3];
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1;
+  dst[lane * p.os2] = from_f32<T>(o0 * inv);
+  if (D > 64) dst[(lane + 64) * p.os2] = from_f32<T>(o1 * inv);
+}
+
+// ========================================================== host glue ====
+namespace {
+
+int g_num_cus = 0;
+
+int device_cus() {
+  if (g_num_cus > 0) return g_num_cus;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+    g_num_cus = cus;
+  else
+    g_num_cus = 256;
+  return g_num_cus;
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
+  if (a.head_dim != 128 || group > 16) return false;
+  if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
+  const int64_t strides[] = {a.q_stride[0], a.q_stride[1], a.k_stride[0], a.k_stride[1], a.k_stride[2],
+                             a.v_stride[0], a.v_stride[1], a.v_stride[2]};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return false;
+  if (!aligned16(a.q) || !aligned16(a.k_cache) || !aligned16(a.v_cache)) return false;
+  if (a.append_k) {
+    if (a.append_k_stride[2] != 1 || a.append_v_stride[2] != 1) return false;
+    const int64_t as[] = {a.append_k_stride[0], a.append_k_stride[1], a.append_v_stride[0],
+                          a.append_v_stride[1]};
+    for (int64_t s : as)
+      if (s % 8 != 0) return false;
+    if (!aligned16(a.append_k) || !aligned16(a.append_v)) return false;
+  }
+  return true;
+}
+
+template <typename T>
+int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t stream) {
+  const int64_t pairs = a.num_seqs * a.num_kv_heads;
+  if (fast_path_ok(a, p.group)) {
+    const dim3 grid(static_cast<unsigned>(pairs * p.splits));
+    switch (a.block_size) {
+      case 8: hipLaunchKernelGGL((decode_mfma_kernel<T, 8>), grid, dim3(256), 0, stream, p); break;
+      case 16: hipLaunchKernelGGL((decode_mfma_kernel<T, 16>), grid, dim3(256), 0, stream, p); break;
+      default: hipLaunchKernelGGL((decode_mfma_kernel<T, 32>), grid, dim3(256), 0, stream, p); break;
+    }
+  } else {
+    const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
+    const dim3 grid(static_cast<unsigned>(pairs * hg), static_cast<unsigned>(p.splits));
+    if (a.head_dim == 64)
+      hipLaunchKernelGGL((decode_generic_kernel<T, 64>), grid, dim3(64), 0, stream, p, hg);
+    else
+      hipLaunchKernelGGL((decode_generic_kernel<T, 128>), grid, dim3(64), 0, stream, p, hg);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FD_E_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
+  if (p.splits > 1) {
+    hipLaunchKernelGGL((split_reduce_kernel<T>), dim3(static_cast<unsigned>(a.num_seqs * a.num_q_heads)),
+                       dim3(64), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
+  }
+  return FD_OK;
+}
+
+}  // namespace
+
+}  // namespace fd
+
+using namespace fd;
+
+extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
+                                    int64_t head_dim, int64_t max_seq_len) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seq_len < 0)
+    return set_error(FD_E_INVALID, "fd_paged_decode_plan: non-positive shape");
+  (void)num_q_heads;
+  (void)head_dim;
+  const int64_t tiles = (max_seq_len + 31) / 32;
+  const int64_t pairs = num_seqs * num_kv_heads;
+  const int64_t target = 2 * static_cast<int64_t>(device_cus());
+  int64_t s = (target + pairs - 1) / pairs;
+  const int64_t cap = (tiles + kWaves - 1) / kWaves;  // >= one tile per wave
+  if (s > cap) s = cap;
+  if (s > 256) s = 256;
+  if (s < 1) s = 1;
+  return static_cast<int>(s);
+}
+
+extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream_) {
+  if (args == nullptr) return set_error(FD_E_INVALID, "fd_paged_decode: args is NULL");
+  const fd_paged_decode_args& a = *args;
+  if (a.struct_size != sizeof(fd_paged_decode_args))
+    return set_error(FD_E_INVALID, "fd_paged_decode: struct_size %u != %zu (ABI mismatch)", a.struct_size,
+                     sizeof(fd_paged_decode_args));
+  if (a.dtype != FD_DTYPE_F16 && a.dtype != FD_DTYPE_BF16)
+    return set_error(FD_E_UNSUPPORTED, "fd_paged_decode: dtype must be float16 or bfloat16");
+  if (a.num_seqs <= 0 || a.num_q_heads <= 0 || a.num_kv_heads <= 0 || a.num_blocks <= 0 ||
+      a.max_blocks_per_seq <= 0)
+    return set_error(FD_E_INVALID, "fd_paged_decode: shapes must be positive");
+  if (a.num_q_heads % a.num_kv_heads != 0)
+    return set_error(FD_E_INVALID, "fd_paged_decode: num_q_heads must be divisible by num_kv_heads");
+  if (a.head_dim != 64 && a.head_dim != 128)
+    return set_error(FD_E_UNSUPPORTED, "fd_paged_decode: head_dim must be 64 or 128");
+  if (a.block_size != 8 && a.block_size != 16 && a.block_size != 32)
+    return set_error(FD_E_UNSUPPORTED, "fd_paged_decode: block_size must be 8, 16 or 32");
+  if (!a.q || !a.k_cache || !a.v_cache || !a.block_tables || !a.seq_lens || !a.out)
+    return set_error(FD_E_INVALID, "fd_paged_decode: NULL tensor pointer");
+  if (a.num_splits < 1 || a.num_splits > 4096)
+    return set_error(FD_E_INVALID, "fd_paged_decode: num_splits must be in [1, 4096]");
+  if (a.num_splits > 1 && (!a.split_acc || !a.split_max || !a.split_sum))
+    return set_error(FD_E_INVALID, "fd_paged_decode: split workspace required for num_splits > 1");
+  const bool fuse = a.append_k != nullptr;
+  if (fuse != (a.append_v != nullptr) || fuse != (a.slot_mapping != nullptr))
+    return set_error(FD_E_INVALID, "fd_paged_decode: append_k, append_v and slot_mapping go together");
+  const int64_t pairs = a.num_seqs * a.num_kv_heads;
+  if (pairs * a.num_splits > 0x7fffffffLL || a.num_seqs * a.num_q_heads > 0x7fffffffLL)
+    return set_error(FD_E_INVALID, "fd_paged_decode: launch grid too large");
+
+  DecodeParams p{};
+  p.q = a.q;
+  p.qs0 = a.q_stride[0];
+  p.qs1 = a.q_stride[1];
+  p.qs2 = a.q_stride[2];
+  p.k = a.k_cache;
+  p.ks0 = a.k_stride[0];
+  p.ks1 = a.k_stride[1];
+  p.ks2 = a.k_stride[2];
+  p.ks3 = a.k_stride[3];
+  p.v = a.v_cache;
+  p.vs0 = a.v_stride[0];
+  p.vs1 = a.v_stride[1];
+  p.vs2 = a.v_stride[2];
+  p.vs3 = a.v_stride[3];
+  p.bt = a.block_tables;
+  p.bts0 = a.block_tables_stride[0];
+  p.bts1 = a.block_tables_stride[1];
+  p.bt_i64 = a.block_tables_dtype == FD_INDEX_I64;
+  p.sl = a.seq_lens;
+  p.sls = a.seq_lens_stride;
+  p.sl_i64 = a.seq_lens_dtype == FD_INDEX_I64;
+  p.out = a.out;
+  p.os0 = a.out_stride[0];
+  p.os1 = a.out_stride[1];
+  p.os2 = a.out_stride[2];
+  p.acc = a.split_acc;
+  p.as0 = a.split_acc_stride[0];
+  p.as1 = a.split_acc_stride[1];
+  p.as2 = a.split_acc_stride[2];
+  p.as3 = a.split_acc_stride[3];
+  p.mx = a.split_max;
+  p.sm = a.split_sum;
+  p.ss0 = a.split_stats_stride[0];
+  p.ss1 = a.split_stats_stride[1];
+  p.ss2 = a.split_stats_stride[2];
+  p.fuse = fuse ? 1 : 0;
+  if (fuse) {
+    p.ak = a.append_k;
+    p.aks0 = a.append_k_stride[0];
+    p.aks1 = a.append_k_stride[1];
+    p.aks2 = a.append_k_stride[2];
+    p.av = a.append_v;
+    p.avs0 = a.append_v_stride[0];
+    p.avs1 = a.append_v_stride[1];
+    p.avs2 = a.append_v_stride[2];
+    p.slot = a.slot_mapping;
+    p.slots = a.slot_mapping_stride;
+    p.slot_i64 = a.slot_mapping_dtype == FD_INDEX_I64;
+  }
+  p.num_seqs = static_cast<int>(a.num_seqs);
+  p.hq = static_cast<int>(a.num_q_heads);
+  p.hkv = static_cast<int>(a.num_kv_heads);
+  p.group = static_cast<int>(a.num_q_heads / a.num_kv_heads);
+  p.head_dim = static_cast<int>(a.head_dim);
+  p.block_size = static_cast<int>(a.block_size);
+  p.num_blocks = a.num_blocks;
+  p.max_blocks_per_seq = a.max_blocks_per_seq;
+  p.splits = a.num_splits;
+  p.scale_log2 = a.sm_scale * kLog2e;
+
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (a.dtype == FD_DTYPE_BF16) return launch_decode<__bf16>(a, p, stream);
+  return launch_decode<_Float16>(a, p, stream);
+}

@@ -1,0 +1,189 @@
+/*
+ * flashdec_hip.h -- C ABI of the MI355X (gfx950) paged-decode data path.
+ *
+ * Every entry point is stateless and re-entrant, allocates no device memory,
+ * never synchronises, launches on the caller's hipStream_t and returns an int
+ * status (FD_OK or a negative FD_E* code).  On error, fd_last_error() returns
+ * a thread-local, human-readable message.  Nothing here throws across the ABI.
+ *
+ * Tensors are passed as raw device pointers plus element strides, so strided
+ * views (vLLM's [block, plane, token, head, dim] cache, NHD/HND permutations,
+ * dim-major caches) are consumed in place without copies.
+ *
+ * Reference interfaces replaced (paths relative to cysong2025/flashdec):
+ *   fd_paged_decode          flashdec/kernels/paged_decode.py:972-1264
+ *                            (paged_decode_attention_into) and :728-919
+ *                            (_vllm_paged_decode_attention_into); the four
+ *                            Triton kernels at :28-642
+ *   fd_fused_rope_kv_append  flashdec/csrc/fused_rope_kv_append.cpp:90-124
+ *                            (bound from _fused_rope_kv_append.py:148-176)
+ *   fd_kv_append             flashdec/csrc/kv_append.cpp:60-73
+ *                            (bound from _cuda_kv_append.py:116-137)
+ *   fd_paged_decode_plan     flashdec/vllm_backend.py:168-188 chooses split
+ *                            counts for its launcher; this is the MI355X policy
+ */
+#ifndef FLASHDEC_HIP_H_
+#define FLASHDEC_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FD_ABI_VERSION 1
+
+/* status codes */
+#define FD_OK 0
+#define FD_E_INVALID (-1)     /* argument / shape / stride contract violated */
+#define FD_E_UNSUPPORTED (-2) /* valid but not implemented (dtype, head_dim) */
+#define FD_E_LAUNCH (-3)      /* hipLaunchKernel / hipGetLastError failure   */
+
+/* element dtypes */
+#define FD_DTYPE_F16 0
+#define FD_DTYPE_BF16 1
+#define FD_DTYPE_F32 2
+/* index dtypes */
+#define FD_INDEX_I32 0
+#define FD_INDEX_I64 1
+
+typedef struct ihipStream_t* fd_stream_t; /* == hipStream_t */
+
+/*
+ * Paged single-token decode attention.
+ *
+ * out[b, h, :] = softmax(q[b, h] . K_b^T * sm_scale) . V_b over the first
+ * seq_lens[b] tokens of request b, whose token t lives at physical block
+ * block_tables[b, t / block_size], offset t % block_size, KV head
+ * h / (num_q_heads / num_kv_heads).  seq_lens[b] == 0 gives a zero row.
+ *
+ * Cache strides are [block, head, token, dim] in elements; a 5-D vLLM cache
+ * is described by these strides plus the plane offset baked into the K and
+ * V base pointers.
+ *
+ * num_splits: 1 = single pass, S > 1 = split-KV with the caller's fp32
+ * workspace (split_acc [>=B, >=Hq, >=S, >=D], split_max/split_sum
+ * [>=B, >=Hq, >=S], identical strides for max and sum), followed by the LSE
+ * merge.  split_max holds base-2 log-domain maxima (internal format).
+ *
+ * Fused append (append_k, append_v, slot_mapping all non-NULL): the
+ * request's newest token (position seq_lens[b]-1) is taken from
+ * append_k/append_v instead of the cache, and written into the cache at
+ * slot_mapping[b] = block * block_size + offset by the split that owns it.
+ * Rows with slot_mapping[b] < 0 or seq_lens[b] == 0 are inert: no cache
+ * write and a zero output row (vLLM's graph-padding rows).
+ */
+typedef struct fd_paged_decode_args {
+  uint32_t struct_size; /* sizeof(fd_paged_decode_args): ABI guard */
+  int32_t dtype;        /* FD_DTYPE_F16 or FD_DTYPE_BF16 */
+  int64_t num_seqs;
+  int64_t num_q_heads;
+  int64_t num_kv_heads;
+  int64_t head_dim;  /* 64 or 128 */
+  int64_t block_size; /* 8, 16 or 32 */
+  int64_t num_blocks; /* physical blocks; ids outside [0, num_blocks) are masked */
+  int64_t max_blocks_per_seq;
+
+  const void* q;
+  int64_t q_stride[3]; /* seq, head, dim */
+  void* k_cache;
+  int64_t k_stride[4]; /* block, head, token, dim */
+  void* v_cache;
+  int64_t v_stride[4];
+  const void* block_tables;
+  int32_t block_tables_dtype; /* FD_INDEX_I32 / FD_INDEX_I64 */
+  int64_t block_tables_stride[2];
+  const void* seq_lens;
+  int32_t seq_lens_dtype;
+  int64_t seq_lens_stride;
+  void* out;
+  int64_t out_stride[3];
+
+  float sm_scale;
+  int32_t num_splits;
+  float* split_acc;
+  int64_t split_acc_stride[4]; /* seq, head, split, dim */
+  float* split_max;
+  float* split_sum;
+  int64_t split_stats_stride[3]; /* seq, head, split */
+
+  const void* append_k; /* optional fused append, all-or-none */
+  int64_t append_k_stride[3];
+  const void* append_v;
+  int64_t append_v_stride[3];
+  const void* slot_mapping;
+  int32_t slot_mapping_dtype;
+  int64_t slot_mapping_stride;
+} fd_paged_decode_args;
+
+int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
+
+/*
+ * Split count the library would pick for a launch of this shape on the
+ * current device (num_splits argument of fd_paged_decode).  max_seq_len is a
+ * host-side upper bound on seq_lens (e.g. max_blocks_per_seq * block_size).
+ * Returns >= 1, or a negative FD_E* code.
+ */
+int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads,
+                         int64_t num_kv_heads, int64_t head_dim,
+                         int64_t max_seq_len);
+
+/*
+ * Fused split-half (NeoX) RoPE of Q and K plus paged append of rotated K and
+ * raw V for one layer.  q/k/v/q_out are contiguous [B, H, D]; caches are
+ * contiguous token-major [num_blocks, Hkv, block_size, D].  Row b is written
+ * at (block_ids[b], block_offsets[b]) and rotated with positions[b].
+ *
+ * The rotation is bit-exact by construction: inv_freq and cos/sin are
+ * evaluated in float64 and rounded once to float32 (the correctly rounded
+ * values of flashdec/rope.py:66-71), then
+ *   out_lo = rn(rn(x_lo * cos) - rn(x_hi * sin)),
+ *   out_hi = rn(rn(x_hi * cos) + rn(x_lo * sin))
+ * without FMA contraction, rounded to the element dtype (RNE).  Dimensions
+ * past rotary_dim are copied.  Indices are range-checked in the kernel: a
+ * row whose block id or offset is out of range, or whose position is
+ * negative, writes nothing (q_out is still produced for valid positions).
+ */
+typedef struct fd_rope_append_args {
+  uint32_t struct_size;
+  int32_t dtype; /* FD_DTYPE_F16 / BF16 / F32 */
+  int64_t batch;
+  int64_t num_q_heads;
+  int64_t num_kv_heads;
+  int64_t head_dim;
+  int64_t block_size;
+  int64_t num_blocks;
+  int64_t rotary_dim;
+  double base;
+  void* q_out; /* may be NULL: K/V only */
+  const void* q;
+  const void* k;
+  const void* v;
+  void* k_cache;
+  void* v_cache;
+  const void* block_ids;
+  const void* block_offsets;
+  const void* positions;
+  int32_t index_dtype; /* FD_INDEX_I32 / FD_INDEX_I64, shared by the three */
+} fd_rope_append_args;
+
+int fd_fused_rope_kv_append(const fd_rope_append_args* args, fd_stream_t stream);
+
+/*
+ * K/V scatter without RoPE: k_cache[block_ids[b], h, block_offsets[b], :]
+ * = k[b, h, :] (same for v).  Uses fd_rope_append_args with q, q_out,
+ * positions, rotary_dim and base ignored.  Bit-exact copy.
+ */
+int fd_kv_append(const fd_rope_append_args* args, fd_stream_t stream);
+
+/* thread-local message for the last failing call on this thread */
+const char* fd_last_error(void);
+
+/* FD_ABI_VERSION of the loaded library */
+int fd_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHDEC_HIP_H_ */

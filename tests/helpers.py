@@ -1,0 +1,73 @@
+"""Shared builders for parity tests: seeded paged inputs and tolerance checks."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+# attention vs an fp32 reference within atol 2e-2 / rtol 1e-2
+ATOL = 2e-2
+RTOL = 1e-2
+
+
+def make_paged_inputs(
+    seq_lens,
+    num_q_heads,
+    num_kv_heads,
+    head_dim,
+    block_size,
+    dtype=torch.bfloat16,
+    seed=61,
+    device="cuda",
+    pool_factor=1.25,
+    kv_layout="token_major",
+    table_width=None,
+    pad_value=-1,
+):
+    """Random N(0,1) q and paged K/V with block tables drawn from a shuffled pool.
+
+    Each request's blocks are a slice of ``randperm(pool)`` so logical
+    neighbours are physically scattered (the reference's fixtures assert the
+    same property, tests/test_paged_decode.py:113).  Unused table slots hold
+    ``pad_value``.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    nblk = [(int(n) + block_size - 1) // block_size for n in seq_lens]
+    total = max(1, sum(nblk))
+    pool = max(total + 1, int(total * pool_factor))
+    width = max(1, max(nblk)) if table_width is None else table_width
+    perm = torch.randperm(pool, generator=gen)
+    table = torch.full((len(seq_lens), width), pad_value, dtype=torch.int32)
+    cursor = 0
+    for b, n in enumerate(nblk):
+        table[b, :n] = perm[cursor:cursor + n].to(torch.int32)
+        cursor += n
+    shape = (pool, num_kv_heads, block_size, head_dim)
+    k = torch.randn(shape, generator=gen).to(dtype)
+    v = torch.randn(shape, generator=gen).to(dtype)
+    q = torch.randn((len(seq_lens), num_q_heads, head_dim), generator=gen).to(dtype)
+    if kv_layout == "dim_major":
+        k = k.permute(0, 1, 3, 2).contiguous()
+        v = v.permute(0, 1, 3, 2).contiguous()
+    sl = torch.tensor([int(x) for x in seq_lens], dtype=torch.int32)
+    return q.to(device), k.to(device), v.to(device), table.to(device), sl.to(device)
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def assert_close_to_oracle(actual, expected, atol=ATOL, rtol=RTOL):
+    a = np32(actual)
+    e = np.asarray(expected, dtype=np.float32)
+    assert a.shape == e.shape, (a.shape, e.shape)
+    assert np.all(np.isfinite(a)), "non-finite output"
+    err = np.abs(a - e)
+    bound = atol + rtol * np.abs(e)
+    worst = float((err - bound).max())
+    assert worst <= 0, f"max |err| {float(err.max()):.3e} exceeds atol {atol} + rtol {rtol}*|ref| (by {worst:.3e})"
+
+
+def bits16(t):
+    """Bit patterns of a 16-bit float tensor (for bit-exact comparisons)."""
+    return t.detach().contiguous().view(torch.int16).cpu().numpy()
