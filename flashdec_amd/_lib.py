@@ -23,6 +23,7 @@ FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
 ABI_VERSION = 1
+SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -61,6 +62,8 @@ class PagedDecodeArgs(ctypes.Structure):
         ("split_max", _vp),
         ("split_sum", _vp),
         ("split_stats_stride", _i64 * 3),
+        ("split_counters", _vp),
+        ("max_seq_len", _i64),
         ("append_k", _vp),
         ("append_k_stride", _i64 * 3),
         ("append_v", _vp),

@@ -65,9 +65,16 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 }
 
 // -------------------------------------------------------------- indices --
-__device__ __forceinline__ int64_t load_index(const void* base, int64_t elem, int is64) {
-  return is64 ? static_cast<const int64_t*>(base)[elem]
-              : static_cast<int64_t>(static_cast<const int32_t*>(base)[elem]);
+// Branch-free read of an int32 or int64 index: the low 32-bit word of either
+// (little endian).  Every index on this path (block ids, lengths, slots,
+// positions) lies in int32 range -- a cache with 2^31 blocks or tokens would
+// not fit in device memory -- so no information is lost, and a uniform shift
+// replaces the per-load branch (and its wait) a dtype switch would compile to.
+// The value stays int32 so that nothing (e.g. a sign extension) consumes the
+// loaded register before its real use, which would force an early wait.
+__device__ __forceinline__ int32_t load_index(const void* base, int64_t elem, int is64) {
+  const char* ptr = static_cast<const char*>(base) + (elem << (is64 ? 3 : 2));
+  return *reinterpret_cast<const int32_t*>(ptr);
 }
 
 // ----------------------------------------------------------- wave utils --

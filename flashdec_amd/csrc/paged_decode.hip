@@ -41,6 +41,7 @@ struct DecodeParams {
   float* mx;
   float* sm;
   int64_t ss0, ss1, ss2;
+  uint32_t* counters;  // in-launch merge arrival counters (nullptr: reducer kernel)
   const void* ak;
   int64_t aks0, aks1, aks2;
   const void* av;
@@ -51,36 +52,49 @@ struct DecodeParams {
   int num_seqs, hq, hkv, group, head_dim, block_size;
   int64_t num_blocks, max_blocks_per_seq;
   int splits;
+  int hint_tiles;    // ceil(bound / 32): bound = max_seq_len or the table capacity
+  int hint_tps;      // tiles per split
   float scale_log2;  // sm_scale * log2(e): scores live in the base-2 domain
 };
 
-// Row-level bookkeeping shared by both decode kernels.
+// Row-level bookkeeping shared by the decode kernels.
 struct RowInfo {
-  int64_t eff_len;  // tokens attended (0 => zero output row)
-  int64_t app_tok;  // token taken from append_k/v (-1: none)
-  int64_t slot;     // cache slot receiving the appended token
-  int t_begin, t_end;  // tile range [t_begin, t_end) of this split (32-token tiles)
+  int64_t eff_len;     // tokens attended (0 => zero output row)
+  int64_t app_tok;     // token taken from append_k/v (-1: none)
+  int64_t slot;        // cache slot receiving the appended token
+  int t_begin, t_end;  // 32-token tiles [t_begin, t_end) of this split
 };
+
+__device__ __forceinline__ int64_t effective_len(const DecodeParams& p, int64_t seq_len, int64_t slot) {
+  bool active = seq_len > 0;
+  if (p.fuse) active = active && slot >= 0;
+  int64_t eff = active ? seq_len : 0;
+  // never walk past the block-table row, whatever seq_lens says
+  const int64_t cap = p.max_blocks_per_seq * p.block_size;
+  return eff < cap ? eff : cap;
+}
+
+// Split s covers tiles [s * tps, (s + 1) * tps) of the row, tps = ceil(T / S),
+// with T from the host bound when given (reads of the block table then need
+// not wait for seq_lens), else from the row's own length
+// (flashdec/kernels/paged_decode.py:408-411).  Tiles past the row's length
+// are skipped by the caller.
+__device__ __forceinline__ void split_range(const DecodeParams& p, int split, int64_t eff, int& t0, int& t1) {
+  const int total = p.hint_tiles > 0 ? p.hint_tiles : static_cast<int>((eff + 31) / 32);
+  const int tps = (total + p.splits - 1) / p.splits;
+  t0 = split * tps;
+  t1 = min(t0 + tps, total);
+}
 
 __device__ __forceinline__ RowInfo row_info(const DecodeParams& p, int b, int split) {
   RowInfo r;
   const int64_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
-  bool active = seq_len > 0;
-  r.slot = -1;
-  if (p.fuse) {
-    r.slot = load_index(p.slot, b * p.slots, p.slot_i64);
-    active = active && r.slot >= 0;
-  }
-  int64_t eff = active ? seq_len : 0;
-  // never walk past the block-table row, whatever seq_lens says
-  const int64_t cap = p.max_blocks_per_seq * p.block_size;
-  eff = eff < cap ? eff : cap;
-  r.eff_len = eff;
-  r.app_tok = (p.fuse && eff > 0) ? eff - 1 : -1;
-  const int num_tiles = static_cast<int>((eff + 31) / 32);
-  const int tps = (num_tiles + p.splits - 1) / p.splits;
-  r.t_begin = split * tps;
-  r.t_end = min(r.t_begin + tps, num_tiles);
+  r.slot = p.fuse ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
+  r.eff_len = effective_len(p, seq_len, r.slot);
+  r.app_tok = (p.fuse && r.eff_len > 0) ? r.eff_len - 1 : -1;
+  split_range(p, split, r.eff_len, r.t_begin, r.t_end);
+  const int live = static_cast<int>((r.eff_len + 31) / 32);
+  r.t_end = min(r.t_end, live);
   return r;
 }
 
@@ -105,106 +119,111 @@ __device__ __forceinline__ f32x4 mfma16x16x32<_Float16>(u32x4 a, u32x4 b, f32x4 
 // vtok(g, i) = 4*g + i (i < 4) or 16 + 4*g + (i - 4): the same tokens whose
 // scores this lane holds after QK (MFMA D layout: rows 4*g + r of each
 // 16-row tile), so P needs no cross-lane movement.
+//
+// Load addresses depend only on the block table, never on seq_lens: tokens
+// past the row's length and rows whose block id is out of range are masked
+// in registers at compute time, so the K/V loads of the first tile can be in
+// flight before the row length arrives.
 struct TileRegs {
   u32x4 kf[2][4];
   u32x4 vf[8];
-  uint32_t vmask;  // bit i: V row i is a real token
+  uint32_t bmask;  // bit i: V row i lies in a valid physical block
 };
 
 __device__ __forceinline__ int vtok(int g, int i) { return i < 4 ? 4 * g + i : 12 + 4 * g + i; }
 
-// Physical block of a token, read with the token clamped to the last attended
-// one so the block-table read stays inside the row.  A 32-token tile shares
-// one table entry for 32-token blocks and two for 16-token blocks.
-template <typename T, int BS>
-__device__ __forceinline__ void load_tile(const DecodeParams& p, int b, int kvh, const RowInfo& r,
-                                          int tile, int c, int g, TileRegs& t) {
-  const int64_t tok0 = static_cast<int64_t>(tile) * 32;
-  const int64_t last = r.eff_len - 1;  // >= tok0 for any tile in range
-  const T* kbase = static_cast<const T*>(p.k);
-  const T* vbase = static_cast<const T*>(p.v);
-  const int64_t btrow = b * p.bts0;
-  int64_t blk_a = 0, blk_b = 0;
+// Physical block ids a tile needs.  The tile index is wave-uniform, so for
+// 32- and 16-token blocks these are scalar loads; pages are clamped to the
+// table row so the read is in bounds whatever the row's length.
+struct TilePages {
+  int32_t a, b;
+};
+
+template <int BS>
+__device__ __forceinline__ TilePages fetch_pages(const DecodeParams& p, int b, int tile) {
+  TilePages tp{0, 0};
+  const int64_t row = b * p.bts0;
+  const int64_t width = p.max_blocks_per_seq;
   if constexpr (BS == 32) {
-    blk_a = load_index(p.bt, btrow + tile * p.bts1, p.bt_i64);
+    const int64_t pg = tile < width ? tile : width - 1;
+    tp.a = load_index(p.bt, row + pg * p.bts1, p.bt_i64);
   } else if constexpr (BS == 16) {
-    const int64_t pa = 2 * static_cast<int64_t>(tile);
+    int64_t pa = 2 * static_cast<int64_t>(tile);
     int64_t pb = pa + 1;
-    pb = pb <= last / 16 ? pb : pa;
-    blk_a = load_index(p.bt, btrow + pa * p.bts1, p.bt_i64);
-    blk_b = load_index(p.bt, btrow + pb * p.bts1, p.bt_i64);
+    pa = pa < width ? pa : width - 1;
+    pb = pb < width ? pb : width - 1;
+    tp.a = load_index(p.bt, row + pa * p.bts1, p.bt_i64);
+    tp.b = load_index(p.bt, row + pb * p.bts1, p.bt_i64);
   }
-  auto block_of = [&](int64_t tok, int64_t tq) -> int64_t {
-    if constexpr (BS == 32) {
-      (void)tok;
-      (void)tq;
-      return blk_a;
-    } else if constexpr (BS == 16) {
-      (void)tq;
-      return (tok - tok0) < 16 ? blk_a : blk_b;
-    } else {
-      (void)tok;
-      return load_index(p.bt, btrow + (tq / BS) * p.bts1, p.bt_i64);
-    }
-  };
-  // K: rows 16*mt + c
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int64_t tok = tok0 + 16 * mt + c;
-    const int64_t tq = tok < last ? tok : last;
-    const int64_t blk = block_of(tok, tq);
-    const bool ok = tok <= last && blk >= 0 && blk < p.num_blocks;
-    const T* row;
-    if (tok == r.app_tok) {
-      row = static_cast<const T*>(p.ak) + b * p.aks0 + kvh * p.aks1;
-    } else {
-      row = ok ? kbase + blk * p.ks0 + kvh * p.ks1 + (tq % BS) * p.ks2 : kbase;
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      t.kf[mt][s] = *reinterpret_cast<const u32x4*>(row + 32 * s + 8 * g);
-  }
-  // V: rows vtok(g, i)
-  uint32_t vm = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t tok = tok0 + vtok(g, i);
-    const int64_t tq = tok < last ? tok : last;
-    const int64_t blk = block_of(tok, tq);
-    const bool ok = tok <= last && blk >= 0 && blk < p.num_blocks;
-    const T* row;
-    if (tok == r.app_tok) {
-      row = static_cast<const T*>(p.av) + b * p.avs0 + kvh * p.avs1;
-      vm |= 1u << i;
-    } else {
-      row = ok ? vbase + blk * p.vs0 + kvh * p.vs1 + (tq % BS) * p.vs2 : vbase;
-      vm |= ok ? (1u << i) : 0u;
-    }
-    t.vf[i] = *reinterpret_cast<const u32x4*>(row + 8 * c);
-  }
-  t.vmask = vm;
+  return tp;
 }
 
-// Fused append: the lanes holding the newest token's K/V pieces store them at
-// the request's slot (the same bytes they feed to QK/PV from registers).
 template <typename T, int BS>
-__device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, const RowInfo& r, int tile,
-                                             int c, int g, const TileRegs& t) {
-  const int64_t blk = r.slot / BS, off = r.slot % BS;
-  if (blk >= p.num_blocks) return;
-  const int at = static_cast<int>(r.app_tok - static_cast<int64_t>(tile) * 32);
-  if ((at & 15) == c) {
-    T* dst = static_cast<T*>(p.k) + blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
+__device__ __forceinline__ void load_tile(const DecodeParams& p, int b, int kvh, int tile, const TilePages& tp,
+                                          int c, int g, TileRegs& t) {
+  const int64_t tok0 = static_cast<int64_t>(tile) * 32;
+  const T* kbase = static_cast<const T*>(p.k);
+  const T* vbase = static_cast<const T*>(p.v);
+  auto block_of = [&](int tt) -> int32_t {  // tt: token within the tile
+    if constexpr (BS == 32) {
+      (void)tt;
+      return tp.a;
+    } else if constexpr (BS == 16) {
+      return tt < 16 ? tp.a : tp.b;
+    } else {
+      int64_t pg = (tok0 + tt) / BS;
+      pg = pg < p.max_blocks_per_seq ? pg : p.max_blocks_per_seq - 1;
+      return load_index(p.bt, b * p.bts0 + pg * p.bts1, p.bt_i64);
+    }
+  };
+  // K: rows 16*mt + c.  Rows in invalid blocks read row 0 of the cache
+  // (in bounds, value discarded by the score mask).
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      *reinterpret_cast<u32x4*>(dst + 32 * s + 8 * g) = (at >> 4) ? t.kf[1][s] : t.kf[0][s];
+  for (int mt = 0; mt < 2; ++mt) {
+    const int tt = 16 * mt + c;
+    const int32_t blk = block_of(tt);
+    const bool ok = blk >= 0 && blk < p.num_blocks;
+    const int64_t off = ok ? blk * p.ks0 + kvh * p.ks1 + (tt % BS) * p.ks2 : 0;
+    const T* row = kbase + off;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) t.kf[mt][s] = *reinterpret_cast<const u32x4*>(row + 32 * s + 8 * g);
   }
+  // V: rows vtok(g, i)
+  uint32_t bm = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    if (vtok(g, i) == at) {
-      T* dst = static_cast<T*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
-      *reinterpret_cast<u32x4*>(dst + 8 * c) = t.vf[i];
-    }
+    const int tt = vtok(g, i);
+    const int32_t blk = block_of(tt);
+    const bool ok = blk >= 0 && blk < p.num_blocks;
+    const int64_t off = ok ? blk * p.vs0 + kvh * p.vs1 + (tt % BS) * p.vs2 : 0;
+    bm |= ok ? (1u << i) : 0u;
+    t.vf[i] = *reinterpret_cast<const u32x4*>(vbase + off + 8 * c);
+  }
+  t.bmask = bm;
+}
+
+// The appended token's pieces in this lane's operand layout: akf[s] = dims
+// [32*s + 8*g, +8) of append_k, avf = dims [8*c, +8) of append_v.
+struct AppendRegs {
+  u32x4 akf[4];
+  u32x4 avf;
+};
+
+// Fused append: store the newest token's K/V at the request's slot.  Lanes
+// c == 0 write the K row (4 x 4 x 16 B), lanes g == 0 the V row (16 x 16 B).
+template <typename T, int BS>
+__device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, int32_t slot, int c, int g,
+                                             const AppendRegs& ar) {
+  const int64_t blk = slot / BS, off = slot % BS;
+  if (blk >= p.num_blocks) return;
+  if (c == 0) {
+    T* dst = static_cast<T*>(p.k) + blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) *reinterpret_cast<u32x4*>(dst + 32 * s + 8 * g) = ar.akf[s];
+  }
+  if (g == 0) {
+    T* dst = static_cast<T*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
+    *reinterpret_cast<u32x4*>(dst + 8 * c) = ar.avf;
   }
 }
 
@@ -215,9 +234,31 @@ struct WaveState {
   float l;       // partial denominator of this lane's tokens
 };
 
-template <typename T>
-__device__ __forceinline__ void process_tile(const TileRegs& t, const u32x4 (&qf)[4], float scale_log2,
+// One tile: mask (row length, invalid blocks), splice in the appended token,
+// QK^T, online softmax, PV.  `last` is the last attended token, `app` the
+// token taken from the append registers (-1: none).
+template <typename T, bool FUSE>
+__device__ __forceinline__ void process_tile(TileRegs& t, const u32x4 (&qf)[4], float scale_log2, int64_t tok0,
+                                             int64_t last, int64_t app, const AppendRegs& ar, int c, int g,
                                              WaveState& st) {
+  uint32_t vmask = t.bmask;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) vmask &= (tok0 + vtok(g, i) <= last) ? ~0u : ~(1u << i);
+  if constexpr (FUSE) {
+    const int64_t at = app - tok0;  // in [0, 32) only for the tile holding it
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const bool hit = at == 16 * mt + c;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) t.kf[mt][s] = hit ? ar.akf[s] : t.kf[mt][s];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool hit = at == vtok(g, i);
+      t.vf[i] = hit ? ar.avf : t.vf[i];
+      vmask |= hit ? (1u << i) : 0u;
+    }
+  }
   // S^T[token][head] = K . Q^T  (two 16-token row tiles)
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -234,7 +275,7 @@ __device__ __forceinline__ void process_tile(const TileRegs& t, const u32x4 (&qf
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    sc[i] = (t.vmask >> i) & 1u ? sc[i] : -INFINITY;
+    sc[i] = (vmask >> i) & 1u ? sc[i] : -INFINITY;
     mx = fmaxf(mx, sc[i]);
   }
   mx = fmaxf(mx, shfl_xor_f32(mx, 16));
@@ -275,7 +316,7 @@ __device__ __forceinline__ void process_tile(const TileRegs& t, const u32x4 (&qf
   u32x4 vz[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const bool keep = (t.vmask >> i) & 1u;
+    const bool keep = (vmask >> i) & 1u;
     vz[i][0] = keep ? t.vf[i][0] : 0u;
     vz[i][1] = keep ? t.vf[i][1] : 0u;
     vz[i][2] = keep ? t.vf[i][2] : 0u;
@@ -297,16 +338,38 @@ __device__ __forceinline__ void process_tile(const TileRegs& t, const u32x4 (&qf
 }
 
 constexpr int kWaves = 4;
-constexpr int kAccPitch = 132;  // floats per head row in LDS (bank spread)
+constexpr int kAccPitch = 132;   // floats per head row in LDS (bank spread)
+constexpr int kMergeChunk = 16;  // splits whose partials one merge pass loads at once
+// One arrival counter per 256-byte line: counters sharing a line serialise
+// every workgroup's atomic on that line (measured ~3x slower arrival).
+constexpr int kCounterStride = FD_SPLIT_COUNTER_STRIDE;
 
-template <typename T, int BS>
+template <typename T>
+__device__ __forceinline__ void store_row(const DecodeParams& p, int b, int qh, int d0, const float (&o)[8],
+                                          float inv) {
+  T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1 + d0 * p.os2;
+  if (p.os2 == 1) {
+    u32x4 w;
+    w[0] = pack2<T>(o[0] * inv, o[1] * inv);
+    w[1] = pack2<T>(o[2] * inv, o[3] * inv);
+    w[2] = pack2<T>(o[4] * inv, o[5] * inv);
+    w[3] = pack2<T>(o[6] * inv, o[7] * inv);
+    *reinterpret_cast<u32x4*>(dst) = w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dst[j * p.os2] = from_f32<T>(o[j] * inv);
+  }
+}
+
+template <typename T, int BS, bool FUSE, bool MERGE>
 __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   __shared__ float s_acc[kWaves][16][kAccPitch];
   __shared__ float s_m[kWaves][16];
   __shared__ float s_l[kWaves][16];
+  __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
   const int split = blockIdx.x % p.splits;
@@ -315,7 +378,14 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   const int kvh = pair % p.hkv;
   const int G = p.group;
 
-  // Q^T operand: query head kvh*G + c, dims [32*s + 8*g, +8)
+  // Independent loads first.  The split geometry comes from the host bound
+  // (hint_tiles / hint_tps); the first tile's block ids and K/V rows, the
+  // Q^T operand, the append row and the row length / slot are all in flight
+  // together -- no load address depends on seq_lens.
+  const int t_begin = split * p.hint_tps;
+  const int t_end = min(t_begin + p.hint_tps, p.hint_tiles);
+  int tile = t_begin + wave;
+  TilePages pages = fetch_pages<BS>(p, b, tile);  // clamped, always in bounds
   u32x4 qf[4];
   {
     const bool hv = c < G;
@@ -326,7 +396,23 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
       qf[s] = hv ? x : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  const RowInfo r = row_info(p, b, split);
+  AppendRegs ar;
+  if constexpr (FUSE) {
+    const T* ak = static_cast<const T*>(p.ak) + b * p.aks0 + kvh * p.aks1;
+    const T* av = static_cast<const T*>(p.av) + b * p.avs0 + kvh * p.avs1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ar.akf[s] = *reinterpret_cast<const u32x4*>(ak + 32 * s + 8 * g);
+    ar.avf = *reinterpret_cast<const u32x4*>(av + 8 * c);
+  }
+  const int32_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
+  const int32_t slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
+  TileRegs cur;
+  load_tile<T, BS>(p, b, kvh, tile, pages, c, g, cur);
+
+  const int64_t eff_len = effective_len(p, seq_len, slot);
+  const int64_t last = eff_len - 1;
+  const int64_t app = (FUSE && eff_len > 0) ? last : -1;
+  const int live_end = min(t_end, static_cast<int>((eff_len + 31) / 32));
 
   WaveState st;
 #pragma unroll
@@ -334,21 +420,27 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   st.m = -INFINITY;
   st.l = 0.f;
 
-  int tile = r.t_begin + wave;
-  if (tile < r.t_end) {
-    TileRegs cur;
-    load_tile<T, BS>(p, b, kvh, r, tile, c, g, cur);
+  if (tile < live_end) {
+    TilePages next_pages{0, 0};
+    if (tile + kWaves < live_end) next_pages = fetch_pages<BS>(p, b, tile + kWaves);
     for (;;) {
-      // issue the next tile's loads before consuming the current one
+      // issue the next tile's loads (and the block ids after it) before
+      // consuming the current tile
       const int next = tile + kWaves;
-      const bool more = next < r.t_end;
+      const bool more = next < live_end;
       TileRegs nxt;
-      if (more) load_tile<T, BS>(p, b, kvh, r, next, c, g, nxt);
-      if (r.app_tok >= 0 && r.app_tok / 32 == tile) store_append<T, BS>(p, kvh, r, tile, c, g, cur);
-      process_tile<T>(cur, qf, p.scale_log2, st);
+      TilePages after{0, 0};
+      if (more) {
+        load_tile<T, BS>(p, b, kvh, next, next_pages, c, g, nxt);
+        if (next + kWaves < live_end) after = fetch_pages<BS>(p, b, next + kWaves);
+      }
+      if constexpr (FUSE)
+        if (app >= 0 && app / 32 == tile) store_append<T, BS>(p, kvh, slot, c, g, ar);
+      process_tile<T, FUSE>(cur, qf, p.scale_log2, static_cast<int64_t>(tile) * 32, last, app, ar, c, g, st);
       if (!more) break;
       cur = nxt;
       tile = next;
+      next_pages = after;
     }
   }
   // denominator over the four lanes (g) that share query head c
@@ -370,7 +462,8 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   // merge the four waves: thread -> (head h, dims [d0, d0 + 8))
   const int h = threadIdx.x >> 4;
   const int d0 = (threadIdx.x & 15) * 8;
-  if (h >= G) return;
+  const bool head_ok = h < G;
+  const int qh = kvh * G + h;
   float M = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
@@ -389,31 +482,104 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
       o[4 + j] += wt * a1[j];
     }
   }
-  const int qh = kvh * G + h;
   if (p.splits == 1) {
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1 + d0 * p.os2;
-    if (p.os2 == 1) {
-      u32x4 w;
-      w[0] = pack2<T>(o[0] * inv, o[1] * inv);
-      w[1] = pack2<T>(o[2] * inv, o[3] * inv);
-      w[2] = pack2<T>(o[4] * inv, o[5] * inv);
-      w[3] = pack2<T>(o[6] * inv, o[7] * inv);
-      *reinterpret_cast<u32x4*>(dst) = w;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) dst[j * p.os2] = from_f32<T>(o[j] * inv);
-    }
-  } else {
+    if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
+    return;
+  }
+  // split partial: unnormalised acc, base-2 max, denominator
+  if (head_ok) {
     float* a = p.acc + b * p.as0 + qh * p.as1 + split * p.as2 + d0 * p.as3;
+    const int64_t so = b * p.ss0 + qh * p.ss1 + split * p.ss2;
+    if constexpr (MERGE) {
+      // device-coherent (sc1) stores, visible to every XCD once acknowledged;
+      // the host guarantees unit dim stride and 8-byte alignment here
+      uint64_t* a64 = reinterpret_cast<uint64_t*>(a);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) a[j * p.as3] = o[j];
-    if (d0 == 0) {
-      const int64_t so = b * p.ss0 + qh * p.ss1 + split * p.ss2;
-      p.mx[so] = M;
-      p.sm[so] = L;
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t bits = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, o[2 * j])) |
+                              (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, o[2 * j + 1])) << 32);
+        __hip_atomic_store(a64 + j, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (d0 == 0) {
+        __hip_atomic_store(p.mx + so, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.sm + so, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      if (p.as3 == 1) {
+        *reinterpret_cast<f32x4*>(a) = f32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<f32x4*>(a + 4) = f32x4{o[4], o[5], o[6], o[7]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j * p.as3] = o[j];
+      }
+      if (d0 == 0) {
+        p.mx[so] = M;
+        p.sm[so] = L;
+      }
     }
   }
+  if constexpr (!MERGE) return;  // the reducer kernel merges
+
+  // In-launch merge.  Partials were written with agent-scope atomic stores
+  // (sc1, coherent across the XCD L2s); waiting for their acknowledgement
+  // (vmcnt 0) before the arrival increment is the release for them, without
+  // the L2-wide write-back an agent-scope fence would do in every
+  // workgroup.  The last workgroup of this (request, KV head) to arrive reads
+  // them back with agent-scope atomic loads -- all loads of a chunk of
+  // splits issued before any is used -- merges, and returns the counter to
+  // zero for the next launch.
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(p.counters + pair * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == static_cast<uint32_t>(p.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(p.counters + pair * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!head_ok) return;
+
+  const int64_t sb = b * p.ss0 + qh * p.ss1;
+  const float* ab = p.acc + b * p.as0 + qh * p.as1 + d0 * p.as3;
+  float GM = -INFINITY;
+  float GL = 0.f;
+  float go[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < p.splits; s0 += kMergeChunk) {
+    uint64_t raw[kMergeChunk][4];
+    float pm[kMergeChunk], pl[kMergeChunk];
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int ss = min(s0 + j, p.splits - 1);  // past the end: re-read, masked below
+      const uint64_t* a64 = reinterpret_cast<const uint64_t*>(ab + ss * p.as2);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) raw[j][k] = __hip_atomic_load(a64 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pm[j] = __hip_atomic_load(p.mx + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pl[j] = __hip_atomic_load(p.sm + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float cm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) cm = s0 + j < p.splits ? fmaxf(cm, pm[j]) : cm;
+    const float nm = fmaxf(GM, cm);
+    const float nmu = nm == -INFINITY ? 0.f : nm;
+    const float sc = exp2f(GM - nmu);
+    GL *= sc;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) go[j] *= sc;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const float w = s0 + j < p.splits ? exp2f(pm[j] - nmu) : 0.f;
+      GL += w * pl[j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        go[2 * k] += w * __builtin_bit_cast(float, static_cast<uint32_t>(raw[j][k]));
+        go[2 * k + 1] += w * __builtin_bit_cast(float, static_cast<uint32_t>(raw[j][k] >> 32));
+      }
+    }
+    GM = nm;
+  }
+  if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
 }
 
 // ====================================================== generic path ====
@@ -558,39 +724,59 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p, int 
 
 // ===================================================== split reducer ====
 // One wave per (request, query head): out = sum_s w_s acc_s / sum_s w_s l_s,
-// w_s = 2^(m_s - max_s m_s).
-template <typename T>
+// w_s = 2^(m_s - max_s m_s).  Splits are taken 16 at a time and every load of
+// a chunk is issued before any is used, so the merge costs one memory round
+// trip per 16 splits (the split statistics are wave-uniform scalar loads).
+constexpr int kReduceChunk = 16;
+
+template <typename T, int D>
 __global__ __launch_bounds__(64) void split_reduce_kernel(DecodeParams p) {
   const int b = blockIdx.x / p.hq;
   const int qh = blockIdx.x % p.hq;
   const int lane = threadIdx.x;
-  const int D = p.head_dim;
+  constexpr int E = D / 64;  // dims per lane
   const int64_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
-  bool has = seq_len > 0;
-  if (p.fuse) has = has && load_index(p.slot, b * p.slots, p.slot_i64) >= 0;
+  const int64_t slot = p.fuse ? load_index(p.slot, b * p.slots, p.slot_i64) : 0;
   const int64_t sb = b * p.ss0 + qh * p.ss1;
-  float M = -INFINITY;
-  if (has)
-    for (int s = 0; s < p.splits; ++s) M = fmaxf(M, p.mx[sb + s * p.ss2]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  float o0 = 0.f, o1 = 0.f;
   const float* ab = p.acc + b * p.as0 + qh * p.as1;
-  if (has) {
-    for (int s = 0; s < p.splits; ++s) {
-      const float ms = p.mx[sb + s * p.ss2];
-      if (ms == -INFINITY) continue;
-      const float w = exp2f(ms - Mu);
-      L += w * p.sm[sb + s * p.ss2];
-      const float* a = ab + s * p.as2;
-      o0 += w * a[lane * p.as3];
-      if (D > 64) o1 += w * a[(lane + 64) * p.as3];
+  float M = -INFINITY;
+  float L = 0.f;
+  float o[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) o[e] = 0.f;
+  for (int s0 = 0; s0 < p.splits; s0 += kReduceChunk) {
+    float m[kReduceChunk], l[kReduceChunk], a[kReduceChunk][E];
+#pragma unroll
+    for (int j = 0; j < kReduceChunk; ++j) {
+      const int s = min(s0 + j, p.splits - 1);  // past the end: re-read, masked below
+      m[j] = p.mx[sb + s * p.ss2];
+      l[j] = p.sm[sb + s * p.ss2];
+#pragma unroll
+      for (int e = 0; e < E; ++e) a[j][e] = ab[s * p.as2 + (lane + 64 * e) * p.as3];
     }
+    float cm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kReduceChunk; ++j) cm = s0 + j < p.splits ? fmaxf(cm, m[j]) : cm;
+    const float nm = fmaxf(M, cm);
+    const float nmu = nm == -INFINITY ? 0.f : nm;
+    const float sc = exp2f(M - nmu);
+    L *= sc;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] *= sc;
+#pragma unroll
+    for (int j = 0; j < kReduceChunk; ++j) {
+      const float w = s0 + j < p.splits ? exp2f(m[j] - nmu) : 0.f;
+      L += w * l[j];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
+    }
+    M = nm;
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const bool has = seq_len > 0 && (!p.fuse || slot >= 0);
+  const float inv = (has && L > 0.f) ? 1.f / L : 0.f;
   T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1;
-  dst[lane * p.os2] = from_f32<T>(o0 * inv);
-  if (D > 64) dst[(lane + 64) * p.os2] = from_f32<T>(o1 * inv);
+#pragma unroll
+  for (int e = 0; e < E; ++e) dst[(lane + 64 * e) * p.os2] = from_f32<T>(o[e] * inv);
 }
 
 // ========================================================== host glue ====
@@ -630,15 +816,37 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
   return true;
 }
 
+template <typename T, int BS>
+void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream) {
+  const bool merge = p.counters != nullptr;
+  if (p.fuse) {
+    if (merge)
+      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, true, true>), grid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, true, false>), grid, dim3(256), 0, stream, p);
+  } else {
+    if (merge)
+      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, false, true>), grid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, false, false>), grid, dim3(256), 0, stream, p);
+  }
+}
+
 template <typename T>
 int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
-  if (fast_path_ok(a, p.group)) {
+  const bool fast = fast_path_ok(a, p.group);
+  // the in-launch merge exists only in the MFMA kernel and writes the
+  // workspace with 8-byte stores (unit dim stride, 8-byte aligned rows)
+  if (!fast || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
+      (reinterpret_cast<uintptr_t>(p.acc) & 7u))
+    p.counters = nullptr;
+  if (fast) {
     const dim3 grid(static_cast<unsigned>(pairs * p.splits));
     switch (a.block_size) {
-      case 8: hipLaunchKernelGGL((decode_mfma_kernel<T, 8>), grid, dim3(256), 0, stream, p); break;
-      case 16: hipLaunchKernelGGL((decode_mfma_kernel<T, 16>), grid, dim3(256), 0, stream, p); break;
-      default: hipLaunchKernelGGL((decode_mfma_kernel<T, 32>), grid, dim3(256), 0, stream, p); break;
+      case 8: launch_mfma<T, 8>(p, grid, stream); break;
+      case 16: launch_mfma<T, 16>(p, grid, stream); break;
+      default: launch_mfma<T, 32>(p, grid, stream); break;
     }
   } else {
     const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
@@ -650,9 +858,12 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
-  if (p.splits > 1) {
-    hipLaunchKernelGGL((split_reduce_kernel<T>), dim3(static_cast<unsigned>(a.num_seqs * a.num_q_heads)),
-                       dim3(64), 0, stream, p);
+  if (p.splits > 1 && p.counters == nullptr) {
+    const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
+    if (a.head_dim == 64)
+      hipLaunchKernelGGL((split_reduce_kernel<T, 64>), grid, dim3(64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((split_reduce_kernel<T, 128>), grid, dim3(64), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
   }
@@ -748,6 +959,7 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
   p.ss0 = a.split_stats_stride[0];
   p.ss1 = a.split_stats_stride[1];
   p.ss2 = a.split_stats_stride[2];
+  p.counters = a.num_splits > 1 ? a.split_counters : nullptr;
   p.fuse = fuse ? 1 : 0;
   if (fuse) {
     p.ak = a.append_k;
@@ -771,6 +983,15 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
   p.num_blocks = a.num_blocks;
   p.max_blocks_per_seq = a.max_blocks_per_seq;
   p.splits = a.num_splits;
+  if (a.max_seq_len < 0) return set_error(FD_E_INVALID, "fd_paged_decode: max_seq_len must be >= 0");
+  {
+    // split geometry: from max_seq_len when given, else from the table width
+    // (seq_lens are clamped to it in the kernels anyway)
+    const int64_t cap = a.max_blocks_per_seq * a.block_size;
+    const int64_t bound = (a.max_seq_len > 0 && a.max_seq_len < cap) ? a.max_seq_len : cap;
+    p.hint_tiles = static_cast<int>((bound + 31) / 32);
+    p.hint_tps = (p.hint_tiles + p.splits - 1) / p.splits;
+  }
   p.scale_log2 = a.sm_scale * kLog2e;
 
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);

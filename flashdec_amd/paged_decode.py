@@ -138,7 +138,7 @@ def _fill_common(args, q, k_cache, v_cache, k_strides, v_strides, block_tables, 
     args.sm_scale = float(sm_scale)
 
 
-def _fill_workspace(args, acc, mx, sm, num_splits):
+def _fill_workspace(args, acc, mx, sm, num_splits, counters=None):
     args.num_splits = num_splits
     if num_splits > 1:
         args.split_acc = acc.data_ptr()
@@ -146,6 +146,8 @@ def _fill_workspace(args, acc, mx, sm, num_splits):
         args.split_max = mx.data_ptr()
         args.split_sum = sm.data_ptr()
         args.split_stats_stride[:] = mx.stride()
+        if counters is not None:
+            args.split_counters = counters.data_ptr()
 
 
 def _fill_append(args, append_k, append_v, slot_mapping):
@@ -158,13 +160,50 @@ def _fill_append(args, append_k, append_v, slot_mapping):
     args.slot_mapping_stride = slot_mapping.stride(0)
 
 
-def _auto_workspace(q, num_splits):
-    """Scratch for library-chosen splits: one fp32 allocation, carved in three."""
+class _SplitWorkspace:
+    """fp32 split partials (plus zeroed arrival counters), reused across calls.
+
+    One per (device, stream): launches on one stream are ordered.  The
+    library-chosen split path merges with the second (reducer) kernel, which
+    measured faster on MI355X than the in-launch merge (whose arrival atomics
+    serialise at the memory side); the counters are kept for callers that opt
+    into the in-launch merge and are left at zero by every launch.  Inside a
+    graph capture with no workspace yet for the capturing stream, a private
+    one is allocated for that call only.
+    """
+
+    __slots__ = ("flat", "counters")
+
+    def __init__(self, device, floats, counters):
+        self.flat = torch.empty(floats, device=device, dtype=torch.float32)
+        self.counters = torch.zeros(counters, device=device, dtype=torch.int32)
+
+    def views(self, num_seqs, num_q_heads, num_splits, head_dim):
+        n = num_seqs * num_q_heads * num_splits * (head_dim + 2)
+        view = self.flat[:n].view(num_seqs, num_q_heads, num_splits, head_dim + 2)
+        return view[..., :head_dim], view[..., head_dim], view[..., head_dim + 1], self.counters
+
+
+_WORKSPACES = {}
+
+
+def _auto_workspace(q, num_kv_heads, num_splits, stream):
     num_seqs, num_q_heads, head_dim = q.shape
-    per = num_splits * (head_dim + 2)
-    flat = torch.empty(num_seqs * num_q_heads * per, device=q.device, dtype=torch.float32)
-    view = flat.view(num_seqs, num_q_heads, num_splits, head_dim + 2)
-    return view[..., :head_dim], view[..., head_dim], view[..., head_dim + 1]
+    floats = num_seqs * num_q_heads * num_splits * (head_dim + 2)
+    counters = num_seqs * num_kv_heads * _lib.SPLIT_COUNTER_STRIDE
+    key = (q.device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.flat.numel() < floats or ws.counters.numel() < counters:
+        if torch.cuda.is_current_stream_capturing():
+            return _SplitWorkspace(q.device, floats, counters).views(num_seqs, num_q_heads, num_splits, head_dim)
+        grow = 1 if ws is None else 2
+        ws = _SplitWorkspace(
+            q.device,
+            max(floats, grow * (ws.flat.numel() if ws else 0)),
+            max(counters, grow * (ws.counters.numel() if ws else 0)),
+        )
+        _WORKSPACES[key] = ws
+    return ws.views(num_seqs, num_q_heads, num_splits, head_dim)
 
 
 def paged_decode_attention(
@@ -301,12 +340,14 @@ def paged_decode_attention_into(
             raise ValueError("split sum workspace is too small")
         if split_sum.stride() != split_max.stride():
             raise ValueError("split max and sum workspaces must have identical strides")
-    else:
-        max_seq_len = block_tables.shape[1] * block_size
+    max_seq_len = block_tables.shape[1] * block_size
+    stream = _lib.current_stream_handle(q.device)
+    counters = None
+    if not use_split_kv:
         num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
         split_acc = split_max = split_sum = None
         if num_splits > 1:
-            split_acc, split_max, split_sum = _auto_workspace(q, num_splits)
+            split_acc, split_max, split_sum, _ = _auto_workspace(q, num_kv_heads, num_splits, stream)
 
     args = _lib.PagedDecodeArgs()
     _fill_common(
@@ -324,10 +365,11 @@ def paged_decode_attention_into(
         sm_scale,
     )
     args.num_blocks = k_cache.shape[0]
-    _fill_workspace(args, split_acc, split_max, split_sum, num_splits)
+    args.max_seq_len = max_seq_len
+    _fill_workspace(args, split_acc, split_max, split_sum, num_splits, counters)
     if fuse_kv_append:
         _fill_append(args, append_k, append_v, slot_mapping)
-    _lib.paged_decode(args, _lib.current_stream_handle(q.device))
+    _lib.paged_decode(args, stream)
     return out
 
 
@@ -351,6 +393,8 @@ def _vllm_paged_decode_attention_into(
     block_size,
     sm_scale,
     num_splits,
+    split_counters=None,
+    max_seq_len=None,
 ):
     """Checked-by-caller vLLM launcher (paged_decode.py:728-919).
 
@@ -359,6 +403,13 @@ def _vllm_paged_decode_attention_into(
     is V.  ``num_reqs`` rows are launched (graph padding included); rows with
     ``slot_mapping == -1`` produce zeros and write nothing; tensor rows past
     ``num_reqs`` are untouched.  No validation, allocation or copy happens.
+
+    Extensions over the reference signature (both optional): ``split_counters``
+    (zeroed int32 ``[>= num_reqs * num_kv_heads * 64]``, one 256-byte line per
+    (request, KV head), left zero after every launch) merges the splits inside
+    the one launch; ``max_seq_len`` (a bound
+    on ``seq_lens``, vLLM's ``attn_metadata.max_seq_len``) lets block-table
+    reads start before ``seq_lens`` arrives.
     """
     sb, sp, st, sh, sd = kv_cache.stride()
     plane_bytes = sp * kv_cache.element_size()
@@ -387,7 +438,8 @@ def _vllm_paged_decode_attention_into(
     args.out = out.data_ptr()
     args.out_stride[:] = out.stride()
     args.sm_scale = float(sm_scale)
-    _fill_workspace(args, split_acc, split_max, split_sum, int(num_splits))
+    args.max_seq_len = int(max_seq_len) if max_seq_len else 0
+    _fill_workspace(args, split_acc, split_max, split_sum, int(num_splits), split_counters)
     _fill_append(args, append_k, append_v, slot_mapping)
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))
     return out

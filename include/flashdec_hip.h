@@ -39,6 +39,10 @@ extern "C" {
 #define FD_E_UNSUPPORTED (-2) /* valid but not implemented (dtype, head_dim) */
 #define FD_E_LAUNCH (-3)      /* hipLaunchKernel / hipGetLastError failure   */
 
+/* uint32 words between the split arrival counters of two (request, KV head)
+ * pairs: one 256-byte line each */
+#define FD_SPLIT_COUNTER_STRIDE 64
+
 /* element dtypes */
 #define FD_DTYPE_F16 0
 #define FD_DTYPE_BF16 1
@@ -65,6 +69,19 @@ typedef struct ihipStream_t* fd_stream_t; /* == hipStream_t */
  * workspace (split_acc [>=B, >=Hq, >=S, >=D], split_max/split_sum
  * [>=B, >=Hq, >=S], identical strides for max and sum), followed by the LSE
  * merge.  split_max holds base-2 log-domain maxima (internal format).
+ *
+ * split_counters (optional, S > 1): >= num_seqs * num_kv_heads *
+ * FD_SPLIT_COUNTER_STRIDE uint32 words (one 256-byte line per (request,
+ * KV head)), all zero before the first launch.  With it the merge happens inside the
+ * same launch (the last workgroup of each (request, KV head) to finish
+ * merges, then returns its counter to zero, so the buffer is zero again
+ * after every launch and replays of a captured graph stay valid).  Launches
+ * that share one counter buffer must not run concurrently (e.g. on two
+ * streams).  Without it a second, reducer kernel performs the merge.
+ *
+ * max_seq_len: host-side upper bound on seq_lens (0 = unknown).  When given,
+ * split ranges derive from it, so block-table reads need not wait for
+ * seq_lens; it must not be smaller than any seq_lens[b].
  *
  * Fused append (append_k, append_v, slot_mapping all non-NULL): the
  * request's newest token (position seq_lens[b]-1) is taken from
@@ -106,6 +123,8 @@ typedef struct fd_paged_decode_args {
   float* split_max;
   float* split_sum;
   int64_t split_stats_stride[3]; /* seq, head, split */
+  uint32_t* split_counters;     /* optional in-launch merge, see above */
+  int64_t max_seq_len;          /* optional bound on seq_lens, 0 = unknown */
 
   const void* append_k; /* optional fused append, all-or-none */
   int64_t append_k_stride[3];

@@ -146,8 +146,10 @@ def test_fused_current_token_append(prior, num_splits, dtype, block_size):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize(("num_splits", "cache_layout"), [(1, "NHD"), (8, "NHD"), (8, "HND")])
-def test_vllm_launcher_full_cache_and_graph_padding(num_splits, cache_layout, dtype):
+@pytest.mark.parametrize(("num_splits", "cache_layout", "in_launch_merge"),
+                         [(1, "NHD", False), (8, "NHD", False), (8, "HND", False), (8, "NHD", True),
+                          (16, "HND", True)])
+def test_vllm_launcher_full_cache_and_graph_padding(num_splits, cache_layout, in_launch_merge, dtype):
     """Rows: 2 active, 1 padding (slot -1) inside the grid, 1 beyond num_reqs."""
     bs = 16
     q_act, k, v, table_act, lens_act = make_paged_inputs([1, 257], 16, 2, 128, bs, dtype, seed=17)
@@ -182,11 +184,15 @@ def test_vllm_launcher_full_cache_and_graph_padding(num_splits, cache_layout, dt
     out = torch.full_like(q, 37)
     from flashdec_amd.paged_decode import _vllm_paged_decode_attention_into
 
+    counters = torch.zeros(8 * 64, device="cuda", dtype=torch.int32) if in_launch_merge else None
     returned = _vllm_paged_decode_attention_into(q, append_k, append_v, cache, table, lens, out, slot_mapping, *ws,
                                                  num_reqs=3, num_q_heads=16, num_kv_heads=2, head_dim=128,
                                                  block_size=bs, sm_scale=1.0 / math.sqrt(128),
-                                                 num_splits=num_splits)
+                                                 num_splits=num_splits, split_counters=counters,
+                                                 max_seq_len=int(lens_act.max()) if in_launch_merge else None)
     assert returned is out
+    if counters is not None:
+        assert torch.count_nonzero(counters) == 0
     assert_close_to_oracle(out[:2], expected)
     assert torch.count_nonzero(out[2]) == 0
     assert bool(torch.all(out[3] == 37))
@@ -236,3 +242,29 @@ def test_graph_capture_replays_match_eager():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_in_launch_merge_leaves_counters_zero_across_calls():
+    """Repeated auto-split calls agree bit for bit and leave the counters at zero."""
+    from flashdec_amd import paged_decode as pd
+
+    q, k, v, table, lens = make_paged_inputs([2048] * 8, 16, 2, 128, 32, torch.bfloat16, seed=31)
+    fd = _fd()
+    outs = [fd.decode(q, k, v, table, lens) for _ in range(5)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    key = (q.device.index, torch.cuda.current_stream().cuda_stream)
+    ws = pd._WORKSPACES[key]
+    assert torch.count_nonzero(ws.counters) == 0
+    assert_close_to_oracle(outs[0], _oracle(q, k, v, table, lens))
+
+
+@pytest.mark.parametrize("num_splits", [2, 16, 64, 100])
+def test_explicit_splits_reducer_kernel_many_splits(num_splits):
+    q, k, v, table, lens = make_paged_inputs([4000, 37, 0], 16, 2, 128, 32, torch.bfloat16, seed=37)
+    ws = (torch.empty((3, 16, num_splits, 128), device="cuda"), torch.empty((3, 16, num_splits), device="cuda"),
+          torch.empty((3, 16, num_splits), device="cuda"))
+    out = torch.empty_like(q)
+    _fd().paged_decode_attention_into(q, k, v, table, lens, out, split_kv_workspace=ws, num_splits=num_splits)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
