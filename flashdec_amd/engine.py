@@ -1,0 +1,562 @@
+"""Decode engine: request lifecycle, RoPE/KV append and paged decode per layer.
+
+Mirrors cysong2025/flashdec ``flashdec/engine.py``: result/handle types
+(:21-68), lifecycle (``add_request``/``admit``/``finish_request``/
+``cancel_request``), the multi-layer token transaction
+(``begin_step``/``step_layer``/``commit_step``/``abort_step``, :594-752) with
+automatic abort on any layer error (:709-711, 1117-1126), the single-layer
+``step`` with its backpressure result (:754-871), ``metrics`` and
+``validate_invariants``.  The scheduler-managed mode (:200-573) is policy,
+not this data path, and is not provided.
+
+Backends.  ``append_backend``: ``"fused_hip"`` (alias ``"fused_cuda"``: one
+HIP kernel rotates Q/K and writes K/V), ``"hip"`` (alias ``"cuda"``: torch
+RoPE + HIP scatter; single-layer ``step`` only, as in the reference),
+``"torch"``.  ``decode_backend``: ``"hip"`` (alias ``"triton"``: the HIP
+paged-decode kernels), ``"reference"`` (torch).  Left as ``None`` they
+resolve to the HIP backends for a GPU-resident cache and to the torch
+backends for a CPU-resident cache (the only ones that can run there); the
+HIP backends never fall back -- they raise if the library is missing.
+
+Per layer on the HIP path the engine launches the fused RoPE + append kernel
+and the decode kernel(s) on torch's current stream, reading the
+transaction's device-resident metadata (one H2D copy per ``begin_step``), and
+performs no host synchronisation.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Hashable
+
+PROFILE_RANGE_PREFLIGHT = "flashdec::engine_preflight"
+PROFILE_RANGE_APPEND = "flashdec::rope_kv_append"
+PROFILE_RANGE_DECODE = "flashdec::paged_decode"
+
+_APPEND_ALIASES = {"torch": "torch", "cuda": "hip", "hip": "hip", "fused_cuda": "fused_hip", "fused_hip": "fused_hip"}
+_DECODE_ALIASES = {"reference": "reference", "triton": "hip", "hip": "hip"}
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+@dataclass(frozen=True)
+class AdmissionResult:
+    """State transition result for a request submitted to the engine."""
+
+    request_id: Hashable
+    status: str
+
+
+@dataclass(frozen=True)
+class DecodeStepResult:
+    """One decode-step result, or an explicit backpressure response."""
+
+    status: str
+    request_ids: tuple
+    output: Any | None
+    positions: Any | None
+    block_tables: Any | None
+    seq_lens: Any | None
+    needed_new_blocks: int
+    free_blocks: int
+    reason: str | None = None
+
+
+@dataclass(frozen=True)
+class DecodeStepTransaction:
+    """Stable engine handle for one open multi-layer token transaction."""
+
+    transaction_id: int
+    engine_version: int
+    request_ids: tuple
+    positions: Any
+    physical_block_ids: Any
+    block_offsets: Any
+    block_tables: Any
+    effective_seq_lens: Any
+
+
+@dataclass(frozen=True)
+class DecodeLayerResult:
+    """Output of one layer inside an open decode token transaction."""
+
+    transaction_id: int
+    layer_idx: int
+    request_ids: tuple
+    output: Any
+    positions: Any
+    block_tables: Any
+    effective_seq_lens: Any
+
+
+@dataclass
+class _OpenStep:
+    handle: DecodeStepTransaction
+    cache_transaction: Any
+    needed_new_blocks: int
+    next_layer_idx: int = 0
+    last_output: Any | None = None
+    state: str = "open"
+
+
+class DecodeEngine:
+    """Coordinate request lifecycle, RoPE/KV append and paged decode."""
+
+    WAITING = "waiting"
+    ACTIVE = "active"
+    FINISHED = "finished"
+    CANCELLED = "cancelled"
+    REJECTED = "rejected"
+
+    STEP_OK = "ok"
+    STEP_BACKPRESSURE = "backpressure"
+
+    def __init__(self, cache, append_backend=None, decode_backend=None, sm_scale=None, num_warps=2, num_stages=None,
+                 profile_ranges=False):
+        from .cache import PagedKVCache
+
+        if not isinstance(cache, PagedKVCache):
+            raise TypeError("cache must be a PagedKVCache")
+        on_gpu = cache.device.type == "cuda"
+        if append_backend is None:
+            append_backend = "fused_hip" if on_gpu else "torch"
+        if decode_backend is None:
+            decode_backend = "hip" if on_gpu else "reference"
+        if append_backend not in _APPEND_ALIASES:
+            raise ValueError("append_backend must be 'torch', 'cuda', or 'fused_cuda'")
+        if decode_backend not in _DECODE_ALIASES:
+            raise ValueError("decode_backend must be 'reference' or 'triton'")
+        if not isinstance(profile_ranges, bool):
+            raise ValueError("profile_ranges must be a bool")
+        self.cache = cache
+        self.append_backend = append_backend
+        self.decode_backend = decode_backend
+        self._append = _APPEND_ALIASES[append_backend]
+        self._decode_kind = _DECODE_ALIASES[decode_backend]
+        self.sm_scale = sm_scale
+        self.num_warps = num_warps
+        self.num_stages = num_stages
+        self.profile_ranges = profile_ranges
+        self._range = _torch().profiler.record_function if profile_ranges else None
+        self._statuses: dict = {}
+        self._completed_step_count = 0
+        self._appended_token_count = 0
+        self._backpressure_count = 0
+        self._state_version = 0
+        self._observed_cache_state_version = cache.state_version
+        self._open: _OpenStep | None = None
+        self._transaction_layer_step_count = 0
+        self._transaction_abort_count = 0
+
+    # ------------------------------------------------------------ lifecycle
+    def register_prefix(self, prefix_id, k_blocks, v_blocks):
+        """Register shared full blocks before any request enters the engine."""
+        self._require_no_open_step("register a shared prefix")
+        if self._statuses:
+            raise RuntimeError("shared prefixes must be registered before request submission")
+        if self.cache.state_version != self._observed_cache_state_version:
+            raise RuntimeError("PagedKVCache mutated outside DecodeEngine")
+        m = self.cache.metrics()
+        if any(m[k] for k in ("active_requests", "finished_requests", "cancelled_requests")):
+            raise RuntimeError("shared prefix registration requires an empty PagedKVCache")
+        result = self.cache.register_prefix(prefix_id, k_blocks, v_blocks)
+        self._sync_cache_version()
+        return result
+
+    def evict_prefix(self, prefix_id):
+        """Evict one inactive prefix after every request is resolved."""
+        self._require_no_open_step("evict a shared prefix")
+        if any(s in (self.WAITING, self.ACTIVE) for s in self._statuses.values()):
+            raise RuntimeError("shared prefixes can only be evicted after all requests are resolved")
+        released = self.cache.evict_prefix(prefix_id)
+        self._sync_cache_version()
+        self._bump_state_version()
+        return released
+
+    def add_request(self, request_id):
+        """Submit a request in ``waiting`` state (no KV memory yet)."""
+        self._require_no_open_step("submit a request")
+        self._check_request_id(request_id)
+        if request_id in self._statuses:
+            raise RuntimeError(f"request_id {request_id!r} already exists in the DecodeEngine")
+        self._statuses[request_id] = self.WAITING
+        self._bump_state_version()
+        return AdmissionResult(request_id=request_id, status=self.WAITING)
+
+    def admit(self, request_ids=None, prefix_id=None):
+        """Move waiting requests to ``active``; optionally attach a resident shared prefix."""
+        self._require_no_open_step("admit requests")
+        if request_ids is None:
+            ids = tuple(r for r, s in self._statuses.items() if s == self.WAITING)
+        else:
+            ids = self._normalize_ids(request_ids)
+        if not ids:
+            raise ValueError("at least one waiting request is required for admission")
+        for rid in ids:
+            self._require_status(rid, self.WAITING)
+        for rid in ids:
+            self.cache.add_request(rid)
+            if prefix_id is not None:
+                self.cache.attach_prefix(rid, prefix_id)
+            self._statuses[rid] = self.ACTIVE
+        self._sync_cache_version()
+        self._bump_state_version()
+        return tuple(AdmissionResult(request_id=rid, status=self.ACTIVE) for rid in ids)
+
+    @property
+    def state_version(self):
+        return self._state_version
+
+    def active_request_ids(self):
+        """Active request ids in admission order."""
+        return tuple(r for r, s in self._statuses.items() if s == self.ACTIVE)
+
+    def request_state(self, request_id):
+        status = self._require_known_request(request_id)
+        result = {"request_id": request_id, "status": status}
+        if status not in (self.WAITING, self.REJECTED):
+            result["cache"] = self.cache.request_state(request_id)
+        return result
+
+    def finish_request(self, request_id):
+        """Finish an active request and release its blocks."""
+        self._require_no_open_step("finish a request")
+        self._require_status(request_id, self.ACTIVE)
+        released = self.cache.finish_request(request_id)
+        self._statuses[request_id] = self.FINISHED
+        self._sync_cache_version()
+        self._bump_state_version()
+        return released
+
+    def cancel_request(self, request_id):
+        """Cancel an active request and release its blocks."""
+        self._require_no_open_step("cancel a request")
+        self._require_status(request_id, self.ACTIVE)
+        released = self.cache.cancel_request(request_id)
+        self._statuses[request_id] = self.CANCELLED
+        self._sync_cache_version()
+        self._bump_state_version()
+        return released
+
+    # ---------------------------------------------------- token transaction
+    def begin_step(self, request_ids=None):
+        """Open one token transaction for a stable batch of active requests."""
+        self._require_no_open_step("begin another decode step")
+        if self._append not in ("torch", "fused_hip"):
+            raise RuntimeError("multi-layer transactions require append_backend='torch' or 'fused_cuda'")
+        ids = self._normalize_active_ids(request_ids)
+        needed = self._needed_new_blocks(ids)
+        if needed > self.cache.num_free_blocks:
+            self._backpressure_count += 1
+            raise RuntimeError("insufficient physical blocks to begin decode step")
+        tx = self.cache.begin_token(ids)
+        handle = DecodeStepTransaction(
+            transaction_id=tx.transaction_id,
+            engine_version=self._state_version + 1,
+            request_ids=ids,
+            positions=tx.positions,
+            physical_block_ids=tx.physical_block_ids,
+            block_offsets=tx.block_offsets,
+            block_tables=tx.block_tables,
+            effective_seq_lens=tx.effective_seq_lens,
+        )
+        self._sync_cache_version()
+        self._bump_state_version()
+        self._open = _OpenStep(handle=handle, cache_transaction=tx, needed_new_blocks=needed)
+        return handle
+
+    def step_layer(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0):
+        """RoPE + KV write + paged decode for one layer; any error aborts the whole token."""
+        state = self._require_open_step(transaction)
+        try:
+            layer_idx = int(layer_idx)
+            if layer_idx != state.next_layer_idx:
+                raise RuntimeError(
+                    f"decode transaction requires layer {state.next_layer_idx}, got layer {layer_idx}")
+            self._validate_step_inputs(state.handle.request_ids, q, k, v)
+            if k.dim() == 2:
+                k = k.unsqueeze(0)
+            if v.dim() == 2:
+                v = v.unsqueeze(0)
+            if self._range is None:
+                q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base)
+                output = self._decode_layer(q_rot, view, meta, layer_idx)
+            else:
+                with self._range(PROFILE_RANGE_APPEND):
+                    q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base)
+                with self._range(PROFILE_RANGE_DECODE):
+                    output = self._decode_layer(q_rot, view, meta, layer_idx)
+        except Exception:
+            self._abort_open_step(state)
+            raise
+        state.next_layer_idx += 1
+        state.last_output = output
+        self._transaction_layer_step_count += 1
+        return DecodeLayerResult(
+            transaction_id=state.handle.transaction_id,
+            layer_idx=layer_idx,
+            request_ids=state.handle.request_ids,
+            output=output,
+            positions=view.positions,
+            block_tables=view.block_tables,
+            effective_seq_lens=view.effective_seq_lens,
+        )
+
+    def commit_step(self, transaction):
+        """Commit the open token after every layer has run."""
+        state = self._require_open_step(transaction)
+        if state.next_layer_idx != self.cache.num_layers:
+            raise RuntimeError("cannot commit decode step before all layers are complete")
+        committed = self.cache.commit_token(state.cache_transaction)
+        state.state = "committed"
+        self._open = None
+        self._completed_step_count += 1
+        self._appended_token_count += len(state.handle.request_ids)
+        self._sync_cache_version()
+        self._bump_state_version()
+        return DecodeStepResult(
+            status=self.STEP_OK,
+            request_ids=state.handle.request_ids,
+            output=state.last_output,
+            positions=committed.positions,
+            block_tables=committed.block_tables,
+            seq_lens=self.cache.seq_lens_tensor(state.handle.request_ids),
+            needed_new_blocks=state.needed_new_blocks,
+            free_blocks=self.cache.num_free_blocks,
+        )
+
+    def abort_step(self, transaction):
+        """Explicitly abort the open token transaction."""
+        return self._abort_open_step(self._require_open_step(transaction))
+
+    def step(self, q, k, v, request_ids=None, layer_idx=0, rotary_dim=None, base=10_000.0):
+        """Single-layer append -> decode step; backpressure returns without mutation."""
+        self._require_no_open_step("run the single-layer step wrapper")
+        if self.cache.num_layers != 1:
+            raise RuntimeError("multi-layer caches require begin_step/step_layer/commit_step")
+        if self._range is None:
+            ids = self._normalize_active_ids(request_ids)
+            self._validate_step_inputs(ids, q, k, v)
+            needed = self._needed_new_blocks(ids)
+        else:
+            with self._range(PROFILE_RANGE_PREFLIGHT):
+                ids = self._normalize_active_ids(request_ids)
+                self._validate_step_inputs(ids, q, k, v)
+                needed = self._needed_new_blocks(ids)
+        if needed > self.cache.num_free_blocks:
+            self._backpressure_count += 1
+            return DecodeStepResult(
+                status=self.STEP_BACKPRESSURE, request_ids=ids, output=None, positions=None, block_tables=None,
+                seq_lens=None, needed_new_blocks=needed, free_blocks=self.cache.num_free_blocks,
+                reason="insufficient_physical_blocks")
+        if self._append in ("torch", "fused_hip"):
+            if int(layer_idx) != 0:
+                raise ValueError("single-layer step requires layer_idx=0")
+            tx = self.begin_step(ids)
+            self.step_layer(tx, 0, q, k, v, rotary_dim=rotary_dim, base=base)
+            return self.commit_step(tx)
+        from .rope import rope_paged_kv_append
+
+        result = rope_paged_kv_append(self.cache, layer_idx, ids, q, k, v, rotary_dim=rotary_dim, base=base,
+                                      append_backend=self._append)
+        output = self._decode(result.q, result.block_tables, result.seq_lens, layer_idx)
+        self._completed_step_count += 1
+        self._appended_token_count += len(ids)
+        self._sync_cache_version()
+        self._bump_state_version()
+        return DecodeStepResult(status=self.STEP_OK, request_ids=ids, output=output, positions=result.positions,
+                                block_tables=result.block_tables, seq_lens=result.seq_lens, needed_new_blocks=needed,
+                                free_blocks=self.cache.num_free_blocks)
+
+    # --------------------------------------------------------------- status
+    def metrics(self):
+        """Engine counters together with the cache metrics."""
+        st = self._statuses.values()
+        return {
+            "waiting_requests": sum(s == self.WAITING for s in st),
+            "active_requests": sum(s == self.ACTIVE for s in st),
+            "finished_requests": sum(s == self.FINISHED for s in st),
+            "cancelled_requests": sum(s == self.CANCELLED for s in st),
+            "rejected_requests": sum(s == self.REJECTED for s in st),
+            "completed_step_count": self._completed_step_count,
+            "appended_token_count": self._appended_token_count,
+            "backpressure_count": self._backpressure_count,
+            "state_version": self._state_version,
+            "cache_state_version": self.cache.state_version,
+            "scheduler_managed": False,
+            "committed_blocks": 0,
+            "committed_but_unallocated_blocks": 0,
+            "stale_decision_count": 0,
+            "applied_decision_count": 0,
+            "open_step_transaction_count": int(self._open is not None),
+            "transaction_layer_step_count": self._transaction_layer_step_count,
+            "transaction_abort_count": self._transaction_abort_count,
+            "append_backend": self.append_backend,
+            "decode_backend": self.decode_backend,
+            "cache": self.cache.metrics(),
+        }
+
+    def validate_invariants(self):
+        """Check engine lifecycle state against cache ownership state."""
+        self.cache.validate_invariants()
+        if self._open is None:
+            if self.cache.has_open_transaction:
+                raise RuntimeError("cache has an open transaction not owned by DecodeEngine")
+        else:
+            if not self.cache.has_open_transaction:
+                raise RuntimeError("Engine transaction is open but cache transaction is not")
+            view = self.cache.transaction_view(self._open.cache_transaction)
+            if view.request_ids != self._open.handle.request_ids:
+                raise RuntimeError("Engine/cache transaction request rows diverged")
+            if view.next_layer_idx != self._open.next_layer_idx:
+                raise RuntimeError("Engine/cache transaction layer progress diverged")
+        for rid, status in self._statuses.items():
+            if status in (self.WAITING, self.REJECTED):
+                try:
+                    self.cache.request_state(rid)
+                except KeyError:
+                    continue
+                raise RuntimeError("waiting request unexpectedly exists in PagedKVCache")
+            if self.cache.request_state(rid)["status"] != status:
+                raise RuntimeError("DecodeEngine and PagedKVCache request status diverged")
+        return True
+
+    # ------------------------------------------------------------ internals
+    def _write_layer(self, state, layer_idx, q, k, v, rotary_dim, base):
+        """Returns (q_rotated, caller view, allocator device metadata or None)."""
+        tx = state.cache_transaction
+        if self._append == "fused_hip":
+            meta = self.cache.transaction_device_metadata(tx)
+            q_rot, view = self.cache.write_token_layer_fused_cuda(tx, layer_idx, q, k, v, rotary_dim=rotary_dim,
+                                                                  base=base)
+            return q_rot, view, meta
+        from .rope import apply_rope
+
+        cur = self.cache.transaction_view(tx)
+        q_rot = apply_rope(q, cur.positions, rotary_dim=rotary_dim, base=base)
+        k_rot = apply_rope(k, cur.positions, rotary_dim=rotary_dim, base=base)
+        view = self.cache.write_token_layer(tx, layer_idx, k_rot, v)
+        return q_rot, view, None
+
+    def _decode_layer(self, q_rot, view, meta, layer_idx):
+        if meta is not None:  # the allocator's own copy, not the caller-visible clone
+            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx)
+        return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx)
+
+    def _decode(self, q, block_tables, seq_lens, layer_idx=0):
+        layer_idx = int(layer_idx)
+        if layer_idx < 0 or layer_idx >= self.cache.num_layers:
+            raise ValueError("layer_idx must be in [0, num_layers)")
+        if self._decode_kind == "reference":
+            from .paged_reference import paged_decode_attention_ref
+
+            return paged_decode_attention_ref(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx],
+                                              block_tables, seq_lens, sm_scale=self.sm_scale)
+        from .paged_decode import paged_decode_attention
+
+        return paged_decode_attention(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx], block_tables,
+                                      seq_lens, sm_scale=self.sm_scale, block_size=self.cache.block_size,
+                                      num_warps=self.num_warps, num_stages=self.num_stages)
+
+    def _abort_open_step(self, state):
+        if self._open is not state or state.state != "open":
+            raise RuntimeError("decode step transaction is not open")
+        aborted = self.cache.abort_token(state.cache_transaction)
+        state.state = "aborted"
+        self._open = None
+        self._transaction_abort_count += 1
+        self._sync_cache_version()
+        self._bump_state_version()
+        return aborted
+
+    def _bump_state_version(self):
+        self._state_version += 1
+
+    def _sync_cache_version(self):
+        self._observed_cache_state_version = self.cache.state_version
+
+    def _require_no_open_step(self, action):
+        if self._open is not None:
+            raise RuntimeError(f"cannot {action} during an open decode step transaction")
+
+    def _require_open_step(self, transaction):
+        if not isinstance(transaction, DecodeStepTransaction):
+            raise TypeError("transaction must be a DecodeStepTransaction")
+        state = self._open
+        if state is None:
+            raise RuntimeError("DecodeEngine has no open decode step transaction")
+        h = state.handle
+        if (transaction.transaction_id != h.transaction_id or transaction.engine_version != h.engine_version
+                or transaction.request_ids != h.request_ids):
+            raise RuntimeError("stale or invalid DecodeEngine transaction handle")
+        if state.state != "open":
+            raise RuntimeError(f"decode step transaction is already {state.state}")
+        return state
+
+    def _validate_step_inputs(self, ids, q, k, v):
+        torch = _torch()
+        if not isinstance(q, torch.Tensor) or not isinstance(k, torch.Tensor) or not isinstance(v, torch.Tensor):
+            raise TypeError("q, k, and v must be torch tensors")
+        if q.dim() != 3:
+            raise ValueError("q must have shape [num_requests, num_q_heads, head_dim]")
+        if k.dim() == 2 and len(ids) == 1:
+            k = k.unsqueeze(0)
+        if v.dim() == 2 and len(ids) == 1:
+            v = v.unsqueeze(0)
+        expected = (len(ids), self.cache.num_kv_heads, self.cache.head_dim)
+        if q.shape[0] != len(ids) or q.shape[1] <= 0 or q.shape[2] != self.cache.head_dim:
+            raise ValueError("q shape must match active request count and cache head_dim")
+        if k.shape != expected or v.shape != expected:
+            raise ValueError("k and v shapes must match active request count and cache dimensions")
+        if q.device != self.cache.device or k.device != self.cache.device or v.device != self.cache.device:
+            raise ValueError("q, k, and v must be on the cache device")
+        if q.dtype != self.cache.dtype or k.dtype != self.cache.dtype or v.dtype != self.cache.dtype:
+            raise ValueError("q, k, and v must use the cache dtype")
+
+    def _needed_new_blocks(self, ids):
+        bs = self.cache.block_size
+        return sum(self.cache.request_state(rid)["seq_len"] % bs == 0 for rid in ids)
+
+    def _normalize_active_ids(self, request_ids):
+        ids = self.active_request_ids() if request_ids is None else self._normalize_ids(request_ids)
+        if not ids:
+            raise ValueError("at least one active request is required for a decode step")
+        for rid in ids:
+            self._require_status(rid, self.ACTIVE)
+        return ids
+
+    def _normalize_ids(self, request_ids):
+        if isinstance(request_ids, (str, bytes)):
+            ids = (request_ids,)
+        else:
+            try:
+                ids = tuple(request_ids)
+            except TypeError:
+                ids = (request_ids,)
+        for rid in ids:
+            self._check_request_id(rid)
+        if len(set(ids)) != len(ids):
+            raise ValueError("request_ids must be unique")
+        return ids
+
+    @staticmethod
+    def _check_request_id(request_id):
+        try:
+            hash(request_id)
+        except TypeError as exc:
+            raise ValueError("request ids must be hashable") from exc
+
+    def _require_known_request(self, request_id):
+        self._check_request_id(request_id)
+        if request_id not in self._statuses:
+            raise KeyError(f"unknown request_id: {request_id!r}")
+        return self._statuses[request_id]
+
+    def _require_status(self, request_id, expected):
+        status = self._require_known_request(request_id)
+        if status != expected:
+            raise RuntimeError(f"request_id {request_id!r} is {status}, expected {expected}")

@@ -159,9 +159,11 @@ int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads,
  *   out_lo = rn(rn(x_lo * cos) - rn(x_hi * sin)),
  *   out_hi = rn(rn(x_hi * cos) + rn(x_lo * sin))
  * without FMA contraction, rounded to the element dtype (RNE).  Dimensions
- * past rotary_dim are copied.  Indices are range-checked in the kernel: a
- * row whose block id or offset is out of range, or whose position is
- * negative, writes nothing (q_out is still produced for valid positions).
+ * past rotary_dim are copied.  Block ids and offsets are range-checked in
+ * the kernel: a row whose block id is outside [0, num_blocks) or whose
+ * offset is outside [0, block_size) writes no K/V (its q_out row is still
+ * produced).  Positions are not checked here; callers validate them
+ * (non-negative) before the launch.
  */
 typedef struct fd_rope_append_args {
   uint32_t struct_size;
