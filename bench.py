@@ -10,11 +10,20 @@ before timing starts.  Steps rotate over ``--pools`` independent KV pools
 Timing:
 * ``ms_per_step``/``value``: K steps captured in one hipGraph, replayed once
   between two synchronisations (the serving-loop view, launch gaps included).
-* ``roofline.achieved``: algorithmic bytes per call / mean per-call device
-  time, bracketed by HIP events on the launch stream around every call, with
-  the queue pre-filled so host submission gaps are excluded.
+* ``roofline.achieved``: algorithmic bytes per call / mean duration of the
+  dominant kernel (the attention kernel), measured live: every call of a
+  separate eager loop passes HIP events through the library's
+  ``timing_events`` hook, which records them around exactly that dispatch
+  (and around the split reducer, reported beside it).
+* ``roofline.traffic``: HBM bytes per attention-kernel dispatch from the
+  committed PMC summary ``profiles/decode_mfma_b8_ctx2048_traffic.json``
+  (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null.
 * ``cpu_baseline``: the repo's numpy oracle (one thread) on a bounded sample
   of the same workload, on this host.
+
+``--profile-kernels N`` instead runs N eager calls and a 64 MiB device copy
+(the counter-scaling reference) and prints one line: the form profiled by
+``rocprofv3 --kernel-trace --stats`` and ``rocprofv3 --pmc``.
 
 Prints one JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 """
@@ -35,6 +44,8 @@ if ROOT not in sys.path:
 
 METRIC = "paged-decode µs/call + achieved HBM GB/s (% of peak), B8 ctx2048 Qwen2.5-3B shape"
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_mfma_b8_ctx2048_traffic.json")
+COPY_PROBE_MIB = 64
 
 
 def log(msg):
@@ -51,11 +62,8 @@ def parse_args():
     p.add_argument("--pools", type=int, default=48)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget for the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--merge", choices=("reducer", "in-launch"), default="reducer",
-                   help="split merge: a second reducer kernel (default, the library's own choice) "
-                        "or inside the decode launch (arrival counters)")
-    p.add_argument("--copy-probe-mib", type=int, default=0,
-                   help="also run a plain device copy of this size (PMC scaling reference)")
+    p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
+                   help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
     return p.parse_args()
 
 
@@ -83,6 +91,37 @@ def algorithmic_bytes(batch, ctx, hq, hkv, d, bs, elt=2):
     return batch * ctx * hkv * d * 2 * elt + 2 * batch * hq * d * elt + 4 * batch * nblk + 4 * batch
 
 
+def prepared_args(pool, sm_scale, block_size, num_kv_heads):
+    """The ctypes argument block ``paged_decode_attention_into`` builds for this pool (auto splits)."""
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    q, k, v, table, lens, out = pool
+    stream = _lib.current_stream_handle(q.device)
+    max_seq_len = table.shape[1] * block_size
+    splits = _lib.paged_decode_plan(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], max_seq_len)
+    args = _lib.PagedDecodeArgs()
+    pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,
+                    num_kv_heads, block_size, sm_scale)
+    args.num_blocks = k.shape[0]
+    args.max_seq_len = max_seq_len
+    acc = mx = sm = None
+    if splits > 1:
+        acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits, stream)
+    pd._fill_workspace(args, acc, mx, sm, splits)
+    return args, stream
+
+
+def load_traffic():
+    """HBM bytes per attention-kernel dispatch from the committed PMC summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            t = json.load(f)
+        return float(t["fetch_bytes_per_dispatch"]) + float(t["write_bytes_per_dispatch"]), t
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def cpu_baseline(pools, budget_s, sm_scale):
     """Median seconds per call of the numpy oracle on pool 0 (one BLAS thread)."""
     import numpy as np
@@ -107,12 +146,42 @@ def cpu_baseline(pools, budget_s, sm_scale):
     return statistics.median(times), len(times)
 
 
+def back_to_back(torch, lib, prepared, n, events=None):
+    """n library calls submitted while the GPU is held busy, so they run back to back.
+
+    A sleep kernel occupies the stream while the host enqueues every call;
+    ``events[i]`` (four HIP events) go through the library's timing hook.
+    """
+    torch.cuda.synchronize()
+    torch.cuda._sleep(200_000_000)
+    for i in range(n):
+        a, st = prepared[i % len(prepared)]
+        if events is not None:
+            a.timing_events[:] = [e.cuda_event for e in events[i]]
+        lib.paged_decode(a, st)
+        if events is not None:
+            a.timing_events[:] = [None] * 4
+    torch.cuda.synchronize()
+
+
+def profile_kernels(torch, dev, lib, prepared, n):
+    """Back-to-back calls and a plain copy of known size, for rocprofv3 runs."""
+    back_to_back(torch, lib, prepared, n)
+    numel = COPY_PROBE_MIB * 2**20 // 2
+    src = torch.ones(numel, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_kernels": n, "copy_probe_mib": COPY_PROBE_MIB, "copies": 4}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(
             f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
-            "(the decode path shards per request/KV head with no exchange; see DESIGN.md).",
+            "(the decode path shards per request / KV head with no exchange).",
             file=sys.stderr,
         )
         sys.exit(2)
@@ -134,38 +203,17 @@ def main():
     splits = _lib.paged_decode_plan(batch, hq, hkv, d, pools[0][3].shape[1] * bs)
     log(f"[bench] KV pool bytes {pool_bytes / 2**20:.0f} MiB, algorithmic bytes/call {nbytes}, splits {splits}")
 
-    if args.merge == "reducer":
-        def call(i):
-            q, k, v, table, lens, out = pools[i % len(pools)]
-            fd.paged_decode_attention_into(q, k, v, table, lens, out, sm_scale=sm_scale)
-    else:
-        # the in-launch merge through the unchecked launcher's counter extension
-        from flashdec_amd.paged_decode import _vllm_paged_decode_attention_into as launch
-
-        ws = (torch.empty((batch, hq, splits, d), device=dev), torch.empty((batch, hq, splits), device=dev),
-              torch.empty((batch, hq, splits), device=dev))
-        counters = torch.zeros(batch * hkv * _lib.SPLIT_COUNTER_STRIDE, device=dev, dtype=torch.int32)
-
-        def call(i):
-            q, k, v, table, lens, out = pools[i % len(pools)]
-            _in_launch(q, k, v, table, lens, out, ws, counters)
-
-    def _in_launch(q, k, v, table, lens, out, ws, counters):
-        from flashdec_amd import paged_decode as pd
-
-        args_ = _lib.PagedDecodeArgs()
-        pd._fill_common(args_, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,
-                        hkv, bs, sm_scale)
-        args_.num_blocks = k.shape[0]
-        args_.max_seq_len = ctx
-        pd._fill_workspace(args_, ws[0], ws[1], ws[2], splits, counters)
-        _lib.paged_decode(args_, _lib.current_stream_handle(dev))
+    def call(i):
+        q, k, v, table, lens, out = pools[i % len(pools)]
+        fd.paged_decode_attention_into(q, k, v, table, lens, out, sm_scale=sm_scale)
 
     stream = torch.cuda.current_stream(dev)
-    # warmup (eager)
-    for i in range(args.warmup):
-        call(i)
-    torch.cuda.synchronize()
+    call(0)  # one call through the public API builds the stream's split workspace
+    prepared = [prepared_args(pool, sm_scale, bs, hkv) for pool in pools]
+    if args.profile_kernels:
+        profile_kernels(torch, dev, _lib, prepared, args.profile_kernels)
+        return
+    back_to_back(torch, _lib, prepared, args.warmup)
     log("[bench] warmup done")
 
     # K steps in one graph, replayed once inside the timed region
@@ -193,33 +241,24 @@ def main():
     ms_per_step = total_ms / args.steps
     log(f"[bench] graph: {args.steps} calls in {total_ms:.3f} ms -> {ms_per_step * 1e3:.2f} us/call")
 
-    # per-call device time: events around each launch, queue pre-filled
-    n_ev = min(2 * len(pools), 192)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    torch.cuda.synchronize()
-    torch.cuda._sleep(200_000_000)
-    for i in range(n_ev):
-        starts[i].record(stream)
-        call(i)
-        stops[i].record(stream)
-    torch.cuda.synchronize()
-    per_call_ms = [s.elapsed_time(e) for s, e in zip(starts, stops)]
-    kernel_ms = statistics.mean(per_call_ms)
-    kernel_med = statistics.median(per_call_ms)
-    log(f"[bench] per-call events: mean {kernel_ms * 1e3:.2f} us, median {kernel_med * 1e3:.2f} us, "
-        f"min {min(per_call_ms) * 1e3:.2f} us")
-
-    if args.copy_probe_mib:
-        n = args.copy_probe_mib * 2**20 // 2
-        src = torch.ones(n, device=dev, dtype=torch.bfloat16)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written x3")
+    # live per-kernel durations: the library records events around each dispatch
+    n_calls = min(4 * len(pools), 192)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_calls)]
+    for evs in events:  # create the HIP events before their handles are passed down
+        for e in evs:
+            e.record(stream)
+    back_to_back(torch, _lib, prepared, n_calls, events)
+    attn_ms = [evs[0].elapsed_time(evs[1]) for evs in events]
+    red_ms = [evs[2].elapsed_time(evs[3]) for evs in events] if splits > 1 else [0.0]
+    kernel_ms = statistics.mean(attn_ms)
+    log(f"[bench] attention kernel: mean {kernel_ms * 1e3:.2f} us, median {statistics.median(attn_ms) * 1e3:.2f} us"
+        f"; reducer: mean {statistics.mean(red_ms) * 1e3:.2f} us ({n_calls} calls)")
 
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    traffic, traffic_meta = load_traffic()
+    traffic_src = None if traffic_meta is None else os.path.relpath(TRAFFIC_SUMMARY, ROOT)
+    if traffic is not None:
+        traffic = int(round(traffic))
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
@@ -261,7 +300,7 @@ def main():
             "kv_pool_mib": round(pool_bytes / 2**20, 1),
             "num_splits": splits,
             "timing": "hipGraph of K calls replayed once; hipEvents",
-            "merge": args.merge,
+            "merge": "reducer kernel" if splits > 1 else "none",
         },
         "roofline": {
             "bound": "hbm",
@@ -269,9 +308,12 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "per_call_us_mean": round(kernel_ms * 1e3, 3),
+            "traffic": traffic,
+            "kernel": "decode_mfma_kernel<bf16, bs32>",
+            "kernel_us_mean": round(kernel_ms * 1e3, 3),
+            "reducer_us_mean": round(statistics.mean(red_ms) * 1e3, 3),
             "algorithmic_bytes_per_call": nbytes,
+            "traffic_source": traffic_src,
         },
         "cpu_baseline": cpu,
     }

@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 
 _i64 = ctypes.c_int64
@@ -71,6 +71,7 @@ class PagedDecodeArgs(ctypes.Structure):
         ("slot_mapping", _vp),
         ("slot_mapping_dtype", _i32),
         ("slot_mapping_stride", _i64),
+        ("timing_events", _vp * 4),
     ]
 
 

@@ -19,6 +19,8 @@
 //                                             append owned by the last tile)
 //   flashdec/kernels/paged_decode.py:546-642  LSE merge; zero rows for
 //                                             seq_len == 0 / slot < 0
+#include <hip/hip_ext.h>
+
 #include "fd_common.h"
 
 namespace fd {
@@ -816,19 +818,30 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
   return true;
 }
 
+// One dispatch; with both events given it is bracketed by them (profiling hook).
+template <typename F, typename... Args>
+void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, void* stop, Args... args) {
+  if (start && stop)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, static_cast<hipEvent_t>(start),
+                          static_cast<hipEvent_t>(stop), 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+}
+
 template <typename T, int BS>
-void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream) {
+void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
   const bool merge = p.counters != nullptr;
+  const dim3 block(256);
   if (p.fuse) {
     if (merge)
-      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, true, true>), grid, dim3(256), 0, stream, p);
+      dispatch(decode_mfma_kernel<T, BS, true, true>, grid, block, stream, ev[0], ev[1], p);
     else
-      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, true, false>), grid, dim3(256), 0, stream, p);
+      dispatch(decode_mfma_kernel<T, BS, true, false>, grid, block, stream, ev[0], ev[1], p);
   } else {
     if (merge)
-      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, false, true>), grid, dim3(256), 0, stream, p);
+      dispatch(decode_mfma_kernel<T, BS, false, true>, grid, block, stream, ev[0], ev[1], p);
     else
-      hipLaunchKernelGGL((decode_mfma_kernel<T, BS, false, false>), grid, dim3(256), 0, stream, p);
+      dispatch(decode_mfma_kernel<T, BS, false, false>, grid, block, stream, ev[0], ev[1], p);
   }
 }
 
@@ -844,26 +857,27 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   if (fast) {
     const dim3 grid(static_cast<unsigned>(pairs * p.splits));
     switch (a.block_size) {
-      case 8: launch_mfma<T, 8>(p, grid, stream); break;
-      case 16: launch_mfma<T, 16>(p, grid, stream); break;
-      default: launch_mfma<T, 32>(p, grid, stream); break;
+      case 8: launch_mfma<T, 8>(p, grid, stream, a.timing_events); break;
+      case 16: launch_mfma<T, 16>(p, grid, stream, a.timing_events); break;
+      default: launch_mfma<T, 32>(p, grid, stream, a.timing_events); break;
     }
   } else {
     const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
     const dim3 grid(static_cast<unsigned>(pairs * hg), static_cast<unsigned>(p.splits));
+    void* const* ev = a.timing_events;
     if (a.head_dim == 64)
-      hipLaunchKernelGGL((decode_generic_kernel<T, 64>), grid, dim3(64), 0, stream, p, hg);
+      dispatch(decode_generic_kernel<T, 64>, grid, dim3(64), stream, ev[0], ev[1], p, hg);
     else
-      hipLaunchKernelGGL((decode_generic_kernel<T, 128>), grid, dim3(64), 0, stream, p, hg);
+      dispatch(decode_generic_kernel<T, 128>, grid, dim3(64), stream, ev[0], ev[1], p, hg);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
   if (p.splits > 1 && p.counters == nullptr) {
     const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
     if (a.head_dim == 64)
-      hipLaunchKernelGGL((split_reduce_kernel<T, 64>), grid, dim3(64), 0, stream, p);
+      dispatch(split_reduce_kernel<T, 64>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], p);
     else
-      hipLaunchKernelGGL((split_reduce_kernel<T, 128>), grid, dim3(64), 0, stream, p);
+      dispatch(split_reduce_kernel<T, 128>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], p);
     e = hipGetLastError();
     if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
   }

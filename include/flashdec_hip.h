@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 1
+#define FD_ABI_VERSION 2
 
 /* status codes */
 #define FD_OK 0
@@ -133,6 +133,13 @@ typedef struct fd_paged_decode_args {
   const void* slot_mapping;
   int32_t slot_mapping_dtype;
   int64_t slot_mapping_stride;
+
+  /* Optional profiling hook, all NULL = off.  Caller-created hipEvent_t
+   * handles recorded around exactly one dispatch each (hipExtLaunchKernel):
+   * [0]/[1] around the attention kernel, [2]/[3] around the split reducer
+   * when the call launches one.  No counterpart in the reference; it lets a
+   * caller time the attention kernel alone on its own stream. */
+  void* timing_events[4];
 } fd_paged_decode_args;
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
