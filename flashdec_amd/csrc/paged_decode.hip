@@ -77,12 +77,12 @@ __device__ __forceinline__ int64_t effective_len(const DecodeParams& p, int64_t 
 }
 
 // Split s covers tiles [s * tps, (s + 1) * tps) of the row, tps = ceil(T / S),
-// with T from the host bound when given (reads of the block table then need
-// not wait for seq_lens), else from the row's own length
-// (flashdec/kernels/paged_decode.py:408-411).  Tiles past the row's length
-// are skipped by the caller.
+// T = the row's own 32-token tile count (flashdec/kernels/paged_decode.py:
+// 408-411).  The host bound (hint_tiles / hint_tps) never decides the range:
+// the MFMA kernel uses it only to guess where its first tile is, so that
+// tile's loads can be issued before seq_lens arrives.
 __device__ __forceinline__ void split_range(const DecodeParams& p, int split, int64_t eff, int& t0, int& t1) {
-  const int total = p.hint_tiles > 0 ? p.hint_tiles : static_cast<int>((eff + 31) / 32);
+  const int total = static_cast<int>((eff + 31) / 32);
   const int tps = (total + p.splits - 1) / p.splits;
   t0 = split * tps;
   t1 = min(t0 + tps, total);
@@ -380,13 +380,12 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   const int kvh = pair % p.hkv;
   const int G = p.group;
 
-  // Independent loads first.  The split geometry comes from the host bound
-  // (hint_tiles / hint_tps); the first tile's block ids and K/V rows, the
-  // Q^T operand, the append row and the row length / slot are all in flight
-  // together -- no load address depends on seq_lens.
-  const int t_begin = split * p.hint_tps;
-  const int t_end = min(t_begin + p.hint_tps, p.hint_tiles);
-  int tile = t_begin + wave;
+  // Independent loads first.  The first tile is guessed from the host bound
+  // (hint_tps), so its block ids and K/V rows, the Q^T operand, the append
+  // row and the row length / slot are all in flight together -- no load
+  // address depends on seq_lens.  The guess is checked below.
+  const int guess_begin = split * p.hint_tps;
+  int tile = guess_begin + wave;
   TilePages pages = fetch_pages<BS>(p, b, tile);  // clamped, always in bounds
   u32x4 qf[4];
   {
@@ -414,7 +413,18 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   const int64_t eff_len = effective_len(p, seq_len, slot);
   const int64_t last = eff_len - 1;
   const int64_t app = (FUSE && eff_len > 0) ? last : -1;
-  const int live_end = min(t_end, static_cast<int>((eff_len + 31) / 32));
+  // The split's tiles come from the row's own length.  When the host bound
+  // predicted where they start (rows as long as the bound), the loads above
+  // are the right ones; otherwise the first tile is fetched again.
+  int t_begin, live_end;
+  split_range(p, split, eff_len, t_begin, live_end);
+  if (t_begin != guess_begin) {
+    tile = t_begin + wave;
+    if (tile < live_end) {
+      pages = fetch_pages<BS>(p, b, tile);
+      load_tile<T, BS>(p, b, kvh, tile, pages, c, g, cur);
+    }
+  }
 
   WaveState st;
 #pragma unroll
@@ -999,8 +1009,8 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
   p.splits = a.num_splits;
   if (a.max_seq_len < 0) return set_error(FD_E_INVALID, "fd_paged_decode: max_seq_len must be >= 0");
   {
-    // split geometry: from max_seq_len when given, else from the table width
-    // (seq_lens are clamped to it in the kernels anyway)
+    // first-tile guess of the MFMA kernel: from max_seq_len when given, else
+    // from the table width; each row's split range uses its own length
     const int64_t cap = a.max_blocks_per_seq * a.block_size;
     const int64_t bound = (a.max_seq_len > 0 && a.max_seq_len < cap) ? a.max_seq_len : cap;
     p.hint_tiles = static_cast<int>((bound + 31) / 32);

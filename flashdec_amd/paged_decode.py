@@ -407,9 +407,10 @@ def _vllm_paged_decode_attention_into(
     Extensions over the reference signature (both optional): ``split_counters``
     (zeroed int32 ``[>= num_reqs * num_kv_heads * 64]``, one 256-byte line per
     (request, KV head), left zero after every launch) merges the splits inside
-    the one launch; ``max_seq_len`` (a bound
-    on ``seq_lens``, vLLM's ``attn_metadata.max_seq_len``) lets block-table
-    reads start before ``seq_lens`` arrives.
+    the one launch; ``max_seq_len`` (a hint such as vLLM's
+    ``attn_metadata.max_seq_len``; any value is correct) lets the first
+    tile's block-table and K/V reads of rows that long start before
+    ``seq_lens`` arrives.
     """
     sb, sp, st, sh, sd = kv_cache.stride()
     plane_bytes = sp * kv_cache.element_size()

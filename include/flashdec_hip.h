@@ -79,9 +79,11 @@ typedef struct ihipStream_t* fd_stream_t; /* == hipStream_t */
  * that share one counter buffer must not run concurrently (e.g. on two
  * streams).  Without it a second, reducer kernel performs the merge.
  *
- * max_seq_len: host-side upper bound on seq_lens (0 = unknown).  When given,
- * split ranges derive from it, so block-table reads need not wait for
- * seq_lens; it must not be smaller than any seq_lens[b].
+ * max_seq_len: optional hint (0 = none), e.g. the batch's longest row.
+ * Each row's split range comes from its own seq_lens[b] (tiles split evenly
+ * over num_splits), so any value is correct; for rows whose length matches
+ * the hint the first tile's block-table and K/V reads are issued before
+ * seq_lens[b] is read, other rows fetch their first tile after it.
  *
  * Fused append (append_k, append_v, slot_mapping all non-NULL): the
  * request's newest token (position seq_lens[b]-1) is taken from
@@ -124,7 +126,10 @@ typedef struct fd_paged_decode_args {
   float* split_sum;
   int64_t split_stats_stride[3]; /* seq, head, split */
   uint32_t* split_counters;     /* optional in-launch merge, see above */
-  int64_t max_seq_len;          /* optional bound on seq_lens, 0 = unknown */
+  int64_t max_seq_len;          /* optional hint, 0 = none: the batch's longest
+                                   row.  Rows of any length are correct; rows
+                                   this long start their K/V loads before
+                                   seq_lens is read. */
 
   const void* append_k; /* optional fused append, all-or-none */
   int64_t append_k_stride[3];

@@ -268,3 +268,78 @@ def test_explicit_splits_reducer_kernel_many_splits(num_splits):
     out = torch.empty_like(q)
     _fd().paged_decode_attention_into(q, k, v, table, lens, out, split_kv_workspace=ws, num_splits=num_splits)
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+@pytest.mark.parametrize("in_launch_merge", [False, True])
+@pytest.mark.parametrize("hint", [1, 100, 700, 5000])
+def test_max_seq_len_is_only_a_hint(hint, in_launch_merge):
+    """Rows longer or shorter than the max_seq_len hint are attended in full."""
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    bs, splits = 16, 8
+    q, k, v, table, lens = make_paged_inputs([700, 1, 333, 1500], 16, 2, 128, bs, torch.bfloat16, seed=41)
+    ws = (torch.empty((4, 16, splits, 128), device="cuda"), torch.empty((4, 16, splits), device="cuda"),
+          torch.empty((4, 16, splits), device="cuda"))
+    counters = torch.zeros(4 * 2 * 64, device="cuda", dtype=torch.int32) if in_launch_merge else None
+    out = torch.empty_like(q)
+    args = _lib.PagedDecodeArgs()
+    pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out, 2, bs,
+                    1.0 / math.sqrt(128))
+    args.num_blocks = k.shape[0]
+    args.max_seq_len = hint
+    pd._fill_workspace(args, *ws, splits, counters)
+    _lib.paged_decode(args, _lib.current_stream_handle(q.device))
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+    if counters is not None:
+        assert torch.count_nonzero(counters) == 0
+
+
+def test_graph_replay_after_rows_grow_past_the_captured_hint():
+    """vLLM's pattern: capture with the current max_seq_len, replay after rows grew in place."""
+    from flashdec_amd.paged_decode import _vllm_paged_decode_attention_into
+
+    bs, full_lens = 16, [900, 400, 1200, 64]
+    q, k, v, table, lens_full = make_paged_inputs(full_lens, 16, 2, 128, bs, torch.bfloat16, seed=43)
+    cache = torch.stack((k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3)), dim=1).contiguous()
+    append_k = cache[:, 0].new_empty((4, 2, 128))
+    append_v = torch.empty_like(append_k)
+    lens = torch.tensor([300, 100, 500, 10], device="cuda", dtype=torch.int32)
+    slot_mapping = torch.empty(4, device="cuda", dtype=torch.int64)
+    splits = 8
+    ws = (torch.empty((4, 16, splits, 128), device="cuda"), torch.empty((4, 16, splits), device="cuda"),
+          torch.empty((4, 16, splits), device="cuda"))
+    out = torch.empty_like(q)
+
+    def set_rows(lengths):
+        lens.copy_(torch.tensor(lengths, device="cuda", dtype=torch.int32))
+        sl = _slots(table, lens.cpu(), bs)
+        slot_mapping.copy_(torch.tensor(sl, device="cuda", dtype=torch.int64))
+        for b, s in enumerate(sl):  # the newest token's K/V, as vLLM's separate update leaves them
+            blk, off = divmod(s, bs)
+            append_k[b] = cache[blk, 0, off]
+            append_v[b] = cache[blk, 1, off]
+
+    def launch():
+        _vllm_paged_decode_attention_into(q, append_k, append_v, cache, table, lens, out, slot_mapping, *ws,
+                                          num_reqs=4, num_q_heads=16, num_kv_heads=2, head_dim=128, block_size=bs,
+                                          sm_scale=1.0 / math.sqrt(128), num_splits=splits, max_seq_len=500)
+
+    set_rows([300, 100, 500, 10])
+    launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph):
+            launch()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for lengths in ([301, 101, 501, 11], [900, 400, 1200, 64], [17, 399, 1100, 63]):
+        set_rows(lengths)
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
