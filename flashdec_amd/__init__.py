@@ -17,6 +17,7 @@ __all__ = [
     "DecodeEngine",
     "DecodeStepTransaction",
     "DecodeStepResult",
+    "DecodeStepGraph",
     "RopeAppendResult",
     "__version__",
     "apply_rope",
@@ -43,6 +44,7 @@ _LAZY = {
     "DecodeEngine": ("engine", "DecodeEngine"),
     "DecodeStepTransaction": ("engine", "DecodeStepTransaction"),
     "DecodeStepResult": ("engine", "DecodeStepResult"),
+    "DecodeStepGraph": ("engine", "DecodeStepGraph"),
     "RopeAppendResult": ("rope", "RopeAppendResult"),
     "apply_rope": ("rope", "apply_rope"),
     "rope_paged_kv_append": ("rope", "rope_paged_kv_append"),

@@ -61,49 +61,68 @@ class KVTokenTransactionView:
     state: str
 
 
+def _meta_nbytes(capacity, width):
+    return 24 * capacity + 4 * capacity * (1 + width)
+
+
 class _DeviceMeta:
     """Transaction metadata resident on the cache device (one packed buffer).
 
-    Layout (bytes): int64 positions[B] | int64 block_ids[B] | int64
-    offsets[B] | int32 effective_seq_lens[B] | int32 block_tables[B, MB].
+    Layout for ``capacity`` rows (bytes): int64 positions[cap] | int64
+    block_ids[cap] | int64 offsets[cap] | int32 effective_seq_lens[cap] |
+    int32 block_tables[cap, width].  The views cover the first ``batch`` rows,
+    so a buffer laid out for a fixed capacity keeps every view's address
+    whatever the batch (the graph-metadata arena).
     """
 
-    __slots__ = ("buf", "positions", "block_ids", "offsets", "eff_lens", "block_tables")
+    __slots__ = ("buf", "capacity", "positions", "block_ids", "offsets", "eff_lens", "block_tables")
 
-    def __init__(self, buf, batch, width):
+    def __init__(self, buf, batch, width, capacity=None):
         import torch
 
+        capacity = batch if capacity is None else capacity
         self.buf = buf
-        i64 = buf[: 24 * batch].view(torch.int64)
+        self.capacity = capacity
+        i64 = buf[: 24 * capacity].view(torch.int64)
         self.positions = i64[:batch]
-        self.block_ids = i64[batch : 2 * batch]
-        self.offsets = i64[2 * batch : 3 * batch]
-        i32 = buf[24 * batch :].view(torch.int32)
+        self.block_ids = i64[capacity : capacity + batch]
+        self.offsets = i64[2 * capacity : 2 * capacity + batch]
+        i32 = buf[24 * capacity : _meta_nbytes(capacity, width)].view(torch.int32)
         self.eff_lens = i32[:batch]
-        self.block_tables = i32[batch:].view(batch, width)
+        self.block_tables = i32[capacity : capacity + batch * width].view(batch, width)
 
     @classmethod
-    def build(cls, device, positions, locations, table_rows, width):
-        """Pack on the host and copy once (pinned staging for GPU caches)."""
+    def build(cls, device, positions, locations, table_rows, width, arena=None):
+        """Pack on the host and copy once (pinned staging for GPU caches).
+
+        With ``arena`` (a device buffer laid out for ``arena_capacity`` rows of
+        ``width`` table entries) the copy lands in the arena instead of a new
+        buffer.  Pinned staging comes from torch's caching host allocator,
+        which does not hand a block out again before its copy has completed.
+        """
         import torch
 
         batch = len(positions)
-        nbytes = 24 * batch + 4 * batch * (1 + width)
+        capacity = batch if arena is None else arena[1]
+        nbytes = _meta_nbytes(capacity, width)
         pinned = device.type == "cuda"
         host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=pinned)
         arr = host.numpy()
-        i64 = arr[: 24 * batch].view(np.int64)
+        i64 = arr[: 24 * capacity].view(np.int64)
         i64[:batch] = positions
-        i64[batch : 2 * batch] = [blk for blk, _ in locations]
-        i64[2 * batch :] = [off for _, off in locations]
-        i32 = arr[24 * batch :].view(np.int32)
+        i64[capacity : capacity + batch] = [blk for blk, _ in locations]
+        i64[2 * capacity : 2 * capacity + batch] = [off for _, off in locations]
+        i32 = arr[24 * capacity :].view(np.int32)
         i32[:batch] = [p + 1 for p in positions]
-        i32[batch:] = table_rows.reshape(-1)
+        i32[capacity : capacity + batch * width] = table_rows.reshape(-1)
+        if arena is not None:
+            arena[0][:nbytes].copy_(host, non_blocking=pinned)
+            return cls(arena[0], batch, width, capacity)
         buf = host.to(device, non_blocking=pinned) if pinned else host
         return cls(buf, batch, width)
 
     def clone(self):
-        return _DeviceMeta(self.buf.clone(), self.positions.numel(), self.block_tables.shape[1])
+        return _DeviceMeta(self.buf.clone(), self.positions.numel(), self.block_tables.shape[1], self.capacity)
 
 
 @dataclass
@@ -213,6 +232,7 @@ class PagedKVCache:
         self._prefix_miss_count = 0
         self._prefix_eviction_count = 0
         self._prefix_capacity_failure_count = 0
+        self._meta_arena = None  # (device buffer, capacity rows, table width) once enabled
 
     # ------------------------------------------------------------ lifecycle
     def add_request(self, request_id):
@@ -447,8 +467,14 @@ class PagedKVCache:
                 locations.append((s.block_ids[pos // self.block_size], off))
             self._validate_reserved_transaction_locations(ids, states, positions, locations)
             width = max(1, max(len(s.block_ids) for s in states))
+            arena = self._meta_arena
+            if arena is not None:
+                if len(ids) > arena[1] or width > arena[2]:
+                    raise RuntimeError("transaction exceeds the graph metadata arena "
+                                       f"({len(ids)} rows x {width} blocks > {arena[1]} x {arena[2]})")
+                width = arena[2]
             rows = self._table_rows(states, width)
-            meta = _DeviceMeta.build(self.device, positions, locations, rows, width)
+            meta = _DeviceMeta.build(self.device, positions, locations, rows, width, arena)
             for s in states:
                 s.transaction_id = transaction_id
         except Exception:
@@ -531,6 +557,16 @@ class PagedKVCache:
 
     write_token_layer_fused_hip = write_token_layer_fused_cuda
 
+    def _record_graph_layers(self, transaction):
+        """Record every layer as written by a replayed step graph (see DecodeEngine.step_graph)."""
+        state = self._require_open_transaction(transaction)
+        if state.next_layer_idx != 0:
+            raise RuntimeError("a step graph writes every layer; this transaction already wrote some")
+        for layer in range(self.num_layers):
+            state.written_layers.add(layer)
+        state.next_layer_idx = self.num_layers
+        self._transaction_layer_write_count += self.num_layers
+
     def commit_token(self, transaction):
         """Publish the token after every layer has been written."""
         state = self._require_open_transaction(transaction)
@@ -585,6 +621,88 @@ class PagedKVCache:
         graph capture) that must not allocate per layer.
         """
         return self._require_open_transaction(transaction).meta
+
+    def enable_graph_metadata(self, max_batch, max_blocks_per_seq):
+        """Give every later transaction's metadata one fixed device address.
+
+        A graph captured against ``graph_metadata()`` replays correctly for
+        any later transaction of up to ``max_batch`` requests whose rows need
+        at most ``max_blocks_per_seq`` blocks: ``begin_token`` packs positions,
+        block ids, offsets, effective lengths and the block table (padded to
+        ``max_blocks_per_seq`` with -1) into the arena with one copy, ordered
+        on the current stream after any earlier replay that reads it.
+        """
+        torch = _torch()
+        if self._open_transaction_id is not None:
+            raise RuntimeError("cannot change the metadata arena during an open token transaction")
+        max_batch, width = int(max_batch), int(max_blocks_per_seq)
+        if max_batch <= 0 or width <= 0:
+            raise ValueError("max_batch and max_blocks_per_seq must be positive")
+        buf = torch.zeros(_meta_nbytes(max_batch, width), dtype=torch.uint8, device=self.device)
+        self._meta_arena = (buf, max_batch, width)
+        return self.graph_metadata(max_batch)
+
+    def graph_metadata(self, batch):
+        """Views of the arena for a ``batch``-row transaction (fixed addresses)."""
+        if self._meta_arena is None:
+            raise RuntimeError("graph metadata arena is not enabled")
+        buf, capacity, width = self._meta_arena
+        if not 0 < int(batch) <= capacity:
+            raise ValueError("batch must be in [1, arena capacity]")
+        return _DeviceMeta(buf, int(batch), width, capacity)
+
+    def seed_context(self, request_ids, num_tokens, k=None, v=None):
+        """Commit ``num_tokens`` tokens per request at once (bulk set-up).
+
+        The allocator ends in the state ``num_tokens`` single-token commits of
+        this batch would leave: blocks are taken from the free list in the
+        same interleaved order (every request's next block at each block
+        boundary, in request order) and ``seq_len`` grows by ``num_tokens``.
+        ``k``/``v`` ``[num_layers, B, num_tokens, Hkv, D]`` are scattered into
+        the new slots; without them the slots keep the pool's bytes (e.g.
+        synthetic benchmark data).  Transaction counters are not advanced.
+        """
+        torch = _torch()
+        if self._open_transaction_id is not None:
+            raise RuntimeError("cannot seed context during an open token transaction")
+        ids = tuple(self._normalize_request_ids(request_ids))
+        if not ids or len(set(ids)) != len(ids):
+            raise ValueError("request_ids must be non-empty and unique")
+        num_tokens = int(num_tokens)
+        if num_tokens <= 0:
+            raise ValueError("num_tokens must be positive")
+        states = [self._require_active_request(rid) for rid in ids]
+        if (k is None) != (v is None):
+            raise ValueError("k and v must be provided together")
+        if k is not None:
+            shape = (self.num_layers, len(ids), num_tokens, self.num_kv_heads, self.head_dim)
+            if tuple(k.shape) != shape or tuple(v.shape) != shape:
+                raise ValueError("seed K/V must have shape [num_layers, num_requests, num_tokens, Hkv, D]")
+            if k.device != self.device or v.device != self.device or k.dtype != self.dtype or v.dtype != self.dtype:
+                raise ValueError("seed K/V must use the cache device and dtype")
+        bs = self.block_size
+        starts = [s.seq_len for s in states]
+        needed = [(p + num_tokens + bs - 1) // bs - (p + bs - 1) // bs for p in starts]
+        if sum(needed) > len(self._free_blocks):
+            self._capacity_failure_count += 1
+            raise RuntimeError("PagedKVCache is out of physical blocks")
+        # block boundaries in token order, requests in order at each token
+        for t in range(num_tokens):
+            for s, p in zip(states, starts):
+                if (p + t) % bs == 0:
+                    s.block_ids.append(self._allocate_block())
+        if k is not None:
+            for row, (s, p) in enumerate(zip(states, starts)):
+                pos = torch.arange(p, p + num_tokens, device=self.device)
+                blk = torch.tensor(s.block_ids, device=self.device)[pos // bs]
+                off = pos % bs
+                # non-adjacent advanced indices put the token axis first: [T, L, Hkv, D]
+                self.k_cache[:, blk, :, off, :] = k[:, row].permute(1, 0, 2, 3)
+                self.v_cache[:, blk, :, off, :] = v[:, row].permute(1, 0, 2, 3)
+        for s in states:
+            s.seq_len += num_tokens
+        self._state_version += 1
+        return self.seq_lens_tensor(ids)
 
     # -------------------------------------------------------------- queries
     def next_positions(self, request_ids, device=None):

@@ -93,6 +93,31 @@ class DecodeLayerResult:
     effective_seq_lens: Any
 
 
+@dataclass(frozen=True)
+class DecodeStepGraph:
+    """A captured hipGraph of one whole token step for a fixed batch size.
+
+    Replaying it runs, for every layer in order, the fused RoPE + K/V append
+    (``q[l]``, ``k[l]``, ``v[l]`` -> the reserved slots, ``q_rot[l]``) and the
+    paged decode (``q_rot[l]`` -> ``out[l]``), reading the open
+    transaction's metadata from the cache's graph-metadata arena.  The
+    caller writes ``q``/``k``/``v`` ``[num_layers, B, H, D]`` before each
+    replay; ``out`` holds every layer's attention output afterwards.
+    """
+
+    graph: Any
+    batch_size: int
+    q: Any
+    k: Any
+    v: Any
+    q_rot: Any
+    out: Any
+    num_splits: int
+    rotary_dim: int
+    base: float
+    metadata: Any
+
+
 @dataclass
 class _OpenStep:
     handle: DecodeStepTransaction
@@ -332,6 +357,92 @@ class DecodeEngine:
     def abort_step(self, transaction):
         """Explicitly abort the open token transaction."""
         return self._abort_open_step(self._require_open_step(transaction))
+
+    def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0):
+        """Capture every layer's launches of one token step into a hipGraph.
+
+        Needs the HIP backends, a GPU cache and its graph-metadata arena
+        (``PagedKVCache.enable_graph_metadata``) with room for ``batch_size``
+        rows.  Nothing runs at capture time and no allocator state changes;
+        input and output buffers are allocated here and returned in the
+        :class:`DecodeStepGraph`.  The decode split count is fixed for the
+        arena's table width; each row's split range follows its own length at
+        replay, so growing sequences stay correct.
+        """
+        torch = _torch()
+        from . import _lib
+        from ._fused_rope_kv_append import _fused_rope_kv_append_trusted
+        from .paged_decode import _auto_workspace, paged_decode_attention_into
+
+        self._require_no_open_step("capture a step graph")
+        cache = self.cache
+        if self._append != "fused_hip" or self._decode_kind != "hip":
+            raise RuntimeError("step graphs require append_backend='fused_cuda' and decode_backend='triton'")
+        if cache.device.type != "cuda":
+            raise ValueError("step graphs require a CUDA-resident PagedKVCache")
+        batch_size, num_q_heads = int(batch_size), int(num_q_heads)
+        if num_q_heads <= 0 or num_q_heads % cache.num_kv_heads:
+            raise ValueError("num_q_heads must be a positive multiple of num_kv_heads")
+        meta = cache.graph_metadata(batch_size)
+        if rotary_dim is None:
+            rotary_dim = cache.head_dim
+        shape_q = (cache.num_layers, batch_size, num_q_heads, cache.head_dim)
+        shape_kv = (cache.num_layers, batch_size, cache.num_kv_heads, cache.head_dim)
+        dev, dt = cache.device, cache.dtype
+        q = torch.zeros(shape_q, device=dev, dtype=dt)
+        k = torch.zeros(shape_kv, device=dev, dtype=dt)
+        v = torch.zeros(shape_kv, device=dev, dtype=dt)
+        q_rot = torch.zeros_like(q)
+        out = torch.zeros_like(q)
+        width = meta.block_tables.shape[1]
+        splits = _lib.paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
+                                        width * cache.block_size)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            if splits > 1:  # the capture stream's split workspace exists before capture
+                _auto_workspace(q_rot[0], cache.num_kv_heads, splits, _lib.current_stream_handle(dev))
+            with torch.cuda.graph(graph, stream=side):
+                for layer in range(cache.num_layers):
+                    _fused_rope_kv_append_trusted(q[layer], k[layer], v[layer], cache.k_cache[layer],
+                                                  cache.v_cache[layer], meta.block_ids, meta.offsets, meta.positions,
+                                                  rotary_dim=rotary_dim, base=base, q_out=q_rot[layer])
+                    paged_decode_attention_into(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
+                                                meta.block_tables, meta.eff_lens, out[layer], sm_scale=self.sm_scale,
+                                                block_size=cache.block_size)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
+                               num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta)
+
+    def step_graph(self, transaction, step_graph):
+        """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.
+
+        The transaction must be fresh (no layer run yet), its batch the
+        graph's size, and its metadata in the cache's arena.  The replay goes
+        on the current stream after the transaction's metadata copy.  An
+        error aborts the whole token, as in ``step_layer``.
+        """
+        state = self._require_open_step(transaction)
+        try:
+            if not isinstance(step_graph, DecodeStepGraph):
+                raise TypeError("step_graph must be a DecodeStepGraph")
+            if state.next_layer_idx != 0:
+                raise RuntimeError("a step graph runs every layer; this step already ran some")
+            if len(state.handle.request_ids) != step_graph.batch_size:
+                raise ValueError("transaction batch size does not match the step graph")
+            meta = self.cache.transaction_device_metadata(state.cache_transaction)
+            if meta.buf.data_ptr() != step_graph.metadata.buf.data_ptr():
+                raise RuntimeError("transaction metadata is not in the graph metadata arena")
+            step_graph.graph.replay()
+            self.cache._record_graph_layers(state.cache_transaction)
+        except Exception:
+            self._abort_open_step(state)
+            raise
+        state.next_layer_idx = self.cache.num_layers
+        state.last_output = step_graph.out[-1]
+        self._transaction_layer_step_count += self.cache.num_layers
+        return step_graph.out
 
     def step(self, q, k, v, request_ids=None, layer_idx=0, rotary_dim=None, base=10_000.0):
         """Single-layer append -> decode step; backpressure returns without mutation."""

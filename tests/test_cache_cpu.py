@@ -524,3 +524,72 @@ def test_shared_prefix_attach_rejections():
     with pytest.raises(ValueError, match="shape does not match"):
         cache.register_prefix("q", torch.zeros(1, 1, 1, 3, 3), torch.zeros(1, 1, 1, 3, 3))
     assert cache.validate_invariants()
+
+
+# -------------------------------------------------------- bulk seeding, arena
+def test_seed_context_equals_token_by_token_commits():
+    a = make_cache(num_layers=2, block_size=4, max_blocks=32)
+    b = make_cache(num_layers=2, block_size=4, max_blocks=32)
+    for c in (a, b):
+        for rid in ("x", "y", "z"):
+            c.add_request(rid)
+    g = torch.Generator().manual_seed(3)
+    # y starts mid-block so the two paths interleave allocations the same way
+    tx = a.begin_token(["y"])
+    write_all_layers(a, tx)
+    a.commit_token(tx)
+    tx = b.begin_token(["y"])
+    write_all_layers(b, tx)
+    b.commit_token(tx)
+    k = torch.randn(2, 3, 9, 1, 2, generator=g)
+    v = torch.randn(2, 3, 9, 1, 2, generator=g)
+    for t in range(9):
+        tx = a.begin_token(["x", "y", "z"])
+        for layer in range(2):
+            a.write_token_layer(tx, layer, k[layer, :, t], v[layer, :, t])
+        a.commit_token(tx)
+    lens = b.seed_context(["x", "y", "z"], 9, k, v)
+    assert lens.tolist() == [9, 10, 9]
+    for rid in ("x", "y", "z"):
+        assert a.request_block_ids(rid) == b.request_block_ids(rid)
+    assert list(a._free_blocks) == list(b._free_blocks)
+    assert torch.equal(a.k_cache, b.k_cache) and torch.equal(a.v_cache, b.v_cache)
+    for key in ("used_blocks", "allocation_count", "fresh_allocation_count", "active_tokens"):
+        assert a.metrics()[key] == b.metrics()[key]
+    assert b.validate_invariants()
+
+
+def test_seed_context_capacity_failure_is_atomic():
+    cache = make_cache(block_size=4, max_blocks=2)
+    cache.add_request(1).add_request(2)
+    with pytest.raises(RuntimeError, match="out of physical blocks"):
+        cache.seed_context([1, 2], 5)
+    assert cache.num_used_blocks == 0 and cache.seq_lens_tensor([1, 2]).tolist() == [0, 0]
+    with pytest.raises(ValueError, match="together"):
+        cache.seed_context([1], 1, k=torch.zeros(1, 1, 1, 1, 2))
+
+
+def test_graph_metadata_arena_layout_and_limits():
+    cache = make_cache(num_layers=1, block_size=2, max_blocks=16)
+    arena = cache.enable_graph_metadata(max_batch=4, max_blocks_per_seq=3)
+    for rid in ("a", "b"):
+        cache.add_request(rid)
+    cache.seed_context(["a"], 3)
+    tx = cache.begin_token(["a", "b"])
+    meta = cache.transaction_device_metadata(tx)
+    view2 = cache.graph_metadata(2)
+    assert meta.buf.data_ptr() == arena.buf.data_ptr()
+    assert meta.block_ids.data_ptr() == view2.block_ids.data_ptr() == arena.block_ids.data_ptr()
+    assert meta.block_tables.data_ptr() == arena.block_tables.data_ptr()
+    assert meta.positions.tolist() == [3, 0] and meta.offsets.tolist() == [1, 0]
+    assert meta.eff_lens.tolist() == [4, 1]
+    assert meta.block_tables.tolist() == [[0, 1, -1], [2, -1, -1]]
+    assert tx.block_tables.tolist() == [[0, 1, -1], [2, -1, -1]]
+    write_all_layers(cache, tx)
+    cache.commit_token(tx)
+    cache.seed_context(["a"], 2)  # a now needs 3 blocks; its next token needs a 4th
+    version = cache.state_version
+    with pytest.raises(RuntimeError, match="graph metadata arena"):
+        cache.begin_token(["a", "b"])
+    assert cache.state_version == version and not cache.has_open_transaction
+    assert cache.request_block_ids("a") == (0, 1, 3) and cache.validate_invariants()
