@@ -64,6 +64,10 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
+    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "engine"), default="decode",
+                   help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
+                        "prefix: C4 ragged long-context and shared-prefix decode; engine: C5 36-layer step")
+    p.add_argument("--engine-steps", type=int, default=200, help="timed steps of the engine workload")
     return p.parse_args()
 
 
@@ -176,6 +180,274 @@ def profile_kernels(torch, dev, lib, prepared, n):
     print(json.dumps({"profile_kernels": n, "copy_probe_mib": COPY_PROBE_MIB, "copies": 4}), flush=True)
 
 
+def graph_ms_per_call(torch, dev, fn, n_calls, warmup=8):
+    """Mean ms per call of ``fn(i)`` for ``n_calls`` calls captured in one hipGraph, replayed once."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn(0)  # per-stream workspaces exist before capture
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(n_calls):
+                fn(i)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / n_calls
+
+
+def attention_kernel_us(torch, prepared, n_calls):
+    """Mean attention-kernel and reducer durations (us) through the library's timing hook."""
+    from flashdec_amd import _lib
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_calls)]
+    for evs in events:
+        for e in evs:
+            e.record()
+    back_to_back(torch, _lib, prepared, n_calls, events)
+    attn = statistics.mean(e[0].elapsed_time(e[1]) for e in events) * 1e3
+    has_reducer = prepared[0][0].num_splits > 1
+    red = statistics.mean(e[2].elapsed_time(e[3]) for e in events) * 1e3 if has_reducer else 0.0
+    return attn, red
+
+
+def common_fields(args, metric, value, unit, ms_per_step, higher_is_better, config, dtype="bf16"):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": higher_is_better,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config}
+
+
+def run_rope(torch, dev, args):
+    """C3: fused RoPE + paged K/V append, B64 Hq16 Hkv2 D128 bf16, theta 1e6, pos ~ U{1..8191}."""
+    from flashdec_amd._fused_rope_kv_append import _fused_rope_kv_append_trusted
+
+    batch, hq, hkv, d, bs = 64, 16, 2, 128, 32
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(251)
+    blocks = batch * 256
+    kc = torch.zeros((blocks, hkv, bs, d), device=dev, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    table = torch.randperm(blocks, device=dev, generator=gen).view(batch, 256)
+    pos = torch.randint(1, 8192, (batch,), device=dev, generator=gen)
+    blk = table.gather(1, (pos // bs).unsqueeze(1)).squeeze(1).contiguous()
+    off = (pos % bs).contiguous()
+    calls = []
+    for i in range(4):
+        q = torch.randn((batch, hq, d), device=dev, generator=gen).to(torch.bfloat16)
+        k = torch.randn((batch, hkv, d), device=dev, generator=gen).to(torch.bfloat16)
+        v = torch.randn((batch, hkv, d), device=dev, generator=gen).to(torch.bfloat16)
+        calls.append((q, k, v, torch.empty_like(q)))
+
+    def fn(i):
+        q, k, v, qo = calls[i % len(calls)]
+        _fused_rope_kv_append_trusted(q, k, v, kc, vc, blk, off, pos, base=1e6, q_out=qo)
+
+    ms = graph_ms_per_call(torch, dev, fn, args.steps)
+    nbytes = batch * (2 * hq + 3 * hkv) * d * 2 + 24 * batch
+    log(f"[bench] rope+append: {ms * 1e3:.2f} us/call, {nbytes} B/call")
+    out = common_fields(args, "fused RoPE + KV append us/call, B64 Hq16 Hkv2 D128 bf16 (C3)", round(ms * 1e3, 3),
+                        "us", ms, False, {"workload": "rope-kv-append-b64-hq16-hkv2-d128-bs32", "batch": batch,
+                                          "rope_theta": 1e6, "positions": "U{1..8191} seed 251"})
+    out["roofline"] = {"bound": "launch", "algorithmic_bytes_per_call": nbytes,
+                       "achieved": round(nbytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "peak": HBM_PEAK_GBS}
+    return out
+
+
+def ragged_lengths(n, seed):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    return [int(round(math.exp(x))) for x in rng.uniform(math.log(128), math.log(32768), size=n)]
+
+
+def decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks=0):
+    """Independent (q, k, v, table, lens, out) sets; the first ``prefix_blocks`` of every row are shared."""
+    nblk = [(n + bs - 1) // bs for n in lens]
+    private = [max(0, b - prefix_blocks) for b in nblk]
+    pool_blocks = int(math.ceil((prefix_blocks + sum(private)) * 1.25)) + 1
+    width = max(nblk)
+    pools = []
+    gen = torch.Generator(device=dev)
+    for i in range(n_pools):
+        gen.manual_seed(seed + i)
+        k = torch.empty((pool_blocks, hkv, bs, d), device=dev, dtype=torch.bfloat16).normal_(generator=gen)
+        v = torch.empty_like(k).normal_(generator=gen)
+        q = torch.randn((len(lens), hq, d), device=dev, generator=gen).to(torch.bfloat16)
+        perm = torch.randperm(pool_blocks, device=dev, generator=gen).to(torch.int32)
+        table = torch.full((len(lens), width), -1, device=dev, dtype=torch.int32)
+        shared = perm[:prefix_blocks]
+        cursor = prefix_blocks
+        for b, nb in enumerate(nblk):
+            table[b, :prefix_blocks] = shared
+            table[b, prefix_blocks:nb] = perm[cursor:cursor + private[b]]
+            cursor += private[b]
+        pools.append((q, k, v, table, torch.tensor(lens, device=dev, dtype=torch.int32), torch.empty_like(q)))
+    return pools
+
+
+def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_blocks=0):
+    import flashdec_amd as fd
+
+    hq, hkv, d, bs = 16, 2, 128, 32
+    sm_scale = 1.0 / math.sqrt(d)
+    pools = decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks)
+
+    def fn(i):
+        q, k, v, table, sl, out = pools[i % len(pools)]
+        fd.paged_decode_attention_into(q, k, v, table, sl, out, sm_scale=sm_scale)
+
+    ms = graph_ms_per_call(torch, dev, fn, args.steps)
+    prepared = [prepared_args(p, sm_scale, bs, hkv) for p in pools]
+    attn_us, red_us = attention_kernel_us(torch, prepared, min(4 * len(pools), 96))
+    nblk = max((n + bs - 1) // bs for n in lens)
+    table_q = 4 * len(lens) * nblk + 4 * len(lens) + 2 * len(lens) * hq * d * 2
+    logical = sum(lens) * hkv * d * 2 * 2 + table_q
+    unique_tokens = prefix_blocks * bs + sum(max(0, n - prefix_blocks * bs) for n in lens)
+    unique = unique_tokens * hkv * d * 2 * 2 + table_q
+    splits = prepared[0][0].num_splits
+    log(f"[bench] {name}: {ms * 1e3:.2f} us/call (graph); attention kernel {attn_us:.2f} us, reducer {red_us:.2f} us;"
+        f" splits {splits}; logical {logical} B, unique {unique} B")
+    out = common_fields(args, f"paged-decode us/call + achieved HBM GB/s, {name}", round(unique / (ms * 1e-3) / 1e9, 2),
+                        "GB/s", ms, True,
+                        {"workload": name, "batch": len(lens), "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d,
+                         "block_size": bs, "seq_lens_sum": sum(lens), "seq_len_max": max(lens),
+                         "prefix_blocks": prefix_blocks, "kv_pools": n_pools, "num_splits": splits})
+    out["us_per_call"] = round(ms * 1e3, 3)
+    out["roofline"] = {"bound": "hbm", "achieved": round(unique / (attn_us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(unique / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "traffic": None, "kernel_us_mean": round(attn_us, 3), "reducer_us_mean": round(red_us, 3),
+                       "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}
+    return out
+
+
+def run_ragged(torch, dev, args):
+    """C4: B32 Hq16 Hkv2 D128 bf16, seq_lens ~ logU[128, 32768] (seed 1701)."""
+    return run_decode_variant(torch, dev, args, "ragged-b32-logU128-32768", ragged_lengths(32, 1701), 3, 1701)
+
+
+def run_prefix(torch, dev, args):
+    """C4 prefix: 16 requests share a 128-block (4096-token) prefix, private tails ~ U{1..512}."""
+    import numpy as np
+
+    tails = np.random.default_rng(1701).integers(1, 513, size=16)
+    lens = [4096 + int(t) for t in tails]
+    return run_decode_variant(torch, dev, args, "shared-prefix-16x4096+U512", lens, 40, 1701, prefix_blocks=128)
+
+
+def run_engine(torch, dev, args):
+    """C5: 36-layer DecodeEngine step, B64 Hq16 Hkv2 D128 bf16, context 8192, abort every 100th step."""
+    from flashdec_amd.cache import PagedKVCache
+    from flashdec_amd.engine import DecodeEngine
+
+    layers, batch, hq, hkv, d, bs, ctx = 36, 64, 16, 2, 128, 32, 8192
+    steps = args.engine_steps
+    width = (ctx + steps + 2 + bs - 1) // bs
+    cache = PagedKVCache(layers, hkv, d, bs, max_blocks=batch * width, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(109)
+    for layer in range(layers):
+        cache.k_cache[layer].normal_(generator=gen)
+        cache.v_cache[layer].normal_(generator=gen)
+    cache.enable_graph_metadata(batch, width)
+    engine = DecodeEngine(cache)
+    ids = list(range(batch))
+    for rid in ids:
+        engine.add_request(rid)
+    engine.admit()
+    cache.seed_context(ids, ctx)
+    log(f"[bench] engine: {layers} layers, B{batch}, context {ctx}, cache {cache.k_cache.numel() * 4 / 2**30:.1f} GiB")
+    sg = engine.capture_step_graph(batch, hq, base=1e6)
+    sg.q.normal_(generator=gen)
+    sg.k.normal_(generator=gen)
+    sg.v.normal_(generator=gen)
+
+    def graph_step():
+        tx = engine.begin_step(ids)
+        engine.step_graph(tx, sg)
+        engine.commit_step(tx)
+
+    def abort_step(bad_layer):
+        before = (cache.num_used_blocks, cache.seq_lens_tensor(ids).cpu())
+        tx = engine.begin_step(ids)
+        try:
+            for layer in range(layers):
+                q = sg.q[layer][..., :-1] if layer == bad_layer else sg.q[layer]
+                engine.step_layer(tx, layer, q, sg.k[layer], sg.v[layer], base=1e6)
+        except ValueError:
+            pass
+        else:
+            raise RuntimeError("the malformed layer input was accepted")
+        after = (cache.num_used_blocks, cache.seq_lens_tensor(ids).cpu())
+        return before[0] == after[0] and torch.equal(before[1], after[1])
+
+    for _ in range(3):
+        graph_step()
+    torch.cuda.synchronize()
+    committed = 0
+    rollbacks_ok = 0
+    aborts = 0
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        if i % 100 == 99:
+            aborts += 1
+            rollbacks_ok += abort_step((i // 100) % layers)
+        else:
+            graph_step()
+            committed += 1
+    stop.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    device_ms = start.elapsed_time(stop)
+    ms_per_step = device_ms / steps
+    # per-layer attention kernel, measured on the same shapes through the timing hook
+    from flashdec_amd import paged_decode as pd
+
+    tx = engine.begin_step(ids)
+    meta = cache.graph_metadata(batch)  # this transaction's metadata lives in the arena
+    prepared = []
+    for layer in range(4):
+        args_ = pd._lib.PagedDecodeArgs()
+        pd._fill_common(args_, sg.q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
+                        pd._cache_strides(cache.k_cache[layer], 2, 3), pd._cache_strides(cache.v_cache[layer], 2, 3),
+                        meta.block_tables, meta.eff_lens, sg.out[layer], hkv, bs, 1.0 / math.sqrt(d))
+        args_.num_blocks = cache.max_blocks
+        args_.max_seq_len = width * bs
+        acc, mx, sm, _ = pd._auto_workspace(sg.q_rot[layer], hkv, sg.num_splits, pd._lib.current_stream_handle(dev))
+        pd._fill_workspace(args_, acc, mx, sm, sg.num_splits)
+        prepared.append((args_, pd._lib.current_stream_handle(dev)))
+    attn_us, red_us = attention_kernel_us(torch, prepared, 16)
+    engine.abort_step(tx)
+    kv_layer = (ctx + committed) * batch * hkv * d * 2 * 2  # K+V bytes one layer's decode reads at the end
+    log(f"[bench] engine: {ms_per_step:.3f} ms/step over {steps} steps ({committed} committed, {aborts} aborted, "
+        f"{rollbacks_ok} clean rollbacks); wall {wall_s * 1e3 / steps:.3f} ms/step; attention kernel {attn_us:.1f} us"
+        f" per layer, reducer {red_us:.2f} us")
+    out = common_fields(args, "36-layer DecodeEngine step ms, B64 ctx8192 Qwen2.5-3B attention shape (C5)",
+                        round(ms_per_step, 4), "ms/step", ms_per_step, False,
+                        {"workload": "engine-36l-b64-ctx8192", "layers": layers, "batch": batch, "context": ctx,
+                         "steps": steps, "committed_steps": committed, "aborted_steps": aborts,
+                         "clean_rollbacks": rollbacks_ok, "num_splits": sg.num_splits,
+                         "timing": "events around the whole loop; graph-replayed steps, eager abort steps"})
+    out["steps"] = steps
+    out["tokens_per_s"] = round(committed * batch / (device_ms * 1e-3), 1)
+    out["wall_ms_per_step"] = round(wall_s * 1e3 / steps, 4)
+    out["roofline"] = {"bound": "hbm", "kernel_us_mean": round(attn_us, 2), "reducer_us_mean": round(red_us, 3),
+                       "algorithmic_bytes_per_layer": kv_layer,
+                       "achieved": round(kv_layer / (attn_us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(kv_layer / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -194,6 +466,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.load_library()
+    if args.workload != "decode":
+        run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "engine": run_engine}[args.workload]
+        print(json.dumps(run(torch, dev, args)), flush=True)
+        return
     batch, ctx, hq, hkv, d, bs = args.batch, args.ctx, 16, 2, 128, 32
     sm_scale = 1.0 / math.sqrt(d)
     log(f"[bench] building {args.pools} KV pools: B{batch} ctx{ctx} Hq{hq}/Hkv{hkv} D{d} bs{bs} bf16")
