@@ -138,7 +138,7 @@ def load_library():
             raise RuntimeError(f"failed to load {path}: {exc}") from exc
         lib.fd_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), _vp]
         lib.fd_paged_decode.restype = ctypes.c_int
-        lib.fd_paged_decode_plan.argtypes = [_i64, _i64, _i64, _i64, _i64]
+        lib.fd_paged_decode_plan.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64]
         lib.fd_paged_decode_plan.restype = ctypes.c_int
         lib.fd_fused_rope_kv_append.argtypes = [ctypes.POINTER(RopeAppendArgs), _vp]
         lib.fd_fused_rope_kv_append.restype = ctypes.c_int
@@ -196,9 +196,9 @@ def paged_decode(args: PagedDecodeArgs, stream: int) -> None:
     check(lib.fd_paged_decode(ctypes.byref(args), stream), "fd_paged_decode")
 
 
-def paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len) -> int:
+def paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len, total_seq_len=0) -> int:
     lib = load_library()
-    rc = lib.fd_paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
+    rc = lib.fd_paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len, total_seq_len)
     if rc < 0:
         check(rc, "fd_paged_decode_plan")
     return rc

@@ -116,6 +116,7 @@ class DecodeStepGraph:
     rotary_dim: int
     base: float
     metadata: Any
+    workspace: Any = None  # split partials the graph writes (kept alive with it)
 
 
 @dataclass
@@ -358,7 +359,7 @@ class DecodeEngine:
         """Explicitly abort the open token transaction."""
         return self._abort_open_step(self._require_open_step(transaction))
 
-    def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0):
+    def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None):
         """Capture every layer's launches of one token step into a hipGraph.
 
         Needs the HIP backends, a GPU cache and its graph-metadata arena
@@ -366,13 +367,14 @@ class DecodeEngine:
         rows.  Nothing runs at capture time and no allocator state changes;
         input and output buffers are allocated here and returned in the
         :class:`DecodeStepGraph`.  The decode split count is fixed for the
-        arena's table width; each row's split range follows its own length at
-        replay, so growing sequences stay correct.
+        arena's table width (``num_splits`` overrides it); each row's split
+        range follows its own length at replay, so growing sequences stay
+        correct.
         """
         torch = _torch()
         from . import _lib
         from ._fused_rope_kv_append import _fused_rope_kv_append_trusted
-        from .paged_decode import _auto_workspace, paged_decode_attention_into
+        from .paged_decode import _decode_with_workspace, _validate_inputs
 
         self._require_no_open_step("capture a step graph")
         cache = self.cache
@@ -395,25 +397,41 @@ class DecodeEngine:
         q_rot = torch.zeros_like(q)
         out = torch.zeros_like(q)
         width = meta.block_tables.shape[1]
-        splits = _lib.paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
-                                        width * cache.block_size)
+        if num_splits is None:
+            # the batch's current lengths tell a uniform batch from a ragged one
+            active = [cache.request_state(rid)["seq_len"] for rid in self.active_request_ids()]
+            longest = max(active, default=0) + 1
+            total = sum(active) + len(active) if len(active) == batch_size else 0
+            splits = _lib.paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
+                                            min(longest, width * cache.block_size) if total else
+                                            width * cache.block_size, total)
+        else:
+            splits = int(num_splits)
+            if splits <= 0:
+                raise ValueError("num_splits must be a positive integer")
+        _validate_inputs(q_rot[0], cache.k_cache[0], cache.v_cache[0], meta.block_tables, meta.eff_lens,
+                         cache.block_size, self.num_warps, self.num_stages, "token_major")
+        workspace = None
+        if splits > 1:
+            workspace = (torch.empty((batch_size, num_q_heads, splits, cache.head_dim), device=dev),
+                         torch.empty((batch_size, num_q_heads, splits), device=dev),
+                         torch.empty((batch_size, num_q_heads, splits), device=dev))
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            if splits > 1:  # the capture stream's split workspace exists before capture
-                _auto_workspace(q_rot[0], cache.num_kv_heads, splits, _lib.current_stream_handle(dev))
             with torch.cuda.graph(graph, stream=side):
                 for layer in range(cache.num_layers):
                     _fused_rope_kv_append_trusted(q[layer], k[layer], v[layer], cache.k_cache[layer],
                                                   cache.v_cache[layer], meta.block_ids, meta.offsets, meta.positions,
                                                   rotary_dim=rotary_dim, base=base, q_out=q_rot[layer])
-                    paged_decode_attention_into(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
-                                                meta.block_tables, meta.eff_lens, out[layer], sm_scale=self.sm_scale,
-                                                block_size=cache.block_size)
+                    _decode_with_workspace(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
+                                           meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
+                                           cache.block_size, splits, workspace, cache.max_blocks)
         torch.cuda.current_stream(dev).wait_stream(side)
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
-                               num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta)
+                               num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,
+                               workspace=workspace)
 
     def step_graph(self, transaction, step_graph):
         """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.

@@ -373,6 +373,27 @@ def paged_decode_attention_into(
     return out
 
 
+def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_splits,
+                           workspace, num_blocks):
+    """Unchecked launch on a token-major cache with a caller-held split workspace (graph capture).
+
+    ``workspace`` is ``(acc [B, Hq, S, D], max [B, Hq, S], sum [B, Hq, S])`` or
+    None for ``num_splits == 1``; any head_dim / group the library supports.
+    """
+    num_kv_heads = k_cache.shape[1]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[2])
+    args = _lib.PagedDecodeArgs()
+    _fill_common(args, q, k_cache, v_cache, _cache_strides(k_cache, 2, 3), _cache_strides(v_cache, 2, 3),
+                 block_tables, seq_lens, out, num_kv_heads, block_size, sm_scale)
+    args.num_blocks = num_blocks
+    args.max_seq_len = block_tables.shape[1] * block_size
+    acc, mx, sm = workspace if workspace is not None else (None, None, None)
+    _fill_workspace(args, acc, mx, sm, int(num_splits))
+    _lib.paged_decode(args, _lib.current_stream_handle(q.device))
+    return out
+
+
 def _vllm_paged_decode_attention_into(
     q,
     append_k,

@@ -151,13 +151,16 @@ int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
 
 /*
  * Split count the library would pick for a launch of this shape on the
- * current device (num_splits argument of fd_paged_decode).  max_seq_len is a
- * host-side upper bound on seq_lens (e.g. max_blocks_per_seq * block_size).
+ * current device (num_splits argument of fd_paged_decode).  max_seq_len is
+ * the longest row (or a bound such as max_blocks_per_seq * block_size);
+ * total_seq_len is the sum of seq_lens when the caller knows it (0 =
+ * unknown), which lets the plan tell a ragged batch (long rows need more
+ * splits) from a uniform one (fewer, longer splits).
  * Returns >= 1, or a negative FD_E* code.
  */
 int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads,
                          int64_t num_kv_heads, int64_t head_dim,
-                         int64_t max_seq_len);
+                         int64_t max_seq_len, int64_t total_seq_len);
 
 /*
  * Fused split-half (NeoX) RoPE of Q and K plus paged append of rotated K and
