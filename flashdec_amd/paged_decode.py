@@ -179,9 +179,12 @@ class _SplitWorkspace:
         self.counters = torch.zeros(counters, device=device, dtype=torch.int32)
 
     def views(self, num_seqs, num_q_heads, num_splits, head_dim):
-        n = num_seqs * num_q_heads * num_splits * (head_dim + 2)
-        view = self.flat[:n].view(num_seqs, num_q_heads, num_splits, head_dim + 2)
-        return view[..., :head_dim], view[..., head_dim], view[..., head_dim + 1], self.counters
+        # acc rows first (16-byte aligned: the kernels store and load them as
+        # float4), then max and sum as two [B, Hq, S] planes with equal strides
+        rows = num_seqs * num_q_heads * num_splits
+        acc = self.flat[: rows * head_dim].view(num_seqs, num_q_heads, num_splits, head_dim)
+        stats = self.flat[rows * head_dim : rows * (head_dim + 2)].view(2, num_seqs, num_q_heads, num_splits)
+        return acc, stats[0], stats[1], self.counters
 
 
 _WORKSPACES = {}
