@@ -17,7 +17,8 @@
 // element dtype.  The CPU oracle defines the same numbers, so K bytes match
 // bit for bit; V is a raw copy.
 //
-// One workgroup per request (launch-bound at decode batch sizes).
+// One workgroup per request (launch-bound at decode batch sizes).  Rows of
+// 16-byte vectors take the vector path below, other shapes the scalar one.
 #include "fd_common.h"
 
 #pragma clang fp contract(off)
@@ -125,6 +126,193 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
   }
 }
 
+// ------------------------------------------------------------------------
+// Vector path (16-byte rows): every global load of a request is issued at
+// the start -- position, slot, and each thread's q/k/v vectors -- so the
+// float64 cos/sin evaluation overlaps them, and the only other round trip is
+// the final 16-byte stores.  Work items of one request, in order: Q rotation
+// pairs (head, vector j of the low half + its partner in the high half), K
+// rotation pairs, Q tail vectors, K tail vectors, V vectors.  Needs
+// head_dim and rotary_dim / 2 to be multiples of the vector width and
+// 16-byte aligned rows (checked on the host).
+constexpr int kThreads = 256;
+constexpr int kPrefetch = 2;  // work items per thread held in registers across the barrier
+
+template <typename T>
+struct VecOps {
+  static constexpr int N = 16 / sizeof(T);
+  __device__ static void unpack(const u32x4& w, float (&x)[N]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[2 * j] = lo_f32<T>(w[j]);
+      x[2 * j + 1] = hi_f32<T>(w[j]);
+    }
+  }
+  __device__ static u32x4 pack(const float (&x)[N]) {
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = pack2<T>(x[2 * j], x[2 * j + 1]);
+    return w;
+  }
+};
+
+template <>
+struct VecOps<float> {
+  static constexpr int N = 4;
+  // Elements go through plain scalars: __builtin_bit_cast applied directly
+  // to an ext-vector element subscript (w[j]) compiled to element 0 for every
+  // j with this hipcc (seen in the gfx950 assembly), broadcasting lane 0.
+  __device__ static void unpack(const u32x4& w, float (&x)[N]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = w[j];
+      x[j] = __builtin_bit_cast(float, u);
+    }
+  }
+  __device__ static u32x4 pack(const float (&x)[N]) {
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f = x[j];
+      w[j] = __builtin_bit_cast(uint32_t, f);
+    }
+    return w;
+  }
+};
+
+struct ItemPlan {
+  int nq, nk, nqt, nkt, nv, total;
+  int hv, tv, dv;  // vectors per half, per tail, per row
+};
+
+// Addresses of work item `it` (element offsets from the row bases).
+template <typename T>
+struct Item {
+  const T* src0;
+  const T* src1;  // rotation partner (high half), else nullptr
+  T* dst0;
+  T* dst1;
+  int freq0;     // first frequency index of a rotation item
+  bool to_cache; // K/V item: stored only when the slot is valid
+};
+
+template <typename T>
+__device__ __forceinline__ Item<T> item_at(const RopeParams& p, const ItemPlan& ip, int b, int it, int64_t slot0) {
+  constexpr int N = VecOps<T>::N;
+  const int D = p.head_dim, half = p.rotary_dim / 2;
+  const int64_t hstride = static_cast<int64_t>(p.block_size) * D;
+  const T* qb = static_cast<const T*>(p.q) + static_cast<int64_t>(b) * p.hq * D;
+  T* ob = static_cast<T*>(p.q_out) + static_cast<int64_t>(b) * p.hq * D;
+  const T* kb = static_cast<const T*>(p.k) + static_cast<int64_t>(b) * p.hkv * D;
+  const T* vb = static_cast<const T*>(p.v) + static_cast<int64_t>(b) * p.hkv * D;
+  T* kc = static_cast<T*>(p.k_cache) + slot0;
+  T* vc = static_cast<T*>(p.v_cache) + slot0;
+  Item<T> r{nullptr, nullptr, nullptr, nullptr, 0, false};
+  if (it < ip.nq) {
+    const int h = it / ip.hv, j = (it % ip.hv) * N;
+    r = {qb + h * D + j, qb + h * D + half + j, ob + h * D + j, ob + h * D + half + j, j, false};
+  } else if ((it -= ip.nq) < ip.nk) {
+    const int h = it / ip.hv, j = (it % ip.hv) * N;
+    r = {kb + h * D + j, kb + h * D + half + j, kc + h * hstride + j, kc + h * hstride + half + j, j, true};
+  } else if ((it -= ip.nk) < ip.nqt) {
+    const int h = it / ip.tv, d = p.rotary_dim + (it % ip.tv) * N;
+    r = {qb + h * D + d, nullptr, ob + h * D + d, nullptr, 0, false};
+  } else if ((it -= ip.nqt) < ip.nkt) {
+    const int h = it / ip.tv, d = p.rotary_dim + (it % ip.tv) * N;
+    r = {kb + h * D + d, nullptr, kc + h * hstride + d, nullptr, 0, true};
+  } else {
+    it -= ip.nkt;
+    const int h = it / ip.dv, d = (it % ip.dv) * N;
+    r = {vb + h * D + d, nullptr, vc + h * hstride + d, nullptr, 0, true};
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void finish_item(const Item<T>& item, const u32x4& a, const u32x4& bvec, bool write_kv,
+                                            const float* s_cos, const float* s_sin) {
+  constexpr int N = VecOps<T>::N;
+  if (item.to_cache && !write_kv) return;
+  if (item.src1 == nullptr) {  // plain copy
+    *reinterpret_cast<u32x4*>(item.dst0) = a;
+    return;
+  }
+  float x1[N], x2[N], lo[N], hi[N];
+  VecOps<T>::unpack(a, x1);
+  VecOps<T>::unpack(bvec, x2);
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float c = s_cos[item.freq0 + e], sn = s_sin[item.freq0 + e];
+    const float t0 = x1[e] * c;
+    const float t1 = x2[e] * sn;
+    const float t2 = x2[e] * c;
+    const float t3 = x1[e] * sn;
+    lo[e] = t0 - t1;
+    hi[e] = t2 + t3;
+  }
+  *reinterpret_cast<u32x4*>(item.dst0) = VecOps<T>::pack(lo);
+  *reinterpret_cast<u32x4*>(item.dst1) = VecOps<T>::pack(hi);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rope_append_vec_kernel(RopeParams p) {
+  constexpr int N = VecOps<T>::N;
+  __shared__ float s_cos[kMaxHalf];
+  __shared__ float s_sin[kMaxHalf];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int D = p.head_dim, R = p.rotary_dim, half = R / 2;
+  const int64_t pos = load_index(p.positions, b, p.idx_i64);
+  const int64_t blk = load_index(p.block_ids, b, p.idx_i64);
+  const int64_t off = load_index(p.block_offsets, b, p.idx_i64);
+  const bool write_kv = blk >= 0 && blk < p.num_blocks && off >= 0 && off < p.block_size;
+  // out-of-range slots are never stored; row 0 keeps the addresses in bounds
+  const int64_t slot0 = write_kv ? (blk * p.hkv * p.block_size + off) * D : 0;
+  ItemPlan ip;
+  ip.hv = half / N;
+  ip.tv = (D - R) / N;
+  ip.dv = D / N;
+  ip.nq = p.q_out != nullptr ? p.hq * ip.hv : 0;
+  ip.nk = p.hkv * ip.hv;
+  ip.nqt = p.q_out != nullptr ? p.hq * ip.tv : 0;
+  ip.nkt = p.hkv * ip.tv;
+  ip.nv = p.hkv * ip.dv;
+  ip.total = ip.nq + ip.nk + ip.nqt + ip.nkt + ip.nv;
+
+  u32x4 ra[kPrefetch], rb[kPrefetch];
+#pragma unroll
+  for (int k = 0; k < kPrefetch; ++k) {
+    const int it = tid + k * kThreads;
+    if (it < ip.total) {
+      const Item<T> item = item_at<T>(p, ip, b, it, slot0);
+      ra[k] = *reinterpret_cast<const u32x4*>(item.src0);
+      if (item.src1 != nullptr) rb[k] = *reinterpret_cast<const u32x4*>(item.src1);
+    }
+  }
+  const float posf = static_cast<float>(pos);
+  for (int i = tid; i < half; i += kThreads) {
+    const float e = static_cast<float>(-2 * i) / static_cast<float>(R);
+    const float inv = static_cast<float>(pow(static_cast<double>(p.base), static_cast<double>(e)));
+    const float ang = posf * inv;
+    double sd, cd;
+    sincos(static_cast<double>(ang), &sd, &cd);
+    s_cos[i] = static_cast<float>(cd);
+    s_sin[i] = static_cast<float>(sd);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPrefetch; ++k) {
+    const int it = tid + k * kThreads;
+    if (it < ip.total) finish_item<T>(item_at<T>(p, ip, b, it, slot0), ra[k], rb[k], write_kv, s_cos, s_sin);
+  }
+  for (int it = tid + kPrefetch * kThreads; it < ip.total; it += kThreads) {  // very wide rows only
+    const Item<T> item = item_at<T>(p, ip, b, it, slot0);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(item.src0);
+    const u32x4 bv = item.src1 != nullptr ? *reinterpret_cast<const u32x4*>(item.src1) : a;
+    finish_item<T>(item, a, bv, write_kv, s_cos, s_sin);
+  }
+}
+
 // K/V scatter: one workgroup per request, 16-byte copies when rows allow.
 template <typename T>
 __global__ __launch_bounds__(256) void kv_append_kernel(RopeParams p) {
@@ -190,9 +378,19 @@ int fill_params(const fd_rope_append_args* args, RopeParams& p, bool need_rope, 
   return FD_OK;
 }
 
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
 template <typename T>
 int launch_rope(const fd_rope_append_args& a, const RopeParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((rope_append_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(256), 0, stream, p);
+  constexpr int N = VecOps<T>::N;
+  const bool vec = a.head_dim % N == 0 && (a.rotary_dim / 2) % N == 0 && aligned16(a.q) && aligned16(a.k) &&
+                   aligned16(a.v) && aligned16(a.k_cache) && aligned16(a.v_cache) &&
+                   (a.q_out == nullptr || aligned16(a.q_out));
+  if (vec)
+    hipLaunchKernelGGL((rope_append_vec_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(kThreads), 0, stream,
+                       p);
+  else
+    hipLaunchKernelGGL((rope_append_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(256), 0, stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "rope append launch failed: %s", hipGetErrorString(e));
   return FD_OK;
