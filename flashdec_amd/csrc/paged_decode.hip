@@ -115,89 +115,109 @@ __device__ __forceinline__ f32x4 mfma16x16x32<_Float16>(u32x4 a, u32x4 b, f32x4 
                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Register footprint of one 32-token tile for one lane (lane = 16*g + c):
-//   kf[mt][s]: K row (token 16*mt + c), dims [32*s + 8*g, +8)   (QK A operand)
-//   vf[i]    : V row (token vtok(g, i)), dims [8*c, +8)          (PV, transposed)
-// vtok(g, i) = 4*g + i (i < 4) or 16 + 4*g + (i - 4): the same tokens whose
-// scores this lane holds after QK (MFMA D layout: rows 4*g + r of each
-// 16-row tile), so P needs no cross-lane movement.
+// 16x16x16 MFMA (k = 16): A rows lane % 16, k = 4 * (lane / 16) + j; the
+// D layout is the same as the 16x16x32 product's.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x16<__bf16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                   0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x16<_Float16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h16x4, a), __builtin_bit_cast(h16x4, b), c, 0,
+                                               0, 0);
+}
+
+// Work unit of one wave: UNIT = 16 or 32 consecutive tokens.  Register
+// footprint for one lane (lane = 16*g + c), MT = UNIT / 16 row blocks:
+//   kf[mt][s]: K row (token UNIT*u + 16*mt + c), dims [32*s + 8*g, +8)  (QK A)
+//   vf[i]    : V row (token UNIT*u + vrow(g, i)), dims [8*c, +8)     (PV, transposed)
+// vrow(g, i) = 4*g + i (i < 4) or 16 + 4*g + (i - 4): the tokens whose scores
+// this lane holds after QK (MFMA D layout: rows 4*g + r of each 16-row
+// block), so P needs no cross-lane movement.  Four waves of 32-token units
+// suit splits of about one unit per wave (their compute runs on four SIMDs
+// at once); eight waves of 16-token units stream better on long splits (a
+// 16.8 MB read: 4.1 vs 4.8 us) and use the 16x16x16 PV product.
 //
 // Load addresses depend only on the block table, never on seq_lens: tokens
 // past the row's length and rows whose block id is out of range are masked
-// in registers at compute time, so the K/V loads of the first tile can be in
+// in registers at compute time, so the K/V loads of the first unit can be in
 // flight before the row length arrives.
-struct TileRegs {
-  u32x4 kf[2][4];
-  u32x4 vf[8];
+template <int UNIT>
+struct UnitRegs {
+  static constexpr int MT = UNIT / 16;
+  static constexpr int VR = UNIT / 4;  // V rows per lane: 4 (UNIT 16) or 8 (UNIT 32)
+  u32x4 kf[MT][4];
+  u32x4 vf[VR];
   uint32_t bmask;  // bit i: V row i lies in a valid physical block
 };
 
-__device__ __forceinline__ int vtok(int g, int i) { return i < 4 ? 4 * g + i : 12 + 4 * g + i; }
+__device__ __forceinline__ int vrow(int g, int i) { return i < 4 ? 4 * g + i : 12 + 4 * g + i; }
 
-// Physical block ids a tile needs.  The tile index is wave-uniform, so for
-// 32- and 16-token blocks these are scalar loads; pages are clamped to the
-// table row so the read is in bounds whatever the row's length.
-struct TilePages {
+template <int UNIT>
+constexpr int waves_for() {
+  return UNIT == 32 ? 4 : 8;
+}
+
+// Physical block ids a unit needs (wave-uniform, so scalar loads); pages are
+// clamped to the table row so the read is in bounds whatever the row's
+// length.  A unit spans one block, or two when the block is half its size.
+struct UnitPages {
   int32_t a, b;
 };
 
-template <int BS>
-__device__ __forceinline__ TilePages fetch_pages(const DecodeParams& p, int b, int tile) {
-  TilePages tp{0, 0};
+template <int BS, int UNIT>
+__device__ __forceinline__ UnitPages fetch_pages(const DecodeParams& p, int b, int unit) {
+  static_assert(BS >= UNIT / 2, "a unit spans at most two blocks");
+  UnitPages up{0, 0};
   const int64_t row = b * p.bts0;
   const int64_t width = p.max_blocks_per_seq;
-  if constexpr (BS == 32) {
-    const int64_t pg = tile < width ? tile : width - 1;
-    tp.a = load_index(p.bt, row + pg * p.bts1, p.bt_i64);
-  } else if constexpr (BS == 16) {
-    int64_t pa = 2 * static_cast<int64_t>(tile);
-    int64_t pb = pa + 1;
-    pa = pa < width ? pa : width - 1;
+  int64_t pa = (static_cast<int64_t>(unit) * UNIT) / BS;
+  pa = pa < width ? pa : width - 1;
+  up.a = load_index(p.bt, row + pa * p.bts1, p.bt_i64);
+  if constexpr (BS < UNIT) {
+    int64_t pb = (static_cast<int64_t>(unit) * UNIT) / BS + 1;
     pb = pb < width ? pb : width - 1;
-    tp.a = load_index(p.bt, row + pa * p.bts1, p.bt_i64);
-    tp.b = load_index(p.bt, row + pb * p.bts1, p.bt_i64);
+    up.b = load_index(p.bt, row + pb * p.bts1, p.bt_i64);
   }
-  return tp;
+  return up;
 }
 
-template <typename T, int BS>
-__device__ __forceinline__ void load_tile(const DecodeParams& p, int b, int kvh, int tile, const TilePages& tp,
-                                          int c, int g, TileRegs& t) {
-  const int64_t tok0 = static_cast<int64_t>(tile) * 32;
+template <typename T, int BS, int UNIT>
+__device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int unit, const UnitPages& up, int c,
+                                          int g, UnitRegs<UNIT>& t) {
   const T* kbase = static_cast<const T*>(p.k);
   const T* vbase = static_cast<const T*>(p.v);
-  auto block_of = [&](int tt) -> int32_t {  // tt: token within the tile
-    if constexpr (BS == 32) {
-      (void)tt;
-      return tp.a;
-    } else if constexpr (BS == 16) {
-      return tt < 16 ? tp.a : tp.b;
-    } else {
-      int64_t pg = (tok0 + tt) / BS;
-      pg = pg < p.max_blocks_per_seq ? pg : p.max_blocks_per_seq - 1;
-      return load_index(p.bt, b * p.bts0 + pg * p.bts1, p.bt_i64);
-    }
-  };
-  // K: rows 16*mt + c.  Rows in invalid blocks read row 0 of the cache
-  // (in bounds, value discarded by the score mask).
+  // tt: token within the unit; its block and the row inside that block
+  auto block_of = [&](int tt) -> int32_t { return (BS < UNIT && tt >= BS) ? up.b : up.a; };
+  auto row_in_block = [&](int tt) -> int { return (UNIT * unit + tt) % BS; };
+  // K rows 16*mt + c.  Rows in invalid blocks read row 0 of the cache (in
+  // bounds, value discarded by the score mask).
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < UnitRegs<UNIT>::MT; ++mt) {
     const int tt = 16 * mt + c;
     const int32_t blk = block_of(tt);
     const bool ok = blk >= 0 && blk < p.num_blocks;
-    const int64_t off = ok ? blk * p.ks0 + kvh * p.ks1 + (tt % BS) * p.ks2 : 0;
+    const int64_t off = ok ? blk * p.ks0 + kvh * p.ks1 + row_in_block(tt) * p.ks2 : 0;
     const T* row = kbase + off;
 #pragma unroll
     for (int s = 0; s < 4; ++s) t.kf[mt][s] = *reinterpret_cast<const u32x4*>(row + 32 * s + 8 * g);
   }
-  // V: rows vtok(g, i)
+  // V rows vrow(g, i)
   uint32_t bm = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int tt = vtok(g, i);
+  for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
+    const int tt = vrow(g, i);
     const int32_t blk = block_of(tt);
     const bool ok = blk >= 0 && blk < p.num_blocks;
-    const int64_t off = ok ? blk * p.vs0 + kvh * p.vs1 + (tt % BS) * p.vs2 : 0;
+    const int64_t off = ok ? blk * p.vs0 + kvh * p.vs1 + row_in_block(tt) * p.vs2 : 0;
     bm |= ok ? (1u << i) : 0u;
     t.vf[i] = *reinterpret_cast<const u32x4*>(vbase + off + 8 * c);
   }
@@ -236,47 +256,46 @@ struct WaveState {
   float l;       // partial denominator of this lane's tokens
 };
 
-// One tile: mask (row length, invalid blocks), splice in the appended token,
+// One unit: mask (row length, invalid blocks), splice in the appended token,
 // QK^T, online softmax, PV.  `last` is the last attended token, `app` the
 // token taken from the append registers (-1: none).
-template <typename T, bool FUSE>
-__device__ __forceinline__ void process_tile(TileRegs& t, const u32x4 (&qf)[4], float scale_log2, int64_t tok0,
-                                             int64_t last, int64_t app, const AppendRegs& ar, int c, int g,
-                                             WaveState& st) {
+template <typename T, bool FUSE, int UNIT>
+__device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf)[4], float scale_log2,
+                                             int64_t tok0, int64_t last, int64_t app, const AppendRegs& ar, int c,
+                                             int g, WaveState& st) {
+  constexpr int MT = UnitRegs<UNIT>::MT;
+  constexpr int VR = UnitRegs<UNIT>::VR;
   uint32_t vmask = t.bmask;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) vmask &= (tok0 + vtok(g, i) <= last) ? ~0u : ~(1u << i);
+  for (int i = 0; i < VR; ++i) vmask &= (tok0 + vrow(g, i) <= last) ? ~0u : ~(1u << i);
   if constexpr (FUSE) {
-    const int64_t at = app - tok0;  // in [0, 32) only for the tile holding it
+    const int64_t at = app - tok0;  // in [0, UNIT) only for the unit holding it
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       const bool hit = at == 16 * mt + c;
 #pragma unroll
       for (int s = 0; s < 4; ++s) t.kf[mt][s] = hit ? ar.akf[s] : t.kf[mt][s];
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool hit = at == vtok(g, i);
+    for (int i = 0; i < VR; ++i) {
+      const bool hit = at == vrow(g, i);
       t.vf[i] = hit ? ar.avf : t.vf[i];
       vmask |= hit ? (1u << i) : 0u;
     }
   }
-  // S^T[token][head] = K . Q^T  (two 16-token row tiles)
-  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  // S^T[token][head] = K . Q^T  (MT 16-token row blocks)
+  float sc[VR];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    s0 = mfma16x16x32<T>(t.kf[0][s], qf[s], s0);
-    s1 = mfma16x16x32<T>(t.kf[1][s], qf[s], s1);
-  }
-  float sc[8];
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4 sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    sc[r] = s0[r] * scale_log2;
-    sc[4 + r] = s1[r] * scale_log2;
+    for (int s = 0; s < 4; ++s) sb = mfma16x16x32<T>(t.kf[mt][s], qf[s], sb);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[4 * mt + r] = sb[r] * scale_log2;
   }
   float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < VR; ++i) {
     sc[i] = (vmask >> i) & 1u ? sc[i] : -INFINITY;
     mx = fmaxf(mx, sc[i]);
   }
@@ -285,39 +304,37 @@ __device__ __forceinline__ void process_tile(TileRegs& t, const u32x4 (&qf)[4], 
   const float m_new = fmaxf(st.m, mx);
   const float m_use = m_new == -INFINITY ? 0.f : m_new;
   const float alpha = exp2f(st.m - m_use);
-  float pr[8];
+  float pr[VR];
   float psum = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < VR; ++i) {
     pr[i] = exp2f(sc[i] - m_use);
     psum += pr[i];
   }
   st.l = st.l * alpha + psum;
   st.m = m_new;
-  // P^T operand, split into a 16-bit head and a 16-bit tail so the PV
-  // product keeps ~16 mantissa bits of the fp32 probabilities.
-  u32x4 ph, pl;
+  // P^T operand (k = VR*g + i: this lane's tokens), split into a 16-bit head
+  // and a 16-bit tail so the PV product keeps ~16 mantissa bits of the fp32
+  // probabilities.
+  uint32_t ph[VR / 2], pl[VR / 2];
   {
-    float lo[8];
+    float lo[VR];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < VR; ++i) {
       const uint32_t hb = pack2<T>(pr[i], 0.f) & 0xffffu;
       lo[i] = pr[i] - lo_f32<T>(hb);
     }
-    ph[0] = pack2<T>(pr[0], pr[1]);
-    ph[1] = pack2<T>(pr[2], pr[3]);
-    ph[2] = pack2<T>(pr[4], pr[5]);
-    ph[3] = pack2<T>(pr[6], pr[7]);
-    pl[0] = pack2<T>(lo[0], lo[1]);
-    pl[1] = pack2<T>(lo[2], lo[3]);
-    pl[2] = pack2<T>(lo[4], lo[5]);
-    pl[3] = pack2<T>(lo[6], lo[7]);
-  }
-  // V^T operands: vt_n holds dim 8*c + n of the lane's eight tokens.  Rows of
-  // masked tokens are zeroed first (their memory may hold NaN/Inf).
-  u32x4 vz[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+    for (int j = 0; j < VR / 2; ++j) {
+      ph[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
+      pl[j] = pack2<T>(lo[2 * j], lo[2 * j + 1]);
+    }
+  }
+  // V^T operands: vt_n holds dim 8*c + n of the lane's tokens.  Rows of masked
+  // tokens are zeroed first (their memory may hold NaN/Inf).
+  u32x4 vz[VR];
+#pragma unroll
+  for (int i = 0; i < VR; ++i) {
     const bool keep = (vmask >> i) & 1u;
     vz[i][0] = keep ? t.vf[i][0] : 0u;
     vz[i][1] = keep ? t.vf[i][1] : 0u;
@@ -328,18 +345,33 @@ __device__ __forceinline__ void process_tile(TileRegs& t, const u32x4 (&qf)[4], 
   for (int n = 0; n < 8; ++n) {
     const int w = n >> 1;
     const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
-    u32x4 vt;
-    vt[0] = __builtin_amdgcn_perm(vz[1][w], vz[0][w], sel);
-    vt[1] = __builtin_amdgcn_perm(vz[3][w], vz[2][w], sel);
-    vt[2] = __builtin_amdgcn_perm(vz[5][w], vz[4][w], sel);
-    vt[3] = __builtin_amdgcn_perm(vz[7][w], vz[6][w], sel);
     f32x4 a = st.acc[n] * alpha;
-    a = mfma16x16x32<T>(vt, ph, a);
-    st.acc[n] = mfma16x16x32<T>(vt, pl, a);
+    if constexpr (UNIT == 32) {
+      u32x4 vt, p_hi, p_lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vt[j] = __builtin_amdgcn_perm(vz[2 * j + 1][w], vz[2 * j][w], sel);
+        p_hi[j] = ph[j];
+        p_lo[j] = pl[j];
+      }
+      a = mfma16x16x32<T>(vt, p_hi, a);
+      st.acc[n] = mfma16x16x32<T>(vt, p_lo, a);
+    } else {
+      u32x2 vt, p_hi, p_lo;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        vt[j] = __builtin_amdgcn_perm(vz[2 * j + 1][w], vz[2 * j][w], sel);
+        p_hi[j] = ph[j];
+        p_lo[j] = pl[j];
+      }
+      a = mfma16x16x16<T>(vt, p_hi, a);
+      st.acc[n] = mfma16x16x16<T>(vt, p_lo, a);
+    }
   }
 }
 
-constexpr int kWaves = 4;
+constexpr int kMaxWaves = 8;          // waves per workgroup of the 16-token variant
+constexpr int kWideUnitMaxTiles = 4;  // splits of at most this many tiles take 32-token units
 constexpr int kAccPitch = 132;   // floats per head row in LDS (bank spread)
 constexpr int kMergeChunk = 16;  // splits whose partials one merge pass loads at once
 constexpr int64_t kMaxSplitTiles = 64;  // split planning: tiles of the longest row per split
@@ -364,8 +396,10 @@ __device__ __forceinline__ void store_row(const DecodeParams& p, int b, int qh, 
   }
 }
 
-template <typename T, int BS, bool FUSE, bool MERGE>
-__global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
+template <typename T, int BS, bool FUSE, bool MERGE, int UNIT>
+__global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
+  constexpr int kWaves = waves_for<UNIT>();
+  constexpr int kUnitsPerTile = 32 / UNIT;
   __shared__ float s_acc[kWaves][16][kAccPitch];
   __shared__ float s_m[kWaves][16];
   __shared__ float s_l[kWaves][16];
@@ -381,13 +415,14 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   const int kvh = pair % p.hkv;
   const int G = p.group;
 
-  // Independent loads first.  The first tile is guessed from the host bound
-  // (hint_tps), so its block ids and K/V rows, the Q^T operand, the append
-  // row and the row length / slot are all in flight together -- no load
-  // address depends on seq_lens.  The guess is checked below.
-  const int guess_begin = split * p.hint_tps;
-  int tile = guess_begin + wave;
-  TilePages pages = fetch_pages<BS>(p, b, tile);  // clamped, always in bounds
+  // Independent loads first.  The first unit is guessed from the host bound
+  // (hint_tps tiles per split), so its block ids and K/V rows, the Q^T
+  // operand, the append row and the row length / slot are all in flight
+  // together -- no load address depends on seq_lens.  The guess is checked
+  // below.
+  const int guess_begin = split * p.hint_tps;  // in 32-token tiles
+  int unit = kUnitsPerTile * guess_begin + wave;
+  UnitPages pages = fetch_pages<BS, UNIT>(p, b, unit);  // clamped, always in bounds
   u32x4 qf[4];
   {
     const bool hv = c < G;
@@ -408,22 +443,26 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   }
   const int32_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
   const int32_t slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
-  TileRegs cur;
-  load_tile<T, BS>(p, b, kvh, tile, pages, c, g, cur);
+  UnitRegs<UNIT> cur;
+  load_unit<T, BS, UNIT>(p, kvh, unit, pages, c, g, cur);
 
   const int64_t eff_len = effective_len(p, seq_len, slot);
   const int64_t last = eff_len - 1;
   const int64_t app = (FUSE && eff_len > 0) ? last : -1;
-  // The split's tiles come from the row's own length.  When the host bound
-  // predicted where they start (rows as long as the bound), the loads above
-  // are the right ones; otherwise the first tile is fetched again.
-  int t_begin, live_end;
-  split_range(p, split, eff_len, t_begin, live_end);
+  // The split's tiles come from the row's own length; its units are the
+  // UNIT-token pieces of those tiles that hold at least one live token.  When
+  // the host bound predicted where they start (rows as long as the bound),
+  // the loads above are the right ones; otherwise the first unit is fetched
+  // again.
+  int t_begin, t_end;
+  split_range(p, split, eff_len, t_begin, t_end);
+  const int live_units = static_cast<int>((eff_len + UNIT - 1) / UNIT);
+  const int u_end = min(kUnitsPerTile * t_end, live_units);
   if (t_begin != guess_begin) {
-    tile = t_begin + wave;
-    if (tile < live_end) {
-      pages = fetch_pages<BS>(p, b, tile);
-      load_tile<T, BS>(p, b, kvh, tile, pages, c, g, cur);
+    unit = kUnitsPerTile * t_begin + wave;
+    if (unit < u_end) {
+      pages = fetch_pages<BS, UNIT>(p, b, unit);
+      load_unit<T, BS, UNIT>(p, kvh, unit, pages, c, g, cur);
     }
   }
 
@@ -433,26 +472,27 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   st.m = -INFINITY;
   st.l = 0.f;
 
-  if (tile < live_end) {
-    TilePages next_pages{0, 0};
-    if (tile + kWaves < live_end) next_pages = fetch_pages<BS>(p, b, tile + kWaves);
+  if (unit < u_end) {
+    UnitPages next_pages{0, 0};
+    if (unit + kWaves < u_end) next_pages = fetch_pages<BS, UNIT>(p, b, unit + kWaves);
     for (;;) {
-      // issue the next tile's loads (and the block ids after it) before
-      // consuming the current tile
-      const int next = tile + kWaves;
-      const bool more = next < live_end;
-      TileRegs nxt;
-      TilePages after{0, 0};
+      // issue the next unit's loads (and the block ids after it) before
+      // consuming the current unit
+      const int next = unit + kWaves;
+      const bool more = next < u_end;
+      UnitRegs<UNIT> nxt;
+      UnitPages after{0, 0};
       if (more) {
-        load_tile<T, BS>(p, b, kvh, next, next_pages, c, g, nxt);
-        if (next + kWaves < live_end) after = fetch_pages<BS>(p, b, next + kWaves);
+        load_unit<T, BS, UNIT>(p, kvh, next, next_pages, c, g, nxt);
+        if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, b, next + kWaves);
       }
       if constexpr (FUSE)
-        if (app >= 0 && app / 32 == tile) store_append<T, BS>(p, kvh, slot, c, g, ar);
-      process_tile<T, FUSE>(cur, qf, p.scale_log2, static_cast<int64_t>(tile) * 32, last, app, ar, c, g, st);
+        if (app >= 0 && app / UNIT == unit) store_append<T, BS>(p, kvh, slot, c, g, ar);
+      process_unit<T, FUSE, UNIT>(cur, qf, p.scale_log2, static_cast<int64_t>(unit) * UNIT, last, app, ar, c, g,
+                                  st);
       if (!more) break;
       cur = nxt;
-      tile = next;
+      unit = next;
       next_pages = after;
     }
   }
@@ -460,6 +500,10 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   float lt = st.l;
   lt += shfl_xor_f32(lt, 16);
   lt += shfl_xor_f32(lt, 32);
+
+  // Every wave publishes its state (one LDS slot each; eight slots take 68 KB,
+  // which gfx950's LDS holds in one workgroup), then threads merge across the
+  // slots.
   if (g == 0) {
     s_m[wave][c] = st.m;
     s_l[wave][c] = lt;
@@ -472,10 +516,11 @@ __global__ __launch_bounds__(256, 1) void decode_mfma_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  // merge the four waves: thread -> (head h, dims [d0, d0 + 8))
-  const int h = threadIdx.x >> 4;
+  // merge the slots: thread -> (head h, dims [d0, d0 + 8)); threads past the
+  // first 256 only take part in the barrier of the in-launch merge
+  const int h = (threadIdx.x >> 4) & 15;
   const int d0 = (threadIdx.x & 15) * 8;
-  const bool head_ok = h < G;
+  const bool head_ok = threadIdx.x < 256 && h < G;
   const int qh = kvh * G + h;
   float M = -INFINITY;
 #pragma unroll
@@ -839,21 +884,36 @@ void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, 
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
 }
 
-template <typename T, int BS>
-void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
+template <typename T, int BS, int UNIT>
+void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
   const bool merge = p.counters != nullptr;
-  const dim3 block(256);
+  const dim3 block(64 * waves_for<UNIT>());
   if (p.fuse) {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, true, true>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, true, true, UNIT>, grid, block, stream, ev[0], ev[1], p);
     else
-      dispatch(decode_mfma_kernel<T, BS, true, false>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, true, false, UNIT>, grid, block, stream, ev[0], ev[1], p);
   } else {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, false, true>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, false, true, UNIT>, grid, block, stream, ev[0], ev[1], p);
     else
-      dispatch(decode_mfma_kernel<T, BS, false, false>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, false, false, UNIT>, grid, block, stream, ev[0], ev[1], p);
   }
+}
+
+// 32-token units on four waves when a split holds about one unit per wave
+// (C2: 4 tiles per split, 6.4 vs 6.7 us), 16-token units on eight waves for
+// longer splits (ragged B32: 70 -> 60 us; C5 layer: 97 -> 93 us).  8-token
+// blocks always take 16-token units (a unit spans at most two blocks).
+template <typename T, int BS>
+void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
+  if constexpr (BS >= 16) {
+    if (p.hint_tps <= kWideUnitMaxTiles) {
+      launch_mfma_unit<T, BS, 32>(p, grid, stream, ev);
+      return;
+    }
+  }
+  launch_mfma_unit<T, BS, 16>(p, grid, stream, ev);
 }
 
 template <typename T>
@@ -935,7 +995,7 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
       s = t;
       break;
     }
-  const int64_t cap = (tiles + kWaves - 1) / kWaves;  // >= one tile per wave
+  const int64_t cap = (2 * tiles + kMaxWaves - 1) / kMaxWaves;  // >= one unit per wave
   if (s > cap) s = cap;
   if (s > 256) s = 256;
   if (s < 1) s = 1;
