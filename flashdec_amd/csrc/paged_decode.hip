@@ -782,19 +782,52 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p, int 
 
 // ===================================================== split reducer ====
 // One wave per (request, query head): out = sum_s w_s acc_s / sum_s w_s l_s,
-// w_s = 2^(m_s - max_s m_s).  Splits are taken 16 at a time and every load of
-// a chunk is issued before any is used, so the merge costs one memory round
-// trip per 16 splits (the split statistics are wave-uniform scalar loads).
-constexpr int kReduceChunk = 16;
+// w_s = 2^(m_s - max_s m_s).  The kernel is pure latency, so every load is a
+// vector load issued up front: lane j holds split j's (max, sum) and
+// readlane broadcasts them.  Scalar loads would not do: they complete out of
+// order, so each use of one waits for all (lgkmcnt(0)), which turned the
+// per-split statistics into a round trip per split.  Row length and slot,
+// needed only for the final zero-row select, are vector loads too.
+constexpr int kReduceChunk = 16;  // splits whose partial rows are in flight at once
+
+// The reducer's own compact arguments: with the full DecodeParams the
+// compiler fetched the workspace fields in a second, dependent batch of
+// kernel-argument loads.
+struct ReduceParams {
+  const float* acc;
+  const float* mx;
+  const float* sm;
+  void* out;
+  const void* sl;
+  const void* slot;  // seq_lens again when there is no fused append
+  int64_t as0, as1, as2, as3;
+  int64_t ss0, ss1, ss2;
+  int64_t os0, os1, os2;
+  int64_t sls, slots;
+  int hq, splits, fuse, sl_i64, slot_i64;
+};
+
+__device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane_idx));
+}
 
 template <typename T, int D>
-__global__ __launch_bounds__(64) void split_reduce_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
+  // every argument in SGPRs before any use: one batch of argument loads, one
+  // wait (left alone the compiler fetched the strides lazily, a second
+  // dependent round trip)
+  asm volatile("" ::"s"(p.acc), "s"(p.mx), "s"(p.sm), "s"(p.out), "s"(p.sl), "s"(p.slot), "s"(p.as0), "s"(p.as1),
+               "s"(p.as2), "s"(p.as3), "s"(p.ss0), "s"(p.ss1), "s"(p.ss2), "s"(p.os0), "s"(p.os1), "s"(p.os2),
+               "s"(p.sls), "s"(p.slots), "s"(p.hq), "s"(p.splits), "s"(p.fuse), "s"(p.sl_i64), "s"(p.slot_i64));
   const int b = blockIdx.x / p.hq;
   const int qh = blockIdx.x % p.hq;
   const int lane = threadIdx.x;
   constexpr int E = D / 64;  // dims per lane
-  const int64_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
-  const int64_t slot = p.fuse ? load_index(p.slot, b * p.slots, p.slot_i64) : 0;
+  // a VGPR zero keeps the uniform row-length / slot loads on the vector path
+  int vzero = 0;
+  asm volatile("" : "+v"(vzero));
+  const int32_t seq_len = load_index(p.sl, b * p.sls + vzero, p.sl_i64);
+  const int32_t slot = load_index(p.slot, b * p.slots + vzero, p.slot_i64);  // seq_lens when not fused
   const int64_t sb = b * p.ss0 + qh * p.ss1;
   const float* ab = p.acc + b * p.as0 + qh * p.as1;
   float M = -INFINITY;
@@ -802,33 +835,45 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(DecodeParams p) {
   float o[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) o[e] = 0.f;
-  for (int s0 = 0; s0 < p.splits; s0 += kReduceChunk) {
-    float m[kReduceChunk], l[kReduceChunk], a[kReduceChunk][E];
+  for (int s64 = 0; s64 < p.splits; s64 += 64) {
+    const int n = min(64, p.splits - s64);  // splits of this pass, one per lane
+    const int sj = s64 + min(lane, n - 1);
+    const float lm = p.mx[sb + sj * p.ss2];
+    const float ll = p.sm[sb + sj * p.ss2];
+    for (int c0 = 0; c0 < n; c0 += kReduceChunk) {
+      float a[kReduceChunk][E];
 #pragma unroll
-    for (int j = 0; j < kReduceChunk; ++j) {
-      const int s = min(s0 + j, p.splits - 1);  // past the end: re-read, masked below
-      m[j] = p.mx[sb + s * p.ss2];
-      l[j] = p.sm[sb + s * p.ss2];
+      for (int j = 0; j < kReduceChunk; ++j) {
+        const int s = s64 + min(c0 + j, n - 1);  // past the end: re-read, masked below
 #pragma unroll
-      for (int e = 0; e < E; ++e) a[j][e] = ab[s * p.as2 + (lane + 64 * e) * p.as3];
+        for (int e = 0; e < E; ++e) a[j][e] = ab[s * p.as2 + (lane + 64 * e) * p.as3];
+      }
+      // keep every load above issued before the broadcasts below (they wait)
+      __builtin_amdgcn_sched_barrier(0);
+      float m[kReduceChunk], l[kReduceChunk];
+      float cm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kReduceChunk; ++j) {
+        const int src = min(c0 + j, n - 1);
+        m[j] = lane_bcast(lm, src);
+        l[j] = lane_bcast(ll, src);
+        cm = c0 + j < n ? fmaxf(cm, m[j]) : cm;
+      }
+      const float nm = fmaxf(M, cm);
+      const float nmu = nm == -INFINITY ? 0.f : nm;
+      const float sc = exp2f(M - nmu);
+      L *= sc;
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] *= sc;
+#pragma unroll
+      for (int j = 0; j < kReduceChunk; ++j) {
+        const float w = c0 + j < n ? exp2f(m[j] - nmu) : 0.f;
+        L += w * l[j];
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
+      }
+      M = nm;
     }
-    float cm = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kReduceChunk; ++j) cm = s0 + j < p.splits ? fmaxf(cm, m[j]) : cm;
-    const float nm = fmaxf(M, cm);
-    const float nmu = nm == -INFINITY ? 0.f : nm;
-    const float sc = exp2f(M - nmu);
-    L *= sc;
-#pragma unroll
-    for (int e = 0; e < E; ++e) o[e] *= sc;
-#pragma unroll
-    for (int j = 0; j < kReduceChunk; ++j) {
-      const float w = s0 + j < p.splits ? exp2f(m[j] - nmu) : 0.f;
-      L += w * l[j];
-#pragma unroll
-      for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
-    }
-    M = nm;
   }
   const bool has = seq_len > 0 && (!p.fuse || slot >= 0);
   const float inv = (has && L > 0.f) ? 1.f / L : 0.f;
@@ -944,11 +989,35 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
   if (p.splits > 1 && p.counters == nullptr) {
+    ReduceParams r;
+    r.acc = p.acc;
+    r.mx = p.mx;
+    r.sm = p.sm;
+    r.out = p.out;
+    r.sl = p.sl;
+    r.slot = p.fuse ? p.slot : p.sl;
+    r.as0 = p.as0;
+    r.as1 = p.as1;
+    r.as2 = p.as2;
+    r.as3 = p.as3;
+    r.ss0 = p.ss0;
+    r.ss1 = p.ss1;
+    r.ss2 = p.ss2;
+    r.os0 = p.os0;
+    r.os1 = p.os1;
+    r.os2 = p.os2;
+    r.sls = p.sls;
+    r.slots = p.fuse ? p.slots : p.sls;
+    r.hq = p.hq;
+    r.splits = p.splits;
+    r.fuse = p.fuse;
+    r.sl_i64 = p.sl_i64;
+    r.slot_i64 = p.fuse ? p.slot_i64 : p.sl_i64;
     const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
     if (a.head_dim == 64)
-      dispatch(split_reduce_kernel<T, 64>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], p);
+      dispatch(split_reduce_kernel<T, 64>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
     else
-      dispatch(split_reduce_kernel<T, 128>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], p);
+      dispatch(split_reduce_kernel<T, 128>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
     e = hipGetLastError();
     if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
   }
