@@ -294,6 +294,57 @@ def decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks=
     return pools
 
 
+def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
+    """The ctypes argument blocks ``paged_decode_attention_cascade_into`` builds for this pool."""
+    from flashdec_amd import _lib, cascade
+    from flashdec_amd import paged_decode as pd
+
+    q, k, v, table, lens, out = pool
+    stream = _lib.current_stream_handle(q.device)
+    splits = _lib.paged_decode_plan(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], max(groups.max_tail_len, 1),
+                                    max(groups.total_tail_len, 1))
+    psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads, groups.max_prefix_len,
+                                         cascade._num_cus(q.device))
+    acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits + psplits, stream)
+    args = _lib.PagedDecodeArgs()
+    pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,
+                    num_kv_heads, block_size, sm_scale)
+    args.num_blocks = k.shape[0]
+    args.max_seq_len = groups.max_prefix_len + groups.max_tail_len
+    pd._fill_workspace(args, acc, mx, sm, splits)
+    args.split_acc, args.split_max, args.split_sum = acc.data_ptr(), mx.data_ptr(), sm.data_ptr()
+    args.split_acc_stride[:] = acc.stride()
+    args.split_stats_stride[:] = mx.stride()
+    cas = _lib.CascadeArgs()
+    cas.num_groups, cas.max_members, cas.prefix_splits = groups.num_groups, groups.max_members, psplits
+    cas.group_members = groups.members.data_ptr()
+    cas.group_prefix_len = groups.prefix_len.data_ptr()
+    cas.row_prefix_len = groups.row_prefix_len.data_ptr()
+    cas.max_prefix_len = groups.max_prefix_len
+    return args, cas, stream
+
+
+def cascade_kernel_us(torch, prepared, n_calls):
+    """Mean (prefix + tail pass) and reducer durations (us) of cascade calls, through the timing hook."""
+    from flashdec_amd import _lib
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_calls)]
+    for evs in events:
+        for e in evs:
+            e.record()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(200_000_000)
+    for i in range(n_calls):
+        a, cas, st = prepared[i % len(prepared)]
+        a.timing_events[:] = [e.cuda_event for e in events[i]]
+        _lib.paged_decode_cascade(a, cas, st)
+        a.timing_events[:] = [None] * 4
+    torch.cuda.synchronize()
+    attn = statistics.mean(e[0].elapsed_time(e[1]) for e in events) * 1e3
+    red = statistics.mean(e[2].elapsed_time(e[3]) for e in events) * 1e3
+    return attn, red
+
+
 def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_blocks=0):
     import flashdec_amd as fd
 
@@ -325,6 +376,35 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
     out["roofline"] = {"bound": "hbm", "achieved": round(unique / (attn_us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(unique / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                        "traffic": None, "kernel_us_mean": round(attn_us, 3), "reducer_us_mean": round(red_us, 3),
+                       "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}
+    if prefix_blocks == 0:
+        return out
+    # the same pools through the cascade (prefix read once per group): the
+    # line reports it, with the per-row path beside it
+    from flashdec_amd import cascade
+
+    groups = [cascade.build_cascade_groups(p[3], p[4], bs, hq, hkv) for p in pools]
+    assert all(g.num_groups == 1 and g.max_prefix_len == prefix_blocks * bs for g in groups)
+
+    def fn_cascade(i):
+        q, k, v, table, sl, o = pools[i % len(pools)]
+        cascade.paged_decode_attention_cascade_into(q, k, v, table, sl, o, groups[i % len(pools)], sm_scale=sm_scale)
+
+    ms_c = graph_ms_per_call(torch, dev, fn_cascade, args.steps)
+    prepared_c = [cascade_prepared(torch, p, g, sm_scale, bs, hkv) for p, g in zip(pools, groups)]
+    attn_c, red_c = cascade_kernel_us(torch, prepared_c, min(4 * len(pools), 96))
+    log(f"[bench] {name} cascade: {ms_c * 1e3:.2f} us/call (graph); prefix + tail passes {attn_c:.2f} us, reducer "
+        f"{red_c:.2f} us; tail splits {prepared_c[0][0].num_splits}, prefix splits {prepared_c[0][1].prefix_splits}")
+    out["per_row_path"] = {"us_per_call": out["us_per_call"], "value": out["value"], "roofline": out["roofline"]}
+    out["value"] = round(unique / (ms_c * 1e-3) / 1e9, 2)
+    out["ms_per_step"] = round(ms_c, 6)
+    out["us_per_call"] = round(ms_c * 1e3, 3)
+    out["config"]["path"] = "cascade"
+    out["config"]["prefix_splits"] = prepared_c[0][1].prefix_splits
+    out["config"]["num_splits"] = prepared_c[0][0].num_splits
+    out["roofline"] = {"bound": "hbm", "achieved": round(unique / (attn_c * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(unique / (attn_c * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "traffic": None, "kernel_us_mean": round(attn_c, 3), "reducer_us_mean": round(red_c, 3),
                        "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}
     return out
 

@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 
 _i64 = ctypes.c_int64
@@ -75,6 +75,19 @@ class PagedDecodeArgs(ctypes.Structure):
     ]
 
 
+class CascadeArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("num_groups", _i32),
+        ("max_members", _i32),
+        ("prefix_splits", _i32),
+        ("group_members", _vp),
+        ("group_prefix_len", _vp),
+        ("row_prefix_len", _vp),
+        ("max_prefix_len", _i64),
+    ]
+
+
 class RopeAppendArgs(ctypes.Structure):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
@@ -102,6 +115,7 @@ class RopeAppendArgs(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "fd_paged_decode",
+    "fd_paged_decode_cascade",
     "fd_paged_decode_plan",
     "fd_fused_rope_kv_append",
     "fd_kv_append",
@@ -138,6 +152,8 @@ def load_library():
             raise RuntimeError(f"failed to load {path}: {exc}") from exc
         lib.fd_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), _vp]
         lib.fd_paged_decode.restype = ctypes.c_int
+        lib.fd_paged_decode_cascade.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(CascadeArgs), _vp]
+        lib.fd_paged_decode_cascade.restype = ctypes.c_int
         lib.fd_paged_decode_plan.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64]
         lib.fd_paged_decode_plan.restype = ctypes.c_int
         lib.fd_fused_rope_kv_append.argtypes = [ctypes.POINTER(RopeAppendArgs), _vp]
@@ -194,6 +210,13 @@ def paged_decode(args: PagedDecodeArgs, stream: int) -> None:
     lib = load_library()
     args.struct_size = ctypes.sizeof(PagedDecodeArgs)
     check(lib.fd_paged_decode(ctypes.byref(args), stream), "fd_paged_decode")
+
+
+def paged_decode_cascade(args: PagedDecodeArgs, cascade: CascadeArgs, stream: int) -> None:
+    lib = load_library()
+    args.struct_size = ctypes.sizeof(PagedDecodeArgs)
+    cascade.struct_size = ctypes.sizeof(CascadeArgs)
+    check(lib.fd_paged_decode_cascade(ctypes.byref(args), ctypes.byref(cascade), stream), "fd_paged_decode_cascade")
 
 
 def paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len, total_seq_len=0) -> int:

@@ -1,0 +1,245 @@
+"""Shared-prefix (cascade) paged decode on MI355X through ``libflashdec_hip.so``.
+
+Rows attached to one registered prefix of the paged cache
+(``PagedKVCache.attach_prefix``, flashdec/cache.py:225-248) lead their block
+tables with the same physical blocks.  The reference's decode kernels read
+that prefix once per row (flashdec/kernels/paged_decode.py:330-543); the
+cascade launch reads it once per group of sharers:
+
+1. a prefix pass attends each group's prefix for all its (member, head)
+   rows at once, writing ``prefix_splits`` partials per row;
+2. a tail pass attends every row's private tokens after its prefix (the
+   whole row for rows in no group);
+3. the split reducer merges both sets of partials (log-sum-exp).
+
+The result equals :func:`flashdec_amd.paged_decode_attention` on the same
+inputs (within floating-point reassociation).  Grouping is host logic over the
+block tables (:func:`build_cascade_groups`); the caller rebuilds the groups
+when tables change.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .paged_decode import _auto_workspace, _cache_strides, _fill_common, _fill_workspace, _validate_inputs
+
+MAX_ROWS_PER_GROUP = 256  # (member, query head) rows of one group per KV head
+
+
+@dataclass(frozen=True)
+class CascadeGroups:
+    """Prefix groups of a batch (host-built, device-resident index tensors).
+
+    ``members`` int32 ``[num_groups, max_members]`` (row indices, -1 after the
+    last member), ``prefix_len`` int32 ``[num_groups]`` (shared tokens, whole
+    blocks), ``row_prefix_len`` int32 ``[num_seqs]`` (0 for rows in no group).
+    ``max_prefix_len``, ``max_tail_len`` and ``total_tail_len`` are host
+    figures for split planning.
+    """
+
+    members: torch.Tensor
+    prefix_len: torch.Tensor
+    row_prefix_len: torch.Tensor
+    max_prefix_len: int
+    max_tail_len: int
+    total_tail_len: int
+
+    @property
+    def num_groups(self) -> int:
+        return int(self.members.shape[0])
+
+    @property
+    def max_members(self) -> int:
+        return int(self.members.shape[1])
+
+
+def group_rows(block_tables, seq_lens, block_size, max_members, min_prefix_blocks=1):
+    """Host grouping: lists of ``(rows, prefix_blocks)``.
+
+    Rows whose first physical block is the same are candidates; a candidate
+    set's prefix is the longest run of leading block ids common to all of
+    them, limited to each member's full blocks (a prefix never reaches past a
+    member's length).  Sets larger than ``max_members`` are cut into the
+    fewest chunks of near-equal size, in row order; sets of one row or with
+    fewer than ``min_prefix_blocks`` shared blocks are dropped (those rows
+    decode without a prefix pass).
+    """
+    bt = np.asarray(block_tables)
+    sl = np.asarray(seq_lens).astype(np.int64)
+    if bt.ndim != 2 or sl.ndim != 1 or sl.shape[0] != bt.shape[0]:
+        raise ValueError("block_tables must be [num_seqs, max_blocks_per_seq] and seq_lens [num_seqs]")
+    if max_members < 2:
+        return []
+    full = np.minimum(sl // block_size, bt.shape[1])
+    buckets = {}
+    for b in range(bt.shape[0]):
+        if full[b] >= max(min_prefix_blocks, 1) and bt[b, 0] >= 0:
+            buckets.setdefault(int(bt[b, 0]), []).append(b)
+    groups = []
+    for rows in buckets.values():
+        pieces = -(-len(rows) // max_members)
+        for part in np.array_split(np.asarray(rows), pieces):
+            chunk = [int(r) for r in part]
+            if len(chunk) < 2:
+                continue
+            limit = int(full[chunk].min())
+            same = (bt[chunk, :limit] == bt[chunk[0], :limit]).all(axis=0)
+            blocks = limit if same.all() else int(np.argmin(same))
+            if blocks >= max(min_prefix_blocks, 1):
+                groups.append((chunk, blocks))
+    return groups
+
+
+def build_cascade_groups(block_tables, seq_lens, block_size, num_q_heads, num_kv_heads, *, device=None,
+                         min_prefix_blocks=1):
+    """Find the batch's prefix groups and return them as :class:`CascadeGroups`.
+
+    ``block_tables``/``seq_lens`` may live on any device (they are read on
+    the host).  ``max_members`` is the most rows one group can hold:
+    ``256 // (num_q_heads // num_kv_heads)``.
+    """
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError("num_q_heads must be divisible by num_kv_heads")
+    group_size = num_q_heads // num_kv_heads
+    max_members = MAX_ROWS_PER_GROUP // group_size
+    if device is None:
+        device = block_tables.device if isinstance(block_tables, torch.Tensor) else "cpu"
+    bt = block_tables.cpu().numpy() if isinstance(block_tables, torch.Tensor) else np.asarray(block_tables)
+    sl = seq_lens.cpu().numpy() if isinstance(seq_lens, torch.Tensor) else np.asarray(seq_lens)
+    groups = group_rows(bt, sl, block_size, max_members, min_prefix_blocks)
+    width = max([len(rows) for rows, _ in groups], default=1)
+    members = np.full((len(groups), width), -1, dtype=np.int32)
+    prefix = np.zeros(len(groups), dtype=np.int32)
+    row_prefix = np.zeros(sl.shape[0], dtype=np.int32)
+    for g, (rows, blocks) in enumerate(groups):
+        members[g, : len(rows)] = rows
+        prefix[g] = blocks * block_size
+        row_prefix[rows] = blocks * block_size
+    tails = np.maximum(sl.astype(np.int64) - row_prefix, 0)
+    return CascadeGroups(
+        members=torch.from_numpy(members).to(device),
+        prefix_len=torch.from_numpy(prefix).to(device),
+        row_prefix_len=torch.from_numpy(row_prefix).to(device),
+        max_prefix_len=int(prefix.max(initial=0)),
+        max_tail_len=int(tails.max(initial=0)),
+        total_tail_len=int(tails.sum()),
+    )
+
+
+def plan_prefix_splits(num_groups, num_kv_heads, max_prefix_len, num_cus):
+    """Prefix partials per (group, KV head): enough workgroups to cover the
+    CUs, at most one per 32-token prefix tile."""
+    tiles = max(1, -(-max_prefix_len // 32))
+    want = max(1, -(-num_cus // max(1, num_groups * num_kv_heads)))
+    return int(min(want, tiles, 1024))
+
+
+_NUM_CUS = {}
+
+
+def _num_cus(device):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _NUM_CUS:
+        _NUM_CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _NUM_CUS[idx]
+
+
+def paged_decode_attention_cascade_into(
+    q,
+    k_cache,
+    v_cache,
+    block_tables,
+    seq_lens,
+    out,
+    groups: CascadeGroups,
+    sm_scale=None,
+    block_size=None,
+    num_splits=None,
+    prefix_splits=None,
+):
+    """Write shared-prefix decode attention into ``out``.
+
+    Token-major caches ``[num_blocks, num_kv_heads, block_size, 128]`` with
+    up to 16 query heads per KV head; same shapes and meaning as
+    :func:`flashdec_amd.paged_decode_attention_into`.  ``groups`` must have
+    been built for these ``block_tables``/``seq_lens`` (see
+    :func:`build_cascade_groups`).  ``num_splits`` (tail) and
+    ``prefix_splits`` default to the library's plan for the tail lengths and
+    to :func:`plan_prefix_splits`.
+    """
+    if block_size is None:
+        if k_cache.dim() != 4:
+            raise ValueError("k_cache must be a 4D tensor")
+        block_size = k_cache.shape[2]
+    block_size = int(block_size)
+    _validate_inputs(q, k_cache, v_cache, block_tables, seq_lens, block_size, 2, None, "token_major")
+    if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError("out must match q in shape, dtype and device")
+    num_seqs, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[1]
+    for name, t in (("members", groups.members), ("prefix_len", groups.prefix_len),
+                    ("row_prefix_len", groups.row_prefix_len)):
+        if t.dtype != torch.int32 or t.device != q.device or not t.is_contiguous():
+            raise ValueError(f"groups.{name} must be a contiguous int32 tensor on q.device")
+    if groups.row_prefix_len.shape != (num_seqs,):
+        raise ValueError("groups.row_prefix_len must have one entry per sequence")
+    if groups.prefix_len.shape != (groups.num_groups,):
+        raise ValueError("groups.prefix_len must have one entry per group")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if num_splits is None:
+        num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                            max(groups.max_tail_len, 1), max(groups.total_tail_len, 1))
+    if prefix_splits is None:
+        prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads, groups.max_prefix_len, _num_cus(q.device))
+    for name, v in (("num_splits", num_splits), ("prefix_splits", prefix_splits)):
+        if isinstance(v, bool) or not isinstance(v, int) or v <= 0:
+            raise ValueError(f"{name} must be a positive integer")
+    stream = _lib.current_stream_handle(q.device)
+    acc, mx, sm, _ = _auto_workspace(q, num_kv_heads, num_splits + prefix_splits, stream)
+
+    args = _lib.PagedDecodeArgs()
+    _fill_common(args, q, k_cache, v_cache, _cache_strides(k_cache, 2, 3), _cache_strides(v_cache, 2, 3),
+                 block_tables, seq_lens, out, num_kv_heads, block_size, sm_scale)
+    args.num_blocks = k_cache.shape[0]
+    args.max_seq_len = groups.max_prefix_len + groups.max_tail_len
+    _fill_workspace(args, acc, mx, sm, num_splits)
+    # the cascade always writes partials, also with a single tail split
+    args.split_acc = acc.data_ptr()
+    args.split_acc_stride[:] = acc.stride()
+    args.split_max = mx.data_ptr()
+    args.split_sum = sm.data_ptr()
+    args.split_stats_stride[:] = mx.stride()
+    cas = _lib.CascadeArgs()
+    cas.num_groups = groups.num_groups
+    cas.max_members = groups.max_members
+    cas.prefix_splits = prefix_splits
+    cas.group_members = groups.members.data_ptr()
+    cas.group_prefix_len = groups.prefix_len.data_ptr()
+    cas.row_prefix_len = groups.row_prefix_len.data_ptr()
+    cas.max_prefix_len = groups.max_prefix_len
+    _lib.paged_decode_cascade(args, cas, stream)
+    return out
+
+
+def paged_decode_attention_cascade(q, k_cache, v_cache, block_tables, seq_lens, groups=None, sm_scale=None,
+                                   block_size=None, num_splits=None, prefix_splits=None):
+    """Allocating form of :func:`paged_decode_attention_cascade_into`; builds
+    the groups from the tables when ``groups`` is None."""
+    if block_size is None:
+        if k_cache.dim() != 4:
+            raise ValueError("k_cache must be a 4D tensor")
+        block_size = k_cache.shape[2]
+    if groups is None:
+        groups = build_cascade_groups(block_tables, seq_lens, int(block_size), q.shape[1], k_cache.shape[1],
+                                      device=q.device)
+    out = torch.empty_like(q)
+    return paged_decode_attention_cascade_into(q, k_cache, v_cache, block_tables, seq_lens, out, groups,
+                                               sm_scale=sm_scale, block_size=block_size, num_splits=num_splits,
+                                               prefix_splits=prefix_splits)

@@ -56,6 +56,10 @@ struct DecodeParams {
   int splits;
   int hint_tiles;    // ceil(bound / 32): bound = max_seq_len or the table capacity
   int hint_tps;      // tiles per split
+  // cascade tail pass: row b attends tokens [tb[b], seq_len); its partials
+  // take workspace splits [0, splits), the prefix pass's come after them
+  const int32_t* tb;
+  int hint_tb;       // guess of tb / 32 for the first unit's early loads
   float scale_log2;  // sm_scale * log2(e): scores live in the base-2 domain
 };
 
@@ -81,10 +85,12 @@ __device__ __forceinline__ int64_t effective_len(const DecodeParams& p, int64_t 
 // 408-411).  The host bound (hint_tiles / hint_tps) never decides the range:
 // the MFMA kernel uses it only to guess where its first tile is, so that
 // tile's loads can be issued before seq_lens arrives.
-__device__ __forceinline__ void split_range(const DecodeParams& p, int split, int64_t eff, int& t0, int& t1) {
+__device__ __forceinline__ void split_range(const DecodeParams& p, int split, int64_t eff, int& t0, int& t1,
+                                            int first_tile = 0) {
   const int total = static_cast<int>((eff + 31) / 32);
-  const int tps = (total + p.splits - 1) / p.splits;
-  t0 = split * tps;
+  const int span = max(total - first_tile, 0);
+  const int tps = (span + p.splits - 1) / p.splits;
+  t0 = first_tile + split * tps;
   t1 = min(t0 + tps, total);
 }
 
@@ -256,18 +262,32 @@ struct WaveState {
   float l;       // partial denominator of this lane's tokens
 };
 
+// 2^x on the hardware's v_exp_f32: results below 2^-126 flush to zero, which
+// only drops probabilities that small relative to the running maximum.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // One unit: mask (row length, invalid blocks), splice in the appended token,
-// QK^T, online softmax, PV.  `last` is the last attended token, `app` the
-// token taken from the append registers (-1: none).
+// QK^T, online softmax, PV.  `last` is the last attended token, `first` the
+// first (0: from the row's start), `app` the token taken from the append
+// registers (-1: none).  The probabilities enter the PV product rounded to
+// the cache dtype, as the reference's grouped kernels do
+// (flashdec/kernels/paged_decode.py:308-310); the denominator sums them in
+// fp32.  Masking is skipped for units whose tokens are all live and the
+// rescale of the accumulator when no lane's maximum moved (wave-uniform
+// tests).
 template <typename T, bool FUSE, int UNIT>
 __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf)[4], float scale_log2,
-                                             int64_t tok0, int64_t last, int64_t app, const AppendRegs& ar, int c,
-                                             int g, WaveState& st) {
+                                             int64_t tok0, int64_t first, int64_t last, int64_t app,
+                                             const AppendRegs& ar, int c, int g, WaveState& st) {
   constexpr int MT = UnitRegs<UNIT>::MT;
   constexpr int VR = UnitRegs<UNIT>::VR;
+  constexpr uint32_t kAll = (1u << VR) - 1u;
   uint32_t vmask = t.bmask;
 #pragma unroll
-  for (int i = 0; i < VR; ++i) vmask &= (tok0 + vrow(g, i) <= last) ? ~0u : ~(1u << i);
+  for (int i = 0; i < VR; ++i) {
+    const int64_t tok = tok0 + vrow(g, i);
+    vmask &= (tok <= last && (first == 0 || tok >= first)) ? ~0u : ~(1u << i);
+  }
   if constexpr (FUSE) {
     const int64_t at = app - tok0;  // in [0, UNIT) only for the unit holding it
 #pragma unroll
@@ -293,79 +313,63 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[4 * mt + r] = sb[r] * scale_log2;
   }
-  float mx = -INFINITY;
+  // masked tokens: -inf scores and zero V rows (their memory may hold
+  // NaN/Inf, and 0 * NaN is NaN)
+  if (__ballot(vmask != kAll)) {
 #pragma unroll
-  for (int i = 0; i < VR; ++i) {
-    sc[i] = (vmask >> i) & 1u ? sc[i] : -INFINITY;
-    mx = fmaxf(mx, sc[i]);
+    for (int i = 0; i < VR; ++i) {
+      const bool keep = (vmask >> i) & 1u;
+      sc[i] = keep ? sc[i] : -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) t.vf[i][k] = keep ? t.vf[i][k] : 0u;
+    }
   }
+  float mx = sc[0];
+#pragma unroll
+  for (int i = 1; i < VR; ++i) mx = fmaxf(mx, sc[i]);
   mx = fmaxf(mx, shfl_xor_f32(mx, 16));
   mx = fmaxf(mx, shfl_xor_f32(mx, 32));
   const float m_new = fmaxf(st.m, mx);
   const float m_use = m_new == -INFINITY ? 0.f : m_new;
-  const float alpha = exp2f(st.m - m_use);
+  const float alpha = exp2_fast(st.m - m_use);
   float pr[VR];
   float psum = 0.f;
 #pragma unroll
   for (int i = 0; i < VR; ++i) {
-    pr[i] = exp2f(sc[i] - m_use);
+    pr[i] = exp2_fast(sc[i] - m_use);
     psum += pr[i];
   }
   st.l = st.l * alpha + psum;
   st.m = m_new;
-  // P^T operand (k = VR*g + i: this lane's tokens), split into a 16-bit head
-  // and a 16-bit tail so the PV product keeps ~16 mantissa bits of the fp32
-  // probabilities.
-  uint32_t ph[VR / 2], pl[VR / 2];
-  {
-    float lo[VR];
+  if (__ballot(alpha != 1.f)) {
 #pragma unroll
-    for (int i = 0; i < VR; ++i) {
-      const uint32_t hb = pack2<T>(pr[i], 0.f) & 0xffffu;
-      lo[i] = pr[i] - lo_f32<T>(hb);
-    }
-#pragma unroll
-    for (int j = 0; j < VR / 2; ++j) {
-      ph[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
-      pl[j] = pack2<T>(lo[2 * j], lo[2 * j + 1]);
-    }
+    for (int n = 0; n < 8; ++n) st.acc[n] *= alpha;
   }
-  // V^T operands: vt_n holds dim 8*c + n of the lane's tokens.  Rows of masked
-  // tokens are zeroed first (their memory may hold NaN/Inf).
-  u32x4 vz[VR];
+  // P^T operand (k = VR*g + i: this lane's tokens)
+  uint32_t ph[VR / 2];
 #pragma unroll
-  for (int i = 0; i < VR; ++i) {
-    const bool keep = (vmask >> i) & 1u;
-    vz[i][0] = keep ? t.vf[i][0] : 0u;
-    vz[i][1] = keep ? t.vf[i][1] : 0u;
-    vz[i][2] = keep ? t.vf[i][2] : 0u;
-    vz[i][3] = keep ? t.vf[i][3] : 0u;
-  }
+  for (int j = 0; j < VR / 2; ++j) ph[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
+  // V^T operands: vt_n holds dim 8*c + n of the lane's tokens
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     const int w = n >> 1;
     const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
-    f32x4 a = st.acc[n] * alpha;
     if constexpr (UNIT == 32) {
-      u32x4 vt, p_hi, p_lo;
+      u32x4 vt, pp;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        vt[j] = __builtin_amdgcn_perm(vz[2 * j + 1][w], vz[2 * j][w], sel);
-        p_hi[j] = ph[j];
-        p_lo[j] = pl[j];
+        vt[j] = __builtin_amdgcn_perm(t.vf[2 * j + 1][w], t.vf[2 * j][w], sel);
+        pp[j] = ph[j];
       }
-      a = mfma16x16x32<T>(vt, p_hi, a);
-      st.acc[n] = mfma16x16x32<T>(vt, p_lo, a);
+      st.acc[n] = mfma16x16x32<T>(vt, pp, st.acc[n]);
     } else {
-      u32x2 vt, p_hi, p_lo;
+      u32x2 vt, pp;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        vt[j] = __builtin_amdgcn_perm(vz[2 * j + 1][w], vz[2 * j][w], sel);
-        p_hi[j] = ph[j];
-        p_lo[j] = pl[j];
+        vt[j] = __builtin_amdgcn_perm(t.vf[2 * j + 1][w], t.vf[2 * j][w], sel);
+        pp[j] = ph[j];
       }
-      a = mfma16x16x16<T>(vt, p_hi, a);
-      st.acc[n] = mfma16x16x16<T>(vt, p_lo, a);
+      st.acc[n] = mfma16x16x16<T>(vt, pp, st.acc[n]);
     }
   }
 }
@@ -396,8 +400,9 @@ __device__ __forceinline__ void store_row(const DecodeParams& p, int b, int qh, 
   }
 }
 
-template <typename T, int BS, bool FUSE, bool MERGE, int UNIT>
+template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, bool CASCADE = false>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
+  static_assert(!(CASCADE && (FUSE || MERGE)), "the cascade tail pass has no fused append or in-launch merge");
   constexpr int kWaves = waves_for<UNIT>();
   constexpr int kUnitsPerTile = 32 / UNIT;
   __shared__ float s_acc[kWaves][16][kAccPitch];
@@ -420,7 +425,7 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   // operand, the append row and the row length / slot are all in flight
   // together -- no load address depends on seq_lens.  The guess is checked
   // below.
-  const int guess_begin = split * p.hint_tps;  // in 32-token tiles
+  const int guess_begin = (CASCADE ? p.hint_tb : 0) + split * p.hint_tps;  // in 32-token tiles
   int unit = kUnitsPerTile * guess_begin + wave;
   UnitPages pages = fetch_pages<BS, UNIT>(p, b, unit);  // clamped, always in bounds
   u32x4 qf[4];
@@ -443,6 +448,7 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   }
   const int32_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
   const int32_t slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
+  const int32_t first = CASCADE ? max(p.tb[b], 0) : 0;
   UnitRegs<UNIT> cur;
   load_unit<T, BS, UNIT>(p, kvh, unit, pages, c, g, cur);
 
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   // the loads above are the right ones; otherwise the first unit is fetched
   // again.
   int t_begin, t_end;
-  split_range(p, split, eff_len, t_begin, t_end);
+  split_range(p, split, eff_len, t_begin, t_end, CASCADE ? first / 32 : 0);
   const int live_units = static_cast<int>((eff_len + UNIT - 1) / UNIT);
   const int u_end = min(kUnitsPerTile * t_end, live_units);
   if (t_begin != guess_begin) {
@@ -488,8 +494,8 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
       }
       if constexpr (FUSE)
         if (app >= 0 && app / UNIT == unit) store_append<T, BS>(p, kvh, slot, c, g, ar);
-      process_unit<T, FUSE, UNIT>(cur, qf, p.scale_log2, static_cast<int64_t>(unit) * UNIT, last, app, ar, c, g,
-                                  st);
+      process_unit<T, FUSE, UNIT>(cur, qf, p.scale_log2, static_cast<int64_t>(unit) * UNIT, first, last, app, ar,
+                                  c, g, st);
       if (!more) break;
       cur = nxt;
       unit = next;
@@ -540,7 +546,7 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
       o[4 + j] += wt * a1[j];
     }
   }
-  if (p.splits == 1) {
+  if (!CASCADE && p.splits == 1) {
     if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
     return;
   }
@@ -638,6 +644,237 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
     GM = nm;
   }
   if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
+}
+
+// =============================================== cascade prefix pass ====
+// One workgroup per (group, KV head, prefix split).  A group's member rows
+// share their first prefix_len tokens (whole blocks: the same physical ids
+// lead every member's table row).  The split's 32-token prefix tiles stream
+// through a ring of LDS stages by LDS-DMA loads (global_load_lds_dwordx4:
+// no register staging, so several tiles are in flight), and every wave
+// attends to each tile for its own query rows -- one or two 16-row chunks
+// of the group's (member, head) rows -- so the prefix K/V leaves HBM once per
+// group instead of once per member.  Each (member, head) gets one partial per
+// prefix split, at workspace split split_base + split (the tail pass owns the
+// splits below); the reducer merges both.
+//
+// Latency: the member list, the lead row and the prefix length are loaded
+// together; then the split's block ids (into LDS) and the query rows; then
+// the tile loads -- three dependent round trips before the first tile.
+struct CascadeParams {
+  const int32_t* members;     // [groups, max_members]; members first, then entries outside [0, num_seqs)
+  const int32_t* prefix_len;  // [groups], tokens
+  int max_members;
+  int prefix_splits;  // a group's prefix tiles are spread evenly over them
+  int split_base;     // first workspace split of the prefix partials
+};
+
+constexpr int kPrefixWaves = 8;
+constexpr int kPrefixChunks = 2;     // rows 16 * (wave + 8 * chunk) + c: up to 256 rows
+constexpr int kPrefixStages = 4;     // LDS ring: tiles in flight
+constexpr int kPrefixIdTiles = 64;   // tiles whose block ids one LDS batch holds
+constexpr int kTokenBytes = 256;     // one token's 128 dims of 16-bit K (or V)
+
+// s_barrier without the release fence of __syncthreads(), which would also
+// wait for every LDS-DMA load still in flight (vmcnt 0).  This wave's LDS
+// writes are complete (lgkmcnt 0) and the compiler moves no memory access
+// across it; LDS-DMA completion is waited for explicitly (vmcnt).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+#define FD_LDS_PTR(ptr) ((__attribute__((address_space(3))) void*)(ptr))
+
+template <typename T, int BS>
+__global__ __launch_bounds__(64 * kPrefixWaves, 1) void cascade_prefix_kernel(DecodeParams p, CascadeParams cp) {
+  // stage s: K tile then V tile, 32 tokens x 256 B each.  Token tt's 16-byte
+  // chunk k sits at slot k ^ (tt & 15) of its row, so the MFMA operand reads
+  // (16 rows at one chunk, or one row's 16 chunks) hit 16 distinct bank groups.
+  __shared__ __align__(16) uint8_t s_kv[kPrefixStages][2][32 * kTokenBytes];
+  __shared__ uint8_t s_ok[kPrefixStages][32];  // token's block id is in range
+  __shared__ int32_t s_ids[kPrefixIdTiles * 32 / BS];
+  __shared__ int s_first_bad[kPrefixWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int split = blockIdx.x % cp.prefix_splits;
+  const int gk = blockIdx.x / cp.prefix_splits;
+  const int grp = gk / p.hkv;
+  const int kvh = gk % p.hkv;
+  const int G = p.group;
+  const int32_t* mem = cp.members + static_cast<int64_t>(grp) * cp.max_members;
+
+  // round 1: this thread's member entry, the member of each of its query
+  // rows, the lead row and the prefix length -- no load depends on another
+  const int32_t my_mem = tid < cp.max_members ? mem[tid] : -1;
+  int32_t row_mem[kPrefixChunks];
+#pragma unroll
+  for (int ch = 0; ch < kPrefixChunks; ++ch)
+    row_mem[ch] = mem[min((16 * (wave + kPrefixWaves * ch) + c) / G, cp.max_members - 1)];
+  const int32_t lead0 = mem[0];
+  const int32_t plen0 = cp.prefix_len[grp];
+  // members are listed first: the count stops at the first entry that is not
+  // a row index
+  const bool bad = !(tid < cp.max_members && my_mem >= 0 && my_mem < p.num_seqs);
+  const uint64_t bad_lanes = __ballot(bad);
+  if (lane == 0) s_first_bad[wave] = bad_lanes ? 64 * wave + __builtin_ctzll(bad_lanes) : 64 * (wave + 1);
+  lds_barrier();
+  int n_members = cp.max_members;
+#pragma unroll
+  for (int w = 0; w < kPrefixWaves; ++w) n_members = min(n_members, s_first_bad[w]);
+  const int lead = n_members > 0 ? lead0 : 0;
+  const int64_t cap = p.max_blocks_per_seq * p.block_size;
+  int64_t plen = n_members > 0 ? plen0 : 0;
+  plen = plen < 0 ? 0 : (plen < cap ? plen : cap);
+  const int ptiles = static_cast<int>((plen + 31) / 32);
+  const int tps = (ptiles + cp.prefix_splits - 1) / cp.prefix_splits;
+  const int t0 = split * tps;
+  const int nt = max(0, min(tps, ptiles - t0));
+  const int n_rows = n_members * G;
+
+  // round 2: block ids of the first batch of tiles, the query rows
+  auto load_ids = [&](int jb, int nb) {
+    const int npg = nb * (32 / BS);  // <= 256 pages: one per thread
+    if (tid < npg) {
+      int64_t pg = static_cast<int64_t>(t0 + jb) * (32 / BS) + tid;
+      pg = pg < p.max_blocks_per_seq ? pg : p.max_blocks_per_seq - 1;
+      s_ids[tid] = load_index(p.bt, lead * p.bts0 + pg * p.bts1, p.bt_i64);
+    }
+  };
+  if (nt > 0) load_ids(0, min(kPrefixIdTiles, nt));
+  u32x4 qf[kPrefixChunks][4];
+  int row_b[kPrefixChunks], row_h[kPrefixChunks];
+#pragma unroll
+  for (int ch = 0; ch < kPrefixChunks; ++ch) {
+    const int r = 16 * (wave + kPrefixWaves * ch) + c;
+    const bool rv = r < n_rows;
+    row_b[ch] = rv ? row_mem[ch] : -1;
+    row_h[ch] = rv ? r % G : 0;
+    const T* qrow = static_cast<const T*>(p.q) + (rv ? row_b[ch] : 0) * p.qs0 + (kvh * G + row_h[ch]) * p.qs1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * g);
+      qf[ch][s] = rv ? x : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // round 3: tiles.  Wave w loads tokens 4w .. 4w + 3 of a tile (K and V,
+  // 1 KB each); lane l takes token 4w + l / 16, slot l % 16.
+  const int my_tok = 4 * wave + (lane >> 4);
+  const int my_chunk = (lane & 15) ^ (my_tok & 15);
+  auto issue = [&](int j, int jb) {
+    const int s = j % kPrefixStages;
+    const int32_t blk = s_ids[(j - jb) * (32 / BS) + my_tok / BS];
+    const bool ok = blk >= 0 && blk < p.num_blocks;
+    const int64_t row = ok ? blk : 0;  // invalid blocks read block 0 (in bounds), masked below
+    const int64_t tok = static_cast<int64_t>(t0 + j) * 32 + my_tok;
+    const T* kp = static_cast<const T*>(p.k) + row * p.ks0 + kvh * p.ks1 + (tok % BS) * p.ks2 + my_chunk * 8;
+    const T* vp = static_cast<const T*>(p.v) + row * p.vs0 + kvh * p.vs1 + (tok % BS) * p.vs2 + my_chunk * 8;
+    // (the builtin's source is a non-const void pointer; given another
+    // pointer type the host pass drops the kernel's launch stub silently)
+    __builtin_amdgcn_global_load_lds(static_cast<void*>(const_cast<T*>(kp)),
+                                     FD_LDS_PTR(&s_kv[s][0][wave * 4 * kTokenBytes]), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(static_cast<void*>(const_cast<T*>(vp)),
+                                     FD_LDS_PTR(&s_kv[s][1][wave * 4 * kTokenBytes]), 16, 0, 0);
+    if ((lane & 15) == 0) s_ok[s][my_tok] = ok ? 1 : 0;
+  };
+
+  WaveState st[kPrefixChunks];
+#pragma unroll
+  for (int ch = 0; ch < kPrefixChunks; ++ch) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st[ch].acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[ch].m = -INFINITY;
+    st[ch].l = 0.f;
+  }
+  const AppendRegs ar{};
+  lds_barrier();  // block ids visible
+  for (int jb = 0; jb < nt; jb += kPrefixIdTiles) {
+    const int nb = min(kPrefixIdTiles, nt - jb);
+    if (jb > 0) {
+      lds_barrier();  // every issue of the previous batch has read its id
+      load_ids(jb, nb);
+      lds_barrier();
+    }
+#pragma unroll
+    for (int s = 0; s < kPrefixStages - 1; ++s)
+      if (s < nb) issue(jb + s, jb);
+    for (int j = 0; j < nb; ++j) {
+      // this wave's two loads of tile j are done when at most the loads of
+      // the tiles issued after it are outstanding
+      const int pending = min(kPrefixStages - 2, nb - 1 - j);
+      if (pending >= 2)
+        __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+      else if (pending == 1)
+        __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+      else
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+      // every wave's part of tile j has landed, and every wave is done with
+      // the stage the next issue overwrites (tile j - 1's)
+      lds_barrier();
+      if (j + kPrefixStages - 1 < nb) issue(jb + j + kPrefixStages - 1, jb);
+      if (16 * wave < n_rows) {  // wave-uniform: the wave holds a row
+        const int s = (jb + j) % kPrefixStages;
+        const uint8_t* kb = s_kv[s][0];
+        const uint8_t* vb = s_kv[s][1];
+        UnitRegs<32> t;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            t.kf[mt][q4] = *reinterpret_cast<const u32x4*>(kb + (16 * mt + c) * kTokenBytes + (((4 * q4 + g) ^ c) << 4));
+        uint32_t bm = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int tt = vrow(g, i);
+          t.vf[i] = *reinterpret_cast<const u32x4*>(vb + tt * kTokenBytes + ((c ^ (tt & 15)) << 4));
+          bm |= static_cast<uint32_t>(s_ok[s][tt]) << i;
+        }
+        // K rows of invalid blocks came from block 0: their scores are
+        // masked through the V-row bits of the same tokens
+        t.bmask = bm;
+#pragma unroll
+        for (int ch = 0; ch < kPrefixChunks; ++ch)
+          if (16 * (wave + kPrefixWaves * ch) < n_rows)
+            process_unit<T, false, 32>(t, qf[ch], p.scale_log2, static_cast<int64_t>(t0 + jb + j) * 32, 0, plen - 1,
+                                       -1, ar, c, g, st[ch]);
+      }
+    }
+  }
+
+  // one partial per (member, head) of this split -- empty ones included
+#pragma unroll
+  for (int ch = 0; ch < kPrefixChunks; ++ch) {
+    float lt = st[ch].l;
+    lt += shfl_xor_f32(lt, 16);
+    lt += shfl_xor_f32(lt, 32);
+    if (row_b[ch] < 0) continue;
+    const int qh = kvh * G + row_h[ch];
+    const int ws = cp.split_base + split;
+    float* a = p.acc + row_b[ch] * p.as0 + qh * p.as1 + ws * p.as2;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int d = 32 * g + 8 * rr;
+      const f32x4 lo = f32x4{st[ch].acc[0][rr], st[ch].acc[1][rr], st[ch].acc[2][rr], st[ch].acc[3][rr]};
+      const f32x4 hi = f32x4{st[ch].acc[4][rr], st[ch].acc[5][rr], st[ch].acc[6][rr], st[ch].acc[7][rr]};
+      if (p.as3 == 1) {
+        *reinterpret_cast<f32x4*>(a + d) = lo;
+        *reinterpret_cast<f32x4*>(a + d + 4) = hi;
+      } else {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          a[(d + n) * p.as3] = lo[n];
+          a[(d + 4 + n) * p.as3] = hi[n];
+        }
+      }
+    }
+    if (g == 0) {
+      const int64_t so = row_b[ch] * p.ss0 + qh * p.ss1 + ws * p.ss2;
+      p.mx[so] = st[ch].m;
+      p.sm[so] = lt;
+    }
+  }
 }
 
 // ====================================================== generic path ====
@@ -805,13 +1042,17 @@ struct ReduceParams {
   int64_t os0, os1, os2;
   int64_t sls, slots;
   int hq, splits, fuse, sl_i64, slot_i64;
+  // cascade: rows with tb[b] == 0 have no prefix partials and merge only the
+  // first tail_splits splits
+  const int32_t* tb;
+  int tail_splits;
 };
 
 __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane_idx));
 }
 
-template <typename T, int D>
+template <typename T, int D, bool CASCADE = false>
 __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
   // every argument in SGPRs before any use: one batch of argument loads, one
   // wait (left alone the compiler fetched the strides lazily, a second
@@ -828,6 +1069,9 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
   asm volatile("" : "+v"(vzero));
   const int32_t seq_len = load_index(p.sl, b * p.sls + vzero, p.sl_i64);
   const int32_t slot = load_index(p.slot, b * p.slots + vzero, p.slot_i64);  // seq_lens when not fused
+  int splits = p.splits;
+  if constexpr (CASCADE)
+    splits = __builtin_amdgcn_readfirstlane(p.tb[b + vzero]) > 0 ? p.splits : p.tail_splits;
   const int64_t sb = b * p.ss0 + qh * p.ss1;
   const float* ab = p.acc + b * p.as0 + qh * p.as1;
   float M = -INFINITY;
@@ -835,8 +1079,8 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
   float o[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) o[e] = 0.f;
-  for (int s64 = 0; s64 < p.splits; s64 += 64) {
-    const int n = min(64, p.splits - s64);  // splits of this pass, one per lane
+  for (int s64 = 0; s64 < splits; s64 += 64) {
+    const int n = min(64, splits - s64);  // splits of this pass, one per lane
     const int sj = s64 + min(lane, n - 1);
     const float lm = p.mx[sb + sj * p.ss2];
     const float ll = p.sm[sb + sj * p.ss2];
@@ -919,10 +1163,10 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
   return true;
 }
 
-// One dispatch; with both events given it is bracketed by them (profiling hook).
+// One dispatch; events given are recorded at its start / end (profiling hook).
 template <typename F, typename... Args>
 void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, void* stop, Args... args) {
-  if (start && stop)
+  if (start || stop)
     hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, static_cast<hipEvent_t>(start),
                           static_cast<hipEvent_t>(stop), 0, args...);
   else
@@ -961,6 +1205,50 @@ void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream, void* con
   launch_mfma_unit<T, BS, 16>(p, grid, stream, ev);
 }
 
+ReduceParams reduce_params(const DecodeParams& p) {
+  ReduceParams r{};
+  r.acc = p.acc;
+  r.mx = p.mx;
+  r.sm = p.sm;
+  r.out = p.out;
+  r.sl = p.sl;
+  r.slot = p.fuse ? p.slot : p.sl;
+  r.as0 = p.as0;
+  r.as1 = p.as1;
+  r.as2 = p.as2;
+  r.as3 = p.as3;
+  r.ss0 = p.ss0;
+  r.ss1 = p.ss1;
+  r.ss2 = p.ss2;
+  r.os0 = p.os0;
+  r.os1 = p.os1;
+  r.os2 = p.os2;
+  r.sls = p.sls;
+  r.slots = p.fuse ? p.slots : p.sls;
+  r.hq = p.hq;
+  r.splits = p.splits;
+  r.fuse = p.fuse;
+  r.sl_i64 = p.sl_i64;
+  r.slot_i64 = p.fuse ? p.slot_i64 : p.sl_i64;
+  r.tb = nullptr;
+  r.tail_splits = p.splits;
+  return r;
+}
+
+template <typename T, bool CASCADE>
+int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
+  if (a.head_dim == 64)
+  dispatch(split_reduce_kernel<T, 64, CASCADE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
+  else
+  dispatch(split_reduce_kernel<T, 128, CASCADE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3],
+           r);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
+  return FD_OK;
+}
+
+
 template <typename T>
 int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
@@ -989,39 +1277,56 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
   if (p.splits > 1 && p.counters == nullptr) {
-    ReduceParams r;
-    r.acc = p.acc;
-    r.mx = p.mx;
-    r.sm = p.sm;
-    r.out = p.out;
-    r.sl = p.sl;
-    r.slot = p.fuse ? p.slot : p.sl;
-    r.as0 = p.as0;
-    r.as1 = p.as1;
-    r.as2 = p.as2;
-    r.as3 = p.as3;
-    r.ss0 = p.ss0;
-    r.ss1 = p.ss1;
-    r.ss2 = p.ss2;
-    r.os0 = p.os0;
-    r.os1 = p.os1;
-    r.os2 = p.os2;
-    r.sls = p.sls;
-    r.slots = p.fuse ? p.slots : p.sls;
-    r.hq = p.hq;
-    r.splits = p.splits;
-    r.fuse = p.fuse;
-    r.sl_i64 = p.sl_i64;
-    r.slot_i64 = p.fuse ? p.slot_i64 : p.sl_i64;
-    const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
-    if (a.head_dim == 64)
-      dispatch(split_reduce_kernel<T, 64>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
-    else
-      dispatch(split_reduce_kernel<T, 128>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
-    e = hipGetLastError();
-    if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
+    const ReduceParams r = reduce_params(p);
+    const int rc = launch_reduce<T, false>(a, r, stream);
+    if (rc != FD_OK) return rc;
   }
   return FD_OK;
+}
+
+
+// Cascade: the prefix pass (one workgroup per group, KV head and prefix
+// split), then the tail pass over each row's private tokens, then the
+// reducer over tail + prefix partials.  The attention timing events bracket
+// the two attention launches.
+template <typename T, int BS>
+void launch_cascade_passes(const DecodeParams& p, const CascadeParams& cp, int64_t num_groups, int64_t pairs,
+                           hipStream_t stream, void* const* ev) {
+  const int64_t prefix_wgs = num_groups * p.hkv * cp.prefix_splits;
+  const dim3 tgrid(static_cast<unsigned>(pairs * p.splits));
+  void* tail_start = ev[0];
+  if (prefix_wgs > 0) {
+    dispatch(cascade_prefix_kernel<T, BS>, dim3(static_cast<unsigned>(prefix_wgs)), dim3(64 * kPrefixWaves), stream,
+             ev[0], nullptr, p, cp);
+    tail_start = nullptr;
+  }
+  if constexpr (BS >= 16) {
+    if (p.hint_tps <= kWideUnitMaxTiles) {
+      dispatch(decode_mfma_kernel<T, BS, false, false, 32, true>, tgrid, dim3(64 * waves_for<32>()), stream,
+               tail_start, ev[1], p);
+      return;
+    }
+  }
+  dispatch(decode_mfma_kernel<T, BS, false, false, 16, true>, tgrid, dim3(64 * waves_for<16>()), stream, tail_start,
+           ev[1], p);
+}
+
+template <typename T>
+int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const CascadeParams& cp, int64_t num_groups,
+                   hipStream_t stream) {
+  const int64_t pairs = a.num_seqs * a.num_kv_heads;
+  switch (a.block_size) {
+    case 8: launch_cascade_passes<T, 8>(p, cp, num_groups, pairs, stream, a.timing_events); break;
+    case 16: launch_cascade_passes<T, 16>(p, cp, num_groups, pairs, stream, a.timing_events); break;
+    default: launch_cascade_passes<T, 32>(p, cp, num_groups, pairs, stream, a.timing_events); break;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FD_E_LAUNCH, "cascade decode launch failed: %s", hipGetErrorString(e));
+  ReduceParams r = reduce_params(p);
+  r.splits = p.splits + cp.prefix_splits;
+  r.tb = p.tb;
+  r.tail_splits = p.splits;
+  return launch_reduce<T, true>(a, r, stream);
 }
 
 }  // namespace
@@ -1071,37 +1376,39 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
   return static_cast<int>(s);
 }
 
-extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream_) {
-  if (args == nullptr) return set_error(FD_E_INVALID, "fd_paged_decode: args is NULL");
+// Validates the launch arguments shared by the decode entry points and fills
+// the kernel parameters; fn names the entry point in error messages.
+static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, DecodeParams& p) {
+  if (args == nullptr) return set_error(FD_E_INVALID, "%s: args is NULL", fn);
   const fd_paged_decode_args& a = *args;
   if (a.struct_size != sizeof(fd_paged_decode_args))
-    return set_error(FD_E_INVALID, "fd_paged_decode: struct_size %u != %zu (ABI mismatch)", a.struct_size,
+    return set_error(FD_E_INVALID, "%s: struct_size %u != %zu (ABI mismatch)", fn, a.struct_size,
                      sizeof(fd_paged_decode_args));
   if (a.dtype != FD_DTYPE_F16 && a.dtype != FD_DTYPE_BF16)
-    return set_error(FD_E_UNSUPPORTED, "fd_paged_decode: dtype must be float16 or bfloat16");
+    return set_error(FD_E_UNSUPPORTED, "%s: dtype must be float16 or bfloat16", fn);
   if (a.num_seqs <= 0 || a.num_q_heads <= 0 || a.num_kv_heads <= 0 || a.num_blocks <= 0 ||
       a.max_blocks_per_seq <= 0)
-    return set_error(FD_E_INVALID, "fd_paged_decode: shapes must be positive");
+    return set_error(FD_E_INVALID, "%s: shapes must be positive", fn);
   if (a.num_q_heads % a.num_kv_heads != 0)
-    return set_error(FD_E_INVALID, "fd_paged_decode: num_q_heads must be divisible by num_kv_heads");
+    return set_error(FD_E_INVALID, "%s: num_q_heads must be divisible by num_kv_heads", fn);
   if (a.head_dim != 64 && a.head_dim != 128)
-    return set_error(FD_E_UNSUPPORTED, "fd_paged_decode: head_dim must be 64 or 128");
+    return set_error(FD_E_UNSUPPORTED, "%s: head_dim must be 64 or 128", fn);
   if (a.block_size != 8 && a.block_size != 16 && a.block_size != 32)
-    return set_error(FD_E_UNSUPPORTED, "fd_paged_decode: block_size must be 8, 16 or 32");
+    return set_error(FD_E_UNSUPPORTED, "%s: block_size must be 8, 16 or 32", fn);
   if (!a.q || !a.k_cache || !a.v_cache || !a.block_tables || !a.seq_lens || !a.out)
-    return set_error(FD_E_INVALID, "fd_paged_decode: NULL tensor pointer");
+    return set_error(FD_E_INVALID, "%s: NULL tensor pointer", fn);
   if (a.num_splits < 1 || a.num_splits > 4096)
-    return set_error(FD_E_INVALID, "fd_paged_decode: num_splits must be in [1, 4096]");
+    return set_error(FD_E_INVALID, "%s: num_splits must be in [1, 4096]", fn);
   if (a.num_splits > 1 && (!a.split_acc || !a.split_max || !a.split_sum))
-    return set_error(FD_E_INVALID, "fd_paged_decode: split workspace required for num_splits > 1");
+    return set_error(FD_E_INVALID, "%s: split workspace required for num_splits > 1", fn);
   const bool fuse = a.append_k != nullptr;
   if (fuse != (a.append_v != nullptr) || fuse != (a.slot_mapping != nullptr))
-    return set_error(FD_E_INVALID, "fd_paged_decode: append_k, append_v and slot_mapping go together");
+    return set_error(FD_E_INVALID, "%s: append_k, append_v and slot_mapping go together", fn);
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
   if (pairs * a.num_splits > 0x7fffffffLL || a.num_seqs * a.num_q_heads > 0x7fffffffLL)
-    return set_error(FD_E_INVALID, "fd_paged_decode: launch grid too large");
+    return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
 
-  DecodeParams p{};
+  p = DecodeParams{};
   p.q = a.q;
   p.qs0 = a.q_stride[0];
   p.qs1 = a.q_stride[1];
@@ -1161,7 +1468,7 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
   p.num_blocks = a.num_blocks;
   p.max_blocks_per_seq = a.max_blocks_per_seq;
   p.splits = a.num_splits;
-  if (a.max_seq_len < 0) return set_error(FD_E_INVALID, "fd_paged_decode: max_seq_len must be >= 0");
+  if (a.max_seq_len < 0) return set_error(FD_E_INVALID, "%s: max_seq_len must be >= 0", fn);
   {
     // first-tile guess of the MFMA kernel: from max_seq_len when given, else
     // from the table width; each row's split range uses its own length
@@ -1171,8 +1478,69 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
     p.hint_tps = (p.hint_tiles + p.splits - 1) / p.splits;
   }
   p.scale_log2 = a.sm_scale * kLog2e;
+  return FD_OK;
+}
+
+extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream_) {
+  DecodeParams p;
+  const int rc = fill_decode_params(args, "fd_paged_decode", p);
+  if (rc != FD_OK) return rc;
+  const fd_paged_decode_args& a = *args;
 
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   if (a.dtype == FD_DTYPE_BF16) return launch_decode<__bf16>(a, p, stream);
   return launch_decode<_Float16>(a, p, stream);
+}
+
+extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const fd_cascade_args* cascade,
+                                       fd_stream_t stream_) {
+  static const char* fn = "fd_paged_decode_cascade";
+  DecodeParams p;
+  const int rc = fill_decode_params(args, fn, p);
+  if (rc != FD_OK) return rc;
+  const fd_paged_decode_args& a = *args;
+  if (cascade == nullptr) return set_error(FD_E_INVALID, "%s: cascade is NULL", fn);
+  const fd_cascade_args& c = *cascade;
+  if (c.struct_size != sizeof(fd_cascade_args))
+    return set_error(FD_E_INVALID, "%s: cascade struct_size %u != %zu (ABI mismatch)", fn, c.struct_size,
+                     sizeof(fd_cascade_args));
+  if (p.fuse) return set_error(FD_E_UNSUPPORTED, "%s: fused append is not supported (append first)", fn);
+  if (!fast_path_ok(a, p.group))
+    return set_error(FD_E_UNSUPPORTED,
+                     "%s: needs head_dim 128, <= 16 query heads per KV head, unit dim stride and 16-byte rows", fn);
+  if (c.num_groups < 0 || c.max_members < 1 || c.prefix_splits < 1)
+    return set_error(FD_E_INVALID, "%s: num_groups must be >= 0, max_members and prefix_splits >= 1", fn);
+  if (static_cast<int64_t>(c.max_members) * p.group > kPrefixWaves * kPrefixChunks * 16)
+    return set_error(FD_E_UNSUPPORTED, "%s: max_members * (num_q_heads / num_kv_heads) must be <= %d", fn,
+                     kPrefixWaves * kPrefixChunks * 16);
+  if (a.num_splits + static_cast<int64_t>(c.prefix_splits) > 4096)
+    return set_error(FD_E_INVALID, "%s: num_splits + prefix_splits must be <= 4096", fn);
+  if (!a.split_acc || !a.split_max || !a.split_sum)
+    return set_error(FD_E_INVALID, "%s: split workspace required", fn);
+  if (!c.row_prefix_len || (c.num_groups > 0 && (!c.group_members || !c.group_prefix_len)))
+    return set_error(FD_E_INVALID, "%s: NULL group pointer", fn);
+  if (c.max_prefix_len < 0) return set_error(FD_E_INVALID, "%s: max_prefix_len must be >= 0", fn);
+  if (static_cast<int64_t>(c.num_groups) * a.num_kv_heads * c.prefix_splits > 0x7fffffffLL)
+    return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
+
+  p.counters = nullptr;
+  p.tb = c.row_prefix_len;
+  {
+    // tail-pass guess of each split's first tile, for a row of the longest
+    // prefix and the bound length
+    const int64_t cap = a.max_blocks_per_seq * a.block_size;
+    const int64_t pre = c.max_prefix_len < cap ? c.max_prefix_len : cap;
+    p.hint_tb = static_cast<int>(pre / 32);
+    const int span = max(p.hint_tiles - p.hint_tb, 0);
+    p.hint_tps = (span + p.splits - 1) / p.splits;
+  }
+  CascadeParams cp{};
+  cp.members = c.group_members;
+  cp.prefix_len = c.group_prefix_len;
+  cp.max_members = c.max_members;
+  cp.prefix_splits = c.num_groups > 0 ? c.prefix_splits : 0;
+  cp.split_base = p.splits;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (a.dtype == FD_DTYPE_BF16) return launch_cascade<__bf16>(a, p, cp, c.num_groups, stream);
+  return launch_cascade<_Float16>(a, p, cp, c.num_groups, stream);
 }

@@ -21,6 +21,8 @@
  *                            (bound from _cuda_kv_append.py:116-137)
  *   fd_paged_decode_plan     flashdec/vllm_backend.py:168-188 chooses split
  *                            counts for its launcher; this is the MI355X policy
+ *   fd_paged_decode_cascade  no counterpart (shared-prefix decode over the
+ *                            prefixes of flashdec/cache.py:192-276)
  */
 #ifndef FLASHDEC_HIP_H_
 #define FLASHDEC_HIP_H_
@@ -31,7 +33,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 2
+#define FD_ABI_VERSION 3
 
 /* status codes */
 #define FD_OK 0
@@ -148,6 +150,46 @@ typedef struct fd_paged_decode_args {
 } fd_paged_decode_args;
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
+
+/*
+ * Shared-prefix (cascade) decode: the result of fd_paged_decode, with the
+ * K/V of a prefix shared by a group of rows read once per group.  No
+ * counterpart in the reference, which reads every row's prefix separately
+ * (flashdec/kernels/paged_decode.py:330-543); groups are the rows attached to
+ * one registered prefix of PagedKVCache (flashdec/cache.py:192-276).
+ *
+ * Group g lists up to max_members row indices in group_members[g, :] (row
+ * stride max_members, members first, -1 after the last) that share their
+ * first group_prefix_len[g] tokens: whole blocks, the same physical block
+ * ids leading each member's block-table row, and no more tokens than any
+ * member's seq_lens.  row_prefix_len[b] is that length for each member row
+ * and 0 for rows in no group; a row belongs to at most one group.  A first
+ * pass attends every group's prefix for all its members and writes
+ * prefix_splits partials per (row, head) at workspace splits
+ * [num_splits, num_splits + prefix_splits); a tail pass attends tokens
+ * [row_prefix_len[b], seq_lens[b]) of each row at splits [0, num_splits);
+ * the reducer merges them (tail splits only for rows with no prefix).
+ *
+ * Needs the MFMA path (head_dim 128, <= 16 query heads per KV head, unit
+ * dim stride, 16-byte aligned rows), a split workspace of num_splits +
+ * prefix_splits splits, no fused append (append first), and
+ * max_members * (num_q_heads / num_kv_heads) <= 256.  max_prefix_len is a
+ * hint (the longest group prefix) for where each tail split starts.  The
+ * timing events [0]/[1] bracket the prefix and tail passes together.
+ */
+typedef struct fd_cascade_args {
+  uint32_t struct_size; /* sizeof(fd_cascade_args): ABI guard */
+  int32_t num_groups;
+  int32_t max_members;
+  int32_t prefix_splits;
+  const int32_t* group_members;    /* [num_groups, max_members] */
+  const int32_t* group_prefix_len; /* [num_groups], tokens */
+  const int32_t* row_prefix_len;   /* [num_seqs], tokens */
+  int64_t max_prefix_len;
+} fd_cascade_args;
+
+int fd_paged_decode_cascade(const fd_paged_decode_args* args, const fd_cascade_args* cascade,
+                            fd_stream_t stream);
 
 /*
  * Split count the library would pick for a launch of this shape on the
