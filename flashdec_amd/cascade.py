@@ -4,12 +4,14 @@ Rows attached to one registered prefix of the paged cache
 (``PagedKVCache.attach_prefix``, flashdec/cache.py:225-248) lead their block
 tables with the same physical blocks.  The reference's decode kernels read
 that prefix once per row (flashdec/kernels/paged_decode.py:330-543); the
-cascade launch reads it once per group of sharers:
+cascade launch reads it once per 16 (member, query head) rows of a group
+and fills all 16 columns of the MFMA tiles with them (one request of a
+GQA group of 8 fills only half):
 
-1. a prefix pass attends each group's prefix for all its (member, head)
-   rows at once, writing ``prefix_splits`` partials per row;
-2. a tail pass attends every row's private tokens after its prefix (the
-   whole row for rows in no group);
+1. prefix-role workgroups attend a group's prefix for 16 of its rows each,
+   writing ``prefix_splits`` partials per row;
+2. tail-role workgroups, in the same launch, attend every row's private
+   tokens after its prefix (the whole row for rows in no group);
 3. the split reducer merges both sets of partials (log-sum-exp).
 
 The result equals :func:`flashdec_amd.paged_decode_attention` on the same
@@ -29,16 +31,15 @@ import torch
 from . import _lib
 from .paged_decode import _auto_workspace, _cache_strides, _fill_common, _fill_workspace, _validate_inputs
 
-MAX_ROWS_PER_GROUP = 256  # (member, query head) rows of one group per KV head
-
-
 @dataclass(frozen=True)
 class CascadeGroups:
     """Prefix groups of a batch (host-built, device-resident index tensors).
 
     ``members`` int32 ``[num_groups, max_members]`` (row indices, -1 after the
-    last member), ``prefix_len`` int32 ``[num_groups]`` (shared tokens, whole
-    blocks), ``row_prefix_len`` int32 ``[num_seqs]`` (0 for rows in no group).
+    last member; entry 0 is the lead, whose block-table row supplies the
+    prefix's block ids), ``prefix_len`` int32 ``[num_groups]`` (shared tokens,
+    whole blocks), ``row_prefix_len`` int32 ``[num_seqs]`` (0 for rows in no
+    group).
     ``max_prefix_len``, ``max_tail_len`` and ``total_tail_len`` are host
     figures for split planning.
     """
@@ -97,22 +98,20 @@ def group_rows(block_tables, seq_lens, block_size, max_members, min_prefix_block
 
 
 def build_cascade_groups(block_tables, seq_lens, block_size, num_q_heads, num_kv_heads, *, device=None,
-                         min_prefix_blocks=1):
+                         min_prefix_blocks=1, max_members=None):
     """Find the batch's prefix groups and return them as :class:`CascadeGroups`.
 
     ``block_tables``/``seq_lens`` may live on any device (they are read on
-    the host).  ``max_members`` is the most rows one group can hold:
-    ``256 // (num_q_heads // num_kv_heads)``.
+    the host).  ``max_members`` bounds the rows of one group (default: no
+    bound); larger sets of sharers are cut into near-equal groups.
     """
     if num_q_heads % num_kv_heads != 0:
         raise ValueError("num_q_heads must be divisible by num_kv_heads")
-    group_size = num_q_heads // num_kv_heads
-    max_members = MAX_ROWS_PER_GROUP // group_size
     if device is None:
         device = block_tables.device if isinstance(block_tables, torch.Tensor) else "cpu"
     bt = block_tables.cpu().numpy() if isinstance(block_tables, torch.Tensor) else np.asarray(block_tables)
     sl = seq_lens.cpu().numpy() if isinstance(seq_lens, torch.Tensor) else np.asarray(seq_lens)
-    groups = group_rows(bt, sl, block_size, max_members, min_prefix_blocks)
+    groups = group_rows(bt, sl, block_size, max_members or max(2, bt.shape[0]), min_prefix_blocks)
     width = max([len(rows) for rows, _ in groups], default=1)
     members = np.full((len(groups), width), -1, dtype=np.int32)
     prefix = np.zeros(len(groups), dtype=np.int32)
@@ -132,12 +131,17 @@ def build_cascade_groups(block_tables, seq_lens, block_size, num_q_heads, num_kv
     )
 
 
-def plan_prefix_splits(num_groups, num_kv_heads, max_prefix_len, num_cus):
-    """Prefix partials per (group, KV head): enough workgroups to cover the
-    CUs, at most one per 32-token prefix tile."""
+def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus):
+    """Prefix partials per (group, KV head, 16-row chunk): about one
+    prefix-role workgroup per CU, at most one split per 32-token prefix tile."""
     tiles = max(1, -(-max_prefix_len // 32))
-    want = max(1, -(-num_cus // max(1, num_groups * num_kv_heads)))
+    want = max(1, -(-num_cus // max(1, num_groups * num_kv_heads * chunks)))
     return int(min(want, tiles, 1024))
+
+
+def prefix_chunks(groups, num_q_heads, num_kv_heads):
+    """16-row chunks per group and KV head (rows = members x query heads per KV head)."""
+    return -(-groups.max_members * (num_q_heads // num_kv_heads) // 16)
 
 
 _NUM_CUS = {}
@@ -197,7 +201,9 @@ def paged_decode_attention_cascade_into(
         num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim,
                                             max(groups.max_tail_len, 1), max(groups.total_tail_len, 1))
     if prefix_splits is None:
-        prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads, groups.max_prefix_len, _num_cus(q.device))
+        prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads,
+                                           prefix_chunks(groups, num_q_heads, num_kv_heads), groups.max_prefix_len,
+                                           _num_cus(q.device))
     for name, v in (("num_splits", num_splits), ("prefix_splits", prefix_splits)):
         if isinstance(v, bool) or not isinstance(v, int) or v <= 0:
             raise ValueError(f"{name} must be a positive integer")

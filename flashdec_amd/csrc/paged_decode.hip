@@ -85,13 +85,17 @@ __device__ __forceinline__ int64_t effective_len(const DecodeParams& p, int64_t 
 // 408-411).  The host bound (hint_tiles / hint_tps) never decides the range:
 // the MFMA kernel uses it only to guess where its first tile is, so that
 // tile's loads can be issued before seq_lens arrives.
-__device__ __forceinline__ void split_range(const DecodeParams& p, int split, int64_t eff, int& t0, int& t1,
-                                            int first_tile = 0) {
+// (first_tile > 0: the cascade tail pass, whose rows start after their prefix)
+__device__ __forceinline__ void split_tiles(int splits, int split, int64_t eff, int first_tile, int& t0, int& t1) {
   const int total = static_cast<int>((eff + 31) / 32);
   const int span = max(total - first_tile, 0);
-  const int tps = (span + p.splits - 1) / p.splits;
+  const int tps = (span + splits - 1) / splits;
   t0 = first_tile + split * tps;
   t1 = min(t0 + tps, total);
+}
+
+__device__ __forceinline__ void split_range(const DecodeParams& p, int split, int64_t eff, int& t0, int& t1) {
+  split_tiles(p.splits, split, eff, 0, t0, t1);
 }
 
 __device__ __forceinline__ RowInfo row_info(const DecodeParams& p, int b, int split) {
@@ -230,6 +234,67 @@ __device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int un
   t.bmask = bm;
 }
 
+// Byte offsets of a lane's K and V rows inside their block (head kvh, the
+// row's token slot, the lane's dims).  They are the same for every unit a
+// wave takes: units advance by kWaves * UNIT = 128 tokens, a multiple of the
+// block size, so (UNIT * unit) % BS depends only on the wave.  The host
+// checks that they fit in 32 bits.
+template <int UNIT>
+struct UnitOffsets {
+  uint32_t k[UnitRegs<UNIT>::MT];
+  uint32_t v[UnitRegs<UNIT>::VR];
+};
+
+template <typename T, int BS, int UNIT>
+__device__ __forceinline__ UnitOffsets<UNIT> unit_offsets(const DecodeParams& p, int kvh, int wave, int c, int g) {
+  UnitOffsets<UNIT> o;
+  const int u0 = UNIT * wave;
+#pragma unroll
+  for (int mt = 0; mt < UnitRegs<UNIT>::MT; ++mt) {
+    const int row = (u0 + 16 * mt + c) % BS;
+    o.k[mt] = static_cast<uint32_t>((kvh * p.ks1 + row * p.ks2 + 8 * g) * static_cast<int64_t>(sizeof(T)));
+  }
+#pragma unroll
+  for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
+    const int row = (u0 + vrow(g, i)) % BS;
+    o.v[i] = static_cast<uint32_t>((kvh * p.vs1 + row * p.vs2 + 8 * c) * static_cast<int64_t>(sizeof(T)));
+  }
+  return o;
+}
+
+// load_unit for block sizes of 16 and 32: each 16-token row group of a unit
+// lies in one block (a 32-token unit on 16-token blocks: rows < 16 in the
+// first, the rest in the second), so a row's address is a uniform block base
+// (scalar) plus the lane's fixed 32-bit offset -- no per-unit vector
+// address arithmetic.
+template <typename T, int BS, int UNIT>
+__device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const UnitPages& up,
+                                                const UnitOffsets<UNIT>& o, UnitRegs<UNIT>& t) {
+  static_assert(BS >= 16, "a 16-token row group must lie in one block");
+  constexpr bool kTwo = BS < UNIT;
+  const bool oka = up.a >= 0 && up.a < p.num_blocks;
+  const bool okb = kTwo ? (up.b >= 0 && up.b < p.num_blocks) : oka;
+  constexpr int64_t E = sizeof(T);
+  const char* ka = static_cast<const char*>(p.k) + (oka ? up.a : 0) * p.ks0 * E;
+  const char* va = static_cast<const char*>(p.v) + (oka ? up.a : 0) * p.vs0 * E;
+  const char* kb = kTwo ? static_cast<const char*>(p.k) + (okb ? up.b : 0) * p.ks0 * E : ka;
+  const char* vb = kTwo ? static_cast<const char*>(p.v) + (okb ? up.b : 0) * p.vs0 * E : va;
+#pragma unroll
+  for (int mt = 0; mt < UnitRegs<UNIT>::MT; ++mt) {
+    const char* base = (kTwo && mt == 1) ? kb : ka;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) t.kf[mt][s] = *reinterpret_cast<const u32x4*>(base + o.k[mt] + 64 * s);
+  }
+  uint32_t bm = 0;
+#pragma unroll
+  for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
+    const bool second = kTwo && i >= 4;  // V rows 16 + 4g + (i - 4)
+    t.vf[i] = *reinterpret_cast<const u32x4*>((second ? vb : va) + o.v[i]);
+    bm |= (second ? okb : oka) ? (1u << i) : 0u;
+  }
+  t.bmask = bm;
+}
+
 // The appended token's pieces in this lane's operand layout: akf[s] = dims
 // [32*s + 8*g, +8) of append_k, avf = dims [8*c, +8) of append_v.
 struct AppendRegs {
@@ -262,6 +327,38 @@ struct WaveState {
   float l;       // partial denominator of this lane's tokens
 };
 
+// Reductions over the four lanes c, c + 16, c + 32, c + 48 (one query
+// column), every lane receiving the result.  With both operands the same
+// value, v_permlane16_swap leaves rows 2k and 2k + 1 of each 32-lane half in
+// its two results (and v_permlane32_swap the two halves), so combining the
+// pair is the xor-16 (xor-32) butterfly step, with no LDS round trip.
+__device__ __forceinline__ float pair_rows16_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float pair_rows32_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float pair_rows16_sum(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float pair_rows32_sum(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float column_max(float x) { return pair_rows32_max(pair_rows16_max(x)); }
+__device__ __forceinline__ float column_sum(float x) { return pair_rows32_sum(pair_rows16_sum(x)); }
+
 // 2^x on the hardware's v_exp_f32: results below 2^-126 flush to zero, which
 // only drops probabilities that small relative to the running maximum.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -276,20 +373,20 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // rescale of the accumulator when no lane's maximum moved (wave-uniform
 // tests).
 template <typename T, bool FUSE, int UNIT>
-__device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf)[4], float scale_log2,
-                                             int64_t tok0, int64_t first, int64_t last, int64_t app,
-                                             const AppendRegs& ar, int c, int g, WaveState& st) {
+__device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf)[4], float scale_log2, int tok0,
+                                             int first, int last, int app, const AppendRegs& ar, int c, int g,
+                                             WaveState& st) {
   constexpr int MT = UnitRegs<UNIT>::MT;
   constexpr int VR = UnitRegs<UNIT>::VR;
   constexpr uint32_t kAll = (1u << VR) - 1u;
   uint32_t vmask = t.bmask;
 #pragma unroll
   for (int i = 0; i < VR; ++i) {
-    const int64_t tok = tok0 + vrow(g, i);
+    const int tok = tok0 + vrow(g, i);
     vmask &= (tok <= last && (first == 0 || tok >= first)) ? ~0u : ~(1u << i);
   }
   if constexpr (FUSE) {
-    const int64_t at = app - tok0;  // in [0, UNIT) only for the unit holding it
+    const int at = app - tok0;  // in [0, UNIT) only for the unit holding it
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const bool hit = at == 16 * mt + c;
@@ -327,8 +424,7 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf
   float mx = sc[0];
 #pragma unroll
   for (int i = 1; i < VR; ++i) mx = fmaxf(mx, sc[i]);
-  mx = fmaxf(mx, shfl_xor_f32(mx, 16));
-  mx = fmaxf(mx, shfl_xor_f32(mx, 32));
+  mx = column_max(mx);
   const float m_new = fmaxf(st.m, mx);
   const float m_use = m_new == -INFINITY ? 0.f : m_new;
   const float alpha = exp2_fast(st.m - m_use);
@@ -400,42 +496,97 @@ __device__ __forceinline__ void store_row(const DecodeParams& p, int b, int qh, 
   }
 }
 
-template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, bool CASCADE = false>
-__global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
-  static_assert(!(CASCADE && (FUSE || MERGE)), "the cascade tail pass has no fused append or in-launch merge");
+// Shared-prefix (cascade) launch: groups of rows share the first
+// prefix_len[g] tokens of their block tables (the same physical blocks).
+// The prefix role attends a group's prefix once per 16 of its (member,
+// head) rows -- MFMA column c is row 16 * chunk + c of the group: member
+// (16 * chunk + c) / group, head (16 * chunk + c) % group -- reading the
+// block ids from the lead member's table row, and writes its partials after
+// the tail splits.  The tail role attends each row's tokens from
+// row_prefix_len[b] on.
+struct CascadeParams {
+  const int32_t* members;     // [groups, max_members]; entry 0 is the lead
+  const int32_t* prefix_len;  // [groups], tokens
+  int max_members;
+  int chunks;         // 16-row chunks per group and KV head
+  int prefix_splits;  // a group's prefix tiles are spread evenly over them
+  int prefix_blocks;  // workgroups of the prefix role: groups * hkv * chunks * prefix_splits
+  int hint_ptps;      // guess of the prefix tiles per split (longest prefix)
+};
+
+enum class Role { kRow, kTail, kPrefix };
+
+// LDS of one decode workgroup: each wave's state for the merge, and the
+// output row of every MFMA column.
+template <int W>
+struct alignas(16) DecodeLds {
+  float acc[W][16][kAccPitch];  // 16-byte rows: merged with 128-bit LDS reads
+  float m[W][16];
+  float l[W][16];
+  int col_b[16];
+  int col_h[16];
+  int last;
+};
+
+template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, Role ROLE>
+__device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
+                                            DecodeLds<waves_for<UNIT>()>& lds) {
+  static_assert(ROLE == Role::kRow || !(FUSE || MERGE), "cascade roles have no fused append or in-launch merge");
   constexpr int kWaves = waves_for<UNIT>();
   constexpr int kUnitsPerTile = 32 / UNIT;
-  __shared__ float s_acc[kWaves][16][kAccPitch];
-  __shared__ float s_m[kWaves][16];
-  __shared__ float s_l[kWaves][16];
-  __shared__ int s_last;
+  constexpr bool PREFIX = ROLE == Role::kPrefix;
+  constexpr bool TAIL = ROLE == Role::kTail;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int split = blockIdx.x % p.splits;
-  const int pair = blockIdx.x / p.splits;
-  const int b = pair / p.hkv;
-  const int kvh = pair % p.hkv;
+  const int nsplit = PREFIX ? cp.prefix_splits : p.splits;
+  const int split = block % nsplit;
+  const int pair = block / nsplit;  // (request, KV head), or (group, KV head, chunk)
   const int G = p.group;
+  int b, kvh, chunk = 0;
+  const int32_t* mem = nullptr;
+  if constexpr (PREFIX) {
+    chunk = pair % cp.chunks;
+    const int gk = pair / cp.chunks;
+    kvh = gk % p.hkv;
+    mem = cp.members + static_cast<int64_t>(gk / p.hkv) * cp.max_members;
+    b = mem[0];  // the lead: its table row holds the prefix's block ids
+  } else {
+    b = pair / p.hkv;
+    kvh = pair % p.hkv;
+  }
+  const bool lead_ok = !PREFIX || (b >= 0 && b < p.num_seqs);
+  const int trow = lead_ok ? b : 0;  // table row read for K/V
+
+  // column c's output row: the request's head kvh * G + c (c < G), or in the
+  // prefix role the group row 16 * chunk + c (member index, head)
+  int col_b = b, col_h = c;
+  bool col_ok = c < G;
+  if constexpr (PREFIX) {
+    const int r = 16 * chunk + c;
+    const int mi = r / G;
+    const int32_t m = mi < cp.max_members ? mem[mi] : -1;
+    col_ok = lead_ok && m >= 0 && m < p.num_seqs;
+    col_b = col_ok ? m : 0;
+    col_h = r % G;
+  }
 
   // Independent loads first.  The first unit is guessed from the host bound
-  // (hint_tps tiles per split), so its block ids and K/V rows, the Q^T
-  // operand, the append row and the row length / slot are all in flight
-  // together -- no load address depends on seq_lens.  The guess is checked
-  // below.
-  const int guess_begin = (CASCADE ? p.hint_tb : 0) + split * p.hint_tps;  // in 32-token tiles
+  // (hint tiles per split), so its block ids and K/V rows, the Q^T operand,
+  // the append row and the row length / slot are all in flight together --
+  // no load address depends on seq_lens.  The guess is checked below.
+  const int guess_begin = PREFIX ? split * cp.hint_ptps : (TAIL ? p.hint_tb : 0) + split * p.hint_tps;  // tiles
   int unit = kUnitsPerTile * guess_begin + wave;
-  UnitPages pages = fetch_pages<BS, UNIT>(p, b, unit);  // clamped, always in bounds
+  UnitPages pages = fetch_pages<BS, UNIT>(p, trow, unit);  // clamped, always in bounds
   u32x4 qf[4];
   {
-    const bool hv = c < G;
-    const T* qrow = static_cast<const T*>(p.q) + b * p.qs0 + (kvh * G + (hv ? c : 0)) * p.qs1;
+    const T* qrow = static_cast<const T*>(p.q) + col_b * p.qs0 + (kvh * G + (col_ok ? col_h : 0)) * p.qs1;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * g);
-      qf[s] = hv ? x : u32x4{0u, 0u, 0u, 0u};
+      qf[s] = col_ok ? x : u32x4{0u, 0u, 0u, 0u};
     }
   }
   AppendRegs ar;
@@ -446,29 +597,51 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
     for (int s = 0; s < 4; ++s) ar.akf[s] = *reinterpret_cast<const u32x4*>(ak + 32 * s + 8 * g);
     ar.avf = *reinterpret_cast<const u32x4*>(av + 8 * c);
   }
-  const int32_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
-  const int32_t slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
-  const int32_t first = CASCADE ? max(p.tb[b], 0) : 0;
+  int64_t eff_len;
+  int32_t slot = -1;
+  if constexpr (PREFIX) {
+    const int64_t cap = p.max_blocks_per_seq * p.block_size;
+    const int64_t plen = lead_ok ? cp.prefix_len[pair / cp.chunks / p.hkv] : 0;
+    eff_len = plen < 0 ? 0 : (plen < cap ? plen : cap);
+  } else {
+    const int32_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
+    slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
+    eff_len = effective_len(p, seq_len, slot);
+  }
+  const int32_t first = TAIL ? max(p.tb[b], 0) : 0;
+  // Long splits (16-token units, several per wave) take the fixed lane
+  // offsets; short ones (32-token units, about one per wave) compute each
+  // address once, which keeps the kernel-argument loads ahead of the first
+  // K/V loads in fewer dependent batches (C2: 6.2 vs 7.1 us).
+  constexpr bool kFixed = BS >= 16 && UNIT == 16;
   UnitRegs<UNIT> cur;
-  load_unit<T, BS, UNIT>(p, kvh, unit, pages, c, g, cur);
+  [[maybe_unused]] UnitOffsets<UNIT> offs;
+  if constexpr (kFixed) offs = unit_offsets<T, BS, UNIT>(p, kvh, wave, c, g);
+  auto load = [&](int u, const UnitPages& up, UnitRegs<UNIT>& dst) {
+    if constexpr (kFixed)
+      load_unit_fixed<T, BS, UNIT>(p, up, offs, dst);
+    else
+      load_unit<T, BS, UNIT>(p, kvh, u, up, c, g, dst);
+  };
+  load(unit, pages, cur);
 
-  const int64_t eff_len = effective_len(p, seq_len, slot);
-  const int64_t last = eff_len - 1;
-  const int64_t app = (FUSE && eff_len > 0) ? last : -1;
+  // token indices fit in 32 bits: eff_len <= seq_lens[b], an int32
+  const int last = static_cast<int>(eff_len) - 1;
+  const int app = (FUSE && eff_len > 0) ? last : -1;
   // The split's tiles come from the row's own length; its units are the
   // UNIT-token pieces of those tiles that hold at least one live token.  When
   // the host bound predicted where they start (rows as long as the bound),
   // the loads above are the right ones; otherwise the first unit is fetched
   // again.
   int t_begin, t_end;
-  split_range(p, split, eff_len, t_begin, t_end, CASCADE ? first / 32 : 0);
+  split_tiles(nsplit, split, eff_len, TAIL ? first / 32 : 0, t_begin, t_end);
   const int live_units = static_cast<int>((eff_len + UNIT - 1) / UNIT);
   const int u_end = min(kUnitsPerTile * t_end, live_units);
   if (t_begin != guess_begin) {
     unit = kUnitsPerTile * t_begin + wave;
     if (unit < u_end) {
-      pages = fetch_pages<BS, UNIT>(p, b, unit);
-      load_unit<T, BS, UNIT>(p, kvh, unit, pages, c, g, cur);
+      pages = fetch_pages<BS, UNIT>(p, trow, unit);
+      load(unit, pages, cur);
     }
   }
 
@@ -480,80 +653,95 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
 
   if (unit < u_end) {
     UnitPages next_pages{0, 0};
-    if (unit + kWaves < u_end) next_pages = fetch_pages<BS, UNIT>(p, b, unit + kWaves);
-    for (;;) {
-      // issue the next unit's loads (and the block ids after it) before
-      // consuming the current unit
+    if (unit + kWaves < u_end) next_pages = fetch_pages<BS, UNIT>(p, trow, unit + kWaves);
+    // One unit: issue the next unit's loads into `ahead` (and the block ids
+    // after it), then consume `now`; false when `now` was the last.  The two
+    // buffers take turns, so no registers are copied between units.
+    auto step = [&](UnitRegs<UNIT>& now, UnitRegs<UNIT>& ahead) -> bool {
       const int next = unit + kWaves;
       const bool more = next < u_end;
-      UnitRegs<UNIT> nxt;
       UnitPages after{0, 0};
       if (more) {
-        load_unit<T, BS, UNIT>(p, kvh, next, next_pages, c, g, nxt);
-        if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, b, next + kWaves);
+        load(next, next_pages, ahead);
+        if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, trow, next + kWaves);
       }
       if constexpr (FUSE)
         if (app >= 0 && app / UNIT == unit) store_append<T, BS>(p, kvh, slot, c, g, ar);
-      process_unit<T, FUSE, UNIT>(cur, qf, p.scale_log2, static_cast<int64_t>(unit) * UNIT, first, last, app, ar,
-                                  c, g, st);
-      if (!more) break;
-      cur = nxt;
+      process_unit<T, FUSE, UNIT>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
       unit = next;
       next_pages = after;
+      return more;
+    };
+    UnitRegs<UNIT> alt;
+    if constexpr (UNIT == 16) {
+      while (step(cur, alt) && step(alt, cur)) {
+      }
+    } else {
+      // about one unit per wave: one copy of the step keeps the code small
+      while (step(cur, alt)) cur = alt;
     }
   }
-  // denominator over the four lanes (g) that share query head c
-  float lt = st.l;
-  lt += shfl_xor_f32(lt, 16);
-  lt += shfl_xor_f32(lt, 32);
+  // denominator over the four lanes (g) that share query column c
+  const float lt = column_sum(st.l);
 
   // Every wave publishes its state (one LDS slot each; eight slots take 68 KB,
   // which gfx950's LDS holds in one workgroup), then threads merge across the
   // slots.
   if (g == 0) {
-    s_m[wave][c] = st.m;
-    s_l[wave][c] = lt;
+    lds.m[wave][c] = st.m;
+    lds.l[wave][c] = lt;
+    if (PREFIX && wave == 0) {
+      lds.col_b[c] = col_ok ? col_b : -1;
+      lds.col_h[c] = col_h;
+    }
   }
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr) {
-    float* dst = &s_acc[wave][c][32 * g + 8 * rr];
+    float* dst = &lds.acc[wave][c][32 * g + 8 * rr];
     *reinterpret_cast<f32x4*>(dst) = f32x4{st.acc[0][rr], st.acc[1][rr], st.acc[2][rr], st.acc[3][rr]};
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
   }
   __syncthreads();
 
-  // merge the slots: thread -> (head h, dims [d0, d0 + 8)); threads past the
-  // first 256 only take part in the barrier of the in-launch merge
+  // merge the slots: thread -> (column h, dims [d0, d0 + 8)); threads past
+  // the first 256 only take part in the barrier of the in-launch merge
   const int h = (threadIdx.x >> 4) & 15;
   const int d0 = (threadIdx.x & 15) * 8;
-  const bool head_ok = threadIdx.x < 256 && h < G;
-  const int qh = kvh * G + h;
+  int ob = b, qh = kvh * G + h;
+  bool head_ok = threadIdx.x < 256 && h < G;
+  if constexpr (PREFIX) {
+    ob = lds.col_b[h];
+    qh = kvh * G + lds.col_h[h];
+    head_ok = threadIdx.x < 256 && ob >= 0;
+  }
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds.m[w][h]);
   const float Mu = M == -INFINITY ? 0.f : M;
   float L = 0.f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    const float wt = exp2f(s_m[w][h] - Mu);
-    L += wt * s_l[w][h];
-    const f32x4 a0 = *reinterpret_cast<const f32x4*>(&s_acc[w][h][d0]);
-    const f32x4 a1 = *reinterpret_cast<const f32x4*>(&s_acc[w][h][d0 + 4]);
+    const float wt = exp2f(lds.m[w][h] - Mu);
+    L += wt * lds.l[w][h];
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0]);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       o[j] += wt * a0[j];
       o[4 + j] += wt * a1[j];
     }
   }
-  if (!CASCADE && p.splits == 1) {
+  if (ROLE == Role::kRow && p.splits == 1) {
     if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
     return;
   }
-  // split partial: unnormalised acc, base-2 max, denominator
+  // split partial: unnormalised acc, base-2 max, denominator; the prefix
+  // role's partials follow the tail splits
   if (head_ok) {
-    float* a = p.acc + b * p.as0 + qh * p.as1 + split * p.as2 + d0 * p.as3;
-    const int64_t so = b * p.ss0 + qh * p.ss1 + split * p.ss2;
+    const int ws = PREFIX ? p.splits + split : split;
+    float* a = p.acc + ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3;
+    const int64_t so = ob * p.ss0 + qh * p.ss1 + ws * p.ss2;
     if constexpr (MERGE) {
       // device-coherent (sc1) stores, visible to every XCD once acknowledged;
       // the host guarantees unit dim stride and 8-byte alignment here
@@ -597,10 +785,10 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   if (threadIdx.x == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(p.counters + pair * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == static_cast<uint32_t>(p.splits - 1);
+    lds.last = prev == static_cast<uint32_t>(p.splits - 1);
   }
   __syncthreads();
-  if (!s_last) return;
+  if (!lds.last) return;
   if (threadIdx.x == 0)
     __hip_atomic_store(p.counters + pair * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (!head_ok) return;
@@ -646,235 +834,22 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
 }
 
-// =============================================== cascade prefix pass ====
-// One workgroup per (group, KV head, prefix split).  A group's member rows
-// share their first prefix_len tokens (whole blocks: the same physical ids
-// lead every member's table row).  The split's 32-token prefix tiles stream
-// through a ring of LDS stages by LDS-DMA loads (global_load_lds_dwordx4:
-// no register staging, so several tiles are in flight), and every wave
-// attends to each tile for its own query rows -- one or two 16-row chunks
-// of the group's (member, head) rows -- so the prefix K/V leaves HBM once per
-// group instead of once per member.  Each (member, head) gets one partial per
-// prefix split, at workspace split split_base + split (the tail pass owns the
-// splits below); the reducer merges both.
-//
-// Latency: the member list, the lead row and the prefix length are loaded
-// together; then the split's block ids (into LDS) and the query rows; then
-// the tile loads -- three dependent round trips before the first tile.
-struct CascadeParams {
-  const int32_t* members;     // [groups, max_members]; members first, then entries outside [0, num_seqs)
-  const int32_t* prefix_len;  // [groups], tokens
-  int max_members;
-  int prefix_splits;  // a group's prefix tiles are spread evenly over them
-  int split_base;     // first workspace split of the prefix partials
-};
+template <typename T, int BS, bool FUSE, bool MERGE, int UNIT>
+__global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
+  __shared__ DecodeLds<waves_for<UNIT>()> lds;
+  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow>(p, CascadeParams{}, blockIdx.x, lds);
+}
 
-constexpr int kPrefixWaves = 8;
-constexpr int kPrefixChunks = 2;     // rows 16 * (wave + 8 * chunk) + c: up to 256 rows
-constexpr int kPrefixStages = 4;     // LDS ring: tiles in flight
-constexpr int kPrefixIdTiles = 64;   // tiles whose block ids one LDS batch holds
-constexpr int kTokenBytes = 256;     // one token's 128 dims of 16-bit K (or V)
-
-// s_barrier without the release fence of __syncthreads(), which would also
-// wait for every LDS-DMA load still in flight (vmcnt 0).  This wave's LDS
-// writes are complete (lgkmcnt 0) and the compiler moves no memory access
-// across it; LDS-DMA completion is waited for explicitly (vmcnt).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-#define FD_LDS_PTR(ptr) ((__attribute__((address_space(3))) void*)(ptr))
-
-template <typename T, int BS>
-__global__ __launch_bounds__(64 * kPrefixWaves, 1) void cascade_prefix_kernel(DecodeParams p, CascadeParams cp) {
-  // stage s: K tile then V tile, 32 tokens x 256 B each.  Token tt's 16-byte
-  // chunk k sits at slot k ^ (tt & 15) of its row, so the MFMA operand reads
-  // (16 rows at one chunk, or one row's 16 chunks) hit 16 distinct bank groups.
-  __shared__ __align__(16) uint8_t s_kv[kPrefixStages][2][32 * kTokenBytes];
-  __shared__ uint8_t s_ok[kPrefixStages][32];  // token's block id is in range
-  __shared__ int32_t s_ids[kPrefixIdTiles * 32 / BS];
-  __shared__ int s_first_bad[kPrefixWaves];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & 15;
-  const int g = lane >> 4;
-  const int split = blockIdx.x % cp.prefix_splits;
-  const int gk = blockIdx.x / cp.prefix_splits;
-  const int grp = gk / p.hkv;
-  const int kvh = gk % p.hkv;
-  const int G = p.group;
-  const int32_t* mem = cp.members + static_cast<int64_t>(grp) * cp.max_members;
-
-  // round 1: this thread's member entry, the member of each of its query
-  // rows, the lead row and the prefix length -- no load depends on another
-  const int32_t my_mem = tid < cp.max_members ? mem[tid] : -1;
-  int32_t row_mem[kPrefixChunks];
-#pragma unroll
-  for (int ch = 0; ch < kPrefixChunks; ++ch)
-    row_mem[ch] = mem[min((16 * (wave + kPrefixWaves * ch) + c) / G, cp.max_members - 1)];
-  const int32_t lead0 = mem[0];
-  const int32_t plen0 = cp.prefix_len[grp];
-  // members are listed first: the count stops at the first entry that is not
-  // a row index
-  const bool bad = !(tid < cp.max_members && my_mem >= 0 && my_mem < p.num_seqs);
-  const uint64_t bad_lanes = __ballot(bad);
-  if (lane == 0) s_first_bad[wave] = bad_lanes ? 64 * wave + __builtin_ctzll(bad_lanes) : 64 * (wave + 1);
-  lds_barrier();
-  int n_members = cp.max_members;
-#pragma unroll
-  for (int w = 0; w < kPrefixWaves; ++w) n_members = min(n_members, s_first_bad[w]);
-  const int lead = n_members > 0 ? lead0 : 0;
-  const int64_t cap = p.max_blocks_per_seq * p.block_size;
-  int64_t plen = n_members > 0 ? plen0 : 0;
-  plen = plen < 0 ? 0 : (plen < cap ? plen : cap);
-  const int ptiles = static_cast<int>((plen + 31) / 32);
-  const int tps = (ptiles + cp.prefix_splits - 1) / cp.prefix_splits;
-  const int t0 = split * tps;
-  const int nt = max(0, min(tps, ptiles - t0));
-  const int n_rows = n_members * G;
-
-  // round 2: block ids of the first batch of tiles, the query rows
-  auto load_ids = [&](int jb, int nb) {
-    const int npg = nb * (32 / BS);  // <= 256 pages: one per thread
-    if (tid < npg) {
-      int64_t pg = static_cast<int64_t>(t0 + jb) * (32 / BS) + tid;
-      pg = pg < p.max_blocks_per_seq ? pg : p.max_blocks_per_seq - 1;
-      s_ids[tid] = load_index(p.bt, lead * p.bts0 + pg * p.bts1, p.bt_i64);
-    }
-  };
-  if (nt > 0) load_ids(0, min(kPrefixIdTiles, nt));
-  u32x4 qf[kPrefixChunks][4];
-  int row_b[kPrefixChunks], row_h[kPrefixChunks];
-#pragma unroll
-  for (int ch = 0; ch < kPrefixChunks; ++ch) {
-    const int r = 16 * (wave + kPrefixWaves * ch) + c;
-    const bool rv = r < n_rows;
-    row_b[ch] = rv ? row_mem[ch] : -1;
-    row_h[ch] = rv ? r % G : 0;
-    const T* qrow = static_cast<const T*>(p.q) + (rv ? row_b[ch] : 0) * p.qs0 + (kvh * G + row_h[ch]) * p.qs1;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * g);
-      qf[ch][s] = rv ? x : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-
-  // round 3: tiles.  Wave w loads tokens 4w .. 4w + 3 of a tile (K and V,
-  // 1 KB each); lane l takes token 4w + l / 16, slot l % 16.
-  const int my_tok = 4 * wave + (lane >> 4);
-  const int my_chunk = (lane & 15) ^ (my_tok & 15);
-  auto issue = [&](int j, int jb) {
-    const int s = j % kPrefixStages;
-    const int32_t blk = s_ids[(j - jb) * (32 / BS) + my_tok / BS];
-    const bool ok = blk >= 0 && blk < p.num_blocks;
-    const int64_t row = ok ? blk : 0;  // invalid blocks read block 0 (in bounds), masked below
-    const int64_t tok = static_cast<int64_t>(t0 + j) * 32 + my_tok;
-    const T* kp = static_cast<const T*>(p.k) + row * p.ks0 + kvh * p.ks1 + (tok % BS) * p.ks2 + my_chunk * 8;
-    const T* vp = static_cast<const T*>(p.v) + row * p.vs0 + kvh * p.vs1 + (tok % BS) * p.vs2 + my_chunk * 8;
-    // (the builtin's source is a non-const void pointer; given another
-    // pointer type the host pass drops the kernel's launch stub silently)
-    __builtin_amdgcn_global_load_lds(static_cast<void*>(const_cast<T*>(kp)),
-                                     FD_LDS_PTR(&s_kv[s][0][wave * 4 * kTokenBytes]), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(static_cast<void*>(const_cast<T*>(vp)),
-                                     FD_LDS_PTR(&s_kv[s][1][wave * 4 * kTokenBytes]), 16, 0, 0);
-    if ((lane & 15) == 0) s_ok[s][my_tok] = ok ? 1 : 0;
-  };
-
-  WaveState st[kPrefixChunks];
-#pragma unroll
-  for (int ch = 0; ch < kPrefixChunks; ++ch) {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) st[ch].acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    st[ch].m = -INFINITY;
-    st[ch].l = 0.f;
-  }
-  const AppendRegs ar{};
-  lds_barrier();  // block ids visible
-  for (int jb = 0; jb < nt; jb += kPrefixIdTiles) {
-    const int nb = min(kPrefixIdTiles, nt - jb);
-    if (jb > 0) {
-      lds_barrier();  // every issue of the previous batch has read its id
-      load_ids(jb, nb);
-      lds_barrier();
-    }
-#pragma unroll
-    for (int s = 0; s < kPrefixStages - 1; ++s)
-      if (s < nb) issue(jb + s, jb);
-    for (int j = 0; j < nb; ++j) {
-      // this wave's two loads of tile j are done when at most the loads of
-      // the tiles issued after it are outstanding
-      const int pending = min(kPrefixStages - 2, nb - 1 - j);
-      if (pending >= 2)
-        __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
-      else if (pending == 1)
-        __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
-      else
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-      // every wave's part of tile j has landed, and every wave is done with
-      // the stage the next issue overwrites (tile j - 1's)
-      lds_barrier();
-      if (j + kPrefixStages - 1 < nb) issue(jb + j + kPrefixStages - 1, jb);
-      if (16 * wave < n_rows) {  // wave-uniform: the wave holds a row
-        const int s = (jb + j) % kPrefixStages;
-        const uint8_t* kb = s_kv[s][0];
-        const uint8_t* vb = s_kv[s][1];
-        UnitRegs<32> t;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            t.kf[mt][q4] = *reinterpret_cast<const u32x4*>(kb + (16 * mt + c) * kTokenBytes + (((4 * q4 + g) ^ c) << 4));
-        uint32_t bm = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int tt = vrow(g, i);
-          t.vf[i] = *reinterpret_cast<const u32x4*>(vb + tt * kTokenBytes + ((c ^ (tt & 15)) << 4));
-          bm |= static_cast<uint32_t>(s_ok[s][tt]) << i;
-        }
-        // K rows of invalid blocks came from block 0: their scores are
-        // masked through the V-row bits of the same tokens
-        t.bmask = bm;
-#pragma unroll
-        for (int ch = 0; ch < kPrefixChunks; ++ch)
-          if (16 * (wave + kPrefixWaves * ch) < n_rows)
-            process_unit<T, false, 32>(t, qf[ch], p.scale_log2, static_cast<int64_t>(t0 + jb + j) * 32, 0, plen - 1,
-                                       -1, ar, c, g, st[ch]);
-      }
-    }
-  }
-
-  // one partial per (member, head) of this split -- empty ones included
-#pragma unroll
-  for (int ch = 0; ch < kPrefixChunks; ++ch) {
-    float lt = st[ch].l;
-    lt += shfl_xor_f32(lt, 16);
-    lt += shfl_xor_f32(lt, 32);
-    if (row_b[ch] < 0) continue;
-    const int qh = kvh * G + row_h[ch];
-    const int ws = cp.split_base + split;
-    float* a = p.acc + row_b[ch] * p.as0 + qh * p.as1 + ws * p.as2;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int d = 32 * g + 8 * rr;
-      const f32x4 lo = f32x4{st[ch].acc[0][rr], st[ch].acc[1][rr], st[ch].acc[2][rr], st[ch].acc[3][rr]};
-      const f32x4 hi = f32x4{st[ch].acc[4][rr], st[ch].acc[5][rr], st[ch].acc[6][rr], st[ch].acc[7][rr]};
-      if (p.as3 == 1) {
-        *reinterpret_cast<f32x4*>(a + d) = lo;
-        *reinterpret_cast<f32x4*>(a + d + 4) = hi;
-      } else {
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          a[(d + n) * p.as3] = lo[n];
-          a[(d + 4 + n) * p.as3] = hi[n];
-        }
-      }
-    }
-    if (g == 0) {
-      const int64_t so = row_b[ch] * p.ss0 + qh * p.ss1 + ws * p.ss2;
-      p.mx[so] = st[ch].m;
-      p.sm[so] = lt;
-    }
-  }
+// Cascade launch: workgroups [0, prefix_blocks) take the prefix role, the
+// rest the tail role (both write split partials; the reducer merges them).
+template <typename T, int BS, int UNIT>
+__global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void cascade_decode_kernel(DecodeParams p,
+                                                                                    CascadeParams cp) {
+  __shared__ DecodeLds<waves_for<UNIT>()> lds;
+  if (static_cast<int>(blockIdx.x) < cp.prefix_blocks)
+    decode_role<T, BS, false, false, UNIT, Role::kPrefix>(p, cp, blockIdx.x, lds);
+  else
+    decode_role<T, BS, false, false, UNIT, Role::kTail>(p, cp, blockIdx.x - cp.prefix_blocks, lds);
 }
 
 // ====================================================== generic path ====
@@ -1152,6 +1127,13 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
   for (int64_t s : strides)
     if (s % 8 != 0) return false;
   if (!aligned16(a.q) || !aligned16(a.k_cache) || !aligned16(a.v_cache)) return false;
+  // a row's byte offset inside its block (head, token slot, dims) is a
+  // 32-bit lane offset in the MFMA kernel's loads
+  for (const int64_t* st : {a.k_stride, a.v_stride}) {
+    if (st[0] < 0 || st[1] < 0 || st[2] < 0) return false;
+    const int64_t in_block = (a.num_kv_heads - 1) * st[1] + (a.block_size - 1) * st[2] + a.head_dim;
+    if (in_block * 2 > 0xffffffffLL) return false;
+  }
   if (a.append_k) {
     if (a.append_k_stride[2] != 1 || a.append_v_stride[2] != 1) return false;
     const int64_t as[] = {a.append_k_stride[0], a.append_k_stride[1], a.append_v_stride[0],
@@ -1285,40 +1267,29 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
 }
 
 
-// Cascade: the prefix pass (one workgroup per group, KV head and prefix
-// split), then the tail pass over each row's private tokens, then the
-// reducer over tail + prefix partials.  The attention timing events bracket
-// the two attention launches.
+// Cascade: one launch of prefix- and tail-role workgroups, then the reducer
+// over tail + prefix partials.  The attention timing events bracket it.
 template <typename T, int BS>
-void launch_cascade_passes(const DecodeParams& p, const CascadeParams& cp, int64_t num_groups, int64_t pairs,
-                           hipStream_t stream, void* const* ev) {
-  const int64_t prefix_wgs = num_groups * p.hkv * cp.prefix_splits;
-  const dim3 tgrid(static_cast<unsigned>(pairs * p.splits));
-  void* tail_start = ev[0];
-  if (prefix_wgs > 0) {
-    dispatch(cascade_prefix_kernel<T, BS>, dim3(static_cast<unsigned>(prefix_wgs)), dim3(64 * kPrefixWaves), stream,
-             ev[0], nullptr, p, cp);
-    tail_start = nullptr;
-  }
+void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, int64_t pairs, hipStream_t stream,
+                           void* const* ev) {
+  const dim3 grid(static_cast<unsigned>(cp.prefix_blocks + pairs * p.splits));
   if constexpr (BS >= 16) {
-    if (p.hint_tps <= kWideUnitMaxTiles) {
-      dispatch(decode_mfma_kernel<T, BS, false, false, 32, true>, tgrid, dim3(64 * waves_for<32>()), stream,
-               tail_start, ev[1], p);
+    if (p.hint_tps <= kWideUnitMaxTiles && cp.hint_ptps <= kWideUnitMaxTiles) {
+      dispatch(cascade_decode_kernel<T, BS, 32>, grid, dim3(64 * waves_for<32>()), stream, ev[0], ev[1], p, cp);
       return;
     }
   }
-  dispatch(decode_mfma_kernel<T, BS, false, false, 16, true>, tgrid, dim3(64 * waves_for<16>()), stream, tail_start,
-           ev[1], p);
+  dispatch(cascade_decode_kernel<T, BS, 16>, grid, dim3(64 * waves_for<16>()), stream, ev[0], ev[1], p, cp);
 }
 
 template <typename T>
-int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const CascadeParams& cp, int64_t num_groups,
+int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const CascadeParams& cp,
                    hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
   switch (a.block_size) {
-    case 8: launch_cascade_passes<T, 8>(p, cp, num_groups, pairs, stream, a.timing_events); break;
-    case 16: launch_cascade_passes<T, 16>(p, cp, num_groups, pairs, stream, a.timing_events); break;
-    default: launch_cascade_passes<T, 32>(p, cp, num_groups, pairs, stream, a.timing_events); break;
+    case 8: launch_cascade_kernel<T, 8>(p, cp, pairs, stream, a.timing_events); break;
+    case 16: launch_cascade_kernel<T, 16>(p, cp, pairs, stream, a.timing_events); break;
+    default: launch_cascade_kernel<T, 32>(p, cp, pairs, stream, a.timing_events); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "cascade decode launch failed: %s", hipGetErrorString(e));
@@ -1510,9 +1481,6 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
                      "%s: needs head_dim 128, <= 16 query heads per KV head, unit dim stride and 16-byte rows", fn);
   if (c.num_groups < 0 || c.max_members < 1 || c.prefix_splits < 1)
     return set_error(FD_E_INVALID, "%s: num_groups must be >= 0, max_members and prefix_splits >= 1", fn);
-  if (static_cast<int64_t>(c.max_members) * p.group > kPrefixWaves * kPrefixChunks * 16)
-    return set_error(FD_E_UNSUPPORTED, "%s: max_members * (num_q_heads / num_kv_heads) must be <= %d", fn,
-                     kPrefixWaves * kPrefixChunks * 16);
   if (a.num_splits + static_cast<int64_t>(c.prefix_splits) > 4096)
     return set_error(FD_E_INVALID, "%s: num_splits + prefix_splits must be <= 4096", fn);
   if (!a.split_acc || !a.split_max || !a.split_sum)
@@ -1520,16 +1488,18 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
   if (!c.row_prefix_len || (c.num_groups > 0 && (!c.group_members || !c.group_prefix_len)))
     return set_error(FD_E_INVALID, "%s: NULL group pointer", fn);
   if (c.max_prefix_len < 0) return set_error(FD_E_INVALID, "%s: max_prefix_len must be >= 0", fn);
-  if (static_cast<int64_t>(c.num_groups) * a.num_kv_heads * c.prefix_splits > 0x7fffffffLL)
+  const int64_t chunks = (static_cast<int64_t>(c.max_members) * p.group + 15) / 16;
+  const int64_t prefix_blocks = static_cast<int64_t>(c.num_groups) * a.num_kv_heads * chunks * c.prefix_splits;
+  if (prefix_blocks + a.num_seqs * a.num_kv_heads * a.num_splits > 0x7fffffffLL)
     return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
 
   p.counters = nullptr;
   p.tb = c.row_prefix_len;
+  const int64_t cap = a.max_blocks_per_seq * a.block_size;
+  const int64_t pre = c.max_prefix_len < cap ? c.max_prefix_len : cap;
   {
-    // tail-pass guess of each split's first tile, for a row of the longest
+    // tail-role guess of each split's first tile, for a row of the longest
     // prefix and the bound length
-    const int64_t cap = a.max_blocks_per_seq * a.block_size;
-    const int64_t pre = c.max_prefix_len < cap ? c.max_prefix_len : cap;
     p.hint_tb = static_cast<int>(pre / 32);
     const int span = max(p.hint_tiles - p.hint_tb, 0);
     p.hint_tps = (span + p.splits - 1) / p.splits;
@@ -1538,9 +1508,11 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
   cp.members = c.group_members;
   cp.prefix_len = c.group_prefix_len;
   cp.max_members = c.max_members;
-  cp.prefix_splits = c.num_groups > 0 ? c.prefix_splits : 0;
-  cp.split_base = p.splits;
+  cp.chunks = static_cast<int>(chunks);
+  cp.prefix_splits = c.prefix_splits;
+  cp.prefix_blocks = static_cast<int>(prefix_blocks);
+  cp.hint_ptps = static_cast<int>(((pre + 31) / 32 + c.prefix_splits - 1) / c.prefix_splits);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (a.dtype == FD_DTYPE_BF16) return launch_cascade<__bf16>(a, p, cp, c.num_groups, stream);
-  return launch_cascade<_Float16>(a, p, cp, c.num_groups, stream);
+  if (a.dtype == FD_DTYPE_BF16) return launch_cascade<__bf16>(a, p, cp, stream);
+  return launch_cascade<_Float16>(a, p, cp, stream);
 }

@@ -153,29 +153,32 @@ int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
 
 /*
  * Shared-prefix (cascade) decode: the result of fd_paged_decode, with the
- * K/V of a prefix shared by a group of rows read once per group.  No
- * counterpart in the reference, which reads every row's prefix separately
- * (flashdec/kernels/paged_decode.py:330-543); groups are the rows attached to
- * one registered prefix of PagedKVCache (flashdec/cache.py:192-276).
+ * K/V of a prefix shared by a group of rows read once per 16 (member, query
+ * head) rows of the group.  No counterpart in the reference, which reads
+ * every row's prefix separately (flashdec/kernels/paged_decode.py:330-543);
+ * groups are the rows attached to one registered prefix of PagedKVCache
+ * (flashdec/cache.py:192-276).
  *
  * Group g lists up to max_members row indices in group_members[g, :] (row
- * stride max_members, members first, -1 after the last) that share their
- * first group_prefix_len[g] tokens: whole blocks, the same physical block
- * ids leading each member's block-table row, and no more tokens than any
- * member's seq_lens.  row_prefix_len[b] is that length for each member row
- * and 0 for rows in no group; a row belongs to at most one group.  A first
- * pass attends every group's prefix for all its members and writes
+ * stride max_members; entries outside [0, num_seqs), e.g. -1, are padding)
+ * that share their first group_prefix_len[g] tokens: whole blocks, the same
+ * physical block ids leading each member's block-table row, and no more
+ * tokens than any member's seq_lens.  Entry 0 is the lead: the prefix's
+ * block ids are read from its table row.  row_prefix_len[b] is that length
+ * for each member row and 0 for rows in no group; a row belongs to at most
+ * one group.  One launch holds prefix-role workgroups -- one per (group, KV
+ * head, 16 of the group's member x query-head rows, prefix split), writing
  * prefix_splits partials per (row, head) at workspace splits
- * [num_splits, num_splits + prefix_splits); a tail pass attends tokens
- * [row_prefix_len[b], seq_lens[b]) of each row at splits [0, num_splits);
- * the reducer merges them (tail splits only for rows with no prefix).
+ * [num_splits, num_splits + prefix_splits) -- and tail-role workgroups
+ * attending tokens [row_prefix_len[b], seq_lens[b]) of each row at splits
+ * [0, num_splits); the reducer merges them (tail splits only for rows with
+ * no prefix).
  *
  * Needs the MFMA path (head_dim 128, <= 16 query heads per KV head, unit
  * dim stride, 16-byte aligned rows), a split workspace of num_splits +
- * prefix_splits splits, no fused append (append first), and
- * max_members * (num_q_heads / num_kv_heads) <= 256.  max_prefix_len is a
- * hint (the longest group prefix) for where each tail split starts.  The
- * timing events [0]/[1] bracket the prefix and tail passes together.
+ * prefix_splits splits and no fused append (append first).  max_prefix_len
+ * is a hint (the longest group prefix) for where each split starts.  The
+ * timing events [0]/[1] bracket the attention launch, [2]/[3] the reducer.
  */
 typedef struct fd_cascade_args {
   uint32_t struct_size; /* sizeof(fd_cascade_args): ABI guard */

@@ -57,21 +57,22 @@ def test_build_cascade_groups_tensors():
     assert g.max_tail_len == 16 and g.total_tail_len == 8 + 16 + 5 + 3
 
 
-def test_group_capacity_follows_the_query_group():
-    # 256 (member, head) rows per group and KV head
+def test_group_size_bound():
     n = 40
     bt = torch.tensor([[1, 100 + i] for i in range(n)], dtype=torch.int32)
     sl = torch.full((n,), 20, dtype=torch.int32)
-    g = cascade.build_cascade_groups(bt, sl, 16, num_q_heads=16, num_kv_heads=1)  # 16 heads per KV head
+    g = cascade.build_cascade_groups(bt, sl, 16, num_q_heads=16, num_kv_heads=2)  # no bound: one group
+    assert g.num_groups == 1 and g.max_members == 40
+    g = cascade.build_cascade_groups(bt, sl, 16, num_q_heads=16, num_kv_heads=2, max_members=16)
     assert g.num_groups == 3 and g.max_members == 14  # 40 rows: 14 + 13 + 13
     assert sorted(len([x for x in m if x >= 0]) for m in g.members.tolist()) == [13, 13, 14]
-    g = cascade.build_cascade_groups(bt, sl, 16, num_q_heads=32, num_kv_heads=8)  # 4 per KV head
-    assert g.num_groups == 1 and g.max_members == 40
+    # 16-row chunks: 40 members x 8 query heads per KV head = 320 rows
+    assert cascade.prefix_chunks(cascade.build_cascade_groups(bt, sl, 16, 16, 2), 16, 2) == 20
 
 
 def test_prefix_split_plan():
-    # enough workgroups for the CUs, at most one per 32-token prefix tile
-    assert cascade.plan_prefix_splits(1, 2, 4096, 256) == 128
-    assert cascade.plan_prefix_splits(1, 2, 1024, 256) == 32
-    assert cascade.plan_prefix_splits(8, 8, 4096, 256) == 4
-    assert cascade.plan_prefix_splits(0, 2, 0, 256) == 1
+    # about one prefix-role workgroup per CU, at most one split per 32-token tile
+    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256) == 16
+    assert cascade.plan_prefix_splits(1, 2, 1, 1024, 256) == 32
+    assert cascade.plan_prefix_splits(8, 8, 8, 4096, 256) == 1
+    assert cascade.plan_prefix_splits(0, 2, 1, 0, 256) == 1

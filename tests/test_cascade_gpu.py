@@ -5,10 +5,11 @@ layout ``PagedKVCache.attach_prefix`` produces, flashdec/cache.py:225-248);
 the cascade result must equal plain paged decode of the same tables, so the
 oracle is the ordinary paged-decode oracle.  Cases: block sizes 8/16/32,
 group sizes 1/8/16, fp16 and bf16, prefixes that end inside a 32-token tile,
-rows whose tail is empty, zero-length rows, rows in no group, a full group
-of 256 (member, head) rows, more prefix splits than prefix tiles, explicit
-tail split counts, groups whose prefix is shorter than what the tables
-share, and padded member lists.  Tolerance: atol 2e-2 / rtol 1e-2.
+rows whose tail is empty, zero-length rows, rows in no group, groups of 32
+and 40 members (16 and 20 sixteen-row chunks per KV head), more prefix
+splits than prefix tiles, explicit tail split counts, groups whose prefix is
+shorter than what the tables share, and padded member lists.  Tolerance:
+atol 2e-2 / rtol 1e-2.
 """
 
 import numpy as np
@@ -102,13 +103,25 @@ def test_shared_prefix_matches_oracle(hq, hkv, block_size, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16])
-def test_full_group_of_256_rows(dtype):
+def test_group_of_32_members(dtype):
     rng = np.random.default_rng(5)
     tails = [int(x) for x in rng.integers(1, 100, size=32)]
     q, k, v, table, lens, expected = make_prefix_inputs([(64, tails)], [300], 16, 2, 16, dtype, seed=9)
     cas = _cascade()
     g = cas.build_cascade_groups(table, lens, 16, 16, 2)
     assert g.num_groups == 1 and g.max_members == 32 and g.max_prefix_len == 1024
+    out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+def test_large_group_spans_many_chunks():
+    # 40 members x 8 query heads per KV head = 320 rows: 20 chunks of 16
+    rng = np.random.default_rng(8)
+    tails = [int(x) for x in rng.integers(0, 70, size=40)]
+    q, k, v, table, lens, _ = make_prefix_inputs([(9, tails)], [33], 16, 2, 16, torch.bfloat16, seed=13)
+    cas = _cascade()
+    g = cas.build_cascade_groups(table, lens, 16, 16, 2)
+    assert g.num_groups == 1 and g.max_members == 40
     out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g)
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
 
