@@ -305,7 +305,8 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
                                     max(groups.total_tail_len, 1))
     psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads,
                                          cascade.prefix_chunks(groups, q.shape[1], num_kv_heads),
-                                         groups.max_prefix_len, cascade._num_cus(q.device))
+                                         groups.max_prefix_len, cascade._num_cus(q.device),
+                                         tail_blocks=q.shape[0] * num_kv_heads * splits)
     acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits + psplits, stream)
     args = _lib.PagedDecodeArgs()
     pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,
@@ -396,17 +397,25 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
     attn_c, red_c = cascade_kernel_us(torch, prepared_c, min(4 * len(pools), 96))
     log(f"[bench] {name} cascade: {ms_c * 1e3:.2f} us/call (graph); prefix + tail passes {attn_c:.2f} us, reducer "
         f"{red_c:.2f} us; tail splits {prepared_c[0][0].num_splits}, prefix splits {prepared_c[0][1].prefix_splits}")
-    out["per_row_path"] = {"us_per_call": out["us_per_call"], "value": out["value"], "roofline": out["roofline"]}
-    out["value"] = round(unique / (ms_c * 1e-3) / 1e9, 2)
-    out["ms_per_step"] = round(ms_c, 6)
-    out["us_per_call"] = round(ms_c * 1e3, 3)
-    out["config"]["path"] = "cascade"
-    out["config"]["prefix_splits"] = prepared_c[0][1].prefix_splits
-    out["config"]["num_splits"] = prepared_c[0][0].num_splits
-    out["roofline"] = {"bound": "hbm", "achieved": round(unique / (attn_c * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
-                       "unit": "GB/s", "frac": round(unique / (attn_c * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                       "traffic": None, "kernel_us_mean": round(attn_c, 3), "reducer_us_mean": round(red_c, 3),
-                       "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}
+    cascade_line = {"us_per_call": round(ms_c * 1e3, 3), "value": round(unique / (ms_c * 1e-3) / 1e9, 2),
+                    "num_splits": prepared_c[0][0].num_splits, "prefix_splits": prepared_c[0][1].prefix_splits,
+                    "roofline": {"bound": "hbm", "achieved": round(unique / (attn_c * 1e-6) / 1e9, 2),
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(unique / (attn_c * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                                 "kernel_us_mean": round(attn_c, 3), "reducer_us_mean": round(red_c, 3),
+                                 "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}}
+    # the line's value is the faster of the two paths; the other rides along
+    if ms_c < ms:
+        per_row = {k: out[k] for k in ("us_per_call", "value", "roofline")}
+        per_row["num_splits"] = out["config"]["num_splits"]
+        out.update({k: cascade_line[k] for k in ("us_per_call", "value", "roofline")})
+        out["ms_per_step"] = round(ms_c, 6)
+        out["config"].update(path="cascade", num_splits=cascade_line["num_splits"],
+                             prefix_splits=cascade_line["prefix_splits"])
+        out["per_row_path"] = per_row
+    else:
+        out["config"]["path"] = "per-row"
+        out["cascade_path"] = cascade_line
     return out
 
 

@@ -50,6 +50,13 @@ def test_library_rejects_bad_arguments_without_touching_a_device():
     rope.struct_size = 3
     assert lib.fd_fused_rope_kv_append(ctypes.byref(rope), None) == -1
     assert lib.fd_kv_append(ctypes.byref(rope), None) == -1
+    # the cascade entry point validates both structs before any HIP call
+    args.struct_size = ctypes.sizeof(args) - 8
+    cas = _lib.CascadeArgs()
+    cas.struct_size = ctypes.sizeof(cas)
+    assert lib.fd_paged_decode_cascade(ctypes.byref(args), ctypes.byref(cas), None) == -1
+    assert b"fd_paged_decode_cascade" in lib.fd_last_error() and b"struct_size" in lib.fd_last_error()
+    assert lib.fd_paged_decode_cascade(None, ctypes.byref(cas), None) == -1
 
 
 LAYOUT_PROBE = r"""
@@ -60,6 +67,7 @@ LAYOUT_PROBE = r"""
 int main(void) {
   printf("fd_paged_decode_args sizeof %zu\n", sizeof(fd_paged_decode_args));
   printf("fd_rope_append_args sizeof %zu\n", sizeof(fd_rope_append_args));
+  printf("fd_cascade_args sizeof %zu\n", sizeof(fd_cascade_args));
 %s
   return 0;
 }
@@ -68,7 +76,8 @@ int main(void) {
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 def test_ctypes_structs_match_c_layout(tmp_path):
-    pairs = [("fd_paged_decode_args", _lib.PagedDecodeArgs), ("fd_rope_append_args", _lib.RopeAppendArgs)]
+    pairs = [("fd_paged_decode_args", _lib.PagedDecodeArgs), ("fd_rope_append_args", _lib.RopeAppendArgs),
+             ("fd_cascade_args", _lib.CascadeArgs)]
     lines = [f"  F({c}, {name})" for c, py in pairs for name, _ in py._fields_]
     src = tmp_path / "probe.c"
     src.write_text(LAYOUT_PROBE.replace("%s", "\n".join(lines)))

@@ -71,8 +71,11 @@ def test_group_size_bound():
 
 
 def test_prefix_split_plan():
-    # about one prefix-role workgroup per CU, at most one split per 32-token tile
+    # the CUs the tail-role workgroups leave (at least a quarter), at most one
+    # split per 32-token tile
     assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256) == 16
+    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256, tail_blocks=128) == 8
+    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256, tail_blocks=1024) == 4
     assert cascade.plan_prefix_splits(1, 2, 1, 1024, 256) == 32
     assert cascade.plan_prefix_splits(8, 8, 8, 4096, 256) == 1
     assert cascade.plan_prefix_splits(0, 2, 1, 0, 256) == 1
