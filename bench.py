@@ -95,7 +95,7 @@ def algorithmic_bytes(batch, ctx, hq, hkv, d, bs, elt=2):
     return batch * ctx * hkv * d * 2 * elt + 2 * batch * hq * d * elt + 4 * batch * nblk + 4 * batch
 
 
-def prepared_args(pool, sm_scale, block_size, num_kv_heads):
+def prepared_args(pool, sm_scale, block_size, num_kv_heads, ragged=False):
     """The ctypes argument block ``paged_decode_attention_into`` builds for this pool (auto splits)."""
     from flashdec_amd import _lib
     from flashdec_amd import paged_decode as pd
@@ -103,12 +103,17 @@ def prepared_args(pool, sm_scale, block_size, num_kv_heads):
     q, k, v, table, lens, out = pool
     stream = _lib.current_stream_handle(q.device)
     max_seq_len = table.shape[1] * block_size
-    splits = _lib.paged_decode_plan(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], max_seq_len)
+    balance = _lib.paged_decode_balance_target(q.shape[0], num_kv_heads) if ragged else 0
+    if balance:
+        splits = max(2, min(balance, -(-max_seq_len // 32)))
+    else:
+        splits = _lib.paged_decode_plan(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], max_seq_len)
     args = _lib.PagedDecodeArgs()
     pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,
                     num_kv_heads, block_size, sm_scale)
     args.num_blocks = k.shape[0]
     args.max_seq_len = max_seq_len
+    args.balance_target = balance
     acc = mx = sm = None
     if splits > 1:
         acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits, stream)
@@ -347,7 +352,7 @@ def cascade_kernel_us(torch, prepared, n_calls):
     return attn, red
 
 
-def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_blocks=0):
+def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_blocks=0, ragged=False):
     import flashdec_amd as fd
 
     hq, hkv, d, bs = 16, 2, 128, 32
@@ -379,6 +384,37 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
                        "unit": "GB/s", "frac": round(unique / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                        "traffic": None, "kernel_us_mean": round(attn_us, 3), "reducer_us_mean": round(red_us, 3),
                        "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}
+    if ragged:
+        # the same pools with per-row split counts (ragged=True); the line's
+        # value is the faster of the two
+        def fn_ragged(i):
+            q, k, v, table, sl, o = pools[i % len(pools)]
+            fd.paged_decode_attention_into(q, k, v, table, sl, o, sm_scale=sm_scale, ragged=True)
+
+        ms_r = graph_ms_per_call(torch, dev, fn_ragged, args.steps)
+        prepared_r = [prepared_args(p, sm_scale, bs, hkv, ragged=True) for p in pools]
+        attn_r, red_r = attention_kernel_us(torch, prepared_r, min(4 * len(pools), 96))
+        log(f"[bench] {name} ragged=True: {ms_r * 1e3:.2f} us/call (graph); attention kernel {attn_r:.2f} us, "
+            f"reducer {red_r:.2f} us; balance target {prepared_r[0][0].balance_target}, "
+            f"splits <= {prepared_r[0][0].num_splits}")
+        balanced = {"us_per_call": round(ms_r * 1e3, 3), "value": round(unique / (ms_r * 1e-3) / 1e9, 2),
+                    "balance_target": prepared_r[0][0].balance_target, "num_splits": prepared_r[0][0].num_splits,
+                    "roofline": {"bound": "hbm", "achieved": round(unique / (attn_r * 1e-6) / 1e9, 2),
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(unique / (attn_r * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                                 "kernel_us_mean": round(attn_r, 3), "reducer_us_mean": round(red_r, 3),
+                                 "algorithmic_bytes_per_call": unique, "logical_bytes_per_call": logical}}
+        if ms_r < ms:
+            uniform = {k: out[k] for k in ("us_per_call", "value", "roofline")}
+            uniform["num_splits"] = out["config"]["num_splits"]
+            out.update({k: balanced[k] for k in ("us_per_call", "value", "roofline")})
+            out["ms_per_step"] = round(ms_r, 6)
+            out["config"].update(splits="per-row (ragged=True)", balance_target=balanced["balance_target"],
+                                 num_splits=balanced["num_splits"])
+            out["uniform_splits_path"] = uniform
+        else:
+            out["config"]["splits"] = "uniform"
+            out["per_row_splits_path"] = balanced
     if prefix_blocks == 0:
         return out
     # the same pools through the cascade (prefix read once per group): the
@@ -421,7 +457,8 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
 
 def run_ragged(torch, dev, args):
     """C4: B32 Hq16 Hkv2 D128 bf16, seq_lens ~ logU[128, 32768] (seed 1701)."""
-    return run_decode_variant(torch, dev, args, "ragged-b32-logU128-32768", ragged_lengths(32, 1701), 3, 1701)
+    return run_decode_variant(torch, dev, args, "ragged-b32-logU128-32768", ragged_lengths(32, 1701), 3, 1701,
+                              ragged=True)
 
 
 def run_prefix(torch, dev, args):

@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 
 _i64 = ctypes.c_int64
@@ -72,6 +72,7 @@ class PagedDecodeArgs(ctypes.Structure):
         ("slot_mapping_dtype", _i32),
         ("slot_mapping_stride", _i64),
         ("timing_events", _vp * 4),
+        ("balance_target", _i32),
     ]
 
 
@@ -117,6 +118,7 @@ EXPORTED_SYMBOLS = (
     "fd_paged_decode",
     "fd_paged_decode_cascade",
     "fd_paged_decode_plan",
+    "fd_paged_decode_balance_target",
     "fd_fused_rope_kv_append",
     "fd_kv_append",
     "fd_last_error",
@@ -154,6 +156,8 @@ def load_library():
         lib.fd_paged_decode.restype = ctypes.c_int
         lib.fd_paged_decode_cascade.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(CascadeArgs), _vp]
         lib.fd_paged_decode_cascade.restype = ctypes.c_int
+        lib.fd_paged_decode_balance_target.argtypes = [_i64, _i64]
+        lib.fd_paged_decode_balance_target.restype = ctypes.c_int
         lib.fd_paged_decode_plan.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64]
         lib.fd_paged_decode_plan.restype = ctypes.c_int
         lib.fd_fused_rope_kv_append.argtypes = [ctypes.POINTER(RopeAppendArgs), _vp]
@@ -224,6 +228,14 @@ def paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len
     rc = lib.fd_paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len, total_seq_len)
     if rc < 0:
         check(rc, "fd_paged_decode_plan")
+    return rc
+
+
+def paged_decode_balance_target(num_seqs, num_kv_heads) -> int:
+    lib = load_library()
+    rc = lib.fd_paged_decode_balance_target(num_seqs, num_kv_heads)
+    if rc < 0:
+        check(rc, "fd_paged_decode_balance_target")
     return rc
 
 

@@ -256,6 +256,10 @@ class PagedKVCache:
         """Mark an active request cancelled and release its private blocks."""
         return self._close_request(request_id, self.CANCELLED)
 
+    def _host_seq_lens(self, request_ids):
+        """Current lengths of known requests, from host state (no device access)."""
+        return [self._require_request(rid).seq_len for rid in request_ids]
+
     def request_state(self, request_id):
         """Detached snapshot of one request's lifecycle state."""
         state = self._require_request(request_id)

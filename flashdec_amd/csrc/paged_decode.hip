@@ -60,6 +60,10 @@ struct DecodeParams {
   // take workspace splits [0, splits), the prefix pass's come after them
   const int32_t* tb;
   int hint_tb;       // guess of tb / 32 for the first unit's early loads
+  // balanced splits (> 0): row b gets clamp(ceil(tiles_b / T), 1, splits)
+  // splits, T = ceil(total tiles / bal_target); workgroup w takes KV head
+  // w % hkv of the batch's (w / hkv)-th split
+  int bal_target;
   float scale_log2;  // sm_scale * log2(e): scores live in the base-2 domain
 };
 
@@ -514,7 +518,74 @@ struct CascadeParams {
   int hint_ptps;      // guess of the prefix tiles per split (longest prefix)
 };
 
-enum class Role { kRow, kTail, kPrefix };
+enum class Role { kRow, kTail, kPrefix, kBalanced };
+
+__device__ __forceinline__ int wave_sum_i32(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan_i32(int x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    x += lane >= o ? y : 0;
+  }
+  return x;
+}
+
+// Balanced splits: tiles per split T for the whole batch, from every row's
+// effective length (one wave; the result is the same in every lane).
+__device__ __forceinline__ int balanced_tiles_per_split(const DecodeParams& p, int lane) {
+  int total = 0;
+  for (int r0 = 0; r0 < p.num_seqs; r0 += 64) {
+    const int r = r0 + lane;
+    int t = 0;
+    if (r < p.num_seqs) t = static_cast<int>((effective_len(p, load_index(p.sl, r * p.sls, p.sl_i64), -1) + 31) / 32);
+    total += wave_sum_i32(t);
+  }
+  return max(1, (total + p.bal_target - 1) / p.bal_target);
+}
+
+__device__ __forceinline__ int balanced_splits(const DecodeParams& p, int64_t eff, int tps) {
+  return min(max(1, static_cast<int>((eff + 31) / 32 + tps - 1) / tps), p.splits);
+}
+
+// Wave 0 of a balanced-split workgroup: which row and split the batch's v-th
+// split is (prefix sums of the rows' split counts), that row's split count and
+// effective length; row -1 when v is past the batch's last split.
+__device__ __forceinline__ void balanced_locate(const DecodeParams& p, int v, int lane, int* out) {
+  const int tps = balanced_tiles_per_split(p, lane);
+  int base = 0;
+  int fb = -1, fs = 0, fn = 1, fe = 0;
+  for (int r0 = 0; r0 < p.num_seqs; r0 += 64) {
+    const int r = r0 + lane;
+    int e = 0, n = 0;
+    if (r < p.num_seqs) {
+      e = static_cast<int>(effective_len(p, load_index(p.sl, r * p.sls, p.sl_i64), -1));
+      n = balanced_splits(p, e, tps);
+    }
+    const int incl = wave_inclusive_scan_i32(n, lane);
+    const bool hit = r < p.num_seqs && v >= base + incl - n && v < base + incl;
+    const uint64_t m = __ballot(hit);
+    if (m) {
+      const int l = __builtin_ctzll(m);
+      fb = r0 + l;
+      fn = __builtin_amdgcn_readlane(n, l);
+      fs = v - base - (__builtin_amdgcn_readlane(incl, l) - fn);
+      fe = __builtin_amdgcn_readlane(e, l);
+      break;
+    }
+    base += __builtin_amdgcn_readlane(incl, 63);
+  }
+  if (lane == 0) {
+    out[0] = fb;
+    out[1] = fs;
+    out[2] = fn;
+    out[3] = fe;
+  }
+}
 
 // LDS of one decode workgroup: each wave's state for the merge, and the
 // output row of every MFMA column.
@@ -525,29 +596,42 @@ struct alignas(16) DecodeLds {
   float l[W][16];
   int col_b[16];
   int col_h[16];
+  int located[4];  // balanced splits: row, split, row's split count, effective length
   int last;
 };
 
 template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, Role ROLE>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
                                             DecodeLds<waves_for<UNIT>()>& lds) {
-  static_assert(ROLE == Role::kRow || !(FUSE || MERGE), "cascade roles have no fused append or in-launch merge");
+  static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
+                "cascade and balanced roles have no fused append or in-launch merge");
   constexpr int kWaves = waves_for<UNIT>();
   constexpr int kUnitsPerTile = 32 / UNIT;
   constexpr bool PREFIX = ROLE == Role::kPrefix;
   constexpr bool TAIL = ROLE == Role::kTail;
+  constexpr bool BAL = ROLE == Role::kBalanced;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int nsplit = PREFIX ? cp.prefix_splits : p.splits;
-  const int split = block % nsplit;
+  int nsplit = PREFIX ? cp.prefix_splits : p.splits;
+  int split = block % nsplit;
   const int pair = block / nsplit;  // (request, KV head), or (group, KV head, chunk)
   const int G = p.group;
   int b, kvh, chunk = 0;
   const int32_t* mem = nullptr;
-  if constexpr (PREFIX) {
+  int64_t bal_eff = 0;
+  if constexpr (BAL) {
+    kvh = block % p.hkv;
+    if (wave == 0) balanced_locate(p, block / p.hkv, lane, lds.located);
+    __syncthreads();
+    b = lds.located[0];
+    if (b < 0) return;  // past the batch's last split: no work (every thread leaves here)
+    split = lds.located[1];
+    nsplit = lds.located[2];
+    bal_eff = lds.located[3];
+  } else if constexpr (PREFIX) {
     chunk = pair % cp.chunks;
     const int gk = pair / cp.chunks;
     kvh = gk % p.hkv;
@@ -577,7 +661,12 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   // (hint tiles per split), so its block ids and K/V rows, the Q^T operand,
   // the append row and the row length / slot are all in flight together --
   // no load address depends on seq_lens.  The guess is checked below.
-  const int guess_begin = PREFIX ? split * cp.hint_ptps : (TAIL ? p.hint_tb : 0) + split * p.hint_tps;  // tiles
+  int guess_begin = PREFIX ? split * cp.hint_ptps : (TAIL ? p.hint_tb : 0) + split * p.hint_tps;  // tiles
+  if constexpr (BAL) {
+    // the row's length is known: the first unit is not a guess
+    int t1;
+    split_tiles(nsplit, split, bal_eff, 0, guess_begin, t1);
+  }
   int unit = kUnitsPerTile * guess_begin + wave;
   UnitPages pages = fetch_pages<BS, UNIT>(p, trow, unit);  // clamped, always in bounds
   u32x4 qf[4];
@@ -599,7 +688,9 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   }
   int64_t eff_len;
   int32_t slot = -1;
-  if constexpr (PREFIX) {
+  if constexpr (BAL) {
+    eff_len = bal_eff;
+  } else if constexpr (PREFIX) {
     const int64_t cap = p.max_blocks_per_seq * p.block_size;
     const int64_t plen = lead_ok ? cp.prefix_len[pair / cp.chunks / p.hkv] : 0;
     eff_len = plen < 0 ? 0 : (plen < cap ? plen : cap);
@@ -840,6 +931,14 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow>(p, CascadeParams{}, blockIdx.x, lds);
 }
 
+// Balanced splits (ragged batches): the row and split of each workgroup come
+// from the batch's lengths on the device.
+template <typename T, int BS>
+__global__ __launch_bounds__(64 * waves_for<16>(), 1) void decode_balanced_kernel(DecodeParams p) {
+  __shared__ DecodeLds<waves_for<16>()> lds;
+  decode_role<T, BS, false, false, 16, Role::kBalanced>(p, CascadeParams{}, blockIdx.x, lds);
+}
+
 // Cascade launch: workgroups [0, prefix_blocks) take the prefix role, the
 // rest the tail role (both write split partials; the reducer merges them).
 template <typename T, int BS, int UNIT>
@@ -1021,13 +1120,18 @@ struct ReduceParams {
   // first tail_splits splits
   const int32_t* tb;
   int tail_splits;
+  // balanced splits: each row's count is recomputed from the batch's lengths
+  int bal_target, num_seqs;
+  int64_t cap;  // table capacity in tokens (effective lengths)
 };
+
+enum ReduceMode { kReducePlain = 0, kReduceCascade = 1, kReduceBalanced = 2 };
 
 __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane_idx));
 }
 
-template <typename T, int D, bool CASCADE = false>
+template <typename T, int D, int MODE = kReducePlain>
 __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
   // every argument in SGPRs before any use: one batch of argument loads, one
   // wait (left alone the compiler fetched the strides lazily, a second
@@ -1045,8 +1149,21 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
   const int32_t seq_len = load_index(p.sl, b * p.sls + vzero, p.sl_i64);
   const int32_t slot = load_index(p.slot, b * p.slots + vzero, p.slot_i64);  // seq_lens when not fused
   int splits = p.splits;
-  if constexpr (CASCADE)
+  if constexpr (MODE == kReduceCascade)
     splits = __builtin_amdgcn_readfirstlane(p.tb[b + vzero]) > 0 ? p.splits : p.tail_splits;
+  if constexpr (MODE == kReduceBalanced) {
+    // the same counts as the attention kernel: T from the batch's total tiles
+    auto eff_of = [&](int64_t len) -> int64_t { return len > 0 ? (len < p.cap ? len : p.cap) : 0; };
+    int total = 0;
+    for (int r0 = 0; r0 < p.num_seqs; r0 += 64) {
+      const int r = r0 + lane;
+      const int t = r < p.num_seqs ? static_cast<int>((eff_of(load_index(p.sl, r * p.sls, p.sl_i64)) + 31) / 32) : 0;
+      total += wave_sum_i32(t);
+    }
+    const int tps = max(1, (total + p.bal_target - 1) / p.bal_target);
+    const int tiles = static_cast<int>((eff_of(__builtin_amdgcn_readfirstlane(seq_len)) + 31) / 32);
+    splits = min(max(1, (tiles + tps - 1) / tps), p.splits);
+  }
   const int64_t sb = b * p.ss0 + qh * p.ss1;
   const float* ab = p.acc + b * p.as0 + qh * p.as1;
   float M = -INFINITY;
@@ -1214,17 +1331,19 @@ ReduceParams reduce_params(const DecodeParams& p) {
   r.slot_i64 = p.fuse ? p.slot_i64 : p.sl_i64;
   r.tb = nullptr;
   r.tail_splits = p.splits;
+  r.bal_target = p.bal_target;
+  r.num_seqs = p.num_seqs;
+  r.cap = p.max_blocks_per_seq * p.block_size;
   return r;
 }
 
-template <typename T, bool CASCADE>
+template <typename T, int MODE>
 int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
   if (a.head_dim == 64)
-  dispatch(split_reduce_kernel<T, 64, CASCADE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
+    dispatch(split_reduce_kernel<T, 64, MODE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
   else
-  dispatch(split_reduce_kernel<T, 128, CASCADE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3],
-           r);
+    dispatch(split_reduce_kernel<T, 128, MODE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
   return FD_OK;
@@ -1240,7 +1359,21 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   if (!fast || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
       (reinterpret_cast<uintptr_t>(p.acc) & 7u))
     p.counters = nullptr;
-  if (fast) {
+  // balanced splits need the MFMA kernel, no fused append and a workspace
+  const bool balanced = p.bal_target > 0 && fast && !p.fuse && p.splits > 1;
+  if (!balanced) p.bal_target = 0;
+  if (balanced) {
+    p.counters = nullptr;
+    // sum over rows of ceil(tiles_b / T) <= bal_target + num_seqs
+    const dim3 grid(static_cast<unsigned>(a.num_kv_heads * (p.bal_target + a.num_seqs)));
+    const dim3 block(64 * waves_for<16>());
+    void* const* ev = a.timing_events;
+    switch (a.block_size) {
+      case 8: dispatch(decode_balanced_kernel<T, 8>, grid, block, stream, ev[0], ev[1], p); break;
+      case 16: dispatch(decode_balanced_kernel<T, 16>, grid, block, stream, ev[0], ev[1], p); break;
+      default: dispatch(decode_balanced_kernel<T, 32>, grid, block, stream, ev[0], ev[1], p); break;
+    }
+  } else if (fast) {
     const dim3 grid(static_cast<unsigned>(pairs * p.splits));
     switch (a.block_size) {
       case 8: launch_mfma<T, 8>(p, grid, stream, a.timing_events); break;
@@ -1260,7 +1393,8 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
   if (p.splits > 1 && p.counters == nullptr) {
     const ReduceParams r = reduce_params(p);
-    const int rc = launch_reduce<T, false>(a, r, stream);
+    const int rc =
+        balanced ? launch_reduce<T, kReduceBalanced>(a, r, stream) : launch_reduce<T, kReducePlain>(a, r, stream);
     if (rc != FD_OK) return rc;
   }
   return FD_OK;
@@ -1297,7 +1431,7 @@ int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const C
   r.splits = p.splits + cp.prefix_splits;
   r.tb = p.tb;
   r.tail_splits = p.splits;
-  return launch_reduce<T, true>(a, r, stream);
+  return launch_reduce<T, kReduceCascade>(a, r, stream);
 }
 
 }  // namespace
@@ -1305,6 +1439,19 @@ int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const C
 }  // namespace fd
 
 using namespace fd;
+
+extern "C" int fd_paged_decode_balance_target(int64_t num_seqs, int64_t num_kv_heads) {
+  if (num_seqs <= 0 || num_kv_heads <= 0)
+    return set_error(FD_E_INVALID, "fd_paged_decode_balance_target: non-positive shape");
+  // One round of workgroups (one per CU): sum over rows of S_b <= V + B, so
+  // V = CUs / Hkv - B keeps the grid within it.  Ragged B32 on MI355X
+  // (Σ L = 206 k, max 30.7 k): attention 58.4 us with 16 uniform splits;
+  // V = 64 / 96 / 128 / 224: 46.9 / 41.9 / 56.2 / 44.2 us (128 spills into
+  // a second, mostly empty round).  A batch that already fills a round gets
+  // 0: uniform splits.
+  const int64_t v = device_cus() / num_kv_heads - num_seqs;
+  return v >= num_seqs && v <= (1 << 20) ? static_cast<int>(v) : 0;
+}
 
 extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
                                     int64_t head_dim, int64_t max_seq_len, int64_t total_seq_len) {
@@ -1440,6 +1587,11 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
   p.max_blocks_per_seq = a.max_blocks_per_seq;
   p.splits = a.num_splits;
   if (a.max_seq_len < 0) return set_error(FD_E_INVALID, "%s: max_seq_len must be >= 0", fn);
+  if (a.balance_target < 0 || a.balance_target > (1 << 20))
+    return set_error(FD_E_INVALID, "%s: balance_target must be in [0, 2^20]", fn);
+  if (a.num_kv_heads * (a.balance_target + a.num_seqs) > 0x7fffffffLL)
+    return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
+  p.bal_target = a.balance_target;
   {
     // first-tile guess of the MFMA kernel: from max_seq_len when given, else
     // from the table width; each row's split range uses its own length

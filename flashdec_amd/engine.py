@@ -117,6 +117,7 @@ class DecodeStepGraph:
     base: float
     metadata: Any
     workspace: Any = None  # split partials the graph writes (kept alive with it)
+    balance_target: int = 0  # > 0: per-row split counts from the lengths at replay
 
 
 @dataclass
@@ -127,6 +128,14 @@ class _OpenStep:
     next_layer_idx: int = 0
     last_output: Any | None = None
     state: str = "open"
+    ragged: bool = False  # the batch's lengths vary widely: per-row split counts
+
+
+def _is_ragged(lengths):
+    """A batch whose longest row is over twice its mean length."""
+    if not lengths:
+        return False
+    return max(lengths) * len(lengths) > 2 * max(1, sum(lengths))
 
 
 class DecodeEngine:
@@ -292,7 +301,8 @@ class DecodeEngine:
         )
         self._sync_cache_version()
         self._bump_state_version()
-        self._open = _OpenStep(handle=handle, cache_transaction=tx, needed_new_blocks=needed)
+        self._open = _OpenStep(handle=handle, cache_transaction=tx, needed_new_blocks=needed,
+                               ragged=_is_ragged(self.cache._host_seq_lens(ids)))
         return handle
 
     def step_layer(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0):
@@ -397,14 +407,21 @@ class DecodeEngine:
         q_rot = torch.zeros_like(q)
         out = torch.zeros_like(q)
         width = meta.block_tables.shape[1]
+        balance = 0
         if num_splits is None:
             # the batch's current lengths tell a uniform batch from a ragged one
-            active = [cache.request_state(rid)["seq_len"] for rid in self.active_request_ids()]
+            active = cache._host_seq_lens(self.active_request_ids())
             longest = max(active, default=0) + 1
             total = sum(active) + len(active) if len(active) == batch_size else 0
-            splits = _lib.paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
-                                            min(longest, width * cache.block_size) if total else
-                                            width * cache.block_size, total)
+            if total and _is_ragged(active):
+                balance = _lib.paged_decode_balance_target(batch_size, cache.num_kv_heads)
+            if balance:
+                # per-row split counts follow the lengths at every replay
+                splits = max(2, min(balance, -(-width * cache.block_size // 32)))
+            else:
+                splits = _lib.paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
+                                                min(longest, width * cache.block_size) if total else
+                                                width * cache.block_size, total)
         else:
             splits = int(num_splits)
             if splits <= 0:
@@ -427,11 +444,12 @@ class DecodeEngine:
                                                   rotary_dim=rotary_dim, base=base, q_out=q_rot[layer])
                     _decode_with_workspace(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
                                            meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
-                                           cache.block_size, splits, workspace, cache.max_blocks)
+                                           cache.block_size, splits, workspace, cache.max_blocks,
+                                           balance_target=balance)
         torch.cuda.current_stream(dev).wait_stream(side)
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
                                num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,
-                               workspace=workspace)
+                               workspace=workspace, balance_target=balance)
 
     def step_graph(self, transaction, step_graph):
         """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.
@@ -572,11 +590,12 @@ class DecodeEngine:
         return q_rot, view, None
 
     def _decode_layer(self, q_rot, view, meta, layer_idx):
+        ragged = self._open is not None and self._open.ragged
         if meta is not None:  # the allocator's own copy, not the caller-visible clone
-            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx)
-        return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx)
+            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx, ragged=ragged)
+        return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx, ragged=ragged)
 
-    def _decode(self, q, block_tables, seq_lens, layer_idx=0):
+    def _decode(self, q, block_tables, seq_lens, layer_idx=0, ragged=False):
         layer_idx = int(layer_idx)
         if layer_idx < 0 or layer_idx >= self.cache.num_layers:
             raise ValueError("layer_idx must be in [0, num_layers)")
@@ -589,7 +608,7 @@ class DecodeEngine:
 
         return paged_decode_attention(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx], block_tables,
                                       seq_lens, sm_scale=self.sm_scale, block_size=self.cache.block_size,
-                                      num_warps=self.num_warps, num_stages=self.num_stages)
+                                      num_warps=self.num_warps, num_stages=self.num_stages, ragged=ragged)
 
     def _abort_open_step(self, state):
         if self._open is not state or state.state != "open":

@@ -220,6 +220,7 @@ def paged_decode_attention(
     num_warps=2,
     kv_layout="token_major",
     num_stages=None,
+    ragged=False,
 ):
     """Return paged single-token decode attention (``flashdec.decode``).
 
@@ -228,7 +229,8 @@ def paged_decode_attention(
     ``[num_blocks, num_kv_heads, head_dim, block_size]``); block_tables
     ``[num_seqs, max_blocks_per_seq]``; seq_lens ``[num_seqs]``.  Returns
     ``[num_seqs, num_q_heads, head_dim]`` in q.dtype.  block_size is inferred
-    from the cache when omitted (paged_decode.py:950-955).
+    from the cache when omitted (paged_decode.py:950-955).  ``ragged``: see
+    :func:`paged_decode_attention_into`.
     """
     token_axis, _ = _layout_axes(kv_layout)
     if block_size is None:
@@ -250,6 +252,7 @@ def paged_decode_attention(
         num_warps=num_warps,
         kv_layout=kv_layout,
         num_stages=num_stages,
+        ragged=ragged,
     )
 
 
@@ -270,6 +273,7 @@ def paged_decode_attention_into(
     append_k=None,
     append_v=None,
     slot_mapping=None,
+    ragged=False,
 ):
     """Write paged decode attention into ``out`` (no output allocation).
 
@@ -277,6 +281,13 @@ def paged_decode_attention_into(
     to the kernel as-is.  ``append_k``/``append_v``/``slot_mapping`` (together)
     fuse the current token's cache write: the kernel stores it at the slot and
     attends to it from registers.  Mirrors paged_decode.py:972-1264.
+
+    ``ragged=True`` (no counterpart in the reference) tells the library-planned
+    path that the batch's lengths vary widely: each row then gets splits in
+    proportion to its length, counted on the device from ``seq_lens``
+    (``balance_target`` of the C ABI).  It applies without fused append and
+    without a caller workspace, and only where the batch leaves room in one
+    round of workgroups; elsewhere it changes nothing.
     """
     token_axis, dim_axis = _layout_axes(kv_layout)
     if block_size is None:
@@ -346,8 +357,14 @@ def paged_decode_attention_into(
     max_seq_len = block_tables.shape[1] * block_size
     stream = _lib.current_stream_handle(q.device)
     counters = None
+    balance = 0
     if not use_split_kv:
-        num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
+        if ragged and not fuse_kv_append and use_grouped_gqa:
+            balance = _lib.paged_decode_balance_target(num_seqs, num_kv_heads)
+        if balance:
+            num_splits = max(2, min(balance, -(-max_seq_len // 32)))
+        else:
+            num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
         split_acc = split_max = split_sum = None
         if num_splits > 1:
             split_acc, split_max, split_sum, _ = _auto_workspace(q, num_kv_heads, num_splits, stream)
@@ -369,6 +386,7 @@ def paged_decode_attention_into(
     )
     args.num_blocks = k_cache.shape[0]
     args.max_seq_len = max_seq_len
+    args.balance_target = balance
     _fill_workspace(args, split_acc, split_max, split_sum, num_splits, counters)
     if fuse_kv_append:
         _fill_append(args, append_k, append_v, slot_mapping)
@@ -377,11 +395,13 @@ def paged_decode_attention_into(
 
 
 def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_splits,
-                           workspace, num_blocks):
+                           workspace, num_blocks, balance_target=0):
     """Unchecked launch on a token-major cache with a caller-held split workspace (graph capture).
 
     ``workspace`` is ``(acc [B, Hq, S, D], max [B, Hq, S], sum [B, Hq, S])`` or
     None for ``num_splits == 1``; any head_dim / group the library supports.
+    ``balance_target`` > 0 selects per-row split counts (at most
+    ``num_splits``) computed on the device from ``seq_lens``.
     """
     num_kv_heads = k_cache.shape[1]
     if sm_scale is None:
@@ -391,6 +411,7 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
                  block_tables, seq_lens, out, num_kv_heads, block_size, sm_scale)
     args.num_blocks = num_blocks
     args.max_seq_len = block_tables.shape[1] * block_size
+    args.balance_target = int(balance_target)
     acc, mx, sm = workspace if workspace is not None else (None, None, None)
     _fill_workspace(args, acc, mx, sm, int(num_splits))
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))

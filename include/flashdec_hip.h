@@ -23,6 +23,8 @@
  *                            counts for its launcher; this is the MI355X policy
  *   fd_paged_decode_cascade  no counterpart (shared-prefix decode over the
  *                            prefixes of flashdec/cache.py:192-276)
+ *   fd_paged_decode_balance_target  no counterpart: the per-row split
+ *                            policy for ragged batches (balance_target)
  */
 #ifndef FLASHDEC_HIP_H_
 #define FLASHDEC_HIP_H_
@@ -33,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 3
+#define FD_ABI_VERSION 4
 
 /* status codes */
 #define FD_OK 0
@@ -147,6 +149,20 @@ typedef struct fd_paged_decode_args {
    * when the call launches one.  No counterpart in the reference; it lets a
    * caller time the attention kernel alone on its own stream. */
   void* timing_events[4];
+
+  /* Balanced splits for ragged batches (0 = off: every row gets num_splits
+   * splits).  With balance_target = V > 0, row b gets
+   *   S_b = clamp(ceil(tiles_b / T), 1, num_splits),  T = ceil(Σ tiles / V)
+   * splits (tiles = 32-token tiles of the row's length), computed on the
+   * device from seq_lens, so long rows get more splits and every split holds
+   * at most T tiles.  The launch has num_kv_heads * (V + num_seqs)
+   * workgroups, the ones past the batch's Σ S_b exit at once.  S_b <= V, so
+   * a workspace of num_splits = min(V, ceil(max_len / 32)) splits suffices.
+   * Needs the MFMA path, num_splits > 1 and no fused append (otherwise
+   * ignored); costs one extra round trip (the lengths) per workgroup.  No
+   * counterpart in the reference, whose split count is per launch
+   * (flashdec/kernels/paged_decode.py:408-411). */
+  int32_t balance_target;
 } fd_paged_decode_args;
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
@@ -206,6 +222,15 @@ int fd_paged_decode_cascade(const fd_paged_decode_args* args, const fd_cascade_a
 int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads,
                          int64_t num_kv_heads, int64_t head_dim,
                          int64_t max_seq_len, int64_t total_seq_len);
+
+/*
+ * balance_target (fd_paged_decode_args) the library would use for a ragged
+ * batch of this shape on the current device: about one round of workgroups
+ * (one per CU) after the per-row rounding.  0 = not worth it (the batch
+ * fills a round already): use uniform splits.  The matching workspace is
+ * num_splits = min(V, ceil(max_seq_len / 32)).
+ */
+int fd_paged_decode_balance_target(int64_t num_seqs, int64_t num_kv_heads);
 
 /*
  * Fused split-half (NeoX) RoPE of Q and K plus paged append of rotated K and
