@@ -116,7 +116,7 @@ class DecodeStepGraph:
     rotary_dim: int
     base: float
     metadata: Any
-    workspace: Any = None  # split partials the graph writes (kept alive with it)
+    workspace: Any = None  # split partials (and merge counters) the graph uses, kept alive with it
     balance_target: int = 0  # > 0: per-row split counts from the lengths at replay
 
 
@@ -369,7 +369,8 @@ class DecodeEngine:
         """Explicitly abort the open token transaction."""
         return self._abort_open_step(self._require_open_step(transaction))
 
-    def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None):
+    def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None,
+                           merge=False):
         """Capture every layer's launches of one token step into a hipGraph.
 
         Needs the HIP backends, a GPU cache and its graph-metadata arena
@@ -379,7 +380,9 @@ class DecodeEngine:
         :class:`DecodeStepGraph`.  The decode split count is fixed for the
         arena's table width (``num_splits`` overrides it); each row's split
         range follows its own length at replay, so growing sequences stay
-        correct.
+        correct.  ``merge=True`` merges the split partials inside the attention
+        launch (the last workgroup of each request and KV head), so each layer
+        runs two kernels instead of three.
         """
         torch = _torch()
         from . import _lib
@@ -429,10 +432,16 @@ class DecodeEngine:
         _validate_inputs(q_rot[0], cache.k_cache[0], cache.v_cache[0], meta.block_tables, meta.eff_lens,
                          cache.block_size, self.num_warps, self.num_stages, "token_major")
         workspace = None
+        counters = None
         if splits > 1:
             workspace = (torch.empty((batch_size, num_q_heads, splits, cache.head_dim), device=dev),
                          torch.empty((batch_size, num_q_heads, splits), device=dev),
                          torch.empty((batch_size, num_q_heads, splits), device=dev))
+            if merge and not balance:
+                # arrival counters, zero before the capture; every launch leaves them at zero
+                counters = torch.zeros(batch_size * cache.num_kv_heads * _lib.SPLIT_COUNTER_STRIDE, device=dev,
+                                       dtype=torch.int32)
+                workspace = workspace + (counters,)
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -444,8 +453,8 @@ class DecodeEngine:
                                                   rotary_dim=rotary_dim, base=base, q_out=q_rot[layer])
                     _decode_with_workspace(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
                                            meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
-                                           cache.block_size, splits, workspace, cache.max_blocks,
-                                           balance_target=balance)
+                                           cache.block_size, splits, workspace[:3] if workspace else None,
+                                           cache.max_blocks, balance_target=balance, counters=counters)
         torch.cuda.current_stream(dev).wait_stream(side)
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
                                num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,

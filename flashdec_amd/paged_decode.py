@@ -395,13 +395,15 @@ def paged_decode_attention_into(
 
 
 def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_splits,
-                           workspace, num_blocks, balance_target=0):
+                           workspace, num_blocks, balance_target=0, counters=None):
     """Unchecked launch on a token-major cache with a caller-held split workspace (graph capture).
 
     ``workspace`` is ``(acc [B, Hq, S, D], max [B, Hq, S], sum [B, Hq, S])`` or
     None for ``num_splits == 1``; any head_dim / group the library supports.
     ``balance_target`` > 0 selects per-row split counts (at most
-    ``num_splits``) computed on the device from ``seq_lens``.
+    ``num_splits``) computed on the device from ``seq_lens``.  ``counters``
+    (zeroed int32, ``B * Hkv * SPLIT_COUNTER_STRIDE``) selects the in-launch
+    merge: one dispatch, no reducer kernel.
     """
     num_kv_heads = k_cache.shape[1]
     if sm_scale is None:
@@ -413,7 +415,7 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     args.max_seq_len = block_tables.shape[1] * block_size
     args.balance_target = int(balance_target)
     acc, mx, sm = workspace if workspace is not None else (None, None, None)
-    _fill_workspace(args, acc, mx, sm, int(num_splits))
+    _fill_workspace(args, acc, mx, sm, int(num_splits), counters)
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))
     return out
 

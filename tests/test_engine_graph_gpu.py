@@ -6,6 +6,8 @@ the other replays a captured :class:`DecodeStepGraph`.  After every step:
 - both engines' outputs must match the oracle within the north-star
   tolerance.
 The batch's membership may change between steps as long as its size does.
+The graph is checked with the split reducer kernel and with the in-launch
+merge (arrival counters, which every replay leaves at zero).
 """
 
 import pytest
@@ -46,12 +48,13 @@ def oracle_layer(cache, layer, q, tx_positions, tables, lens):
                                      lens.cpu().numpy())
 
 
-def test_step_graph_matches_eager_steps():
+@pytest.mark.parametrize("merge", [False, True])
+def test_step_graph_matches_eager_steps(merge):
     eager = make_engine()
     graphed = make_engine(arena=(4, 16))
     for e in (eager, graphed):
         admit(e, [0, 1, 2, 3], 40)
-    sg = graphed.capture_step_graph(4, HQ, base=1e6)
+    sg = graphed.capture_step_graph(4, HQ, base=1e6, num_splits=3 if merge else None, merge=merge)
     assert isinstance(sg, DecodeStepGraph) and sg.out.shape == (L, 4, HQ, D)
     g = torch.Generator(device="cuda").manual_seed(11)
     for step in range(24):
