@@ -610,6 +610,16 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   constexpr bool PREFIX = ROLE == Role::kPrefix;
   constexpr bool TAIL = ROLE == Role::kTail;
   constexpr bool BAL = ROLE == Role::kBalanced;
+  if constexpr (ROLE == Role::kRow && UNIT == 32) {
+    // Short splits (about one unit per wave) spend most of their time before
+    // the first K/V loads.  Every argument those loads need goes into SGPRs
+    // first: one batch of kernel-argument loads and one wait (left alone the
+    // compiler fetched them in three dependent batches).
+    asm volatile("" ::"s"(p.q), "s"(p.qs0), "s"(p.qs1), "s"(p.k), "s"(p.ks0), "s"(p.ks1), "s"(p.ks2), "s"(p.v),
+                 "s"(p.vs0), "s"(p.vs1), "s"(p.vs2), "s"(p.bt), "s"(p.bts0), "s"(p.bts1), "s"(p.bt_i64), "s"(p.sl),
+                 "s"(p.sls), "s"(p.sl_i64), "s"(p.splits), "s"(p.hkv), "s"(p.group), "s"(p.hint_tps),
+                 "s"(p.max_blocks_per_seq), "s"(p.num_blocks), "s"(p.block_size));
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
