@@ -129,3 +129,37 @@ def test_engine_step_graph_on_a_ragged_batch():
             assert_close_to_oracle(out[layer], expected)
         engine.commit_step(tx)
     assert engine.validate_invariants()
+
+
+def test_full_c4_ragged_shape_rows_match_oracle():
+    """BASELINE config 4 at full size: B32, L ~ logU[128, 32768] (seed 1701),
+    Hq16/Hkv2, D128, bf16, bs32.  Both split policies are checked against the
+    oracle on the longest row, the shortest and three others."""
+    import numpy as np
+
+    import flashdec_amd as fd
+
+    rng = np.random.default_rng(1701)
+    lens_list = [int(round(math.exp(x))) for x in rng.uniform(math.log(128), math.log(32768), size=32)]
+    bs, hkv, hq, d = 32, 2, 16, 128
+    nblk = [-(-n // bs) for n in lens_list]
+    pool = int(sum(nblk) * 1.25) + 1
+    g = torch.Generator(device="cuda").manual_seed(1701)
+    perm = torch.randperm(pool, device="cuda", generator=g).to(torch.int32)
+    table = torch.full((32, max(nblk)), -1, device="cuda", dtype=torch.int32)
+    cursor = 0
+    for b, n in enumerate(nblk):
+        table[b, :n] = perm[cursor:cursor + n]
+        cursor += n
+    k = torch.randn((pool, hkv, bs, d), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((pool, hkv, bs, d), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((32, hq, d), device="cuda", generator=g).to(torch.bfloat16)
+    lens = torch.tensor(lens_list, device="cuda", dtype=torch.int32)
+    rows = sorted({int(np.argmax(lens_list)), int(np.argmin(lens_list)), 3, 17, 30})
+    k_np, v_np = np32(k), np32(v)
+    for ragged in (False, True):
+        out = fd.decode(q, k, v, table, lens, ragged=ragged)
+        torch.cuda.synchronize()
+        sel = torch.tensor(rows, device="cuda")
+        expected = oracle_decode(np32(q[sel]), k_np, v_np, table[sel].cpu().numpy(), lens[sel].cpu().numpy())
+        assert_close_to_oracle(out[sel], expected)
