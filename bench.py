@@ -64,9 +64,11 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "engine"), default="decode",
+    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine"),
+                   default="decode",
                    help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
-                        "prefix: C4 ragged long-context and shared-prefix decode; engine: C5 36-layer step")
+                        "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
+                        "sharing a 16384-token prefix; engine: C5 36-layer step")
     p.add_argument("--engine-steps", type=int, default=200, help="timed steps of the engine workload")
     return p.parse_args()
 
@@ -310,8 +312,7 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
                                     max(groups.total_tail_len, 1))
     psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads,
                                          cascade.prefix_chunks(groups, q.shape[1], num_kv_heads),
-                                         groups.max_prefix_len, cascade._num_cus(q.device),
-                                         tail_blocks=q.shape[0] * num_kv_heads * splits)
+                                         groups.max_prefix_len, cascade._num_cus(q.device))
     acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits + psplits, stream)
     args = _lib.PagedDecodeArgs()
     pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,
@@ -470,6 +471,15 @@ def run_prefix(torch, dev, args):
     return run_decode_variant(torch, dev, args, "shared-prefix-16x4096+U512", lens, 40, 1701, prefix_blocks=128)
 
 
+def run_prefix_large(torch, dev, args):
+    """Shared prefix at scale: 64 requests share a 512-block (16384-token) prefix, private tails ~ U{1..512}."""
+    import numpy as np
+
+    tails = np.random.default_rng(7).integers(1, 513, size=64)
+    lens = [16384 + int(t) for t in tails]
+    return run_decode_variant(torch, dev, args, "shared-prefix-64x16384+U512", lens, 3, 7, prefix_blocks=512)
+
+
 def run_engine(torch, dev, args):
     """C5: 36-layer DecodeEngine step, B64 Hq16 Hkv2 D128 bf16, context 8192, abort every 100th step."""
     from flashdec_amd.cache import PagedKVCache
@@ -594,7 +604,8 @@ def main():
     torch.cuda.set_device(dev)
     _lib.load_library()
     if args.workload != "decode":
-        run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "engine": run_engine}[args.workload]
+        run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
+               "engine": run_engine}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
         return
     batch, ctx, hq, hkv, d, bs = args.batch, args.ctx, 16, 2, 128, 32

@@ -131,19 +131,18 @@ def build_cascade_groups(block_tables, seq_lens, block_size, num_q_heads, num_kv
     )
 
 
-def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus, tail_blocks=0):
+def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus):
     """Prefix partials per (group, KV head, 16-row chunk).
 
-    The launch holds the prefix-role workgroups and ``tail_blocks`` tail-role
-    ones; the prefix role gets the CUs the tail leaves free (at least a
-    quarter of them), at most one split per 32-token prefix tile.  On MI355X
-    with 16 x 4096-token sharers and 128 tail workgroups this picks 8 (the
-    best of 2..32 measured).
+    About one prefix-role workgroup per CU, and at least 16 prefix tiles per
+    split.  Best of a same-box sweep on MI355X (sharers x prefix tokens:
+    prefix splits chosen -> cascade vs per-row us/call): 16 x 4096: 8 ->
+    14.2 vs 14.5; 32 x 8192: 8 -> 23.4 vs 32.8; 64 x 16384: 4 -> 50.5 vs
+    96.0; 128 x 16384: 2 -> 88.7 vs 183.0.
     """
     tiles = max(1, -(-max_prefix_len // 32))
-    budget = max(num_cus - tail_blocks, -(-num_cus // 4))
-    want = max(1, -(-budget // max(1, num_groups * num_kv_heads * chunks)))
-    return int(min(want, tiles, 1024))
+    want = max(1, num_cus // max(1, num_groups * num_kv_heads * chunks))
+    return int(min(want, -(-tiles // 16), 1024))
 
 
 def prefix_chunks(groups, num_q_heads, num_kv_heads):
@@ -210,7 +209,7 @@ def paged_decode_attention_cascade_into(
     if prefix_splits is None:
         prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads,
                                            prefix_chunks(groups, num_q_heads, num_kv_heads), groups.max_prefix_len,
-                                           _num_cus(q.device), tail_blocks=num_seqs * num_kv_heads * num_splits)
+                                           _num_cus(q.device))
     for name, v in (("num_splits", num_splits), ("prefix_splits", prefix_splits)):
         if isinstance(v, bool) or not isinstance(v, int) or v <= 0:
             raise ValueError(f"{name} must be a positive integer")

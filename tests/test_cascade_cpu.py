@@ -71,11 +71,10 @@ def test_group_size_bound():
 
 
 def test_prefix_split_plan():
-    # the CUs the tail-role workgroups leave (at least a quarter), at most one
-    # split per 32-token tile
-    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256) == 16
-    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256, tail_blocks=128) == 8
-    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256, tail_blocks=1024) == 4
-    assert cascade.plan_prefix_splits(1, 2, 1, 1024, 256) == 32
+    # about one prefix-role workgroup per CU, at least 16 prefix tiles per split
+    assert cascade.plan_prefix_splits(1, 2, 8, 4096, 256) == 8     # 16 sharers x 4096
+    assert cascade.plan_prefix_splits(1, 2, 16, 8192, 256) == 8    # 32 x 8192
+    assert cascade.plan_prefix_splits(1, 2, 32, 16384, 256) == 4   # 64 x 16384
+    assert cascade.plan_prefix_splits(1, 2, 64, 16384, 256) == 2   # 128 x 16384
     assert cascade.plan_prefix_splits(8, 8, 8, 4096, 256) == 1
     assert cascade.plan_prefix_splits(0, 2, 1, 0, 256) == 1
