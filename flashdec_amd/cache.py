@@ -256,6 +256,17 @@ class PagedKVCache:
         """Mark an active request cancelled and release its private blocks."""
         return self._close_request(request_id, self.CANCELLED)
 
+    def _prefix_groups(self, request_ids):
+        """Rows of ``request_ids`` attached to the same resident prefix, from
+        host state: ``[(rows, prefix_blocks)]`` for prefixes with two or more
+        of them (the rows' tables all lead with the prefix's blocks)."""
+        by_prefix = {}
+        for row, rid in enumerate(request_ids):
+            state = self._require_request(rid)
+            if state.prefix_id is not None and state.shared_block_count > 0:
+                by_prefix.setdefault(state.prefix_id, (state.shared_block_count, []))[1].append(row)
+        return [(rows, blocks) for blocks, rows in by_prefix.values() if len(rows) >= 2]
+
     def _host_seq_lens(self, request_ids):
         """Current lengths of known requests, from host state (no device access)."""
         return [self._require_request(rid).seq_len for rid in request_ids]

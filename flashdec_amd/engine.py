@@ -129,6 +129,7 @@ class _OpenStep:
     last_output: Any | None = None
     state: str = "open"
     ragged: bool = False  # the batch's lengths vary widely: per-row split counts
+    cascade: Any = None  # CascadeGroups: rows sharing a resident prefix decode it once per group
 
 
 def _is_ragged(lengths):
@@ -186,6 +187,13 @@ class DecodeEngine:
         self._open: _OpenStep | None = None
         self._transaction_layer_step_count = 0
         self._transaction_abort_count = 0
+        # Eager steps decode rows attached to one resident prefix with the
+        # shared-prefix (cascade) launch once a group's sharers x prefix tokens
+        # reach this many (None: never).  On MI355X the cascade is at parity
+        # with per-row decode at 16 x 4096 and 1.4x faster at 32 x 8192.
+        self.cascade_min_shared_tokens = 128 * 1024
+        self._cascade_cache = None
+        self._cascade_decode_count = 0
 
     # ------------------------------------------------------------ lifecycle
     def register_prefix(self, prefix_id, k_blocks, v_blocks):
@@ -301,9 +309,44 @@ class DecodeEngine:
         )
         self._sync_cache_version()
         self._bump_state_version()
+        lengths = self.cache._host_seq_lens(ids)
         self._open = _OpenStep(handle=handle, cache_transaction=tx, needed_new_blocks=needed,
-                               ragged=_is_ragged(self.cache._host_seq_lens(ids)))
+                               ragged=_is_ragged(lengths), cascade=self._step_cascade(ids, lengths))
         return handle
+
+    def _step_cascade(self, ids, lengths):
+        """Prefix groups of this step's batch when the shared-prefix decode pays
+        (the eager HIP path), else None.  Device tensors are kept per batch
+        composition; only the planning figures follow the lengths."""
+        if self._decode_kind != "hip" or self.cache.device.type != "cuda" or self.cascade_min_shared_tokens is None:
+            return None
+        groups = self.cache._prefix_groups(ids)
+        bs = self.cache.block_size
+        if not groups or max(len(rows) * blocks * bs for rows, blocks in groups) < self.cascade_min_shared_tokens:
+            return None
+        import dataclasses
+
+        from .cascade import CascadeGroups
+
+        key = (tuple(ids), tuple((tuple(rows), blocks) for rows, blocks in groups))
+        if self._cascade_cache is None or self._cascade_cache[0] != key:
+            torch = _torch()
+            width = max(len(rows) for rows, _ in groups)
+            members = torch.full((len(groups), width), -1, dtype=torch.int32)
+            prefix = torch.zeros(len(groups), dtype=torch.int32)
+            row_prefix = torch.zeros(len(ids), dtype=torch.int32)
+            for g, (rows, blocks) in enumerate(groups):
+                members[g, : len(rows)] = torch.tensor(rows, dtype=torch.int32)
+                prefix[g] = blocks * bs
+                row_prefix[rows] = blocks * bs
+            dev = self.cache.device
+            self._cascade_cache = (key, CascadeGroups(members=members.to(dev), prefix_len=prefix.to(dev),
+                                                      row_prefix_len=row_prefix.to(dev),
+                                                      max_prefix_len=int(prefix.max()), max_tail_len=0,
+                                                      total_tail_len=0), row_prefix.tolist())
+        _, cached, row_prefix = self._cascade_cache
+        tails = [max(0, n + 1 - p) for n, p in zip(lengths, row_prefix)]  # the new token included
+        return dataclasses.replace(cached, max_tail_len=max(tails), total_tail_len=sum(tails))
 
     def step_layer(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0):
         """RoPE + KV write + paged decode for one layer; any error aborts the whole token."""
@@ -600,11 +643,13 @@ class DecodeEngine:
 
     def _decode_layer(self, q_rot, view, meta, layer_idx):
         ragged = self._open is not None and self._open.ragged
+        cascade = self._open.cascade if self._open is not None else None
         if meta is not None:  # the allocator's own copy, not the caller-visible clone
-            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx, ragged=ragged)
-        return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx, ragged=ragged)
+            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx, ragged=ragged, cascade=cascade)
+        return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx, ragged=ragged,
+                            cascade=cascade)
 
-    def _decode(self, q, block_tables, seq_lens, layer_idx=0, ragged=False):
+    def _decode(self, q, block_tables, seq_lens, layer_idx=0, ragged=False, cascade=None):
         layer_idx = int(layer_idx)
         if layer_idx < 0 or layer_idx >= self.cache.num_layers:
             raise ValueError("layer_idx must be in [0, num_layers)")
@@ -613,6 +658,13 @@ class DecodeEngine:
 
             return paged_decode_attention_ref(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx],
                                               block_tables, seq_lens, sm_scale=self.sm_scale)
+        if cascade is not None:
+            from .cascade import paged_decode_attention_cascade
+
+            self._cascade_decode_count += 1
+            return paged_decode_attention_cascade(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx],
+                                                  block_tables, seq_lens, groups=cascade, sm_scale=self.sm_scale,
+                                                  block_size=self.cache.block_size)
         from .paged_decode import paged_decode_attention
 
         return paged_decode_attention(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx], block_tables,
