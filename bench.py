@@ -97,7 +97,7 @@ def algorithmic_bytes(batch, ctx, hq, hkv, d, bs, elt=2):
     return batch * ctx * hkv * d * 2 * elt + 2 * batch * hq * d * elt + 4 * batch * nblk + 4 * batch
 
 
-def prepared_args(pool, sm_scale, block_size, num_kv_heads, ragged=False):
+def prepared_args(pool, sm_scale, block_size, num_kv_heads, ragged=False, kv_reuse=False):
     """The ctypes argument block ``paged_decode_attention_into`` builds for this pool (auto splits)."""
     from flashdec_amd import _lib
     from flashdec_amd import paged_decode as pd
@@ -116,6 +116,7 @@ def prepared_args(pool, sm_scale, block_size, num_kv_heads, ragged=False):
     args.num_blocks = k.shape[0]
     args.max_seq_len = max_seq_len
     args.balance_target = balance
+    args.kv_reuse = 1 if kv_reuse else 0
     acc = mx = sm = None
     if splits > 1:
         acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits, stream)
@@ -319,6 +320,7 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
                     num_kv_heads, block_size, sm_scale)
     args.num_blocks = k.shape[0]
     args.max_seq_len = groups.max_prefix_len + groups.max_tail_len
+    args.kv_reuse = 1  # the cascade's default: plain loads
     pd._fill_workspace(args, acc, mx, sm, splits)
     args.split_acc, args.split_max, args.split_sum = acc.data_ptr(), mx.data_ptr(), sm.data_ptr()
     args.split_acc_stride[:] = acc.stride()
@@ -359,13 +361,16 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
     hq, hkv, d, bs = 16, 2, 128, 32
     sm_scale = 1.0 / math.sqrt(d)
     pools = decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks)
+    # rows sharing a prefix: the per-row path reads K/V with plain, cached
+    # loads (kv_reuse), as a caller that knows its tables share blocks would
+    reuse = prefix_blocks > 0
 
     def fn(i):
         q, k, v, table, sl, out = pools[i % len(pools)]
-        fd.paged_decode_attention_into(q, k, v, table, sl, out, sm_scale=sm_scale)
+        fd.paged_decode_attention_into(q, k, v, table, sl, out, sm_scale=sm_scale, kv_reuse=reuse)
 
     ms = graph_ms_per_call(torch, dev, fn, args.steps)
-    prepared = [prepared_args(p, sm_scale, bs, hkv) for p in pools]
+    prepared = [prepared_args(p, sm_scale, bs, hkv, kv_reuse=reuse) for p in pools]
     attn_us, red_us = attention_kernel_us(torch, prepared, min(4 * len(pools), 96))
     nblk = max((n + bs - 1) // bs for n in lens)
     table_q = 4 * len(lens) * nblk + 4 * len(lens) + 2 * len(lens) * hq * d * 2
@@ -379,7 +384,8 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
                         "GB/s", ms, True,
                         {"workload": name, "batch": len(lens), "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d,
                          "block_size": bs, "seq_lens_sum": sum(lens), "seq_len_max": max(lens),
-                         "prefix_blocks": prefix_blocks, "kv_pools": n_pools, "num_splits": splits})
+                         "prefix_blocks": prefix_blocks, "kv_pools": n_pools, "num_splits": splits,
+                         "kv_loads": "plain (kv_reuse)" if reuse else "non-temporal"})
     out["us_per_call"] = round(ms * 1e3, 3)
     out["roofline"] = {"bound": "hbm", "achieved": round(unique / (attn_us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(unique / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),

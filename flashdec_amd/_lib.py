@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 
 _i64 = ctypes.c_int64
@@ -73,6 +73,7 @@ class PagedDecodeArgs(ctypes.Structure):
         ("slot_mapping_stride", _i64),
         ("timing_events", _vp * 4),
         ("balance_target", _i32),
+        ("kv_reuse", _i32),
     ]
 
 

@@ -183,6 +183,17 @@ constexpr int waves_for() {
 // Physical block ids a unit needs (wave-uniform, so scalar loads); pages are
 // clamped to the table row so the read is in bounds whatever the row's
 // length.  A unit spans one block, or two when the block is half its size.
+// One 16-byte K/V load.  NT: non-temporal, for K/V that a launch reads once
+// (streamed past the caches: a 550 MB read runs at 6.8 instead of 6.1 TB/s
+// on MI355X); plain loads where rows re-read shared blocks.
+template <bool NT>
+__device__ __forceinline__ u32x4 kv_load(const void* a) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
+  else
+    return *reinterpret_cast<const u32x4*>(a);
+}
+
 struct UnitPages {
   int32_t a, b;
 };
@@ -204,7 +215,7 @@ __device__ __forceinline__ UnitPages fetch_pages(const DecodeParams& p, int b, i
   return up;
 }
 
-template <typename T, int BS, int UNIT>
+template <typename T, int BS, int UNIT, bool NT>
 __device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int unit, const UnitPages& up, int c,
                                           int g, UnitRegs<UNIT>& t) {
   const T* kbase = static_cast<const T*>(p.k);
@@ -222,7 +233,7 @@ __device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int un
     const int64_t off = ok ? blk * p.ks0 + kvh * p.ks1 + row_in_block(tt) * p.ks2 : 0;
     const T* row = kbase + off;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) t.kf[mt][s] = *reinterpret_cast<const u32x4*>(row + 32 * s + 8 * g);
+    for (int s = 0; s < 4; ++s) t.kf[mt][s] = kv_load<NT>(row + 32 * s + 8 * g);
   }
   // V rows vrow(g, i)
   uint32_t bm = 0;
@@ -233,7 +244,7 @@ __device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int un
     const bool ok = blk >= 0 && blk < p.num_blocks;
     const int64_t off = ok ? blk * p.vs0 + kvh * p.vs1 + row_in_block(tt) * p.vs2 : 0;
     bm |= ok ? (1u << i) : 0u;
-    t.vf[i] = *reinterpret_cast<const u32x4*>(vbase + off + 8 * c);
+    t.vf[i] = kv_load<NT>(vbase + off + 8 * c);
   }
   t.bmask = bm;
 }
@@ -271,7 +282,7 @@ __device__ __forceinline__ UnitOffsets<UNIT> unit_offsets(const DecodeParams& p,
 // first, the rest in the second), so a row's address is a uniform block base
 // (scalar) plus the lane's fixed 32-bit offset -- no per-unit vector
 // address arithmetic.
-template <typename T, int BS, int UNIT>
+template <typename T, int BS, int UNIT, bool NT>
 __device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const UnitPages& up,
                                                 const UnitOffsets<UNIT>& o, UnitRegs<UNIT>& t) {
   static_assert(BS >= 16, "a 16-token row group must lie in one block");
@@ -287,13 +298,13 @@ __device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const Uni
   for (int mt = 0; mt < UnitRegs<UNIT>::MT; ++mt) {
     const char* base = (kTwo && mt == 1) ? kb : ka;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) t.kf[mt][s] = *reinterpret_cast<const u32x4*>(base + o.k[mt] + 64 * s);
+    for (int s = 0; s < 4; ++s) t.kf[mt][s] = kv_load<NT>(base + o.k[mt] + 64 * s);
   }
   uint32_t bm = 0;
 #pragma unroll
   for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
     const bool second = kTwo && i >= 4;  // V rows 16 + 4g + (i - 4)
-    t.vf[i] = *reinterpret_cast<const u32x4*>((second ? vb : va) + o.v[i]);
+    t.vf[i] = kv_load<NT>((second ? vb : va) + o.v[i]);
     bm |= (second ? okb : oka) ? (1u << i) : 0u;
   }
   t.bmask = bm;
@@ -600,7 +611,7 @@ struct alignas(16) DecodeLds {
   int last;
 };
 
-template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, Role ROLE>
+template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, Role ROLE, bool NT>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
                                             DecodeLds<waves_for<UNIT>()>& lds) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
@@ -718,11 +729,14 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   UnitRegs<UNIT> cur;
   [[maybe_unused]] UnitOffsets<UNIT> offs;
   if constexpr (kFixed) offs = unit_offsets<T, BS, UNIT>(p, kvh, wave, c, g);
+  // the prefix role's blocks are read again by the group's other chunks:
+  // plain loads, so the re-reads hit the caches
+  constexpr bool kNT = NT && !PREFIX;
   auto load = [&](int u, const UnitPages& up, UnitRegs<UNIT>& dst) {
     if constexpr (kFixed)
-      load_unit_fixed<T, BS, UNIT>(p, up, offs, dst);
+      load_unit_fixed<T, BS, UNIT, kNT>(p, up, offs, dst);
     else
-      load_unit<T, BS, UNIT>(p, kvh, u, up, c, g, dst);
+      load_unit<T, BS, UNIT, kNT>(p, kvh, u, up, c, g, dst);
   };
   load(unit, pages, cur);
 
@@ -935,30 +949,30 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
 }
 
-template <typename T, int BS, bool FUSE, bool MERGE, int UNIT>
+template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, bool NT>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
-  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow>(p, CascadeParams{}, blockIdx.x, lds);
+  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT>(p, CascadeParams{}, blockIdx.x, lds);
 }
 
 // Balanced splits (ragged batches): the row and split of each workgroup come
 // from the batch's lengths on the device.
-template <typename T, int BS>
+template <typename T, int BS, bool NT>
 __global__ __launch_bounds__(64 * waves_for<16>(), 1) void decode_balanced_kernel(DecodeParams p) {
   __shared__ DecodeLds<waves_for<16>()> lds;
-  decode_role<T, BS, false, false, 16, Role::kBalanced>(p, CascadeParams{}, blockIdx.x, lds);
+  decode_role<T, BS, false, false, 16, Role::kBalanced, NT>(p, CascadeParams{}, blockIdx.x, lds);
 }
 
 // Cascade launch: workgroups [0, prefix_blocks) take the prefix role, the
 // rest the tail role (both write split partials; the reducer merges them).
-template <typename T, int BS, int UNIT>
+template <typename T, int BS, int UNIT, bool NT>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void cascade_decode_kernel(DecodeParams p,
                                                                                     CascadeParams cp) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
   if (static_cast<int>(blockIdx.x) < cp.prefix_blocks)
-    decode_role<T, BS, false, false, UNIT, Role::kPrefix>(p, cp, blockIdx.x, lds);
+    decode_role<T, BS, false, false, UNIT, Role::kPrefix, NT>(p, cp, blockIdx.x, lds);
   else
-    decode_role<T, BS, false, false, UNIT, Role::kTail>(p, cp, blockIdx.x - cp.prefix_blocks, lds);
+    decode_role<T, BS, false, false, UNIT, Role::kTail, NT>(p, cp, blockIdx.x - cp.prefix_blocks, lds);
 }
 
 // ====================================================== generic path ====
@@ -1282,20 +1296,20 @@ void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, 
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
 }
 
-template <typename T, int BS, int UNIT>
+template <typename T, int BS, int UNIT, bool NT>
 void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
   const bool merge = p.counters != nullptr;
   const dim3 block(64 * waves_for<UNIT>());
   if (p.fuse) {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, true, true, UNIT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, true, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
     else
-      dispatch(decode_mfma_kernel<T, BS, true, false, UNIT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, true, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
   } else {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, false, true, UNIT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, false, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
     else
-      dispatch(decode_mfma_kernel<T, BS, false, false, UNIT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, false, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
   }
 }
 
@@ -1303,15 +1317,23 @@ void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void
 // (C2: 4 tiles per split, 6.4 vs 6.7 us), 16-token units on eight waves for
 // longer splits (ragged B32: 70 -> 60 us; C5 layer: 97 -> 93 us).  8-token
 // blocks always take 16-token units (a unit spans at most two blocks).
-template <typename T, int BS>
+template <typename T, int BS, bool NT>
 void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
   if constexpr (BS >= 16) {
     if (p.hint_tps <= kWideUnitMaxTiles) {
-      launch_mfma_unit<T, BS, 32>(p, grid, stream, ev);
+      launch_mfma_unit<T, BS, 32, NT>(p, grid, stream, ev);
       return;
     }
   }
-  launch_mfma_unit<T, BS, 16>(p, grid, stream, ev);
+  launch_mfma_unit<T, BS, 16, NT>(p, grid, stream, ev);
+}
+
+template <typename T, int BS>
+void launch_mfma(const DecodeParams& p, bool nt, dim3 grid, hipStream_t stream, void* const* ev) {
+  if (nt)
+    launch_mfma<T, BS, true>(p, grid, stream, ev);
+  else
+    launch_mfma<T, BS, false>(p, grid, stream, ev);
 }
 
 ReduceParams reduce_params(const DecodeParams& p) {
@@ -1364,6 +1386,7 @@ template <typename T>
 int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
   const bool fast = fast_path_ok(a, p.group);
+  const bool nt = a.kv_reuse == 0;  // stream K/V past the caches
   // the in-launch merge exists only in the MFMA kernel and writes the
   // workspace with 8-byte stores (unit dim stride, 8-byte aligned rows)
   if (!fast || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
@@ -1379,16 +1402,25 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
     const dim3 block(64 * waves_for<16>());
     void* const* ev = a.timing_events;
     switch (a.block_size) {
-      case 8: dispatch(decode_balanced_kernel<T, 8>, grid, block, stream, ev[0], ev[1], p); break;
-      case 16: dispatch(decode_balanced_kernel<T, 16>, grid, block, stream, ev[0], ev[1], p); break;
-      default: dispatch(decode_balanced_kernel<T, 32>, grid, block, stream, ev[0], ev[1], p); break;
+      case 8:
+        nt ? dispatch(decode_balanced_kernel<T, 8, true>, grid, block, stream, ev[0], ev[1], p)
+           : dispatch(decode_balanced_kernel<T, 8, false>, grid, block, stream, ev[0], ev[1], p);
+        break;
+      case 16:
+        nt ? dispatch(decode_balanced_kernel<T, 16, true>, grid, block, stream, ev[0], ev[1], p)
+           : dispatch(decode_balanced_kernel<T, 16, false>, grid, block, stream, ev[0], ev[1], p);
+        break;
+      default:
+        nt ? dispatch(decode_balanced_kernel<T, 32, true>, grid, block, stream, ev[0], ev[1], p)
+           : dispatch(decode_balanced_kernel<T, 32, false>, grid, block, stream, ev[0], ev[1], p);
+        break;
     }
   } else if (fast) {
     const dim3 grid(static_cast<unsigned>(pairs * p.splits));
     switch (a.block_size) {
-      case 8: launch_mfma<T, 8>(p, grid, stream, a.timing_events); break;
-      case 16: launch_mfma<T, 16>(p, grid, stream, a.timing_events); break;
-      default: launch_mfma<T, 32>(p, grid, stream, a.timing_events); break;
+      case 8: launch_mfma<T, 8>(p, nt, grid, stream, a.timing_events); break;
+      case 16: launch_mfma<T, 16>(p, nt, grid, stream, a.timing_events); break;
+      default: launch_mfma<T, 32>(p, nt, grid, stream, a.timing_events); break;
     }
   } else {
     const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
@@ -1413,17 +1445,28 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
 
 // Cascade: one launch of prefix- and tail-role workgroups, then the reducer
 // over tail + prefix partials.  The attention timing events bracket it.
-template <typename T, int BS>
+template <typename T, int BS, bool NT>
 void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, int64_t pairs, hipStream_t stream,
                            void* const* ev) {
   const dim3 grid(static_cast<unsigned>(cp.prefix_blocks + pairs * p.splits));
   if constexpr (BS >= 16) {
     if (p.hint_tps <= kWideUnitMaxTiles && cp.hint_ptps <= kWideUnitMaxTiles) {
-      dispatch(cascade_decode_kernel<T, BS, 32>, grid, dim3(64 * waves_for<32>()), stream, ev[0], ev[1], p, cp);
+      dispatch(cascade_decode_kernel<T, BS, 32, NT>, grid, dim3(64 * waves_for<32>()), stream, ev[0], ev[1], p,
+               cp);
       return;
     }
   }
-  dispatch(cascade_decode_kernel<T, BS, 16>, grid, dim3(64 * waves_for<16>()), stream, ev[0], ev[1], p, cp);
+  dispatch(cascade_decode_kernel<T, BS, 16, NT>, grid, dim3(64 * waves_for<16>()), stream, ev[0], ev[1], p, cp);
+}
+
+// NT applies to the tail role; the prefix role always uses plain loads
+template <typename T, int BS>
+void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, bool nt, int64_t pairs,
+                           hipStream_t stream, void* const* ev) {
+  if (nt)
+    launch_cascade_kernel<T, BS, true>(p, cp, pairs, stream, ev);
+  else
+    launch_cascade_kernel<T, BS, false>(p, cp, pairs, stream, ev);
 }
 
 template <typename T>
@@ -1431,9 +1474,9 @@ int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const C
                    hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
   switch (a.block_size) {
-    case 8: launch_cascade_kernel<T, 8>(p, cp, pairs, stream, a.timing_events); break;
-    case 16: launch_cascade_kernel<T, 16>(p, cp, pairs, stream, a.timing_events); break;
-    default: launch_cascade_kernel<T, 32>(p, cp, pairs, stream, a.timing_events); break;
+    case 8: launch_cascade_kernel<T, 8>(p, cp, a.kv_reuse == 0, pairs, stream, a.timing_events); break;
+    case 16: launch_cascade_kernel<T, 16>(p, cp, a.kv_reuse == 0, pairs, stream, a.timing_events); break;
+    default: launch_cascade_kernel<T, 32>(p, cp, a.kv_reuse == 0, pairs, stream, a.timing_events); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "cascade decode launch failed: %s", hipGetErrorString(e));
@@ -1602,6 +1645,7 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
   if (a.num_kv_heads * (a.balance_target + a.num_seqs) > 0x7fffffffLL)
     return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
   p.bal_target = a.balance_target;
+  if (a.kv_reuse != 0 && a.kv_reuse != 1) return set_error(FD_E_INVALID, "%s: kv_reuse must be 0 or 1", fn);
   {
     // first-tile guess of the MFMA kernel: from max_seq_len when given, else
     // from the table width; each row's split range uses its own length

@@ -118,6 +118,7 @@ class DecodeStepGraph:
     metadata: Any
     workspace: Any = None  # split partials (and merge counters) the graph uses, kept alive with it
     balance_target: int = 0  # > 0: per-row split counts from the lengths at replay
+    kv_reuse: bool = False  # rows shared prefix blocks at capture: plain (cached) K/V loads
 
 
 @dataclass
@@ -130,6 +131,7 @@ class _OpenStep:
     state: str = "open"
     ragged: bool = False  # the batch's lengths vary widely: per-row split counts
     cascade: Any = None  # CascadeGroups: rows sharing a resident prefix decode it once per group
+    kv_reuse: bool = False  # rows share prefix blocks (per-row path): plain, cached K/V loads
 
 
 def _is_ragged(lengths):
@@ -310,17 +312,19 @@ class DecodeEngine:
         self._sync_cache_version()
         self._bump_state_version()
         lengths = self.cache._host_seq_lens(ids)
+        groups = self.cache._prefix_groups(ids)
+        cascade = self._step_cascade(ids, lengths, groups)
         self._open = _OpenStep(handle=handle, cache_transaction=tx, needed_new_blocks=needed,
-                               ragged=_is_ragged(lengths), cascade=self._step_cascade(ids, lengths))
+                               ragged=_is_ragged(lengths), cascade=cascade,
+                               kv_reuse=bool(groups) and cascade is None)
         return handle
 
-    def _step_cascade(self, ids, lengths):
+    def _step_cascade(self, ids, lengths, groups):
         """Prefix groups of this step's batch when the shared-prefix decode pays
         (the eager HIP path), else None.  Device tensors are kept per batch
         composition; only the planning figures follow the lengths."""
         if self._decode_kind != "hip" or self.cache.device.type != "cuda" or self.cascade_min_shared_tokens is None:
             return None
-        groups = self.cache._prefix_groups(ids)
         bs = self.cache.block_size
         if not groups or max(len(rows) * blocks * bs for rows, blocks in groups) < self.cascade_min_shared_tokens:
             return None
@@ -413,7 +417,7 @@ class DecodeEngine:
         return self._abort_open_step(self._require_open_step(transaction))
 
     def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None,
-                           merge=False):
+                           merge=False, kv_reuse=None):
         """Capture every layer's launches of one token step into a hipGraph.
 
         Needs the HIP backends, a GPU cache and its graph-metadata arena
@@ -425,7 +429,9 @@ class DecodeEngine:
         range follows its own length at replay, so growing sequences stay
         correct.  ``merge=True`` merges the split partials inside the attention
         launch (the last workgroup of each request and KV head), so each layer
-        runs two kernels instead of three.
+        runs two kernels instead of three.  ``kv_reuse`` (default: whether
+        active requests share a resident prefix now) reads K/V with plain,
+        cached loads instead of streaming them.
         """
         torch = _torch()
         from . import _lib
@@ -453,6 +459,9 @@ class DecodeEngine:
         q_rot = torch.zeros_like(q)
         out = torch.zeros_like(q)
         width = meta.block_tables.shape[1]
+        if kv_reuse is None:
+            kv_reuse = bool(cache._prefix_groups(self.active_request_ids()))
+        kv_reuse = bool(kv_reuse)
         balance = 0
         if num_splits is None:
             # the batch's current lengths tell a uniform batch from a ragged one
@@ -497,11 +506,12 @@ class DecodeEngine:
                     _decode_with_workspace(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
                                            meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
                                            cache.block_size, splits, workspace[:3] if workspace else None,
-                                           cache.max_blocks, balance_target=balance, counters=counters)
+                                           cache.max_blocks, balance_target=balance, counters=counters,
+                                           kv_reuse=kv_reuse)
         torch.cuda.current_stream(dev).wait_stream(side)
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
                                num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,
-                               workspace=workspace, balance_target=balance)
+                               workspace=workspace, balance_target=balance, kv_reuse=kv_reuse)
 
     def step_graph(self, transaction, step_graph):
         """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.
@@ -644,12 +654,14 @@ class DecodeEngine:
     def _decode_layer(self, q_rot, view, meta, layer_idx):
         ragged = self._open is not None and self._open.ragged
         cascade = self._open.cascade if self._open is not None else None
+        kv_reuse = self._open is not None and self._open.kv_reuse
         if meta is not None:  # the allocator's own copy, not the caller-visible clone
-            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx, ragged=ragged, cascade=cascade)
+            return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx, ragged=ragged, cascade=cascade,
+                                kv_reuse=kv_reuse)
         return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx, ragged=ragged,
-                            cascade=cascade)
+                            cascade=cascade, kv_reuse=kv_reuse)
 
-    def _decode(self, q, block_tables, seq_lens, layer_idx=0, ragged=False, cascade=None):
+    def _decode(self, q, block_tables, seq_lens, layer_idx=0, ragged=False, cascade=None, kv_reuse=False):
         layer_idx = int(layer_idx)
         if layer_idx < 0 or layer_idx >= self.cache.num_layers:
             raise ValueError("layer_idx must be in [0, num_layers)")
@@ -669,7 +681,8 @@ class DecodeEngine:
 
         return paged_decode_attention(q, self.cache.k_cache[layer_idx], self.cache.v_cache[layer_idx], block_tables,
                                       seq_lens, sm_scale=self.sm_scale, block_size=self.cache.block_size,
-                                      num_warps=self.num_warps, num_stages=self.num_stages, ragged=ragged)
+                                      num_warps=self.num_warps, num_stages=self.num_stages, ragged=ragged,
+                                      kv_reuse=kv_reuse)
 
     def _abort_open_step(self, state):
         if self._open is not state or state.state != "open":

@@ -221,6 +221,7 @@ def paged_decode_attention(
     kv_layout="token_major",
     num_stages=None,
     ragged=False,
+    kv_reuse=False,
 ):
     """Return paged single-token decode attention (``flashdec.decode``).
 
@@ -229,8 +230,8 @@ def paged_decode_attention(
     ``[num_blocks, num_kv_heads, head_dim, block_size]``); block_tables
     ``[num_seqs, max_blocks_per_seq]``; seq_lens ``[num_seqs]``.  Returns
     ``[num_seqs, num_q_heads, head_dim]`` in q.dtype.  block_size is inferred
-    from the cache when omitted (paged_decode.py:950-955).  ``ragged``: see
-    :func:`paged_decode_attention_into`.
+    from the cache when omitted (paged_decode.py:950-955).  ``ragged`` and
+    ``kv_reuse``: see :func:`paged_decode_attention_into`.
     """
     token_axis, _ = _layout_axes(kv_layout)
     if block_size is None:
@@ -253,6 +254,7 @@ def paged_decode_attention(
         kv_layout=kv_layout,
         num_stages=num_stages,
         ragged=ragged,
+        kv_reuse=kv_reuse,
     )
 
 
@@ -274,6 +276,7 @@ def paged_decode_attention_into(
     append_v=None,
     slot_mapping=None,
     ragged=False,
+    kv_reuse=False,
 ):
     """Write paged decode attention into ``out`` (no output allocation).
 
@@ -288,6 +291,12 @@ def paged_decode_attention_into(
     (``balance_target`` of the C ABI).  It applies without fused append and
     without a caller workspace, and only where the batch leaves room in one
     round of workgroups; elsewhere it changes nothing.
+
+    ``kv_reuse=True`` (no counterpart in the reference) says that rows share
+    cache blocks (a common prefix in several rows' tables): K/V are then read
+    with plain loads, so re-reads hit the caches.  By default each K/V row is
+    assumed to be read once per call and is streamed with non-temporal loads.
+    The result is the same either way.
     """
     token_axis, dim_axis = _layout_axes(kv_layout)
     if block_size is None:
@@ -387,6 +396,7 @@ def paged_decode_attention_into(
     args.num_blocks = k_cache.shape[0]
     args.max_seq_len = max_seq_len
     args.balance_target = balance
+    args.kv_reuse = 1 if kv_reuse else 0
     _fill_workspace(args, split_acc, split_max, split_sum, num_splits, counters)
     if fuse_kv_append:
         _fill_append(args, append_k, append_v, slot_mapping)
@@ -395,7 +405,7 @@ def paged_decode_attention_into(
 
 
 def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_splits,
-                           workspace, num_blocks, balance_target=0, counters=None):
+                           workspace, num_blocks, balance_target=0, counters=None, kv_reuse=False):
     """Unchecked launch on a token-major cache with a caller-held split workspace (graph capture).
 
     ``workspace`` is ``(acc [B, Hq, S, D], max [B, Hq, S], sum [B, Hq, S])`` or
@@ -403,7 +413,8 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     ``balance_target`` > 0 selects per-row split counts (at most
     ``num_splits``) computed on the device from ``seq_lens``.  ``counters``
     (zeroed int32, ``B * Hkv * SPLIT_COUNTER_STRIDE``) selects the in-launch
-    merge: one dispatch, no reducer kernel.
+    merge: one dispatch, no reducer kernel.  ``kv_reuse``: plain instead of
+    non-temporal K/V loads (rows share blocks).
     """
     num_kv_heads = k_cache.shape[1]
     if sm_scale is None:
@@ -414,6 +425,7 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     args.num_blocks = num_blocks
     args.max_seq_len = block_tables.shape[1] * block_size
     args.balance_target = int(balance_target)
+    args.kv_reuse = 1 if kv_reuse else 0
     acc, mx, sm = workspace if workspace is not None else (None, None, None)
     _fill_workspace(args, acc, mx, sm, int(num_splits), counters)
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))
@@ -442,6 +454,7 @@ def _vllm_paged_decode_attention_into(
     num_splits,
     split_counters=None,
     max_seq_len=None,
+    kv_reuse=False,
 ):
     """Checked-by-caller vLLM launcher (paged_decode.py:728-919).
 
@@ -457,7 +470,9 @@ def _vllm_paged_decode_attention_into(
     the one launch; ``max_seq_len`` (a hint such as vLLM's
     ``attn_metadata.max_seq_len``; any value is correct) lets the first
     tile's block-table and K/V reads of rows that long start before
-    ``seq_lens`` arrives.
+    ``seq_lens`` arrives.  ``kv_reuse`` (rows share cache blocks, as with
+    prefix caching) reads K/V with plain, cached loads instead of streaming
+    them.
     """
     sb, sp, st, sh, sd = kv_cache.stride()
     plane_bytes = sp * kv_cache.element_size()
@@ -487,6 +502,7 @@ def _vllm_paged_decode_attention_into(
     args.out_stride[:] = out.stride()
     args.sm_scale = float(sm_scale)
     args.max_seq_len = int(max_seq_len) if max_seq_len else 0
+    args.kv_reuse = 1 if kv_reuse else 0
     _fill_workspace(args, split_acc, split_max, split_sum, int(num_splits), split_counters)
     _fill_append(args, append_k, append_v, slot_mapping)
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))

@@ -50,6 +50,13 @@ def _parse_requested_splits(value: str) -> int:
     return requested
 
 
+def _parse_kv_reuse(value: str) -> bool:
+    """``FLASHDEC_VLLM_KV_REUSE`` -> plain (cached) K/V loads; no counterpart in the reference."""
+    if value not in ("0", "1"):
+        raise ValueError("FLASHDEC_VLLM_KV_REUSE must be 0 or 1")
+    return value == "1"
+
+
 def _select_num_splits(requested_splits: int, *, num_reqs: int, num_kv_heads: int, logical_blocks: int,
                        target_programs: int = _REFERENCE_TARGET_PROGRAMS) -> int:
     """Split count: the power of two whose program count is nearest the target, capped by the context."""
@@ -96,6 +103,9 @@ class FlashDecAttentionImpl(TritonAttentionImpl):
     def __init__(self, *args, **kwargs) -> None:
         super().__init__(*args, **kwargs)
         self._requested_splits = _parse_requested_splits(os.environ.get("FLASHDEC_VLLM_NUM_SPLITS", "0"))
+        # "1" when requests share cache blocks (prefix caching with common
+        # prompts): K/V re-reads then come from the caches instead of HBM
+        self._kv_reuse = _parse_kv_reuse(os.environ.get("FLASHDEC_VLLM_KV_REUSE", "0"))
 
     def _supports_flashdec_decode(self, query, key, value, kv_cache, attn_metadata, output, output_scale,
                                   output_block_scale) -> bool:
@@ -166,5 +176,6 @@ class FlashDecAttentionImpl(TritonAttentionImpl):
             sm_scale=self.scale,
             num_splits=num_splits,
             max_seq_len=attn_metadata.max_seq_len,
+            kv_reuse=self._kv_reuse,
         )
         return output

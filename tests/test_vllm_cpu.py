@@ -89,7 +89,7 @@ def test_eligible_decode_passes_vllm_tensors_to_the_hip_launcher(vb, monkeypatch
                      md.softmax_segm_max, md.softmax_segm_expsum)
     assert len(args) == len(expected_args) and all(a is b for a, b in zip(args, expected_args))
     assert kwargs == {"num_reqs": 3, "num_q_heads": 16, "num_kv_heads": 2, "head_dim": 128, "block_size": 16,
-                      "sm_scale": 128 ** -0.5, "num_splits": 16, "max_seq_len": max_seq_len}
+                      "sm_scale": 128 ** -0.5, "num_splits": 16, "max_seq_len": max_seq_len, "kv_reuse": False}
     assert vllm_fakes.TritonAttentionImpl.fallback_calls == []
 
 
@@ -163,6 +163,23 @@ def test_invalid_split_environment_rejected_at_construction(vb, monkeypatch, val
 def test_valid_split_environment(vb, monkeypatch, value):
     monkeypatch.setenv("FLASHDEC_VLLM_NUM_SPLITS", value)
     assert make_impl(vb)._requested_splits == int(value)
+
+
+@pytest.mark.parametrize("value,expected", [("0", False), ("1", True)])
+def test_kv_reuse_environment_reaches_the_launcher(vb, monkeypatch, value, expected):
+    monkeypatch.setenv("FLASHDEC_VLLM_KV_REUSE", value)
+    calls = record_launches(vb, monkeypatch)
+    q, k, v, cache, out = tensors()
+    make_impl(vb).forward(owning_layer(), q, k, v, cache, metadata(), out)
+    (_, kwargs), = calls
+    assert kwargs["kv_reuse"] is expected
+
+
+@pytest.mark.parametrize("value", ["", "yes", "2", "true"])
+def test_invalid_kv_reuse_environment_rejected_at_construction(vb, monkeypatch, value):
+    monkeypatch.setenv("FLASHDEC_VLLM_KV_REUSE", value)
+    with pytest.raises(ValueError, match="FLASHDEC_VLLM_KV_REUSE must be 0 or 1"):
+        make_impl(vb)
 
 
 def test_reference_split_policy_is_the_default_target(vb):
