@@ -493,7 +493,8 @@ def run_engine(torch, dev, args):
 
     layers, batch, hq, hkv, d, bs, ctx = 36, 64, 16, 2, 128, 32, 8192
     steps = args.engine_steps
-    width = (ctx + steps + 2 + bs - 1) // bs
+    # room for the warm-ups, the timed steps and the separate-RoPE comparison steps
+    width = (ctx + 2 * 20 + steps + max(10, steps // 2) + 2 + bs - 1) // bs
     cache = PagedKVCache(layers, hkv, d, bs, max_blocks=batch * width, dtype=torch.bfloat16, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(109)
@@ -532,7 +533,10 @@ def run_engine(torch, dev, args):
         after = (cache.num_used_blocks, cache.seq_lens_tensor(ids).cpu())
         return before[0] == after[0] and torch.equal(before[1], after[1])
 
-    for _ in range(3):
+    # warm-up: the host runs ahead of the replays, so the first steps also
+    # grow the pinned staging pool of the per-step metadata copies
+    warm = 20
+    for _ in range(warm):
         graph_step()
     torch.cuda.synchronize()
     committed = 0
@@ -553,6 +557,32 @@ def run_engine(torch, dev, args):
     wall_s = time.perf_counter() - t0
     device_ms = start.elapsed_time(stop)
     ms_per_step = device_ms / steps
+    separate = None
+    if sg.fused_rope:
+        # the same steps with RoPE + append as its own kernel per layer
+        sg_sep = engine.capture_step_graph(batch, hq, base=1e6, fuse_rope=False)
+        sg_sep.q.copy_(sg.q)
+        sg_sep.k.copy_(sg.k)
+        sg_sep.v.copy_(sg.v)
+
+        def graph_step_sep():
+            tx_ = engine.begin_step(ids)
+            engine.step_graph(tx_, sg_sep)
+            engine.commit_step(tx_)
+
+        n_sep = max(10, steps // 2)
+        for _ in range(warm):
+            graph_step_sep()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(n_sep):
+            graph_step_sep()
+        stop.record()
+        torch.cuda.synchronize()
+        separate = start.elapsed_time(stop) / n_sep
+        committed_sep = n_sep + warm
+    else:
+        committed_sep = 0
     # per-layer attention kernel, measured on the same shapes through the timing hook
     from flashdec_amd import paged_decode as pd
 
@@ -560,18 +590,25 @@ def run_engine(torch, dev, args):
     meta = cache.graph_metadata(batch)  # this transaction's metadata lives in the arena
     prepared = []
     for layer in range(4):
+        # the launch the graph replays: with fused RoPE the raw q and this
+        # step's K/V row (stored to its slot, which the abort below frees)
         args_ = pd._lib.PagedDecodeArgs()
-        pd._fill_common(args_, sg.q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
+        q_in = sg.q[layer] if sg.fused_rope else sg.q_rot[layer]
+        pd._fill_common(args_, q_in, cache.k_cache[layer], cache.v_cache[layer],
                         pd._cache_strides(cache.k_cache[layer], 2, 3), pd._cache_strides(cache.v_cache[layer], 2, 3),
                         meta.block_tables, meta.eff_lens, sg.out[layer], hkv, bs, 1.0 / math.sqrt(d))
         args_.num_blocks = cache.max_blocks
         args_.max_seq_len = width * bs
-        acc, mx, sm, _ = pd._auto_workspace(sg.q_rot[layer], hkv, sg.num_splits, pd._lib.current_stream_handle(dev))
+        acc, mx, sm, _ = pd._auto_workspace(q_in, hkv, sg.num_splits, pd._lib.current_stream_handle(dev))
         pd._fill_workspace(args_, acc, mx, sm, sg.num_splits)
+        if sg.fused_rope:
+            pd._fill_append(args_, sg.k[layer], sg.v[layer], meta.slots)
+            args_.rotary_dim = sg.rotary_dim
+            args_.rope_base = sg.base
         prepared.append((args_, pd._lib.current_stream_handle(dev)))
     attn_us, red_us = attention_kernel_us(torch, prepared, 16)
     engine.abort_step(tx)
-    kv_layer = (ctx + committed) * batch * hkv * d * 2 * 2  # K+V bytes one layer's decode reads at the end
+    kv_layer = (ctx + warm + committed + committed_sep) * batch * hkv * d * 2 * 2  # K+V bytes one layer's decode reads at the end
     log(f"[bench] engine: {ms_per_step:.3f} ms/step over {steps} steps ({committed} committed, {aborts} aborted, "
         f"{rollbacks_ok} clean rollbacks); wall {wall_s * 1e3 / steps:.3f} ms/step; attention kernel {attn_us:.1f} us"
         f" per layer, reducer {red_us:.2f} us")
@@ -580,10 +617,15 @@ def run_engine(torch, dev, args):
                         {"workload": "engine-36l-b64-ctx8192", "layers": layers, "batch": batch, "context": ctx,
                          "steps": steps, "committed_steps": committed, "aborted_steps": aborts,
                          "clean_rollbacks": rollbacks_ok, "num_splits": sg.num_splits,
+                         "fused_rope": sg.fused_rope, "kernels_per_layer": 2 if sg.fused_rope else 3,
                          "timing": "events around the whole loop; graph-replayed steps, eager abort steps"})
     out["steps"] = steps
     out["tokens_per_s"] = round(committed * batch / (device_ms * 1e-3), 1)
     out["wall_ms_per_step"] = round(wall_s * 1e3 / steps, 4)
+    if separate is not None:
+        out["separate_rope_kernel_path"] = {"ms_per_step": round(separate, 4), "kernels_per_layer": 3,
+                                            "steps": committed_sep - 1}
+        log(f"[bench] engine: RoPE + append as its own kernel: {separate:.3f} ms/step")
     out["roofline"] = {"bound": "hbm", "kernel_us_mean": round(attn_us, 2), "reducer_us_mean": round(red_us, 3),
                        "algorithmic_bytes_per_layer": kv_layer,
                        "achieved": round(kv_layer / (attn_us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

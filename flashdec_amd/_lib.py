@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 
 _i64 = ctypes.c_int64
@@ -74,6 +74,8 @@ class PagedDecodeArgs(ctypes.Structure):
         ("timing_events", _vp * 4),
         ("balance_target", _i32),
         ("kv_reuse", _i32),
+        ("rotary_dim", _i32),
+        ("rope_base", ctypes.c_double),
     ]
 
 

@@ -62,20 +62,21 @@ class KVTokenTransactionView:
 
 
 def _meta_nbytes(capacity, width):
-    return 24 * capacity + 4 * capacity * (1 + width)
+    return 32 * capacity + 4 * capacity * (1 + width)
 
 
 class _DeviceMeta:
     """Transaction metadata resident on the cache device (one packed buffer).
 
     Layout for ``capacity`` rows (bytes): int64 positions[cap] | int64
-    block_ids[cap] | int64 offsets[cap] | int32 effective_seq_lens[cap] |
-    int32 block_tables[cap, width].  The views cover the first ``batch`` rows,
-    so a buffer laid out for a fixed capacity keeps every view's address
-    whatever the batch (the graph-metadata arena).
+    block_ids[cap] | int64 offsets[cap] | int64 slots[cap] (block_id *
+    block_size + offset, the fused-append slot) | int32
+    effective_seq_lens[cap] | int32 block_tables[cap, width].  The views
+    cover the first ``batch`` rows, so a buffer laid out for a fixed capacity
+    keeps every view's address whatever the batch (the graph-metadata arena).
     """
 
-    __slots__ = ("buf", "capacity", "positions", "block_ids", "offsets", "eff_lens", "block_tables")
+    __slots__ = ("buf", "capacity", "positions", "block_ids", "offsets", "slots", "eff_lens", "block_tables")
 
     def __init__(self, buf, batch, width, capacity=None):
         import torch
@@ -83,16 +84,17 @@ class _DeviceMeta:
         capacity = batch if capacity is None else capacity
         self.buf = buf
         self.capacity = capacity
-        i64 = buf[: 24 * capacity].view(torch.int64)
+        i64 = buf[: 32 * capacity].view(torch.int64)
         self.positions = i64[:batch]
         self.block_ids = i64[capacity : capacity + batch]
         self.offsets = i64[2 * capacity : 2 * capacity + batch]
-        i32 = buf[24 * capacity : _meta_nbytes(capacity, width)].view(torch.int32)
+        self.slots = i64[3 * capacity : 3 * capacity + batch]
+        i32 = buf[32 * capacity : _meta_nbytes(capacity, width)].view(torch.int32)
         self.eff_lens = i32[:batch]
         self.block_tables = i32[capacity : capacity + batch * width].view(batch, width)
 
     @classmethod
-    def build(cls, device, positions, locations, table_rows, width, arena=None):
+    def build(cls, device, positions, locations, table_rows, width, block_size, arena=None):
         """Pack on the host and copy once (pinned staging for GPU caches).
 
         With ``arena`` (a device buffer laid out for ``arena_capacity`` rows of
@@ -108,11 +110,12 @@ class _DeviceMeta:
         pinned = device.type == "cuda"
         host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=pinned)
         arr = host.numpy()
-        i64 = arr[: 24 * capacity].view(np.int64)
+        i64 = arr[: 32 * capacity].view(np.int64)
         i64[:batch] = positions
         i64[capacity : capacity + batch] = [blk for blk, _ in locations]
         i64[2 * capacity : 2 * capacity + batch] = [off for _, off in locations]
-        i32 = arr[24 * capacity :].view(np.int32)
+        i64[3 * capacity : 3 * capacity + batch] = [blk * block_size + off for blk, off in locations]
+        i32 = arr[32 * capacity :].view(np.int32)
         i32[:batch] = [p + 1 for p in positions]
         i32[capacity : capacity + batch * width] = table_rows.reshape(-1)
         if arena is not None:
@@ -155,6 +158,23 @@ def _torch():
     import torch
 
     return torch
+
+
+def _host_to_device(data, dtype, device):
+    """A device tensor of host-side values, without a host wait.
+
+    For a GPU the values are staged in pinned memory and copied on the
+    current stream (``non_blocking``): a pageable copy would block the host
+    until the stream's earlier work -- e.g. a replayed decode step -- has
+    finished.  Pinned staging comes from torch's caching host allocator,
+    which does not reuse the block before the copy has completed.
+    """
+    torch = _torch()
+    device = torch.device(device)
+    if device.type != "cuda":
+        return torch.as_tensor(data, dtype=dtype).to(device)
+    host = torch.as_tensor(data, dtype=dtype)
+    return host.pin_memory().to(device, non_blocking=True)
 
 
 class PagedKVCache:
@@ -489,7 +509,7 @@ class PagedKVCache:
                                        f"({len(ids)} rows x {width} blocks > {arena[1]} x {arena[2]})")
                 width = arena[2]
             rows = self._table_rows(states, width)
-            meta = _DeviceMeta.build(self.device, positions, locations, rows, width, arena)
+            meta = _DeviceMeta.build(self.device, positions, locations, rows, width, self.block_size, arena)
             for s in states:
                 s.transaction_id = transaction_id
         except Exception:
@@ -631,8 +651,8 @@ class PagedKVCache:
     def transaction_device_metadata(self, transaction):
         """The allocator's device-resident metadata of the open transaction.
 
-        Read-only by contract: ``positions``/``block_ids``/``offsets`` (int64),
-        ``eff_lens`` and ``block_tables`` (int32).  For launch paths (e.g.
+        Read-only by contract: ``positions``/``block_ids``/``offsets``/``slots``
+        (int64), ``eff_lens`` and ``block_tables`` (int32).  For launch paths (e.g.
         graph capture) that must not allocate per layer.
         """
         return self._require_open_transaction(transaction).meta
@@ -643,7 +663,7 @@ class PagedKVCache:
         A graph captured against ``graph_metadata()`` replays correctly for
         any later transaction of up to ``max_batch`` requests whose rows need
         at most ``max_blocks_per_seq`` blocks: ``begin_token`` packs positions,
-        block ids, offsets, effective lengths and the block table (padded to
+        block ids, offsets, slots, effective lengths and the block table (padded to
         ``max_blocks_per_seq`` with -1) into the arena with one copy, ordered
         on the current stream after any earlier replay that reads it.
         """
@@ -739,7 +759,7 @@ class PagedKVCache:
                 raise RuntimeError(f"request_id {rid!r} belongs to an open token transaction")
             else:
                 positions.append(s.seq_len)
-        return torch.tensor(positions, device=self.device if device is None else device, dtype=torch.int64)
+        return _host_to_device(positions, torch.int64, self.device if device is None else device)
 
     def block_tables(self, request_ids=None, max_blocks_per_seq=None, pad_value=-1):
         """Padded physical block ids ``[num_requests, max_blocks_per_seq]`` (int32)."""
@@ -754,14 +774,14 @@ class PagedKVCache:
         if any(len(s.block_ids) > max_blocks_per_seq for s in states):
             raise ValueError("max_blocks_per_seq is smaller than a request's block count")
         rows = self._table_rows(states, max_blocks_per_seq, int(pad_value))
-        return torch.from_numpy(rows).to(self.device)
+        return _host_to_device(rows, torch.int32, self.device)
 
     def seq_lens_tensor(self, request_ids=None, device=None):
         """Sequence lengths (int32) for the requested rows."""
         torch = _torch()
         ids = self._normalize_active_request_ids(request_ids)
         lens = [self._requests[r].seq_len for r in ids]
-        return torch.tensor(lens, device=self.device if device is None else device, dtype=torch.int32)
+        return _host_to_device(lens, torch.int32, self.device if device is None else device)
 
     def request_block_ids(self, request_id):
         """Logical-to-physical block list of one request."""

@@ -22,6 +22,7 @@
 #include <hip/hip_ext.h>
 
 #include "fd_common.h"
+#include "rope_math.h"
 
 namespace fd {
 
@@ -65,6 +66,10 @@ struct DecodeParams {
   // w % hkv of the batch's (w / hkv)-th split
   int bal_target;
   float scale_log2;  // sm_scale * log2(e): scores live in the base-2 domain
+  // fused RoPE (rope_dim 64 or 128, with the fused append): q and append_k
+  // arrive unrotated and are rotated at position seq_len - 1
+  int rope_dim;
+  float rope_base;
 };
 
 // Row-level bookkeeping shared by the decode kernels.
@@ -332,6 +337,55 @@ __device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, int
   if (g == 0) {
     T* dst = static_cast<T*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
     *reinterpret_cast<u32x4*>(dst + 8 * c) = ar.avf;
+  }
+}
+
+// Fused RoPE: rotate this lane's Q^T operand pieces and the appended K row
+// in place, at position seq_len - 1 (the row's length counts the appended
+// token), with the RoPE kernel's arithmetic (rope_math.h) so the cached K
+// bytes and the scores are those of RoPE + append followed by decode.  Piece
+// s of a lane holds dims [32*s + 8*g, +8); with half = rope_dim / 2 its
+// rotation partner is piece s + half / 32 (rope_dim 64: 0 <-> 1, dims 64-127
+// unrotated; 128: 0 <-> 2 and 1 <-> 3).  Lane l evaluates frequency l in
+// float64, and ds_bpermute hands each lane the 8 frequencies of a piece.
+template <typename T>
+__device__ __forceinline__ void rope_operands(const DecodeParams& p, int32_t seq_len, int lane, int g,
+                                              u32x4 (&qf)[4], AppendRegs& ar) {
+  const int half = p.rope_dim / 2;  // 32 or 64, checked on the host
+  const int64_t pos = seq_len > 0 ? seq_len - 1 : 0;
+  float cl, sl;
+  rope_cos_sin(p.rope_base, p.rope_dim, pos, lane < half ? lane : 0, cl, sl);
+  const int ci = __builtin_bit_cast(int, cl), si = __builtin_bit_cast(int, sl);
+  auto rotate = [&](u32x4& lo_w, u32x4& hi_w, const float (&c)[8], const float (&sn)[8]) {
+    u32x4 a = lo_w, b = hi_w;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t ua = a[w], ub = b[w];
+      float l0, h0, l1, h1;
+      rope_rotate(lo_f32<T>(ua), lo_f32<T>(ub), c[2 * w], sn[2 * w], l0, h0);
+      rope_rotate(hi_f32<T>(ua), hi_f32<T>(ub), c[2 * w + 1], sn[2 * w + 1], l1, h1);
+      a[w] = pack2<T>(l0, l1);
+      b[w] = pack2<T>(h0, h1);
+    }
+    lo_w = a;
+    hi_w = b;
+  };
+  auto piece = [&](int s, int partner) {
+    float c[8], sn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int src = (32 * s + 8 * g + j) * 4;
+      c[j] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, ci));
+      sn[j] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, si));
+    }
+    rotate(qf[s], qf[partner], c, sn);
+    rotate(ar.akf[s], ar.akf[partner], c, sn);
+  };
+  if (half == 64) {
+    piece(0, 2);
+    piece(1, 3);
+  } else {
+    piece(0, 1);
   }
 }
 
@@ -611,7 +665,7 @@ struct alignas(16) DecodeLds {
   int last;
 };
 
-template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, Role ROLE, bool NT>
+template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
                                             DecodeLds<waves_for<UNIT>()>& lds) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
@@ -621,6 +675,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   constexpr bool PREFIX = ROLE == Role::kPrefix;
   constexpr bool TAIL = ROLE == Role::kTail;
   constexpr bool BAL = ROLE == Role::kBalanced;
+  constexpr bool ROPE = FUSE == 2;  // fused append with RoPE of q and the appended K
   if constexpr (ROLE == Role::kRow && UNIT == 32) {
     // Short splits (about one unit per wave) spend most of their time before
     // the first K/V loads.  Every argument those loads need goes into SGPRs
@@ -709,6 +764,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   }
   int64_t eff_len;
   int32_t slot = -1;
+  [[maybe_unused]] int32_t seq_len = 0;
   if constexpr (BAL) {
     eff_len = bal_eff;
   } else if constexpr (PREFIX) {
@@ -716,7 +772,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     const int64_t plen = lead_ok ? cp.prefix_len[pair / cp.chunks / p.hkv] : 0;
     eff_len = plen < 0 ? 0 : (plen < cap ? plen : cap);
   } else {
-    const int32_t seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
+    seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
     slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
     eff_len = effective_len(p, seq_len, slot);
   }
@@ -739,6 +795,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       load_unit<T, BS, UNIT, kNT>(p, kvh, u, up, c, g, dst);
   };
   load(unit, pages, cur);
+  // the float64 cos/sin evaluation overlaps the K/V loads just issued
+  if constexpr (ROPE) rope_operands<T>(p, seq_len, lane, g, qf, ar);
 
   // token indices fit in 32 bits: eff_len <= seq_lens[b], an int32
   const int last = static_cast<int>(eff_len) - 1;
@@ -782,7 +840,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       }
       if constexpr (FUSE)
         if (app >= 0 && app / UNIT == unit) store_append<T, BS>(p, kvh, slot, c, g, ar);
-      process_unit<T, FUSE, UNIT>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
+      process_unit<T, (FUSE != 0), UNIT>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
       unit = next;
       next_pages = after;
       return more;
@@ -949,7 +1007,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
 }
 
-template <typename T, int BS, bool FUSE, bool MERGE, int UNIT, bool NT>
+// FUSE: 0 none, 1 fused append, 2 fused append with RoPE of q and the new K
+template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
   decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT>(p, CascadeParams{}, blockIdx.x, lds);
@@ -1300,16 +1359,19 @@ template <typename T, int BS, int UNIT, bool NT>
 void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
   const bool merge = p.counters != nullptr;
   const dim3 block(64 * waves_for<UNIT>());
-  if (p.fuse) {
+  if (p.fuse && p.rope_dim > 0) {
+    // the host refuses RoPE with the in-launch merge
+    dispatch(decode_mfma_kernel<T, BS, 2, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
+  } else if (p.fuse) {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, true, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, 1, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
     else
-      dispatch(decode_mfma_kernel<T, BS, true, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, 1, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
   } else {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, false, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, 0, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
     else
-      dispatch(decode_mfma_kernel<T, BS, false, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
+      dispatch(decode_mfma_kernel<T, BS, 0, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
   }
 }
 
@@ -1646,6 +1708,23 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
     return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
   p.bal_target = a.balance_target;
   if (a.kv_reuse != 0 && a.kv_reuse != 1) return set_error(FD_E_INVALID, "%s: kv_reuse must be 0 or 1", fn);
+  if (a.rotary_dim != 0) {
+    if (a.rotary_dim != 64 && a.rotary_dim != 128)
+      return set_error(FD_E_UNSUPPORTED, "%s: rotary_dim must be 0, 64 or 128", fn);
+    if (!fuse)
+      return set_error(FD_E_INVALID, "%s: rotary_dim needs the fused append (append_k, append_v, slot_mapping)", fn);
+    if (!(a.rope_base > 0.0) || a.rope_base > 3.4e38)
+      return set_error(FD_E_INVALID, "%s: rope_base must be a positive finite number", fn);
+    if (!fast_path_ok(a, p.group))
+      return set_error(FD_E_UNSUPPORTED,
+                       "%s: fused RoPE needs head_dim 128, <= 16 query heads per KV head, unit dim stride and "
+                       "16-byte rows",
+                       fn);
+    if (p.counters != nullptr)
+      return set_error(FD_E_UNSUPPORTED, "%s: fused RoPE does not combine with the in-launch merge", fn);
+    p.rope_dim = static_cast<int>(a.rotary_dim);
+    p.rope_base = static_cast<float>(a.rope_base);  // the reference's pow runs on an fp32 base
+  }
   {
     // first-tile guess of the MFMA kernel: from max_seq_len when given, else
     // from the table width; each row's split range uses its own length

@@ -20,6 +20,7 @@
 // One workgroup per request (launch-bound at decode batch sizes).  Rows of
 // 16-byte vectors take the vector path below, other shapes the scalar one.
 #include "fd_common.h"
+#include "rope_math.h"
 
 #pragma clang fp contract(off)
 
@@ -53,16 +54,9 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
   const int R = p.rotary_dim;
   const int half = R / 2;
   const int64_t pos = load_index(p.positions, b, p.idx_i64);
-  const float posf = static_cast<float>(pos);
   for (int i = tid; i < half; i += blockDim.x) {
     // e = -(2i) / R in fp32, as torch evaluates -arange(0, R, 2) / R
-    const float e = static_cast<float>(-2 * i) / static_cast<float>(R);
-    const float inv = static_cast<float>(pow(static_cast<double>(p.base), static_cast<double>(e)));
-    const float ang = posf * inv;
-    double sd, cd;
-    sincos(static_cast<double>(ang), &sd, &cd);
-    s_cos[i] = static_cast<float>(cd);
-    s_sin[i] = static_cast<float>(sd);
+    rope_cos_sin(p.base, R, pos, i, s_cos[i], s_sin[i]);
   }
   __syncthreads();
 
@@ -79,13 +73,10 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
       const T* row = qb + h * D;
       const float x1 = to_f32(row[i]);
       const float x2 = to_f32(row[i + half]);
-      const float c = s_cos[i], s = s_sin[i];
-      const float a = x1 * c;
-      const float bb = x2 * s;
-      const float e = x2 * c;
-      const float f = x1 * s;
-      ob[h * D + i] = from_f32<T>(a - bb);
-      ob[h * D + i + half] = from_f32<T>(e + f);
+      float lo, hi;
+      rope_rotate(x1, x2, s_cos[i], s_sin[i], lo, hi);
+      ob[h * D + i] = from_f32<T>(lo);
+      ob[h * D + i + half] = from_f32<T>(hi);
     }
     const int tail = D - R;
     for (int idx = tid; idx < p.hq * tail; idx += blockDim.x) {
@@ -106,14 +97,11 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
     const T* row = kb + h * D;
     const float x1 = to_f32(row[i]);
     const float x2 = to_f32(row[i + half]);
-    const float c = s_cos[i], s = s_sin[i];
-    const float a = x1 * c;
-    const float bb = x2 * s;
-    const float e = x2 * c;
-    const float f = x1 * s;
+    float lo, hi;
+    rope_rotate(x1, x2, s_cos[i], s_sin[i], lo, hi);
     T* dst = kc + slot0 + h * hstride;
-    dst[i] = from_f32<T>(a - bb);
-    dst[i + half] = from_f32<T>(e + f);
+    dst[i] = from_f32<T>(lo);
+    dst[i + half] = from_f32<T>(hi);
   }
   const int tail = D - R;
   for (int idx = tid; idx < p.hkv * tail; idx += blockDim.x) {
@@ -242,13 +230,7 @@ __device__ __forceinline__ void finish_item(const Item<T>& item, const u32x4& a,
   VecOps<T>::unpack(bvec, x2);
 #pragma unroll
   for (int e = 0; e < N; ++e) {
-    const float c = s_cos[item.freq0 + e], sn = s_sin[item.freq0 + e];
-    const float t0 = x1[e] * c;
-    const float t1 = x2[e] * sn;
-    const float t2 = x2[e] * c;
-    const float t3 = x1[e] * sn;
-    lo[e] = t0 - t1;
-    hi[e] = t2 + t3;
+    rope_rotate(x1[e], x2[e], s_cos[item.freq0 + e], s_sin[item.freq0 + e], lo[e], hi[e]);
   }
   *reinterpret_cast<u32x4*>(item.dst0) = VecOps<T>::pack(lo);
   *reinterpret_cast<u32x4*>(item.dst1) = VecOps<T>::pack(hi);
@@ -289,15 +271,8 @@ __global__ __launch_bounds__(kThreads) void rope_append_vec_kernel(RopeParams p)
       if (item.src1 != nullptr) rb[k] = *reinterpret_cast<const u32x4*>(item.src1);
     }
   }
-  const float posf = static_cast<float>(pos);
   for (int i = tid; i < half; i += kThreads) {
-    const float e = static_cast<float>(-2 * i) / static_cast<float>(R);
-    const float inv = static_cast<float>(pow(static_cast<double>(p.base), static_cast<double>(e)));
-    const float ang = posf * inv;
-    double sd, cd;
-    sincos(static_cast<double>(ang), &sd, &cd);
-    s_cos[i] = static_cast<float>(cd);
-    s_sin[i] = static_cast<float>(sd);
+    rope_cos_sin(p.base, R, pos, i, s_cos[i], s_sin[i]);
   }
   __syncthreads();
 #pragma unroll

@@ -100,9 +100,12 @@ class DecodeStepGraph:
     Replaying it runs, for every layer in order, the fused RoPE + K/V append
     (``q[l]``, ``k[l]``, ``v[l]`` -> the reserved slots, ``q_rot[l]``) and the
     paged decode (``q_rot[l]`` -> ``out[l]``), reading the open
-    transaction's metadata from the cache's graph-metadata arena.  The
-    caller writes ``q``/``k``/``v`` ``[num_layers, B, H, D]`` before each
-    replay; ``out`` holds every layer's attention output afterwards.
+    transaction's metadata from the cache's graph-metadata arena.  With
+    ``fused_rope`` the two are one launch per layer: the decode kernel rotates
+    q and the new K itself, stores K/V to the slots and leaves ``q_rot``
+    untouched (same outputs and cache bytes).  The caller writes
+    ``q``/``k``/``v`` ``[num_layers, B, H, D]`` before each replay; ``out``
+    holds every layer's attention output afterwards.
     """
 
     graph: Any
@@ -119,6 +122,7 @@ class DecodeStepGraph:
     workspace: Any = None  # split partials (and merge counters) the graph uses, kept alive with it
     balance_target: int = 0  # > 0: per-row split counts from the lengths at replay
     kv_reuse: bool = False  # rows shared prefix blocks at capture: plain (cached) K/V loads
+    fused_rope: bool = False  # RoPE + append inside the decode launch (q_rot unused)
 
 
 @dataclass
@@ -417,7 +421,7 @@ class DecodeEngine:
         return self._abort_open_step(self._require_open_step(transaction))
 
     def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None,
-                           merge=False, kv_reuse=None):
+                           merge=False, kv_reuse=None, fuse_rope=None):
         """Capture every layer's launches of one token step into a hipGraph.
 
         Needs the HIP backends, a GPU cache and its graph-metadata arena
@@ -431,7 +435,10 @@ class DecodeEngine:
         launch (the last workgroup of each request and KV head), so each layer
         runs two kernels instead of three.  ``kv_reuse`` (default: whether
         active requests share a resident prefix now) reads K/V with plain,
-        cached loads instead of streaming them.
+        cached loads instead of streaming them.  ``fuse_rope`` (default: where
+        supported -- head_dim 128, rotary_dim 64 or 128, a 16-bit cache, no
+        merge and no per-row splits) runs RoPE + append inside each layer's
+        decode launch, one kernel fewer per layer.
         """
         torch = _torch()
         from . import _lib
@@ -483,6 +490,14 @@ class DecodeEngine:
                 raise ValueError("num_splits must be a positive integer")
         _validate_inputs(q_rot[0], cache.k_cache[0], cache.v_cache[0], meta.block_tables, meta.eff_lens,
                          cache.block_size, self.num_warps, self.num_stages, "token_major")
+        eligible = (cache.head_dim == 128 and int(rotary_dim) in (64, 128) and not merge and not balance
+                     and dt in (torch.bfloat16, torch.float16) and num_q_heads // cache.num_kv_heads <= 16)
+        if fuse_rope is None:
+            fuse_rope = eligible
+        elif fuse_rope and not eligible:
+            raise ValueError("fuse_rope needs head_dim 128, rotary_dim 64 or 128, a bf16/fp16 cache, <= 16 query "
+                             "heads per KV head, no merge and uniform splits")
+        fuse_rope = bool(fuse_rope)
         workspace = None
         counters = None
         if splits > 1:
@@ -500,6 +515,14 @@ class DecodeEngine:
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
                 for layer in range(cache.num_layers):
+                    if fuse_rope:
+                        _decode_with_workspace(q[layer], cache.k_cache[layer], cache.v_cache[layer],
+                                               meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
+                                               cache.block_size, splits, workspace[:3] if workspace else None,
+                                               cache.max_blocks, kv_reuse=kv_reuse,
+                                               append=(k[layer], v[layer], meta.slots),
+                                               rope=(int(rotary_dim), float(base)))
+                        continue
                     _fused_rope_kv_append_trusted(q[layer], k[layer], v[layer], cache.k_cache[layer],
                                                   cache.v_cache[layer], meta.block_ids, meta.offsets, meta.positions,
                                                   rotary_dim=rotary_dim, base=base, q_out=q_rot[layer])
@@ -511,7 +534,8 @@ class DecodeEngine:
         torch.cuda.current_stream(dev).wait_stream(side)
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
                                num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,
-                               workspace=workspace, balance_target=balance, kv_reuse=kv_reuse)
+                               workspace=workspace, balance_target=balance, kv_reuse=kv_reuse,
+                               fused_rope=fuse_rope)
 
     def step_graph(self, transaction, step_graph):
         """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.

@@ -405,7 +405,8 @@ def paged_decode_attention_into(
 
 
 def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_splits,
-                           workspace, num_blocks, balance_target=0, counters=None, kv_reuse=False):
+                           workspace, num_blocks, balance_target=0, counters=None, kv_reuse=False, append=None,
+                           rope=None):
     """Unchecked launch on a token-major cache with a caller-held split workspace (graph capture).
 
     ``workspace`` is ``(acc [B, Hq, S, D], max [B, Hq, S], sum [B, Hq, S])`` or
@@ -414,7 +415,13 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     ``num_splits``) computed on the device from ``seq_lens``.  ``counters``
     (zeroed int32, ``B * Hkv * SPLIT_COUNTER_STRIDE``) selects the in-launch
     merge: one dispatch, no reducer kernel.  ``kv_reuse``: plain instead of
-    non-temporal K/V loads (rows share blocks).
+    non-temporal K/V loads (rows share blocks).  ``append`` = ``(append_k,
+    append_v, slot_mapping)`` fuses the current token's cache write; with it,
+    ``rope`` = ``(rotary_dim, base)`` (rotary_dim 64 or 128, head_dim 128)
+    takes ``q`` and ``append_k`` unrotated and rotates both at position
+    ``seq_len - 1`` inside the launch -- the same bits as the RoPE + append
+    kernel followed by this decode on the rotated q.  No counterpart in the
+    reference.
     """
     num_kv_heads = k_cache.shape[1]
     if sm_scale is None:
@@ -428,6 +435,11 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     args.kv_reuse = 1 if kv_reuse else 0
     acc, mx, sm = workspace if workspace is not None else (None, None, None)
     _fill_workspace(args, acc, mx, sm, int(num_splits), counters)
+    if append is not None:
+        _fill_append(args, *append)
+    if rope is not None:
+        args.rotary_dim = int(rope[0])
+        args.rope_base = float(rope[1])
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))
     return out
 

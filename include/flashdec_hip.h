@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 5
+#define FD_ABI_VERSION 6
 
 /* status codes */
 #define FD_OK 0
@@ -171,6 +171,17 @@ typedef struct fd_paged_decode_args {
    * prefix pass always uses plain loads.  Results are identical either way.
    * No counterpart in the reference. */
   int32_t kv_reuse;
+
+  /* Fused RoPE: 0 = off; 64 or 128 = rotary width (head_dim 128, split-half
+   * rotation as flashdec/rope.py:26-85, frequencies rope_base^(-2i/R)).  Needs
+   * the fused append: q and append_k are then unrotated, both are rotated at
+   * position seq_len - 1 (the appended token's index) and the cache receives
+   * the rotated K.  Bit-identical to fd_fused_rope_kv_append at those
+   * positions followed by fd_paged_decode on the rotated q.  Refused with the
+   * in-launch merge.  No counterpart in the reference, which runs RoPE +
+   * append as its own kernel. */
+  int32_t rotary_dim;
+  double rope_base;
 } fd_paged_decode_args;
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);

@@ -6,8 +6,10 @@ the other replays a captured :class:`DecodeStepGraph`.  After every step:
 - both engines' outputs must match the oracle within the north-star
   tolerance.
 The batch's membership may change between steps as long as its size does.
-The graph is checked with the split reducer kernel and with the in-launch
-merge (arrival counters, which every replay leaves at zero).
+The graph is checked with the split reducer kernel, with RoPE + append
+fused into the decode launch, and with the in-launch merge (arrival
+counters, which every replay leaves at zero).  A fused and an unfused graph
+of identical engines must agree bit for bit.
 """
 
 import pytest
@@ -48,14 +50,16 @@ def oracle_layer(cache, layer, q, tx_positions, tables, lens):
                                      lens.cpu().numpy())
 
 
-@pytest.mark.parametrize("merge", [False, True])
-def test_step_graph_matches_eager_steps(merge):
+@pytest.mark.parametrize(("merge", "fuse_rope"), [(False, False), (False, None), (True, None)])
+def test_step_graph_matches_eager_steps(merge, fuse_rope):
     eager = make_engine()
     graphed = make_engine(arena=(4, 16))
     for e in (eager, graphed):
         admit(e, [0, 1, 2, 3], 40)
-    sg = graphed.capture_step_graph(4, HQ, base=1e6, num_splits=3 if merge else None, merge=merge)
+    sg = graphed.capture_step_graph(4, HQ, base=1e6, num_splits=3 if merge else None, merge=merge,
+                                    fuse_rope=fuse_rope)
     assert isinstance(sg, DecodeStepGraph) and sg.out.shape == (L, 4, HQ, D)
+    assert sg.fused_rope == (not merge and fuse_rope is None)  # by default fused wherever supported
     g = torch.Generator(device="cuda").manual_seed(11)
     for step in range(24):
         if step == 12:  # membership change at a fixed batch size
@@ -92,6 +96,44 @@ def test_step_graph_matches_eager_steps(merge):
     m = graphed.metrics()
     assert m["transaction_layer_step_count"] == 24 * L and m["cache"]["transaction_layer_write_count"] == 24 * L
     assert graphed.validate_invariants() and eager.validate_invariants()
+
+
+@pytest.mark.parametrize("rotary_dim", [64, 128])
+def test_fused_and_unfused_step_graphs_agree_bit_for_bit(rotary_dim):
+    engines = [make_engine(arena=(4, 16)) for _ in range(2)]
+    for e in engines:
+        admit(e, [0, 1, 2, 3], 31)  # the first step's token opens a new block
+    graphs = [e.capture_step_graph(4, HQ, rotary_dim=rotary_dim, base=5e5, fuse_rope=f)
+              for e, f in zip(engines, (False, True))]
+    assert not graphs[0].fused_rope and graphs[1].fused_rope
+    g = torch.Generator(device="cuda").manual_seed(21)
+    for step in range(6):
+        q = torch.randn((L, 4, HQ, D), device="cuda", generator=g).to(torch.bfloat16)
+        k = torch.randn((L, 4, HKV, D), device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn((L, 4, HKV, D), device="cuda", generator=g).to(torch.bfloat16)
+        outs = []
+        for e, sg in zip(engines, graphs):
+            tx = e.begin_step()
+            sg.q.copy_(q)
+            sg.k.copy_(k)
+            sg.v.copy_(v)
+            outs.append(e.step_graph(tx, sg).clone())
+            e.commit_step(tx)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), step
+    assert torch.equal(engines[0].cache.k_cache.view(torch.int16), engines[1].cache.k_cache.view(torch.int16))
+    assert torch.equal(engines[0].cache.v_cache.view(torch.int16), engines[1].cache.v_cache.view(torch.int16))
+    assert all(e.validate_invariants() for e in engines)
+
+
+def test_fuse_rope_refused_where_unsupported():
+    engine = make_engine(arena=(2, 8))
+    admit(engine, ["a", "b"], 5)
+    with pytest.raises(ValueError, match="fuse_rope needs"):
+        engine.capture_step_graph(2, HQ, rotary_dim=96, fuse_rope=True)
+    with pytest.raises(ValueError, match="fuse_rope needs"):
+        engine.capture_step_graph(2, HQ, merge=True, num_splits=2, fuse_rope=True)
+    assert not engine.capture_step_graph(2, HQ, rotary_dim=96).fused_rope
 
 
 def test_step_graph_limits_abort_cleanly():
