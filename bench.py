@@ -494,7 +494,7 @@ def run_engine(torch, dev, args):
     layers, batch, hq, hkv, d, bs, ctx = 36, 64, 16, 2, 128, 32, 8192
     steps = args.engine_steps
     # room for the warm-ups, the timed steps and the separate-RoPE comparison steps
-    width = (ctx + 2 * 20 + steps + max(10, steps // 2) + 2 + bs - 1) // bs
+    width = (ctx + 2 * 20 + 2 * steps + 2 + bs - 1) // bs
     cache = PagedKVCache(layers, hkv, d, bs, max_blocks=batch * width, dtype=torch.bfloat16, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(109)
@@ -538,6 +538,9 @@ def run_engine(torch, dev, args):
     warm = 20
     for _ in range(warm):
         graph_step()
+    # and the eager path the timed aborts take (its first launches load kernels)
+    if not abort_step(1):
+        raise RuntimeError("warm-up abort did not roll back cleanly")
     torch.cuda.synchronize()
     committed = 0
     rollbacks_ok = 0
@@ -570,17 +573,22 @@ def run_engine(torch, dev, args):
             engine.step_graph(tx_, sg_sep)
             engine.commit_step(tx_)
 
-        n_sep = max(10, steps // 2)
+        # the same schedule as the timed loop above: every 100th step aborts
+        n_sep = steps
         for _ in range(warm):
             graph_step_sep()
         torch.cuda.synchronize()
+        committed_sep = warm
         start.record()
-        for _ in range(n_sep):
-            graph_step_sep()
+        for i in range(n_sep):
+            if i % 100 == 99:
+                abort_step((i // 100) % layers)
+            else:
+                graph_step_sep()
+                committed_sep += 1
         stop.record()
         torch.cuda.synchronize()
         separate = start.elapsed_time(stop) / n_sep
-        committed_sep = n_sep + warm
     else:
         committed_sep = 0
     # per-layer attention kernel, measured on the same shapes through the timing hook
@@ -624,7 +632,7 @@ def run_engine(torch, dev, args):
     out["wall_ms_per_step"] = round(wall_s * 1e3 / steps, 4)
     if separate is not None:
         out["separate_rope_kernel_path"] = {"ms_per_step": round(separate, 4), "kernels_per_layer": 3,
-                                            "steps": committed_sep - 1}
+                                            "steps": steps}
         log(f"[bench] engine: RoPE + append as its own kernel: {separate:.3f} ms/step")
     out["roofline"] = {"bound": "hbm", "kernel_us_mean": round(attn_us, 2), "reducer_us_mean": round(red_us, 3),
                        "algorithmic_bytes_per_layer": kv_layer,

@@ -94,12 +94,13 @@ class _DeviceMeta:
         self.block_tables = i32[capacity : capacity + batch * width].view(batch, width)
 
     @classmethod
-    def build(cls, device, positions, locations, table_rows, width, block_size, arena=None):
+    def build(cls, device, positions, locations, table_rows, width, block_size, arena=None, staging=None):
         """Pack on the host and copy once (pinned staging for GPU caches).
 
         With ``arena`` (a device buffer laid out for ``arena_capacity`` rows of
         ``width`` table entries) the copy lands in the arena instead of a new
-        buffer.  Pinned staging comes from torch's caching host allocator,
+        buffer, staged through ``staging`` (a :class:`_StagingRing`).
+        Otherwise pinned staging comes from torch's caching host allocator,
         which does not hand a block out again before its copy has completed.
         """
         import torch
@@ -108,7 +109,11 @@ class _DeviceMeta:
         capacity = batch if arena is None else arena[1]
         nbytes = _meta_nbytes(capacity, width)
         pinned = device.type == "cuda"
-        host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=pinned)
+        slot = None
+        if staging is not None and pinned:
+            slot, host = staging.acquire()
+        else:
+            host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=pinned)
         arr = host.numpy()
         i64 = arr[: 32 * capacity].view(np.int64)
         i64[:batch] = positions
@@ -119,13 +124,47 @@ class _DeviceMeta:
         i32[:batch] = [p + 1 for p in positions]
         i32[capacity : capacity + batch * width] = table_rows.reshape(-1)
         if arena is not None:
-            arena[0][:nbytes].copy_(host, non_blocking=pinned)
+            arena[0][:nbytes].copy_(host[:nbytes], non_blocking=pinned)
+            if slot is not None:
+                staging.release(slot)
             return cls(arena[0], batch, width, capacity)
         buf = host.to(device, non_blocking=pinned) if pinned else host
         return cls(buf, batch, width)
 
     def clone(self):
         return _DeviceMeta(self.buf.clone(), self.positions.numel(), self.block_tables.shape[1], self.capacity)
+
+
+class _StagingRing:
+    """A few pinned host buffers for the per-step metadata copies, reused in turn.
+
+    A buffer is refilled only after the copy that last read it has completed
+    (its event), so the host runs at most ``depth`` steps ahead of the device
+    and no pinned memory is allocated once the ring exists: letting torch's
+    host allocator grow a pool while the host runs far ahead cost ~0.1 ms per
+    step on MI355X.
+    """
+
+    def __init__(self, nbytes, depth=4):
+        import torch
+
+        self.bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(depth)]
+        self.events = [None] * depth
+        self.next = 0
+
+    def acquire(self):
+        i = self.next
+        self.next = (i + 1) % len(self.bufs)
+        if self.events[i] is not None:
+            self.events[i].synchronize()
+        return i, self.bufs[i]
+
+    def release(self, i):
+        import torch
+
+        ev = torch.cuda.Event()
+        ev.record()  # after the copy, on the current stream
+        self.events[i] = ev
 
 
 @dataclass
@@ -253,6 +292,7 @@ class PagedKVCache:
         self._prefix_eviction_count = 0
         self._prefix_capacity_failure_count = 0
         self._meta_arena = None  # (device buffer, capacity rows, table width) once enabled
+        self._meta_staging = None  # pinned staging ring of the arena copies
 
     # ------------------------------------------------------------ lifecycle
     def add_request(self, request_id):
@@ -509,7 +549,8 @@ class PagedKVCache:
                                        f"({len(ids)} rows x {width} blocks > {arena[1]} x {arena[2]})")
                 width = arena[2]
             rows = self._table_rows(states, width)
-            meta = _DeviceMeta.build(self.device, positions, locations, rows, width, self.block_size, arena)
+            meta = _DeviceMeta.build(self.device, positions, locations, rows, width, self.block_size, arena,
+                                     self._meta_staging)
             for s in states:
                 s.transaction_id = transaction_id
         except Exception:
@@ -675,6 +716,7 @@ class PagedKVCache:
             raise ValueError("max_batch and max_blocks_per_seq must be positive")
         buf = torch.zeros(_meta_nbytes(max_batch, width), dtype=torch.uint8, device=self.device)
         self._meta_arena = (buf, max_batch, width)
+        self._meta_staging = _StagingRing(buf.numel()) if self.device.type == "cuda" else None
         return self.graph_metadata(max_batch)
 
     def graph_metadata(self, batch):
@@ -1012,7 +1054,7 @@ class PagedKVCache:
     def _location_tensors(self, locations):
         torch = _torch()
         arr = np.asarray(locations, dtype=np.int64).reshape(-1, 2)
-        both = torch.from_numpy(np.ascontiguousarray(arr.T)).to(self.device)
+        both = _host_to_device(np.ascontiguousarray(arr.T), torch.int64, self.device)
         return both[0], both[1]
 
     def _transaction_view(self, transaction):

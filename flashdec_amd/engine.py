@@ -411,7 +411,9 @@ class DecodeEngine:
             output=state.last_output,
             positions=committed.positions,
             block_tables=committed.block_tables,
-            seq_lens=self.cache.seq_lens_tensor(state.handle.request_ids),
+            # the committed lengths are the token's effective lengths, already on
+            # the device: no host-to-device copy per step
+            seq_lens=committed.effective_seq_lens,
             needed_new_blocks=state.needed_new_blocks,
             free_blocks=self.cache.num_free_blocks,
         )
