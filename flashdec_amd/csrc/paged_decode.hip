@@ -21,6 +21,8 @@
 //                                             seq_len == 0 / slot < 0
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "fd_common.h"
 #include "rope_math.h"
 
@@ -155,9 +157,10 @@ __device__ __forceinline__ f32x4 mfma16x16x16<_Float16>(u32x2 a, u32x2 b, f32x4 
 }
 
 // Work unit of one wave: UNIT = 16 or 32 consecutive tokens.  Register
-// footprint for one lane (lane = 16*g + c), MT = UNIT / 16 row blocks:
-//   kf[mt][s]: K row (token UNIT*u + 16*mt + c), dims [32*s + 8*g, +8)  (QK A)
-//   vf[i]    : V row (token UNIT*u + vrow(g, i)), dims [8*c, +8)     (PV, transposed)
+// footprint for one lane (lane = 16*g + c), MT = UNIT / 16 row blocks, head
+// dim D = 128 or 64:
+//   kf[mt][s]: K row (token UNIT*u + 16*mt + c), dims [32*s + 8*g, +8), s < D/32  (QK A)
+//   vf[i]    : V row (token UNIT*u + vrow(g, i)), dims [(D/16)*c, +D/16)  (PV, transposed)
 // vrow(g, i) = 4*g + i (i < 4) or 16 + 4*g + (i - 4): the tokens whose scores
 // this lane holds after QK (MFMA D layout: rows 4*g + r of each 16-row
 // block), so P needs no cross-lane movement.  Four waves of 32-token units
@@ -169,12 +172,18 @@ __device__ __forceinline__ f32x4 mfma16x16x16<_Float16>(u32x2 a, u32x2 b, f32x4 
 // past the row's length and rows whose block id is out of range are masked
 // in registers at compute time, so the K/V loads of the first unit can be in
 // flight before the row length arrives.
-template <int UNIT>
+// A lane's piece of one V row: D/16 dims (16 bytes at D = 128, 8 at 64)
+template <int D>
+using VPiece = std::conditional_t<D == 128, u32x4, u32x2>;
+
+template <int UNIT, int D = 128>
 struct UnitRegs {
+  static_assert(D == 128 || D == 64, "head_dim 128 or 64");
   static constexpr int MT = UNIT / 16;
   static constexpr int VR = UNIT / 4;  // V rows per lane: 4 (UNIT 16) or 8 (UNIT 32)
-  u32x4 kf[MT][4];
-  u32x4 vf[VR];
+  static constexpr int KS = D / 32;    // 32-dim pieces of a K row (QK k-steps)
+  u32x4 kf[MT][KS];
+  VPiece<D> vf[VR];
   uint32_t bmask;  // bit i: V row i lies in a valid physical block
 };
 
@@ -185,20 +194,21 @@ constexpr int waves_for() {
   return UNIT == 32 ? 4 : 8;
 }
 
+// One K/V vector load (16 or 8 bytes).  NT: non-temporal, for K/V that a
+// launch reads once (streamed past the caches: a 550 MB read runs at 6.8
+// instead of 6.1 TB/s on MI355X); plain loads where rows re-read shared
+// blocks.
+template <bool NT, typename V = u32x4>
+__device__ __forceinline__ V kv_load(const void* a) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const V*>(a));
+  else
+    return *reinterpret_cast<const V*>(a);
+}
+
 // Physical block ids a unit needs (wave-uniform, so scalar loads); pages are
 // clamped to the table row so the read is in bounds whatever the row's
 // length.  A unit spans one block, or two when the block is half its size.
-// One 16-byte K/V load.  NT: non-temporal, for K/V that a launch reads once
-// (streamed past the caches: a 550 MB read runs at 6.8 instead of 6.1 TB/s
-// on MI355X); plain loads where rows re-read shared blocks.
-template <bool NT>
-__device__ __forceinline__ u32x4 kv_load(const void* a) {
-  if constexpr (NT)
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a));
-  else
-    return *reinterpret_cast<const u32x4*>(a);
-}
-
 struct UnitPages {
   int32_t a, b;
 };
@@ -220,9 +230,9 @@ __device__ __forceinline__ UnitPages fetch_pages(const DecodeParams& p, int b, i
   return up;
 }
 
-template <typename T, int BS, int UNIT, bool NT>
+template <typename T, int BS, int UNIT, bool NT, int D>
 __device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int unit, const UnitPages& up, int c,
-                                          int g, UnitRegs<UNIT>& t) {
+                                          int g, UnitRegs<UNIT, D>& t) {
   const T* kbase = static_cast<const T*>(p.k);
   const T* vbase = static_cast<const T*>(p.v);
   // tt: token within the unit; its block and the row inside that block
@@ -231,25 +241,25 @@ __device__ __forceinline__ void load_unit(const DecodeParams& p, int kvh, int un
   // K rows 16*mt + c.  Rows in invalid blocks read row 0 of the cache (in
   // bounds, value discarded by the score mask).
 #pragma unroll
-  for (int mt = 0; mt < UnitRegs<UNIT>::MT; ++mt) {
+  for (int mt = 0; mt < UnitRegs<UNIT, D>::MT; ++mt) {
     const int tt = 16 * mt + c;
     const int32_t blk = block_of(tt);
     const bool ok = blk >= 0 && blk < p.num_blocks;
     const int64_t off = ok ? blk * p.ks0 + kvh * p.ks1 + row_in_block(tt) * p.ks2 : 0;
     const T* row = kbase + off;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) t.kf[mt][s] = kv_load<NT>(row + 32 * s + 8 * g);
+    for (int s = 0; s < UnitRegs<UNIT, D>::KS; ++s) t.kf[mt][s] = kv_load<NT>(row + 32 * s + 8 * g);
   }
   // V rows vrow(g, i)
   uint32_t bm = 0;
 #pragma unroll
-  for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
+  for (int i = 0; i < UnitRegs<UNIT, D>::VR; ++i) {
     const int tt = vrow(g, i);
     const int32_t blk = block_of(tt);
     const bool ok = blk >= 0 && blk < p.num_blocks;
     const int64_t off = ok ? blk * p.vs0 + kvh * p.vs1 + row_in_block(tt) * p.vs2 : 0;
     bm |= ok ? (1u << i) : 0u;
-    t.vf[i] = kv_load<NT>(vbase + off + 8 * c);
+    t.vf[i] = kv_load<NT, VPiece<D>>(vbase + off + (D / 16) * c);
   }
   t.bmask = bm;
 }
@@ -265,7 +275,7 @@ struct UnitOffsets {
   uint32_t v[UnitRegs<UNIT>::VR];
 };
 
-template <typename T, int BS, int UNIT>
+template <typename T, int BS, int UNIT, int D>
 __device__ __forceinline__ UnitOffsets<UNIT> unit_offsets(const DecodeParams& p, int kvh, int wave, int c, int g) {
   UnitOffsets<UNIT> o;
   const int u0 = UNIT * wave;
@@ -277,7 +287,7 @@ __device__ __forceinline__ UnitOffsets<UNIT> unit_offsets(const DecodeParams& p,
 #pragma unroll
   for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
     const int row = (u0 + vrow(g, i)) % BS;
-    o.v[i] = static_cast<uint32_t>((kvh * p.vs1 + row * p.vs2 + 8 * c) * static_cast<int64_t>(sizeof(T)));
+    o.v[i] = static_cast<uint32_t>((kvh * p.vs1 + row * p.vs2 + (D / 16) * c) * static_cast<int64_t>(sizeof(T)));
   }
   return o;
 }
@@ -287,9 +297,9 @@ __device__ __forceinline__ UnitOffsets<UNIT> unit_offsets(const DecodeParams& p,
 // first, the rest in the second), so a row's address is a uniform block base
 // (scalar) plus the lane's fixed 32-bit offset -- no per-unit vector
 // address arithmetic.
-template <typename T, int BS, int UNIT, bool NT>
+template <typename T, int BS, int UNIT, bool NT, int D>
 __device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const UnitPages& up,
-                                                const UnitOffsets<UNIT>& o, UnitRegs<UNIT>& t) {
+                                                const UnitOffsets<UNIT>& o, UnitRegs<UNIT, D>& t) {
   static_assert(BS >= 16, "a 16-token row group must lie in one block");
   constexpr bool kTwo = BS < UNIT;
   const bool oka = up.a >= 0 && up.a < p.num_blocks;
@@ -300,43 +310,45 @@ __device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const Uni
   const char* kb = kTwo ? static_cast<const char*>(p.k) + (okb ? up.b : 0) * p.ks0 * E : ka;
   const char* vb = kTwo ? static_cast<const char*>(p.v) + (okb ? up.b : 0) * p.vs0 * E : va;
 #pragma unroll
-  for (int mt = 0; mt < UnitRegs<UNIT>::MT; ++mt) {
+  for (int mt = 0; mt < UnitRegs<UNIT, D>::MT; ++mt) {
     const char* base = (kTwo && mt == 1) ? kb : ka;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) t.kf[mt][s] = kv_load<NT>(base + o.k[mt] + 64 * s);
+    for (int s = 0; s < UnitRegs<UNIT, D>::KS; ++s) t.kf[mt][s] = kv_load<NT>(base + o.k[mt] + 64 * s);
   }
   uint32_t bm = 0;
 #pragma unroll
-  for (int i = 0; i < UnitRegs<UNIT>::VR; ++i) {
+  for (int i = 0; i < UnitRegs<UNIT, D>::VR; ++i) {
     const bool second = kTwo && i >= 4;  // V rows 16 + 4g + (i - 4)
-    t.vf[i] = kv_load<NT>((second ? vb : va) + o.v[i]);
+    t.vf[i] = kv_load<NT, VPiece<D>>((second ? vb : va) + o.v[i]);
     bm |= (second ? okb : oka) ? (1u << i) : 0u;
   }
   t.bmask = bm;
 }
 
 // The appended token's pieces in this lane's operand layout: akf[s] = dims
-// [32*s + 8*g, +8) of append_k, avf = dims [8*c, +8) of append_v.
+// [32*s + 8*g, +8) of append_k, avf = dims [(D/16)*c, +D/16) of append_v.
+template <int D = 128>
 struct AppendRegs {
-  u32x4 akf[4];
-  u32x4 avf;
+  u32x4 akf[D / 32];
+  VPiece<D> avf;
 };
 
 // Fused append: store the newest token's K/V at the request's slot.  Lanes
-// c == 0 write the K row (4 x 4 x 16 B), lanes g == 0 the V row (16 x 16 B).
-template <typename T, int BS>
+// c == 0 write the K row (4 x D/32 x 16 B), lanes g == 0 the V row
+// (16 x 2D/16 B).
+template <typename T, int BS, int D>
 __device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, int32_t slot, int c, int g,
-                                             const AppendRegs& ar) {
+                                             const AppendRegs<D>& ar) {
   const int64_t blk = slot / BS, off = slot % BS;
   if (blk >= p.num_blocks) return;
   if (c == 0) {
     T* dst = static_cast<T*>(p.k) + blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) *reinterpret_cast<u32x4*>(dst + 32 * s + 8 * g) = ar.akf[s];
+    for (int s = 0; s < D / 32; ++s) *reinterpret_cast<u32x4*>(dst + 32 * s + 8 * g) = ar.akf[s];
   }
   if (g == 0) {
     T* dst = static_cast<T*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
-    *reinterpret_cast<u32x4*>(dst + 8 * c) = ar.avf;
+    *reinterpret_cast<VPiece<D>*>(dst + (D / 16) * c) = ar.avf;
   }
 }
 
@@ -350,7 +362,7 @@ __device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, int
 // float64, and ds_bpermute hands each lane the 8 frequencies of a piece.
 template <typename T>
 __device__ __forceinline__ void rope_operands(const DecodeParams& p, int32_t seq_len, int lane, int g,
-                                              u32x4 (&qf)[4], AppendRegs& ar) {
+                                              u32x4 (&qf)[4], AppendRegs<128>& ar) {
   const int half = p.rope_dim / 2;  // 32 or 64, checked on the host
   const int64_t pos = seq_len > 0 ? seq_len - 1 : 0;
   float cl, sl;
@@ -389,11 +401,12 @@ __device__ __forceinline__ void rope_operands(const DecodeParams& p, int32_t seq
   }
 }
 
-// Online-softmax state of one lane: query head c, dims 32*g + 8*r + n.
+// Online-softmax state of one lane: query head c, dims (D/4)*g + (D/16)*r + n.
+template <int D = 128>
 struct WaveState {
-  f32x4 acc[8];  // acc[n][r]
-  float m;       // running max (base-2 domain), uniform over g
-  float l;       // partial denominator of this lane's tokens
+  f32x4 acc[D / 16];  // acc[n][r]
+  float m;            // running max (base-2 domain), uniform over g
+  float l;            // partial denominator of this lane's tokens
 };
 
 // Reductions over the four lanes c, c + 16, c + 32, c + 48 (one query
@@ -441,12 +454,15 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // fp32.  Masking is skipped for units whose tokens are all live and the
 // rescale of the accumulator when no lane's maximum moved (wave-uniform
 // tests).
-template <typename T, bool FUSE, int UNIT>
-__device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf)[4], float scale_log2, int tok0,
-                                             int first, int last, int app, const AppendRegs& ar, int c, int g,
-                                             WaveState& st) {
-  constexpr int MT = UnitRegs<UNIT>::MT;
-  constexpr int VR = UnitRegs<UNIT>::VR;
+template <typename T, bool FUSE, int UNIT, int D>
+__device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (&qf)[D / 32], float scale_log2,
+                                             int tok0, int first, int last, int app, const AppendRegs<D>& ar, int c,
+                                             int g, WaveState<D>& st) {
+  constexpr int MT = UnitRegs<UNIT, D>::MT;
+  constexpr int VR = UnitRegs<UNIT, D>::VR;
+  constexpr int KS = UnitRegs<UNIT, D>::KS;
+  constexpr int NW = D / 32;  // 32-bit words of a lane's V piece
+  constexpr int NTILE = D / 16;  // PV output tiles (16 dims each)
   constexpr uint32_t kAll = (1u << VR) - 1u;
   uint32_t vmask = t.bmask;
 #pragma unroll
@@ -460,7 +476,7 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf
     for (int mt = 0; mt < MT; ++mt) {
       const bool hit = at == 16 * mt + c;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) t.kf[mt][s] = hit ? ar.akf[s] : t.kf[mt][s];
+      for (int s = 0; s < KS; ++s) t.kf[mt][s] = hit ? ar.akf[s] : t.kf[mt][s];
     }
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
@@ -475,7 +491,7 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf
   for (int mt = 0; mt < MT; ++mt) {
     f32x4 sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) sb = mfma16x16x32<T>(t.kf[mt][s], qf[s], sb);
+    for (int s = 0; s < KS; ++s) sb = mfma16x16x32<T>(t.kf[mt][s], qf[s], sb);
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[4 * mt + r] = sb[r] * scale_log2;
   }
@@ -487,7 +503,7 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf
       const bool keep = (vmask >> i) & 1u;
       sc[i] = keep ? sc[i] : -INFINITY;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) t.vf[i][k] = keep ? t.vf[i][k] : 0u;
+      for (int k = 0; k < NW; ++k) t.vf[i][k] = keep ? t.vf[i][k] : 0u;
     }
   }
   float mx = sc[0];
@@ -508,15 +524,15 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT>& t, const u32x4 (&qf
   st.m = m_new;
   if (__ballot(alpha != 1.f)) {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) st.acc[n] *= alpha;
+    for (int n = 0; n < NTILE; ++n) st.acc[n] *= alpha;
   }
   // P^T operand (k = VR*g + i: this lane's tokens)
   uint32_t ph[VR / 2];
 #pragma unroll
   for (int j = 0; j < VR / 2; ++j) ph[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
-  // V^T operands: vt_n holds dim 8*c + n of the lane's tokens
+  // V^T operands: vt_n holds dim (D/16)*c + n of the lane's tokens
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
+  for (int n = 0; n < NTILE; ++n) {
     const int w = n >> 1;
     const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
     if constexpr (UNIT == 32) {
@@ -665,11 +681,14 @@ struct alignas(16) DecodeLds {
   int last;
 };
 
-template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT>
+template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT, int D = 128>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
                                             DecodeLds<waves_for<UNIT>()>& lds) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
                 "cascade and balanced roles have no fused append or in-launch merge");
+  static_assert(D == 128 || (ROLE == Role::kRow && FUSE != 2 && !MERGE),
+                "head_dim 64 runs the row role without RoPE or in-launch merge");
+  constexpr int KS = D / 32;  // 32-dim pieces of q / K rows
   constexpr int kWaves = waves_for<UNIT>();
   constexpr int kUnitsPerTile = 32 / UNIT;
   constexpr bool PREFIX = ROLE == Role::kPrefix;
@@ -745,22 +764,22 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   }
   int unit = kUnitsPerTile * guess_begin + wave;
   UnitPages pages = fetch_pages<BS, UNIT>(p, trow, unit);  // clamped, always in bounds
-  u32x4 qf[4];
+  u32x4 qf[KS];
   {
     const T* qrow = static_cast<const T*>(p.q) + col_b * p.qs0 + (kvh * G + (col_ok ? col_h : 0)) * p.qs1;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < KS; ++s) {
       u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * g);
       qf[s] = col_ok ? x : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  AppendRegs ar;
+  AppendRegs<D> ar;
   if constexpr (FUSE) {
     const T* ak = static_cast<const T*>(p.ak) + b * p.aks0 + kvh * p.aks1;
     const T* av = static_cast<const T*>(p.av) + b * p.avs0 + kvh * p.avs1;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) ar.akf[s] = *reinterpret_cast<const u32x4*>(ak + 32 * s + 8 * g);
-    ar.avf = *reinterpret_cast<const u32x4*>(av + 8 * c);
+    for (int s = 0; s < KS; ++s) ar.akf[s] = *reinterpret_cast<const u32x4*>(ak + 32 * s + 8 * g);
+    ar.avf = *reinterpret_cast<const VPiece<D>*>(av + (D / 16) * c);
   }
   int64_t eff_len;
   int32_t slot = -1;
@@ -782,21 +801,21 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   // address once, which keeps the kernel-argument loads ahead of the first
   // K/V loads in fewer dependent batches (C2: 6.2 vs 7.1 us).
   constexpr bool kFixed = BS >= 16 && UNIT == 16;
-  UnitRegs<UNIT> cur;
+  UnitRegs<UNIT, D> cur;
   [[maybe_unused]] UnitOffsets<UNIT> offs;
-  if constexpr (kFixed) offs = unit_offsets<T, BS, UNIT>(p, kvh, wave, c, g);
+  if constexpr (kFixed) offs = unit_offsets<T, BS, UNIT, D>(p, kvh, wave, c, g);
   // the prefix role's blocks are read again by the group's other chunks:
   // plain loads, so the re-reads hit the caches
   constexpr bool kNT = NT && !PREFIX;
-  auto load = [&](int u, const UnitPages& up, UnitRegs<UNIT>& dst) {
+  auto load = [&](int u, const UnitPages& up, UnitRegs<UNIT, D>& dst) {
     if constexpr (kFixed)
-      load_unit_fixed<T, BS, UNIT, kNT>(p, up, offs, dst);
+      load_unit_fixed<T, BS, UNIT, kNT, D>(p, up, offs, dst);
     else
-      load_unit<T, BS, UNIT, kNT>(p, kvh, u, up, c, g, dst);
+      load_unit<T, BS, UNIT, kNT, D>(p, kvh, u, up, c, g, dst);
   };
   load(unit, pages, cur);
   // the float64 cos/sin evaluation overlaps the K/V loads just issued
-  if constexpr (ROPE) rope_operands<T>(p, seq_len, lane, g, qf, ar);
+  if constexpr (ROPE && D == 128) rope_operands<T>(p, seq_len, lane, g, qf, ar);
 
   // token indices fit in 32 bits: eff_len <= seq_lens[b], an int32
   const int last = static_cast<int>(eff_len) - 1;
@@ -818,9 +837,9 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     }
   }
 
-  WaveState st;
+  WaveState<D> st;
 #pragma unroll
-  for (int n = 0; n < 8; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < D / 16; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = -INFINITY;
   st.l = 0.f;
 
@@ -830,7 +849,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     // One unit: issue the next unit's loads into `ahead` (and the block ids
     // after it), then consume `now`; false when `now` was the last.  The two
     // buffers take turns, so no registers are copied between units.
-    auto step = [&](UnitRegs<UNIT>& now, UnitRegs<UNIT>& ahead) -> bool {
+    auto step = [&](UnitRegs<UNIT, D>& now, UnitRegs<UNIT, D>& ahead) -> bool {
       const int next = unit + kWaves;
       const bool more = next < u_end;
       UnitPages after{0, 0};
@@ -839,13 +858,13 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, trow, next + kWaves);
       }
       if constexpr (FUSE)
-        if (app >= 0 && app / UNIT == unit) store_append<T, BS>(p, kvh, slot, c, g, ar);
-      process_unit<T, (FUSE != 0), UNIT>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
+        if (app >= 0 && app / UNIT == unit) store_append<T, BS, D>(p, kvh, slot, c, g, ar);
+      process_unit<T, (FUSE != 0), UNIT, D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
       unit = next;
       next_pages = after;
       return more;
     };
-    UnitRegs<UNIT> alt;
+    UnitRegs<UNIT, D> alt;
     if constexpr (UNIT == 16) {
       while (step(cur, alt) && step(alt, cur)) {
       }
@@ -868,24 +887,28 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       lds.col_h[c] = col_h;
     }
   }
+  // this lane's dims (D/4)*g + (D/16)*rr + n, n < D/16: one or two 16-byte rows
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr) {
-    float* dst = &lds.acc[wave][c][32 * g + 8 * rr];
+    float* dst = &lds.acc[wave][c][(D / 4) * g + (D / 16) * rr];
     *reinterpret_cast<f32x4*>(dst) = f32x4{st.acc[0][rr], st.acc[1][rr], st.acc[2][rr], st.acc[3][rr]};
-    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
+    if constexpr (D == 128)
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
   }
   __syncthreads();
 
-  // merge the slots: thread -> (column h, dims [d0, d0 + 8)); threads past
-  // the first 256 only take part in the barrier of the in-launch merge
-  const int h = (threadIdx.x >> 4) & 15;
-  const int d0 = (threadIdx.x & 15) * 8;
+  // merge the slots: thread -> (column h, dims [d0, d0 + 8)), D/8 threads
+  // per column; threads past the first 2D only take part in the barrier of
+  // the in-launch merge
+  constexpr int kDimThreads = D / 8;
+  const int h = (threadIdx.x / kDimThreads) & 15;
+  const int d0 = (threadIdx.x % kDimThreads) * 8;
   int ob = b, qh = kvh * G + h;
-  bool head_ok = threadIdx.x < 256 && h < G;
+  bool head_ok = threadIdx.x < 16 * kDimThreads && h < G;
   if constexpr (PREFIX) {
     ob = lds.col_b[h];
     qh = kvh * G + lds.col_h[h];
-    head_ok = threadIdx.x < 256 && ob >= 0;
+    head_ok = threadIdx.x < 16 * kDimThreads && ob >= 0;
   }
   float M = -INFINITY;
 #pragma unroll
@@ -1007,11 +1030,12 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
 }
 
-// FUSE: 0 none, 1 fused append, 2 fused append with RoPE of q and the new K
-template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT>
+// FUSE: 0 none, 1 fused append, 2 fused append with RoPE of q and the new K;
+// D: head_dim 128 or 64
+template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 128>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
-  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT>(p, CascadeParams{}, blockIdx.x, lds);
+  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT, D>(p, CascadeParams{}, blockIdx.x, lds);
 }
 
 // Balanced splits (ragged batches): the row and split of each workgroup come
@@ -1319,8 +1343,11 @@ int device_cus() {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+// The MFMA row kernel: head_dim 128 or 64, <= 16 query heads per KV head,
+// unit dim strides and 16-byte aligned rows.  The cascade, per-row splits,
+// fused RoPE and the in-launch merge need head_dim 128 as well.
 bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
-  if (a.head_dim != 128 || group > 16) return false;
+  if ((a.head_dim != 128 && a.head_dim != 64) || group > 16) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
   const int64_t strides[] = {a.q_stride[0], a.q_stride[1], a.k_stride[0], a.k_stride[1], a.k_stride[2],
                              a.v_stride[0], a.v_stride[1], a.v_stride[2]};
@@ -1359,6 +1386,14 @@ template <typename T, int BS, int UNIT, bool NT>
 void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
   const bool merge = p.counters != nullptr;
   const dim3 block(64 * waves_for<UNIT>());
+  if (p.head_dim == 64) {
+    // head_dim 64: the host gives it no RoPE and no in-launch merge
+    if (p.fuse)
+      dispatch(decode_mfma_kernel<T, BS, 1, false, UNIT, NT, 64>, grid, block, stream, ev[0], ev[1], p);
+    else
+      dispatch(decode_mfma_kernel<T, BS, 0, false, UNIT, NT, 64>, grid, block, stream, ev[0], ev[1], p);
+    return;
+  }
   if (p.fuse && p.rope_dim > 0) {
     // the host refuses RoPE with the in-launch merge
     dispatch(decode_mfma_kernel<T, BS, 2, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], p);
@@ -1451,11 +1486,11 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   const bool nt = a.kv_reuse == 0;  // stream K/V past the caches
   // the in-launch merge exists only in the MFMA kernel and writes the
   // workspace with 8-byte stores (unit dim stride, 8-byte aligned rows)
-  if (!fast || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
+  if (!fast || a.head_dim != 128 || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
       (reinterpret_cast<uintptr_t>(p.acc) & 7u))
     p.counters = nullptr;
-  // balanced splits need the MFMA kernel, no fused append and a workspace
-  const bool balanced = p.bal_target > 0 && fast && !p.fuse && p.splits > 1;
+  // balanced splits need the MFMA kernel at head_dim 128, no fused append and a workspace
+  const bool balanced = p.bal_target > 0 && fast && a.head_dim == 128 && !p.fuse && p.splits > 1;
   if (!balanced) p.bal_target = 0;
   if (balanced) {
     p.counters = nullptr;
@@ -1715,7 +1750,7 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
       return set_error(FD_E_INVALID, "%s: rotary_dim needs the fused append (append_k, append_v, slot_mapping)", fn);
     if (!(a.rope_base > 0.0) || a.rope_base > 3.4e38)
       return set_error(FD_E_INVALID, "%s: rope_base must be a positive finite number", fn);
-    if (!fast_path_ok(a, p.group))
+    if (a.head_dim != 128 || !fast_path_ok(a, p.group))
       return set_error(FD_E_UNSUPPORTED,
                        "%s: fused RoPE needs head_dim 128, <= 16 query heads per KV head, unit dim stride and "
                        "16-byte rows",
@@ -1761,7 +1796,7 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
     return set_error(FD_E_INVALID, "%s: cascade struct_size %u != %zu (ABI mismatch)", fn, c.struct_size,
                      sizeof(fd_cascade_args));
   if (p.fuse) return set_error(FD_E_UNSUPPORTED, "%s: fused append is not supported (append first)", fn);
-  if (!fast_path_ok(a, p.group))
+  if (a.head_dim != 128 || !fast_path_ok(a, p.group))
     return set_error(FD_E_UNSUPPORTED,
                      "%s: needs head_dim 128, <= 16 query heads per KV head, unit dim stride and 16-byte rows", fn);
   if (c.num_groups < 0 || c.max_members < 1 || c.prefix_splits < 1)

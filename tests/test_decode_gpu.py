@@ -119,12 +119,12 @@ def _slots(table, lens, block_size):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("prior", [(0, 17), (256, 193), (31, 63)])
 @pytest.mark.parametrize("block_size", [16, 32])
-def test_fused_current_token_append(prior, num_splits, dtype, block_size):
+def test_fused_current_token_append(prior, num_splits, dtype, block_size, head_dim=128):
     lens_after = [p + 1 for p in prior]
-    q, k, v, table, lens = make_paged_inputs(lens_after, 16, 2, 128, block_size, dtype, seed=13)
+    q, k, v, table, lens = make_paged_inputs(lens_after, 16, 2, head_dim, block_size, dtype, seed=13)
     expected = _oracle(q, k, v, table, lens)  # cache already holding the new token
     slots = _slots(table, lens.cpu(), block_size)
-    append_k = torch.empty((2, 2, 128), device="cuda", dtype=dtype)
+    append_k = torch.empty((2, 2, head_dim), device="cuda", dtype=dtype)
     append_v = torch.empty_like(append_k)
     k_expected = k.clone()
     v_expected = v.clone()
@@ -134,7 +134,7 @@ def test_fused_current_token_append(prior, num_splits, dtype, block_size):
         append_v[b] = v[blk, :, off]
         k[blk, :, off] = float("nan")  # must come from append_k, never from the cache
         v[blk, :, off] = float("nan")
-    ws = (torch.empty((2, 16, 16, 128), device="cuda"), torch.empty((2, 16, 16), device="cuda"),
+    ws = (torch.empty((2, 16, 16, head_dim), device="cuda"), torch.empty((2, 16, 16), device="cuda"),
           torch.empty((2, 16, 16), device="cuda"))
     out = torch.empty_like(q)
     _fd().paged_decode_attention_into(q, k, v, table, lens, out, block_size=block_size, split_kv_workspace=ws,
@@ -343,3 +343,57 @@ def test_graph_replay_after_rows_grow_past_the_captured_hint():
         graph.replay()
         torch.cuda.synchronize()
         assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+@pytest.mark.parametrize("num_splits", [None, 1, 3, 16])
+@pytest.mark.parametrize("lens", [[2048] * 8, [1, 31, 32, 33, 700, 5000]])
+def test_head_dim_64_long_rows_match_oracle(lens, num_splits):
+    """head_dim 64 on the MFMA kernel (Qwen2.5-0.5B heads: 14 query, 2 KV), 32-token units on short
+    splits and 16-token units on long ones.  The public API plans the splits itself at head_dim 64
+    (the reference's split-KV path is head_dim 128 only), so explicit counts go through the C ABI."""
+    from flashdec_amd.paged_decode import _decode_with_workspace
+
+    q, k, v, table, sl = make_paged_inputs(lens, 14, 2, 64, 32, torch.bfloat16, seed=64 + len(lens))
+    if num_splits is None:
+        out = _fd().decode(q, k, v, table, sl)
+    else:
+        ws = None
+        if num_splits > 1:
+            ws = (torch.empty((len(lens), 14, num_splits, 64), device="cuda"),
+                  torch.empty((len(lens), 14, num_splits), device="cuda"),
+                  torch.empty((len(lens), 14, num_splits), device="cuda"))
+        out = torch.empty_like(q)
+        _decode_with_workspace(q, k, v, table, sl, out, 1.0 / 8.0, 32, num_splits, ws, k.shape[0])
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("num_splits", [1, 8])
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_head_dim_64_fused_append_through_the_abi(num_splits, block_size):
+    """The C ABI's fused append at head_dim 64 (the public API keeps the reference's refusal)."""
+    from flashdec_amd.paged_decode import _decode_with_workspace
+
+    prior = (0, 17, 256, 31)
+    lens_after = [p + 1 for p in prior]
+    q, k, v, table, lens = make_paged_inputs(lens_after, 16, 2, 64, block_size, torch.float16, seed=17)
+    expected = _oracle(q, k, v, table, lens)
+    slots = _slots(table, lens.cpu(), block_size)
+    append_k = torch.empty((4, 2, 64), device="cuda", dtype=torch.float16)
+    append_v = torch.empty_like(append_k)
+    k_expected, v_expected = k.clone(), v.clone()
+    for b, s in enumerate(slots):
+        blk, off = divmod(s, block_size)
+        append_k[b] = k[blk, :, off]
+        append_v[b] = v[blk, :, off]
+        k[blk, :, off] = float("nan")
+        v[blk, :, off] = float("nan")
+    ws = None
+    if num_splits > 1:
+        ws = (torch.empty((4, 16, num_splits, 64), device="cuda"), torch.empty((4, 16, num_splits), device="cuda"),
+              torch.empty((4, 16, num_splits), device="cuda"))
+    out = torch.empty_like(q)
+    _decode_with_workspace(q, k, v, table, lens, out, 1.0 / 8.0, block_size, num_splits, ws, k.shape[0],
+                           append=(append_k, append_v, torch.tensor(slots, device="cuda", dtype=torch.int64)))
+    assert_close_to_oracle(out, expected)
+    assert np.array_equal(bits16(k), bits16(k_expected))
+    assert np.array_equal(bits16(v), bits16(v_expected))
