@@ -712,9 +712,13 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   const int g = lane >> 4;
   int nsplit = PREFIX ? cp.prefix_splits : p.splits;
   int split = block % nsplit;
-  const int pair = block / nsplit;  // (request, KV head), or (group, KV head, chunk)
+  // (request, KV head[, head block]), or (group, KV head, chunk)
+  const int pair = block / nsplit;
   const int G = p.group;
-  int b, kvh, chunk = 0;
+  // Row role: more than 16 query heads per KV head take ceil(G / 16) head
+  // blocks of 16 MFMA columns, one per workgroup (each reads the K/V again).
+  const int hblocks = ROLE == Role::kRow ? (G + 15) >> 4 : 1;
+  int b, kvh, chunk = 0, hb = 0;
   const int32_t* mem = nullptr;
   int64_t bal_eff = 0;
   if constexpr (BAL) {
@@ -733,16 +737,19 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     mem = cp.members + static_cast<int64_t>(gk / p.hkv) * cp.max_members;
     b = mem[0];  // the lead: its table row holds the prefix's block ids
   } else {
-    b = pair / p.hkv;
-    kvh = pair % p.hkv;
+    const int pk = pair / hblocks;
+    hb = pair - pk * hblocks;
+    b = pk / p.hkv;
+    kvh = pk % p.hkv;
   }
   const bool lead_ok = !PREFIX || (b >= 0 && b < p.num_seqs);
   const int trow = lead_ok ? b : 0;  // table row read for K/V
 
-  // column c's output row: the request's head kvh * G + c (c < G), or in the
-  // prefix role the group row 16 * chunk + c (member index, head)
-  int col_b = b, col_h = c;
-  bool col_ok = c < G;
+  // column c's output row: the request's head kvh * G + 16 * hb + c (below
+  // G), or in the prefix role the group row 16 * chunk + c (member index,
+  // head)
+  int col_b = b, col_h = 16 * hb + c;
+  bool col_ok = col_h < G;
   if constexpr (PREFIX) {
     const int r = 16 * chunk + c;
     const int mi = r / G;
@@ -858,7 +865,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, trow, next + kWaves);
       }
       if constexpr (FUSE)
-        if (app >= 0 && app / UNIT == unit) store_append<T, BS, D>(p, kvh, slot, c, g, ar);
+        if (app >= 0 && app / UNIT == unit && hb == 0) store_append<T, BS, D>(p, kvh, slot, c, g, ar);
       process_unit<T, (FUSE != 0), UNIT, D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
       unit = next;
       next_pages = after;
@@ -903,8 +910,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   constexpr int kDimThreads = D / 8;
   const int h = (threadIdx.x / kDimThreads) & 15;
   const int d0 = (threadIdx.x % kDimThreads) * 8;
-  int ob = b, qh = kvh * G + h;
-  bool head_ok = threadIdx.x < 16 * kDimThreads && h < G;
+  int ob = b, qh = kvh * G + 16 * hb + h;
+  bool head_ok = threadIdx.x < 16 * kDimThreads && 16 * hb + h < G;
   if constexpr (PREFIX) {
     ob = lds.col_b[h];
     qh = kvh * G + lds.col_h[h];
@@ -1343,11 +1350,12 @@ int device_cus() {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// The MFMA row kernel: head_dim 128 or 64, <= 16 query heads per KV head,
-// unit dim strides and 16-byte aligned rows.  The cascade, per-row splits,
-// fused RoPE and the in-launch merge need head_dim 128 as well.
+// The MFMA row kernel: head_dim 128 or 64, unit dim strides and 16-byte
+// aligned rows (groups of more than 16 query heads per KV head take several
+// head blocks).  The cascade, per-row splits, fused RoPE and the in-launch
+// merge need head_dim 128 and <= 16 query heads per KV head as well.
 bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
-  if ((a.head_dim != 128 && a.head_dim != 64) || group > 16) return false;
+  if ((a.head_dim != 128 && a.head_dim != 64) || group > 256) return false;
   if (a.q_stride[2] != 1 || a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
   const int64_t strides[] = {a.q_stride[0], a.q_stride[1], a.k_stride[0], a.k_stride[1], a.k_stride[2],
                              a.v_stride[0], a.v_stride[1], a.v_stride[2]};
@@ -1486,11 +1494,13 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   const bool nt = a.kv_reuse == 0;  // stream K/V past the caches
   // the in-launch merge exists only in the MFMA kernel and writes the
   // workspace with 8-byte stores (unit dim stride, 8-byte aligned rows)
-  if (!fast || a.head_dim != 128 || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
+  const bool narrow = a.head_dim == 128 && p.group <= 16;  // one head block of 128-dim heads
+  if (!fast || !narrow || p.splits == 1 || p.as3 != 1 || (p.as2 & 1) || (p.as1 & 1) || (p.as0 & 1) ||
       (reinterpret_cast<uintptr_t>(p.acc) & 7u))
     p.counters = nullptr;
-  // balanced splits need the MFMA kernel at head_dim 128, no fused append and a workspace
-  const bool balanced = p.bal_target > 0 && fast && a.head_dim == 128 && !p.fuse && p.splits > 1;
+  // balanced splits need the MFMA kernel with one head block of 128-dim
+  // heads, no fused append and a workspace
+  const bool balanced = p.bal_target > 0 && fast && narrow && !p.fuse && p.splits > 1;
   if (!balanced) p.bal_target = 0;
   if (balanced) {
     p.counters = nullptr;
@@ -1513,7 +1523,8 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
         break;
     }
   } else if (fast) {
-    const dim3 grid(static_cast<unsigned>(pairs * p.splits));
+    const int64_t hblocks = (p.group + 15) / 16;
+    const dim3 grid(static_cast<unsigned>(pairs * hblocks * p.splits));
     switch (a.block_size) {
       case 8: launch_mfma<T, 8>(p, nt, grid, stream, a.timing_events); break;
       case 16: launch_mfma<T, 16>(p, nt, grid, stream, a.timing_events); break;
@@ -1608,10 +1619,12 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
   if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seq_len < 0 ||
       total_seq_len < 0)
     return set_error(FD_E_INVALID, "fd_paged_decode_plan: non-positive shape");
-  (void)num_q_heads;
-  (void)head_dim;
   const int64_t tiles = (max_seq_len + 31) / 32;
-  const int64_t pairs = num_seqs * num_kv_heads;
+  // groups of more than 16 query heads per KV head: one workgroup per head
+  // block of 16, each reading the row's K/V
+  const int64_t group = num_q_heads / num_kv_heads;
+  const int64_t hblocks = (head_dim == 128 || head_dim == 64) ? (group + 15) / 16 : 1;
+  const int64_t pairs = num_seqs * num_kv_heads * hblocks;
   const int64_t cus = device_cus();
   // one workgroup per CU for a batch of equal rows: fewer, longer splits
   // measured best for long uniform rows (36-layer B64 ctx8192 step: 2 splits
@@ -1623,7 +1636,7 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
   int64_t balance;
   if (total_seq_len > 0) {
     // in tokens, with 1/8 slack so rounding never lifts a uniform batch
-    const int64_t work = 8 * total_seq_len * num_kv_heads;
+    const int64_t work = 8 * total_seq_len * num_kv_heads * hblocks;
     balance = (7 * max_seq_len * cus + work - 1) / work;
   } else {
     balance = (tiles + kMaxSplitTiles - 1) / kMaxSplitTiles;
@@ -1673,7 +1686,8 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
   if (fuse != (a.append_v != nullptr) || fuse != (a.slot_mapping != nullptr))
     return set_error(FD_E_INVALID, "%s: append_k, append_v and slot_mapping go together", fn);
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
-  if (pairs * a.num_splits > 0x7fffffffLL || a.num_seqs * a.num_q_heads > 0x7fffffffLL)
+  const int64_t hblocks = (a.num_q_heads / a.num_kv_heads + 15) / 16;
+  if (pairs * hblocks * a.num_splits > 0x7fffffffLL || a.num_seqs * a.num_q_heads > 0x7fffffffLL)
     return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
 
   p = DecodeParams{};
@@ -1796,7 +1810,7 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
     return set_error(FD_E_INVALID, "%s: cascade struct_size %u != %zu (ABI mismatch)", fn, c.struct_size,
                      sizeof(fd_cascade_args));
   if (p.fuse) return set_error(FD_E_UNSUPPORTED, "%s: fused append is not supported (append first)", fn);
-  if (a.head_dim != 128 || !fast_path_ok(a, p.group))
+  if (a.head_dim != 128 || p.group > 16 || !fast_path_ok(a, p.group))
     return set_error(FD_E_UNSUPPORTED,
                      "%s: needs head_dim 128, <= 16 query heads per KV head, unit dim stride and 16-byte rows", fn);
   if (c.num_groups < 0 || c.max_members < 1 || c.prefix_splits < 1)

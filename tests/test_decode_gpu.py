@@ -397,3 +397,43 @@ def test_head_dim_64_fused_append_through_the_abi(num_splits, block_size):
     assert_close_to_oracle(out, expected)
     assert np.array_equal(bits16(k), bits16(k_expected))
     assert np.array_equal(bits16(v), bits16(v_expected))
+
+
+@pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(32, 2, 128), (48, 2, 128), (24, 1, 64), (71, 1, 64),
+                                                     (64, 1, 128)])
+def test_groups_above_16_heads_take_head_blocks(hq, hkv, head_dim):
+    """More than 16 query heads per KV head: ceil(G / 16) head blocks on the MFMA kernel."""
+    lens = [1, 100, 2048, 3000]
+    q, k, v, table, sl = make_paged_inputs(lens, hq, hkv, head_dim, 32, torch.bfloat16, seed=hq + head_dim)
+    out = _fd().decode(q, k, v, table, sl)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("num_splits", [1, 5])
+def test_groups_above_16_fused_append_written_once(num_splits):
+    """Every head block attends to the appended token; the cache holds it exactly."""
+    from flashdec_amd.paged_decode import _decode_with_workspace
+
+    lens_after = [18, 257, 64]
+    q, k, v, table, lens = make_paged_inputs(lens_after, 40, 2, 128, 32, torch.bfloat16, seed=41)
+    expected = _oracle(q, k, v, table, lens)
+    slots = _slots(table, lens.cpu(), 32)
+    ak = torch.empty((3, 2, 128), device="cuda", dtype=torch.bfloat16)
+    av = torch.empty_like(ak)
+    k_expected, v_expected = k.clone(), v.clone()
+    for b, s in enumerate(slots):
+        blk, off = divmod(s, 32)
+        ak[b] = k[blk, :, off]
+        av[b] = v[blk, :, off]
+        k[blk, :, off] = float("nan")
+        v[blk, :, off] = float("nan")
+    ws = None
+    if num_splits > 1:
+        ws = (torch.empty((3, 40, num_splits, 128), device="cuda"), torch.empty((3, 40, num_splits), device="cuda"),
+              torch.empty((3, 40, num_splits), device="cuda"))
+    out = torch.empty_like(q)
+    _decode_with_workspace(q, k, v, table, lens, out, 1.0 / math.sqrt(128), 32, num_splits, ws, k.shape[0],
+                           append=(ak, av, torch.tensor(slots, device="cuda", dtype=torch.int64)))
+    assert_close_to_oracle(out, expected)
+    assert np.array_equal(bits16(k), bits16(k_expected))
+    assert np.array_equal(bits16(v), bits16(v_expected))
