@@ -374,6 +374,11 @@ def paged_decode_attention_into(
             num_splits = max(2, min(balance, -(-max_seq_len // 32)))
         else:
             num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
+            if kv_layout == "dim_major" or head_dim not in (64, 128):
+                # the generic kernel runs one wave per workgroup: 8x the splits
+                # keeps ~8 waves per CU (dim-major B16 ctx8192: 515 -> 128 us),
+                # at most one 64-token tile per split
+                num_splits = max(1, min(8 * num_splits, -(-max_seq_len // 64), 4096))
         split_acc = split_max = split_sum = None
         if num_splits > 1:
             split_acc, split_max, split_sum, _ = _auto_workspace(q, num_kv_heads, num_splits, stream)
