@@ -64,11 +64,12 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine"),
+    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine", "formats"),
                    default="decode",
                    help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
                         "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
-                        "sharing a 16384-token prefix; engine: C5 36-layer step")
+                        "sharing a 16384-token prefix; engine: C5 36-layer step; formats: head_dim 64, large "
+                        "groups, MHA and dim-major caches")
     p.add_argument("--engine-steps", type=int, default=200, help="timed steps of the engine workload")
     return p.parse_args()
 
@@ -486,6 +487,48 @@ def run_prefix_large(torch, dev, args):
     return run_decode_variant(torch, dev, args, "shared-prefix-64x16384+U512", lens, 3, 7, prefix_blocks=512)
 
 
+def run_formats(torch, dev, args):
+    """General-path formats (beyond the C2 shape): head_dim 64, more than 16 query heads per KV
+    head, MHA, and dim-major caches, each B16 x 8192 tokens, bf16, block size 32, through the
+    public API (library-planned splits).  3 rotating pools each."""
+    import flashdec_amd as fd
+
+    cases = [  # name, Hq, Hkv, D, layout, kernel the library runs
+        ("d128-g8-token-major", 16, 2, 128, "token_major", "mfma"),
+        ("d64-g8-token-major", 16, 2, 64, "token_major", "mfma"),
+        ("d64-g7-token-major (Qwen2.5-0.5B heads)", 14, 2, 64, "token_major", "mfma"),
+        ("d128-g32-token-major", 64, 2, 128, "token_major", "mfma, 2 head blocks"),
+        ("d64-g71-token-major (MQA)", 71, 1, 64, "token_major", "mfma, 5 head blocks"),
+        ("d128-mha-token-major (B4)", 16, 16, 128, "token_major", "mfma"),
+        ("d128-g8-dim-major", 16, 2, 128, "dim_major", "generic"),
+        ("d64-g8-dim-major", 16, 2, 64, "dim_major", "generic"),
+    ]
+    lines = []
+    for name, hq, hkv, d, layout, kernel in cases:
+        batch = 4 if hq == hkv else 16
+        lens = [8192] * batch
+        pools = decode_pools(torch, dev, lens, hq, hkv, d, 32, 3, 31)
+        if layout == "dim_major":
+            pools = [(q, k.transpose(2, 3).contiguous(), v.transpose(2, 3).contiguous(), t, sl, o)
+                     for q, k, v, t, sl, o in pools]
+
+        def fn(i, pools=pools, layout=layout):
+            q, k, v, table, sl, o = pools[i % len(pools)]
+            fd.paged_decode_attention_into(q, k, v, table, sl, o, kv_layout=layout)
+
+        ms = graph_ms_per_call(torch, dev, fn, 60)
+        kv = sum(lens) * hkv * d * 2 * 2
+        log(f"[bench] formats {name}: {ms * 1e3:.2f} us/call, K/V {kv / (ms * 1e-3) / 1e12:.2f} TB/s ({kernel})")
+        lines.append({"case": name, "us_per_call": round(ms * 1e3, 2), "kv_bytes": kv,
+                      "kv_tb_per_s": round(kv / (ms * 1e-3) / 1e12, 3), "kernel": kernel})
+        del pools
+    out = common_fields(args, "paged-decode us/call over general-path formats, B16 x 8192 tokens bf16",
+                        lines[0]["us_per_call"], "us", lines[0]["us_per_call"] * 1e-3, False,
+                        {"workload": "formats-b16-ctx8192", "block_size": 32})
+    out["cases"] = lines
+    return out
+
+
 def run_engine(torch, dev, args):
     """C5: 36-layer DecodeEngine step, B64 Hq16 Hkv2 D128 bf16, context 8192, abort every 100th step."""
     from flashdec_amd.cache import PagedKVCache
@@ -661,7 +704,7 @@ def main():
     _lib.load_library()
     if args.workload != "decode":
         run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
-               "engine": run_engine}[args.workload]
+               "engine": run_engine, "formats": run_formats}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
         return
     batch, ctx, hq, hkv, d, bs = args.batch, args.ctx, 16, 2, 128, 32
