@@ -1,4 +1,4 @@
-"""Paged-decode benchmark on one MI355X (ctx 2048).
+"""Paged-decode benchmark on one MI355X (the headline B8 ctx2048 decode shape).
 
 A step is one ``paged_decode_attention_into`` call (the hot path) over one
 synthetic batch: B=8 requests, Hq=16 / Hkv=2 (Qwen2.5-3B attention shape),

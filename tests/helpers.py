@@ -5,7 +5,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-# attention vs an fp32 reference within atol 2e-2 / rtol 1e-2
+# Parity bar for attention against an fp32 reference: atol 2e-2 / rtol 1e-2
 ATOL = 2e-2
 RTOL = 1e-2
 

@@ -201,14 +201,14 @@ def test_vllm_launcher_full_cache_and_graph_padding(num_splits, cache_layout, in
 
 @pytest.mark.parametrize("ctx", [1024, 2048])
 def test_qwen_b8_shape_matches_oracle(ctx):
-    """B8, Hq16/Hkv2, D128, bf16, bs32, all seq_lens = ctx."""
+    """The headline shape: B8, Hq16/Hkv2, D128, bf16, bs32, all seq_lens = ctx."""
     q, k, v, table, lens = make_paged_inputs([ctx] * 8, 16, 2, 128, 32, torch.bfloat16, seed=20260830 + 8 + ctx)
     out = _fd().decode(q, k, v, table, lens, sm_scale=1.0 / math.sqrt(128))
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens, sm_scale=1.0 / math.sqrt(128)))
 
 
 def test_ragged_long_context_matches_oracle():
-    """BASELINE config 4 (scaled to 8 rows): L ~ logU[128, 32768]."""
+    """Ragged long context (scaled to 8 rows): L ~ logU[128, 32768]."""
     rng = np.random.default_rng(1701)
     lens = [int(round(math.exp(x))) for x in rng.uniform(math.log(128), math.log(32768), size=8)]
     q, k, v, table, sl = make_paged_inputs(lens, 16, 2, 128, 32, torch.bfloat16, seed=1701)

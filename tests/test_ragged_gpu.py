@@ -132,7 +132,7 @@ def test_engine_step_graph_on_a_ragged_batch():
 
 
 def test_full_c4_ragged_shape_rows_match_oracle():
-    """BASELINE config 4 at full size: B32, L ~ logU[128, 32768] (seed 1701),
+    """The ragged long-context shape at full size: B32, L ~ logU[128, 32768] (seed 1701),
     Hq16/Hkv2, D128, bf16, bs32.  Both split policies are checked against the
     oracle on the longest row, the shortest and three others."""
     import numpy as np
