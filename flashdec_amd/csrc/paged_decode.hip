@@ -681,15 +681,16 @@ struct alignas(16) DecodeLds {
   int last;
 };
 
-template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT, int D = 128>
+template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT, int D = 128,
+          int WAVES = waves_for<UNIT>()>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
-                                            DecodeLds<waves_for<UNIT>()>& lds) {
+                                            DecodeLds<WAVES>& lds) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
                 "cascade and balanced roles have no fused append or in-launch merge");
   static_assert(D == 128 || (ROLE == Role::kRow && FUSE != 2 && !MERGE),
                 "head_dim 64 runs the row role without RoPE or in-launch merge");
   constexpr int KS = D / 32;  // 32-dim pieces of q / K rows
-  constexpr int kWaves = waves_for<UNIT>();
+  constexpr int kWaves = WAVES;
   constexpr int kUnitsPerTile = 32 / UNIT;
   constexpr bool PREFIX = ROLE == Role::kPrefix;
   constexpr bool TAIL = ROLE == Role::kTail;
@@ -1047,10 +1048,16 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
 
 // Balanced splits (ragged batches): the row and split of each workgroup come
 // from the batch's lengths on the device.
+// Four waves per workgroup and two workgroups per CU: twice the splits of
+// the eight-wave layout at half the tiles each, so the heaviest CU carries
+// less above the mean.
+constexpr int kBalWaves = 4;
+constexpr int kBalPerCU = 2;
+
 template <typename T, int BS, bool NT>
-__global__ __launch_bounds__(64 * waves_for<16>(), 1) void decode_balanced_kernel(DecodeParams p) {
-  __shared__ DecodeLds<waves_for<16>()> lds;
-  decode_role<T, BS, false, false, 16, Role::kBalanced, NT>(p, CascadeParams{}, blockIdx.x, lds);
+__global__ __launch_bounds__(64 * kBalWaves, kBalPerCU) void decode_balanced_kernel(DecodeParams p) {
+  __shared__ DecodeLds<kBalWaves> lds;
+  decode_role<T, BS, false, false, 16, Role::kBalanced, NT, 128, kBalWaves>(p, CascadeParams{}, blockIdx.x, lds);
 }
 
 // Cascade launch: workgroups [0, prefix_blocks) take the prefix role, the
@@ -1245,8 +1252,11 @@ __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane_idx));
 }
 
-template <typename T, int D, int MODE = kReducePlain>
-__global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
+// W waves per (request, query head): wave w merges the w-th quarter of the
+// row's splits (W = 4, for rows with many splits: a single wave would wait
+// on its chunks one after another), then wave 0 merges the waves' states.
+template <typename T, int D, int MODE = kReducePlain, int W = 1>
+__global__ __launch_bounds__(64 * W) void split_reduce_kernel(ReduceParams p) {
   // every argument in SGPRs before any use: one batch of argument loads, one
   // wait (left alone the compiler fetched the strides lazily, a second
   // dependent round trip)
@@ -1255,7 +1265,8 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
                "s"(p.sls), "s"(p.slots), "s"(p.hq), "s"(p.splits), "s"(p.fuse), "s"(p.sl_i64), "s"(p.slot_i64));
   const int b = blockIdx.x / p.hq;
   const int qh = blockIdx.x % p.hq;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = W > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
   constexpr int E = D / 64;  // dims per lane
   // a VGPR zero keeps the uniform row-length / slot loads on the vector path
   int vzero = 0;
@@ -1285,8 +1296,11 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
   float o[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) o[e] = 0.f;
-  for (int s64 = 0; s64 < splits; s64 += 64) {
-    const int n = min(64, splits - s64);  // splits of this pass, one per lane
+  const int per = (splits + W - 1) / W;  // this wave's splits: [s_lo, s_hi)
+  const int s_lo = wave * per;
+  const int s_hi = min(splits, s_lo + per);
+  for (int s64 = s_lo; s64 < s_hi; s64 += 64) {
+    const int n = min(64, s_hi - s64);  // splits of this pass, one per lane
     const int sj = s64 + min(lane, n - 1);
     const float lm = p.mx[sb + sj * p.ss2];
     const float ll = p.sm[sb + sj * p.ss2];
@@ -1323,6 +1337,33 @@ __global__ __launch_bounds__(64) void split_reduce_kernel(ReduceParams p) {
         for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
       }
       M = nm;
+    }
+  }
+  if constexpr (W > 1) {
+    // the waves' states (a wave without splits holds M = -inf, L = 0, o = 0)
+    __shared__ float s_m[W], s_l[W];
+    __shared__ float s_o[W][D];
+    if (lane == 0) {
+      s_m[wave] = M;
+      s_l[wave] = L;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) s_o[wave][lane + 64 * e] = o[e];
+    __syncthreads();
+    if (wave != 0) return;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) mm = fmaxf(mm, s_m[w]);
+    const float mu = mm == -INFINITY ? 0.f : mm;
+    L = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float wt = exp2f(s_m[w] - mu);
+      L += wt * s_l[w];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] += wt * s_o[w][lane + 64 * e];
     }
   }
   const bool has = seq_len > 0 && (!p.fuse || slot >= 0);
@@ -1477,10 +1518,19 @@ ReduceParams reduce_params(const DecodeParams& p) {
 template <typename T, int MODE>
 int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
-  if (a.head_dim == 64)
-    dispatch(split_reduce_kernel<T, 64, MODE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
-  else
-    dispatch(split_reduce_kernel<T, 128, MODE>, grid, dim3(64), stream, a.timing_events[2], a.timing_events[3], r);
+  void* e0 = a.timing_events[2];
+  void* e1 = a.timing_events[3];
+  // more than 32 splits: four waves per row share them
+  if (r.splits > 32) {
+    if (a.head_dim == 64)
+      dispatch(split_reduce_kernel<T, 64, MODE, 4>, grid, dim3(256), stream, e0, e1, r);
+    else
+      dispatch(split_reduce_kernel<T, 128, MODE, 4>, grid, dim3(256), stream, e0, e1, r);
+  } else if (a.head_dim == 64) {
+    dispatch(split_reduce_kernel<T, 64, MODE>, grid, dim3(64), stream, e0, e1, r);
+  } else {
+    dispatch(split_reduce_kernel<T, 128, MODE>, grid, dim3(64), stream, e0, e1, r);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "split reduce launch failed: %s", hipGetErrorString(e));
   return FD_OK;
@@ -1506,7 +1556,7 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
     p.counters = nullptr;
     // sum over rows of ceil(tiles_b / T) <= bal_target + num_seqs
     const dim3 grid(static_cast<unsigned>(a.num_kv_heads * (p.bal_target + a.num_seqs)));
-    const dim3 block(64 * waves_for<16>());
+    const dim3 block(64 * kBalWaves);
     void* const* ev = a.timing_events;
     switch (a.block_size) {
       case 8:
@@ -1604,13 +1654,13 @@ using namespace fd;
 extern "C" int fd_paged_decode_balance_target(int64_t num_seqs, int64_t num_kv_heads) {
   if (num_seqs <= 0 || num_kv_heads <= 0)
     return set_error(FD_E_INVALID, "fd_paged_decode_balance_target: non-positive shape");
-  // One round of workgroups (one per CU): sum over rows of S_b <= V + B, so
-  // V = CUs / Hkv - B keeps the grid within it.  Ragged B32 on MI355X
-  // (Σ L = 206 k, max 30.7 k): attention 58.4 us with 16 uniform splits;
-  // V = 64 / 96 / 128 / 224: 46.9 / 41.9 / 56.2 / 44.2 us (128 spills into
-  // a second, mostly empty round).  A batch that already fills a round gets
-  // 0: uniform splits.
-  const int64_t v = device_cus() / num_kv_heads - num_seqs;
+  // One round of workgroups (kBalPerCU per CU): sum over rows of S_b <=
+  // V + B, so V = kBalPerCU * CUs / Hkv - B keeps the grid within it.
+  // Ragged B32 on MI355X (Σ L = 206 k, max 30.7 k): attention 58.4 us with
+  // 16 uniform splits; one 8-wave workgroup per CU, V = 64 / 96 / 128 / 224:
+  // 46.9 / 41.9 / 56.2 / 44.2 us; two 4-wave workgroups per CU, V = 224:
+  // 38.7 us.  A batch that already fills a round gets 0: uniform splits.
+  const int64_t v = kBalPerCU * device_cus() / num_kv_heads - num_seqs;
   return v >= num_seqs && v <= (1 << 20) ? static_cast<int>(v) : 0;
 }
 

@@ -245,7 +245,7 @@ int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads,
 /*
  * balance_target (fd_paged_decode_args) the library would use for a ragged
  * batch of this shape on the current device: about one round of workgroups
- * (one per CU) after the per-row rounding.  0 = not worth it (the batch
+ * (two per CU) after the per-row rounding.  0 = not worth it (the batch
  * fills a round already): use uniform splits.  The matching workspace is
  * num_splits = min(V, ceil(max_seq_len / 32)).
  */
