@@ -173,6 +173,7 @@ def paged_decode_attention_cascade_into(
     num_splits=None,
     prefix_splits=None,
     kv_reuse=True,
+    workspace=None,
 ):
     """Write shared-prefix decode attention into ``out``.
 
@@ -187,6 +188,9 @@ def paged_decode_attention_cascade_into(
     streams the private tails with non-temporal loads instead; the default
     keeps plain loads there too (on MI355X streamed tails took 14.0 vs 15.1 us
     for 16 rows x 4096 shared tokens but 55.4 vs 52.9 us for 64 x 16384).
+    ``workspace`` = ``(acc, max, sum)`` fp32 ``[>= B, >= Hq, >= S + S_p, D]`` /
+    ``[..., >= S + S_p]`` (equal max/sum strides) replaces the library's own,
+    e.g. for graph capture.
     """
     if block_size is None:
         if k_cache.dim() != 4:
@@ -219,7 +223,17 @@ def paged_decode_attention_cascade_into(
         if isinstance(v, bool) or not isinstance(v, int) or v <= 0:
             raise ValueError(f"{name} must be a positive integer")
     stream = _lib.current_stream_handle(q.device)
-    acc, mx, sm, _ = _auto_workspace(q, num_kv_heads, num_splits + prefix_splits, stream)
+    if workspace is None:
+        acc, mx, sm, _ = _auto_workspace(q, num_kv_heads, num_splits + prefix_splits, stream)
+    else:
+        acc, mx, sm = workspace
+        need = num_splits + prefix_splits
+        if (any(t.dtype != torch.float32 or t.device != q.device for t in (acc, mx, sm)) or acc.dim() != 4
+                or acc.shape[0] < num_seqs or acc.shape[1] < num_q_heads or acc.shape[2] < need
+                or acc.shape[3] != head_dim or mx.shape[:3] != acc.shape[:3] or sm.shape != mx.shape
+                or sm.stride() != mx.stride() or acc.stride(3) != 1):
+            raise ValueError("workspace must be fp32 (acc [>=B, >=Hq, >=S+S_p, D], max/sum [>=B, >=Hq, >=S+S_p]) "
+                             "on q.device with equal max/sum strides")
 
     args = _lib.PagedDecodeArgs()
     _fill_common(args, q, k_cache, v_cache, _cache_strides(k_cache, 2, 3), _cache_strides(v_cache, 2, 3),

@@ -29,6 +29,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Any, Hashable
 
+import numpy as np
+
 PROFILE_RANGE_PREFLIGHT = "flashdec::engine_preflight"
 PROFILE_RANGE_APPEND = "flashdec::rope_kv_append"
 PROFILE_RANGE_DECODE = "flashdec::paged_decode"
@@ -123,6 +125,23 @@ class DecodeStepGraph:
     balance_target: int = 0  # > 0: per-row split counts from the lengths at replay
     kv_reuse: bool = False  # rows shared prefix blocks at capture: plain (cached) K/V loads
     fused_rope: bool = False  # RoPE + append inside the decode launch (q_rot unused)
+    cascade: Any = None  # _GraphCascade: shared-prefix decode with per-replay group tables
+
+
+@dataclass
+class _GraphCascade:
+    """Group tables a cascade step graph reads at every replay.
+
+    The launch grid is fixed at capture for ``num_groups`` groups of at most
+    ``max_members`` rows; ``step_graph`` writes each step's groups (unused
+    slots -1 / 0) into ``buf`` before the replay, through a pinned staging ring.
+    """
+
+    groups: Any  # CascadeGroups whose tensors are views of buf
+    buf: Any
+    num_groups: int
+    max_members: int
+    staging: Any
 
 
 @dataclass
@@ -323,15 +342,40 @@ class DecodeEngine:
                                kv_reuse=bool(groups) and cascade is None)
         return handle
 
+    def _cascade_pays(self, groups):
+        """Whether a batch with these prefix groups should decode them with the cascade."""
+        if self._decode_kind != "hip" or self.cache.device.type != "cuda" or self.cascade_min_shared_tokens is None:
+            return False
+        bs = self.cache.block_size
+        return bool(groups) and max(len(rows) * blocks * bs for rows, blocks in groups) >= self.cascade_min_shared_tokens
+
+    def _write_graph_cascade(self, ids, gc):
+        """Pack this step's prefix groups into the cascade graph's tables (one async copy)."""
+        groups = self.cache._prefix_groups(ids)
+        if len(groups) > gc.num_groups or any(len(rows) > gc.max_members for rows, _ in groups):
+            raise RuntimeError(f"the step's prefix groups exceed the cascade step graph's capacity ({gc.num_groups} "
+                               f"groups of {gc.max_members} rows)")
+        bs = self.cache.block_size
+        ng, mm = gc.num_groups, gc.max_members
+        slot, host = gc.staging.acquire()
+        arr = host.numpy().view(np.int32)
+        members = arr[: ng * mm].reshape(ng, mm)
+        members.fill(-1)
+        arr[ng * mm:] = 0
+        for g, (rows, blocks) in enumerate(groups):
+            members[g, : len(rows)] = rows
+            arr[ng * mm + g] = blocks * bs
+            arr[ng * mm + ng + np.asarray(rows)] = blocks * bs
+        gc.buf.copy_(host.view(_torch().int32)[: gc.buf.numel()], non_blocking=True)
+        gc.staging.release(slot)
+
     def _step_cascade(self, ids, lengths, groups):
         """Prefix groups of this step's batch when the shared-prefix decode pays
         (the eager HIP path), else None.  Device tensors are kept per batch
         composition; only the planning figures follow the lengths."""
-        if self._decode_kind != "hip" or self.cache.device.type != "cuda" or self.cascade_min_shared_tokens is None:
+        if not self._cascade_pays(groups):
             return None
         bs = self.cache.block_size
-        if not groups or max(len(rows) * blocks * bs for rows, blocks in groups) < self.cascade_min_shared_tokens:
-            return None
         import dataclasses
 
         from .cascade import CascadeGroups
@@ -423,7 +467,7 @@ class DecodeEngine:
         return self._abort_open_step(self._require_open_step(transaction))
 
     def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None,
-                           merge=False, kv_reuse=None, fuse_rope=None):
+                           merge=False, kv_reuse=None, fuse_rope=None, cascade=None):
         """Capture every layer's launches of one token step into a hipGraph.
 
         Needs the HIP backends, a GPU cache and its graph-metadata arena
@@ -440,7 +484,11 @@ class DecodeEngine:
         cached loads instead of streaming them.  ``fuse_rope`` (default: where
         supported -- head_dim 128, rotary_dim 64 or 128, a 16-bit cache, no
         merge and no per-row splits) runs RoPE + append inside each layer's
-        decode launch, one kernel fewer per layer.
+        decode launch, one kernel fewer per layer.  ``cascade`` (default: when
+        active requests share a resident prefix as the eager steps' cascade
+        threshold asks) decodes each layer with the shared-prefix launch; the
+        group count and size of the active batch at capture bound every later
+        step's prefix groups, which each replay reads from the graph's tables.
         """
         torch = _torch()
         from . import _lib
@@ -468,11 +516,53 @@ class DecodeEngine:
         q_rot = torch.zeros_like(q)
         out = torch.zeros_like(q)
         width = meta.block_tables.shape[1]
+        groups_now = cache._prefix_groups(self.active_request_ids())
         if kv_reuse is None:
-            kv_reuse = bool(cache._prefix_groups(self.active_request_ids()))
+            kv_reuse = bool(groups_now)
         kv_reuse = bool(kv_reuse)
+        cas_ok = (self._cascade_pays(groups_now) and cache.head_dim == 128 and not merge
+                  and num_q_heads // cache.num_kv_heads <= 16 and dt in (torch.bfloat16, torch.float16))
+        if cascade is None:
+            cascade = cas_ok and not fuse_rope
+        elif cascade and (not cas_ok or fuse_rope):
+            raise ValueError("cascade needs active requests sharing a resident prefix (at least "
+                             "cascade_min_shared_tokens sharer-tokens), head_dim 128, <= 16 query heads per KV "
+                             "head, a bf16/fp16 cache, no merge and no fuse_rope")
+        cascade = bool(cascade)
         balance = 0
-        if num_splits is None:
+        gc = None
+        prefix_splits = 0
+        if cascade:
+            from ._lib import paged_decode_plan
+            from .cache import _StagingRing
+            from .cascade import CascadeGroups, _num_cus, plan_prefix_splits, prefix_chunks
+
+            ng = len(groups_now)
+            mm = max(len(rows) for rows, _ in groups_now)
+            buf = torch.zeros(ng * mm + ng + batch_size, dtype=torch.int32, device=dev)
+            prefix_tokens = [blocks * cache.block_size for _, blocks in groups_now]
+            active = cache._host_seq_lens(self.active_request_ids())
+            row_prefix = [0] * len(active)
+            for (rows, _), plen in zip(groups_now, prefix_tokens):
+                for r in rows:
+                    row_prefix[r] = plen
+            tails = [max(1, n + 1 - pr) for n, pr in zip(active, row_prefix)] or [1]
+            groups = CascadeGroups(members=buf[: ng * mm].view(ng, mm), prefix_len=buf[ng * mm: ng * mm + ng],
+                                   row_prefix_len=buf[ng * mm + ng:], max_prefix_len=max(prefix_tokens),
+                                   max_tail_len=max(tails), total_tail_len=sum(tails))
+            gc = _GraphCascade(groups=groups, buf=buf, num_groups=ng, max_members=mm,
+                               staging=_StagingRing(buf.numel() * 4))
+            if num_splits is None:
+                num_splits = paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
+                                               groups.max_tail_len, groups.total_tail_len)
+            prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads, prefix_chunks(groups, num_q_heads,
+                                                                                     cache.num_kv_heads),
+                                               groups.max_prefix_len, _num_cus(dev))
+        if cascade:
+            splits = int(num_splits)
+            if splits <= 0:
+                raise ValueError("num_splits must be a positive integer")
+        elif num_splits is None:
             # the batch's current lengths tell a uniform batch from a ragged one
             active = cache._host_seq_lens(self.active_request_ids())
             longest = max(active, default=0) + 1
@@ -493,7 +583,8 @@ class DecodeEngine:
         _validate_inputs(q_rot[0], cache.k_cache[0], cache.v_cache[0], meta.block_tables, meta.eff_lens,
                          cache.block_size, self.num_warps, self.num_stages, "token_major")
         eligible = (cache.head_dim == 128 and int(rotary_dim) in (64, 128) and not merge and not balance
-                     and dt in (torch.bfloat16, torch.float16) and num_q_heads // cache.num_kv_heads <= 16)
+                     and not cascade and dt in (torch.bfloat16, torch.float16)
+                     and num_q_heads // cache.num_kv_heads <= 16)
         if fuse_rope is None:
             fuse_rope = eligible
         elif fuse_rope and not eligible:
@@ -502,10 +593,11 @@ class DecodeEngine:
         fuse_rope = bool(fuse_rope)
         workspace = None
         counters = None
-        if splits > 1:
-            workspace = (torch.empty((batch_size, num_q_heads, splits, cache.head_dim), device=dev),
-                         torch.empty((batch_size, num_q_heads, splits), device=dev),
-                         torch.empty((batch_size, num_q_heads, splits), device=dev))
+        if splits + prefix_splits > 1:
+            ws_splits = splits + prefix_splits
+            workspace = (torch.empty((batch_size, num_q_heads, ws_splits, cache.head_dim), device=dev),
+                         torch.empty((batch_size, num_q_heads, ws_splits), device=dev),
+                         torch.empty((batch_size, num_q_heads, ws_splits), device=dev))
             if merge and not balance:
                 # arrival counters, zero before the capture; every launch leaves them at zero
                 counters = torch.zeros(batch_size * cache.num_kv_heads * _lib.SPLIT_COUNTER_STRIDE, device=dev,
@@ -517,6 +609,19 @@ class DecodeEngine:
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
                 for layer in range(cache.num_layers):
+                    if cascade:
+                        from .cascade import paged_decode_attention_cascade_into
+
+                        _fused_rope_kv_append_trusted(q[layer], k[layer], v[layer], cache.k_cache[layer],
+                                                      cache.v_cache[layer], meta.block_ids, meta.offsets,
+                                                      meta.positions, rotary_dim=rotary_dim, base=base,
+                                                      q_out=q_rot[layer])
+                        paged_decode_attention_cascade_into(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
+                                                            meta.block_tables, meta.eff_lens, out[layer],
+                                                            gc.groups, sm_scale=self.sm_scale,
+                                                            block_size=cache.block_size, num_splits=splits,
+                                                            prefix_splits=prefix_splits, workspace=workspace)
+                        continue
                     if fuse_rope:
                         _decode_with_workspace(q[layer], cache.k_cache[layer], cache.v_cache[layer],
                                                meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
@@ -537,7 +642,7 @@ class DecodeEngine:
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
                                num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,
                                workspace=workspace, balance_target=balance, kv_reuse=kv_reuse,
-                               fused_rope=fuse_rope)
+                               fused_rope=fuse_rope, cascade=gc)
 
     def step_graph(self, transaction, step_graph):
         """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.
@@ -558,6 +663,8 @@ class DecodeEngine:
             meta = self.cache.transaction_device_metadata(state.cache_transaction)
             if meta.buf.data_ptr() != step_graph.metadata.buf.data_ptr():
                 raise RuntimeError("transaction metadata is not in the graph metadata arena")
+            if step_graph.cascade is not None:
+                self._write_graph_cascade(state.handle.request_ids, step_graph.cascade)
             step_graph.graph.replay()
             self.cache._record_graph_layers(state.cache_transaction)
         except Exception:

@@ -75,3 +75,70 @@ def test_prefix_group_decodes_with_the_cascade():
     assert cascaded._cascade_decode_count == 4 * L and per_row._cascade_decode_count == 0
     assert torch.equal(cascaded.cache.k_cache, per_row.cache.k_cache)
     assert cascaded.validate_invariants() and per_row.validate_invariants()
+
+
+def test_cascade_step_graph_matches_per_row_graph():
+    """Step graphs with the shared-prefix launch: every replay reads the step's groups, also after the
+    group's membership changes; outputs match a per-row graph and the oracle, cache bytes are equal."""
+    cascaded, per_row = make_engine(1), make_engine(None)
+    for e in (cascaded, per_row):
+        e.cache.enable_graph_metadata(5, 16)
+    sg_c = cascaded.capture_step_graph(5, HQ, base=1e6)
+    sg_p = per_row.capture_step_graph(5, HQ, base=1e6)
+    assert sg_c.cascade is not None and sg_c.cascade.num_groups == 1 and sg_c.cascade.max_members == 4
+    assert sg_p.cascade is None and sg_p.kv_reuse
+    g = torch.Generator(device="cuda").manual_seed(8)
+    for step in range(6):
+        if step == 3:  # 'c' leaves, 'late' joins the prefix group: same batch size and group capacity
+            for e in (cascaded, per_row):
+                e.finish_request("c")
+                e.add_request("late")
+                e.admit(["late"], prefix_id="sys")
+                e.cache.seed_context(["late"], 5)
+        ids = cascaded.active_request_ids()
+        assert ids == per_row.active_request_ids() and len(ids) == 5
+        q = torch.randn((L, 5, HQ, D), device="cuda", generator=g).to(torch.bfloat16)
+        k = torch.randn((L, 5, HKV, D), device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn((L, 5, HKV, D), device="cuda", generator=g).to(torch.bfloat16)
+        outs, txs = [], []
+        for e, sg in ((cascaded, sg_c), (per_row, sg_p)):
+            tx = e.begin_step(ids)
+            sg.q.copy_(q)
+            sg.k.copy_(k)
+            sg.v.copy_(v)
+            outs.append(e.step_graph(tx, sg).clone())
+            txs.append(tx)
+        torch.cuda.synchronize()
+        tx = txs[0]
+        for layer in range(L):
+            q_rot = orope.apply_rope(q[layer].float().cpu().numpy(), tx.positions.cpu().numpy(), base=1e6,
+                                     out_dtype="bfloat16")
+            expected = oa.paged_decode_attention(q_rot, cascaded.cache.k_cache[layer].float().cpu().numpy(),
+                                                 cascaded.cache.v_cache[layer].float().cpu().numpy(),
+                                                 tx.block_tables.cpu().numpy(), tx.effective_seq_lens.cpu().numpy())
+            assert_close_to_oracle(outs[0][layer], expected)
+            assert_close_to_oracle(outs[0][layer], outs[1][layer].float().cpu().numpy())
+        for e, t in zip((cascaded, per_row), txs):
+            e.commit_step(t)
+    assert torch.equal(cascaded.cache.k_cache.view(torch.int16), per_row.cache.k_cache.view(torch.int16))
+    assert torch.equal(cascaded.cache.v_cache.view(torch.int16), per_row.cache.v_cache.view(torch.int16))
+    assert cascaded.validate_invariants() and per_row.validate_invariants()
+
+
+def test_cascade_step_graph_refuses_a_larger_group():
+    engine = make_engine(1)
+    engine.cache.enable_graph_metadata(5, 16)
+    sg = engine.capture_step_graph(5, HQ, base=1e6)
+    assert sg.cascade is not None
+    engine.finish_request("solo")
+    engine.add_request("e")
+    engine.admit(["e"], prefix_id="sys")  # the group grows to 5 rows, the graph holds 4
+    engine.cache.seed_context(["e"], 2)
+    tx = engine.begin_step()
+    with pytest.raises(RuntimeError, match="exceed the cascade step graph's capacity"):
+        engine.step_graph(tx, sg)
+    assert engine.metrics()["open_step_transaction_count"] == 0 and engine.validate_invariants()
+    no_cascade = make_engine(None)
+    no_cascade.cache.enable_graph_metadata(5, 16)
+    with pytest.raises(ValueError, match="cascade needs"):
+        no_cascade.capture_step_graph(5, HQ, cascade=True)
