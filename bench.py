@@ -64,12 +64,14 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine", "formats"),
+    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine",
+                                          "engine-prefix", "formats"),
                    default="decode",
                    help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
                         "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
-                        "sharing a 16384-token prefix; engine: C5 36-layer step; formats: head_dim 64, large "
-                        "groups, MHA and dim-major caches")
+                        "sharing a 16384-token prefix; engine: C5 36-layer step; engine-prefix: 36-layer steps "
+                        "of 64 rows sharing a 16384-token prefix; formats: head_dim 64, large groups, MHA and "
+                        "dim-major caches")
     p.add_argument("--engine-steps", type=int, default=200, help="timed steps of the engine workload")
     return p.parse_args()
 
@@ -529,6 +531,73 @@ def run_formats(torch, dev, args):
     return out
 
 
+def run_engine_prefix(torch, dev, args):
+    """36-layer DecodeEngine steps over a shared prefix: B64 rows attached to one resident
+    16384-token prefix, private tails ~ U{64..512}, Hq16 Hkv2 D128 bf16.  Two step graphs on the
+    same engine and schedule: the cascade (the engine's default here) and the per-row decode with
+    cached K/V loads."""
+    import numpy as np
+
+    from flashdec_amd.cache import PagedKVCache
+    from flashdec_amd.engine import DecodeEngine
+
+    layers, batch, hq, hkv, d, bs, prefix = 36, 64, 16, 2, 128, 32, 16384
+    steps = max(20, args.engine_steps // 2)
+    tails = np.random.default_rng(77).integers(64, 513, size=batch)
+    pb = prefix // bs
+    width = pb + (int(tails.max()) + 2 * steps + 64 + bs - 1) // bs
+    cache = PagedKVCache(layers, hkv, d, bs, max_blocks=pb + batch * (width - pb), dtype=torch.bfloat16,
+                         device=dev, prefix_cache_capacity_blocks=pb)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(113)
+    for layer in range(layers):
+        cache.k_cache[layer].normal_(generator=gen)
+        cache.v_cache[layer].normal_(generator=gen)
+    cache.enable_graph_metadata(batch, width)
+    engine = DecodeEngine(cache)
+    shape = (layers, pb, hkv, bs, d)
+    engine.register_prefix("sys", torch.empty(shape, device=dev, dtype=torch.bfloat16).normal_(generator=gen),
+                           torch.empty(shape, device=dev, dtype=torch.bfloat16).normal_(generator=gen))
+    ids = list(range(batch))
+    for rid in ids:
+        engine.add_request(rid)
+    engine.admit(ids, prefix_id="sys")
+    for rid, t in zip(ids, tails):
+        cache.seed_context([rid], int(t))
+    log(f"[bench] engine-prefix: {layers} layers, B{batch} sharing {prefix} tokens, tails U{{64..512}}")
+    result = {}
+    for name, cascade in (("cascade", True), ("per_row", False)):
+        sg = engine.capture_step_graph(batch, hq, base=1e6, cascade=cascade)
+        sg.q.normal_(generator=gen)
+        sg.k.normal_(generator=gen)
+        sg.v.normal_(generator=gen)
+
+        def step(sg=sg):
+            tx = engine.begin_step(ids)
+            engine.step_graph(tx, sg)
+            engine.commit_step(tx)
+
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            step()
+        stop.record()
+        torch.cuda.synchronize()
+        result[name] = start.elapsed_time(stop) / steps
+        log(f"[bench] engine-prefix {name}: {result[name]:.3f} ms/step")
+        del sg
+    out = common_fields(args, "36-layer DecodeEngine step ms over a shared 16384-token prefix, B64",
+                        round(result["cascade"], 4), "ms/step", result["cascade"], False,
+                        {"workload": "engine-prefix-36l-b64-16384", "layers": layers, "batch": batch,
+                         "prefix_tokens": prefix, "tails": "U{64..512}", "steps": steps, "path": "cascade graph"})
+    out["tokens_per_s"] = round(batch / (result["cascade"] * 1e-3), 1)
+    out["per_row_path"] = {"ms_per_step": round(result["per_row"], 4), "kv_loads": "plain (kv_reuse)"}
+    return out
+
+
 def run_engine(torch, dev, args):
     """C5: 36-layer DecodeEngine step, B64 Hq16 Hkv2 D128 bf16, context 8192, abort every 100th step."""
     from flashdec_amd.cache import PagedKVCache
@@ -704,7 +773,7 @@ def main():
     _lib.load_library()
     if args.workload != "decode":
         run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
-               "engine": run_engine, "formats": run_formats}[args.workload]
+               "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
         return
     batch, ctx, hq, hkv, d, bs = args.batch, args.ctx, 16, 2, 128, 32
