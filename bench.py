@@ -502,8 +502,8 @@ def run_formats(torch, dev, args):
         ("d128-g32-token-major", 64, 2, 128, "token_major", "mfma, 2 head blocks"),
         ("d64-g71-token-major (MQA)", 71, 1, 64, "token_major", "mfma, 5 head blocks"),
         ("d128-mha-token-major (B4)", 16, 16, 128, "token_major", "mfma"),
-        ("d128-g8-dim-major", 16, 2, 128, "dim_major", "generic"),
-        ("d64-g8-dim-major", 16, 2, 64, "dim_major", "generic"),
+        ("d128-g8-dim-major", 16, 2, 128, "dim_major", "mfma, K staged through LDS"),
+        ("d64-g8-dim-major", 16, 2, 64, "dim_major", "mfma, K staged through LDS"),
     ]
     lines = []
     for name, hq, hkv, d, layout, kernel in cases:

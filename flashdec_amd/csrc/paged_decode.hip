@@ -1,16 +1,20 @@
 // Paged single-token decode attention for gfx950 (MI355X).
 //
-// Work decomposition: one workgroup per (request, KV head, KV split).  The
-// split covers a contiguous range of 32-token tiles; the four waves of the
-// workgroup take its tiles round-robin, each keeping its own online-softmax
-// state for all query heads of the KV head (grouped GQA), and the waves are
-// merged in LDS so that one partial (or the final row) leaves the workgroup.
+// Work decomposition: one workgroup per (request, KV head, head block of 16
+// query heads, KV split).  The split covers a contiguous range of 32-token
+// tiles; the waves of the workgroup take its units round-robin, each keeping
+// its own online-softmax state for the block's query heads (grouped GQA), and
+// the waves are merged in LDS so that one partial (or the final row) leaves
+// the workgroup.
 //
-//  * decode_mfma_kernel  -- head_dim 128, <= 16 query heads per KV head,
-//    unit dim stride (token-major, vLLM NHD/HND views).  QK^T and PV run on
-//    v_mfma_f32_16x16x32_{bf16,f16}; V is transposed in registers.
-//  * decode_generic_kernel -- any strides (dim-major caches), head_dim 64,
-//    any group size; VALU only.
+//  * decode_mfma_kernel  -- token-major caches with unit dim stride (vLLM
+//    NHD/HND views too), head_dim 64 or 128, any group size.  QK^T and PV
+//    run on v_mfma_f32_16x16x{32,16}_{bf16,f16}; V is transposed in
+//    registers.  Also the body of the per-row (balanced) and cascade kernels.
+//  * decode_dm_kernel    -- dim-major caches (16/32-token blocks): V loads
+//    straight into the PV operand, K goes through LDS and comes back
+//    transposed (ds_read_b64_tr_b16).
+//  * decode_generic_kernel -- any strides; VALU only.
 //  * split_reduce_kernel -- LSE merge of the split partials.
 //
 // Reference semantics followed (cysong2025/flashdec):
@@ -325,6 +329,94 @@ __device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const Uni
   t.bmask = bm;
 }
 
+// ------------------------------------------------- dim-major caches ----
+// A dim-major cache ([blocks, KV heads, head_dim, block_size], token stride
+// 1) stores a head's block as head_dim rows of block_size tokens.  A 32-token
+// unit is read as 16-byte pieces of those rows (eight tokens of one dim), and
+// the lane tokens are reordered so that lane 16*g + c scores tokens 8*g + i,
+// i < 8 (i = 4*mt + r: row 4*g + r of QK row block mt):
+//   K piece i of lane l: dim 16*i + l/4, tokens 8*(l%4) + [0, 8) -- staged
+//     through LDS and read back transposed into the QK A operand
+//   vf[n] of lane 16*g + c: dim (D/16)*c + n, tokens 8*g + [0, 8) -- already
+//     the PV A operand (V^T row (D/16)*c + n, k = the lane's eight tokens)
+// (D = 128: K pieces i < 8 and V operands n < 8; D = 64: four of each.)
+// Block sizes 16 and 32: a piece lies in one block (block a, or b for the
+// second half of a unit on 16-token blocks).
+constexpr int kDmWaves = 4;
+constexpr int kDmRowBytes = 64;  // one staged dim row: 32 tokens x 2 bytes
+
+template <int D>
+struct DmRegs {
+  static constexpr int KS = D / 32;  // QK k-steps
+  u32x4 kf[2][KS];                   // raw K pieces, then QK A operands
+  u32x4 vf[D / 16];                  // PV A operands
+  uint32_t bmask;                    // bit i: token 8*g + i lies in a valid block
+};
+
+template <typename T, int BS, bool NT, int D>
+__device__ __forceinline__ void load_unit_dm(const DecodeParams& p, int kvh, const UnitPages& up, int lane,
+                                             DmRegs<D>& t) {
+  constexpr int KS = DmRegs<D>::KS;
+  static_assert(BS == 16 || BS == 32, "dim-major units need 16- or 32-token blocks");
+  constexpr int64_t E = sizeof(T);
+  const bool oka = up.a >= 0 && up.a < p.num_blocks;
+  const bool okb = BS == 16 ? (up.b >= 0 && up.b < p.num_blocks) : oka;
+  const int32_t blk_a = oka ? up.a : 0;  // invalid blocks read block 0 (masked later)
+  const int32_t blk_b = okb ? up.b : 0;
+  const int q = lane & 3;   // K: the lane's eight-token quarter of the unit
+  const int g = lane >> 4;  // V: the lane's eight tokens
+  const int c = lane & 15;
+  const int32_t kblk = (BS == 16 && q >= 2) ? blk_b : blk_a;
+  const int32_t vblk = (BS == 16 && g >= 2) ? blk_b : blk_a;
+  const char* kp = static_cast<const char*>(p.k) +
+                   (kblk * p.ks0 + kvh * p.ks1 + (lane >> 2) * p.ks3 + (8 * q) % BS) * E;
+  const char* vp =
+      static_cast<const char*>(p.v) + (vblk * p.vs0 + kvh * p.vs1 + (D / 16) * c * p.vs3 + (8 * g) % BS) * E;
+  const int64_t kstep = 16 * p.ks3 * E;
+  const int64_t vstep = p.vs3 * E;
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) t.kf[i / KS][i % KS] = kv_load<NT>(kp + i * kstep);
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) t.vf[n] = kv_load<NT>(vp + n * vstep);
+  t.bmask = ((BS == 16 && g >= 2) ? okb : oka) ? 0xffu : 0u;
+}
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// The unit's raw K pieces go to the wave's LDS stage (row = dim, 64 bytes
+// of tokens) and come back as QK A operands: kf[mt][s] of lane 16*g + c =
+// token 8*(c/4) + 4*mt + c%4 (A row c), dims 32*s + 8*g + [0, 8).  One
+// ds_read_b64_tr_b16 gives lane c of a 16-lane group element j of the
+// 8-byte piece addressed by lane 4*j + c/4, element c%4; so lane c' of the
+// group addresses dim row base + c'/4 at tokens 8*(c'%4) + 4*mt + [0, 4).
+// A wave's LDS operations run in order, so the stage needs no barrier
+// between the writes and the reads, nor before the next unit's writes.
+template <int D>
+__device__ __forceinline__ void stage_k_dm(DmRegs<D>& t, uint8_t* stage, int lane) {
+  constexpr int KS = DmRegs<D>::KS;
+  lds_u8* st = (lds_u8*)stage;
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i)
+    *(lds_u32x4*)(st + (16 * i + (lane >> 2)) * kDmRowBytes + 16 * (lane & 3)) = t.kf[i / KS][i % KS];
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  lds_u8* rd = st + (8 * g + (c >> 2)) * kDmRowBytes + 16 * (c & 3);
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      lds_u8* a = rd + 32 * s * kDmRowBytes + 8 * mt;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a + 4 * kDmRowBytes));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+      const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+      t.kf[mt][s] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    }
+  }
+}
+
 // The appended token's pieces in this lane's operand layout: akf[s] = dims
 // [32*s + 8*g, +8) of append_k, avf = dims [(D/16)*c, +D/16) of append_v.
 template <int D = 128>
@@ -555,6 +647,72 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (
   }
 }
 
+// process_unit for a dim-major unit (load_unit_dm's layout): the lane's
+// scores and V columns are tokens 8*g + i, and V needs no transposes.
+template <typename T, int D>
+__device__ __forceinline__ void process_unit_dm(DmRegs<D>& t, const u32x4 (&qf)[D / 32], float scale_log2,
+                                                int tok0, int first, int last, int lane, uint8_t* stage,
+                                                WaveState<D>& st) {
+  constexpr int KS = DmRegs<D>::KS;
+  constexpr int NTILE = D / 16;
+  const int g = lane >> 4;
+  stage_k_dm<D>(t, stage, lane);
+  uint32_t vmask = t.bmask;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int tok = tok0 + 8 * g + i;
+    vmask &= (tok <= last && (first == 0 || tok >= first)) ? ~0u : ~(1u << i);
+  }
+  float sc[8];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    f32x4 sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) sb = mfma16x16x32<T>(t.kf[mt][s], qf[s], sb);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[4 * mt + r] = sb[r] * scale_log2;
+  }
+  // masked tokens: -inf scores and zeroed V elements (word w of every V
+  // operand holds tokens 2w and 2w + 1)
+  if (__ballot(vmask != 0xffu)) {
+    uint32_t keep[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      keep[w] = (((vmask >> (2 * w)) & 1u) ? 0x0000ffffu : 0u) | (((vmask >> (2 * w + 1)) & 1u) ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sc[i] = ((vmask >> i) & 1u) ? sc[i] : -INFINITY;
+#pragma unroll
+    for (int n = 0; n < NTILE; ++n)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) t.vf[n][w] &= keep[w];
+  }
+  float mx = sc[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[i]);
+  mx = column_max(mx);
+  const float m_new = fmaxf(st.m, mx);
+  const float m_use = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = exp2_fast(st.m - m_use);
+  float pr[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pr[i] = exp2_fast(sc[i] - m_use);
+    psum += pr[i];
+  }
+  st.l = st.l * alpha + psum;
+  st.m = m_new;
+  if (__ballot(alpha != 1.f)) {
+#pragma unroll
+    for (int n = 0; n < NTILE; ++n) st.acc[n] *= alpha;
+  }
+  u32x4 pp;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) pp[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
+#pragma unroll
+  for (int n = 0; n < NTILE; ++n) st.acc[n] = mfma16x16x32<T>(t.vf[n], pp, st.acc[n]);
+}
+
 constexpr int kMaxWaves = 8;          // waves per workgroup of the 16-token variant
 constexpr int kWideUnitMaxTiles = 4;  // splits of at most this many tiles take 32-token units
 constexpr int kAccPitch = 132;   // floats per head row in LDS (bank spread)
@@ -681,14 +839,17 @@ struct alignas(16) DecodeLds {
   int last;
 };
 
+// DM: dim-major cache (load_unit_dm), staged through the LDS at kstage
 template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT, int D = 128,
-          int WAVES = waves_for<UNIT>()>
+          int WAVES = waves_for<UNIT>(), bool DM = false>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
-                                            DecodeLds<WAVES>& lds) {
+                                            DecodeLds<WAVES>& lds, [[maybe_unused]] uint8_t* kstage = nullptr) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
                 "cascade and balanced roles have no fused append or in-launch merge");
   static_assert(D == 128 || (ROLE == Role::kRow && FUSE != 2 && !MERGE),
                 "head_dim 64 runs the row role without RoPE or in-launch merge");
+  static_assert(!DM || (ROLE == Role::kRow && FUSE == 0 && !MERGE && UNIT == 32),
+                "dim-major caches run the row role on 32-token units");
   constexpr int KS = D / 32;  // 32-dim pieces of q / K rows
   constexpr int kWaves = WAVES;
   constexpr int kUnitsPerTile = 32 / UNIT;
@@ -809,14 +970,17 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   // address once, which keeps the kernel-argument loads ahead of the first
   // K/V loads in fewer dependent batches (C2: 6.2 vs 7.1 us).
   constexpr bool kFixed = BS >= 16 && UNIT == 16;
-  UnitRegs<UNIT, D> cur;
+  using Regs = std::conditional_t<DM, DmRegs<D>, UnitRegs<UNIT, D>>;
+  Regs cur;
   [[maybe_unused]] UnitOffsets<UNIT> offs;
   if constexpr (kFixed) offs = unit_offsets<T, BS, UNIT, D>(p, kvh, wave, c, g);
   // the prefix role's blocks are read again by the group's other chunks:
   // plain loads, so the re-reads hit the caches
   constexpr bool kNT = NT && !PREFIX;
-  auto load = [&](int u, const UnitPages& up, UnitRegs<UNIT, D>& dst) {
-    if constexpr (kFixed)
+  auto load = [&](int u, const UnitPages& up, Regs& dst) {
+    if constexpr (DM)
+      load_unit_dm<T, BS, kNT, D>(p, kvh, up, lane, dst);
+    else if constexpr (kFixed)
       load_unit_fixed<T, BS, UNIT, kNT, D>(p, up, offs, dst);
     else
       load_unit<T, BS, UNIT, kNT, D>(p, kvh, u, up, c, g, dst);
@@ -857,7 +1021,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     // One unit: issue the next unit's loads into `ahead` (and the block ids
     // after it), then consume `now`; false when `now` was the last.  The two
     // buffers take turns, so no registers are copied between units.
-    auto step = [&](UnitRegs<UNIT, D>& now, UnitRegs<UNIT, D>& ahead) -> bool {
+    auto step = [&](Regs& now, Regs& ahead) -> bool {
       const int next = unit + kWaves;
       const bool more = next < u_end;
       UnitPages after{0, 0};
@@ -867,13 +1031,17 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       }
       if constexpr (FUSE)
         if (app >= 0 && app / UNIT == unit && hb == 0) store_append<T, BS, D>(p, kvh, slot, c, g, ar);
-      process_unit<T, (FUSE != 0), UNIT, D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
+      if constexpr (DM)
+        process_unit_dm<T, D>(now, qf, p.scale_log2, unit * UNIT, first, last, lane,
+                              kstage + wave * D * kDmRowBytes, st);
+      else
+        process_unit<T, (FUSE != 0), UNIT, D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
       unit = next;
       next_pages = after;
       return more;
     };
-    UnitRegs<UNIT, D> alt;
-    if constexpr (UNIT == 16) {
+    Regs alt;
+    if constexpr (UNIT == 16 || DM) {
       while (step(cur, alt) && step(alt, cur)) {
       }
     } else {
@@ -1044,6 +1212,19 @@ template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 1
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(DecodeParams p) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
   decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT, D>(p, CascadeParams{}, blockIdx.x, lds);
+}
+
+// Dim-major caches: 32-token units on kDmWaves waves, K staged through LDS.
+// Two workgroups per CU (67 KB of LDS each): B16 x 8192 tokens, 16 splits,
+// 28.8 us against 30.0 us with one per CU and 29.9 us with one 8-wave
+// workgroup per CU at its best split count.
+constexpr int kDmPerCU = 2;
+
+template <typename T, int BS, bool NT, int D>
+__global__ __launch_bounds__(64 * kDmWaves, kDmPerCU) void decode_dm_kernel(DecodeParams p) {
+  __shared__ DecodeLds<kDmWaves> lds;
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kDmWaves * D * kDmRowBytes];
+  decode_role<T, BS, 0, false, 32, Role::kRow, NT, D, kDmWaves, true>(p, CascadeParams{}, blockIdx.x, lds, stage);
 }
 
 // Balanced splits (ragged batches): the row and split of each workgroup come
@@ -1421,6 +1602,21 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
   return true;
 }
 
+// Dim-major caches on the MFMA path (decode_dm_kernel): 64- or 128-dim heads,
+// 16- or 32-token blocks, token stride 1, 16-byte aligned dim rows, no fused
+// append.
+bool dm_path_ok(const fd_paged_decode_args& a, int64_t group) {
+  if ((a.head_dim != 128 && a.head_dim != 64) || group > 256 || (a.block_size != 16 && a.block_size != 32) ||
+      a.append_k)
+    return false;
+  if (a.q_stride[2] != 1 || a.k_stride[2] != 1 || a.v_stride[2] != 1) return false;
+  const int64_t strides[] = {a.q_stride[0], a.q_stride[1], a.k_stride[0], a.k_stride[1], a.k_stride[3],
+                             a.v_stride[0], a.v_stride[1], a.v_stride[3]};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return false;
+  return aligned16(a.q) && aligned16(a.k_cache) && aligned16(a.v_cache);
+}
+
 // One dispatch; events given are recorded at its start / end (profiling hook).
 template <typename F, typename... Args>
 void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, void* stop, Args... args) {
@@ -1480,6 +1676,17 @@ void launch_mfma(const DecodeParams& p, bool nt, dim3 grid, hipStream_t stream, 
     launch_mfma<T, BS, true>(p, grid, stream, ev);
   else
     launch_mfma<T, BS, false>(p, grid, stream, ev);
+}
+
+template <typename T, int D>
+void launch_dm(const DecodeParams& p, int64_t block_size, bool nt, dim3 grid, dim3 block, hipStream_t stream,
+               void* const* ev) {
+  if (block_size == 16)
+    nt ? dispatch(decode_dm_kernel<T, 16, true, D>, grid, block, stream, ev[0], ev[1], p)
+       : dispatch(decode_dm_kernel<T, 16, false, D>, grid, block, stream, ev[0], ev[1], p);
+  else
+    nt ? dispatch(decode_dm_kernel<T, 32, true, D>, grid, block, stream, ev[0], ev[1], p)
+       : dispatch(decode_dm_kernel<T, 32, false, D>, grid, block, stream, ev[0], ev[1], p);
 }
 
 ReduceParams reduce_params(const DecodeParams& p) {
@@ -1580,6 +1787,15 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
       case 16: launch_mfma<T, 16>(p, nt, grid, stream, a.timing_events); break;
       default: launch_mfma<T, 32>(p, nt, grid, stream, a.timing_events); break;
     }
+  } else if (dm_path_ok(a, p.group)) {
+    const int64_t hblocks = (p.group + 15) / 16;
+    const dim3 grid(static_cast<unsigned>(pairs * hblocks * p.splits));
+    const dim3 block(64 * kDmWaves);
+    void* const* ev = a.timing_events;
+    if (a.head_dim == 64)
+      launch_dm<T, 64>(p, a.block_size, nt, grid, block, stream, ev);
+    else
+      launch_dm<T, 128>(p, a.block_size, nt, grid, block, stream, ev);
   } else {
     const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
     const dim3 grid(static_cast<unsigned>(pairs * hg), static_cast<unsigned>(p.splits));

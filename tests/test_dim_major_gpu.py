@@ -1,0 +1,165 @@
+"""GPU parity of the dim-major MFMA decode kernel against the CPU oracle.
+
+Dim-major caches (``[blocks, kv_heads, head_dim, block_size]``, the
+reference's ``kv_layout="dim_major"``, flashdec/paged_reference.py:19-125)
+with 64- or 128-dim heads and 16- or 32-token blocks run the MFMA kernel that stages
+K through LDS.  These cases cover what that kernel adds over the token-major
+one: lengths that end inside a unit, a block or a quarter of a unit, head
+blocks (G > 16), explicit and planned splits, strided views, non-finite
+values past a row's end, table padding past the used range, and streamed
+against cached K/V loads (bit-identical).  Views whose strides or alignment
+the kernel does not take run the generic kernel and must agree as well.
+Tolerance: atol 2e-2 / rtol 1e-2 against the fp32 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import paged_decode_attention as oracle_decode
+from tests.helpers import assert_close_to_oracle, make_paged_inputs, np32
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16]
+
+
+def _fd():
+    import flashdec_amd
+
+    return flashdec_amd
+
+
+def _oracle(q, k, v, table, lens, sm_scale=None):
+    return oracle_decode(np32(q), np32(k), np32(v), table.cpu().numpy(), lens.cpu().numpy(), sm_scale=sm_scale,
+                         kv_layout="dim_major")
+
+
+def _workspace(b, hq, splits, head_dim=128):
+    return (torch.empty((b, hq, splits, head_dim), device="cuda"), torch.empty((b, hq, splits), device="cuda"),
+            torch.empty((b, hq, splits), device="cuda"))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("lens", [[1, 7, 8, 9], [15, 16, 17, 31], [32, 33, 63, 64], [65, 100, 129, 0]])
+def test_lengths_end_inside_units(lens, block_size, head_dim, dtype):
+    q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, dtype, kv_layout="dim_major",
+                                           seed=21)
+    out = _fd().decode(q, k, v, table, sl, block_size=block_size, kv_layout="dim_major")
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(8, 8, 128), (4, 1, 128), (16, 2, 128), (32, 2, 128),
+                                                     (40, 2, 128), (64, 1, 128), (14, 2, 64), (71, 1, 64),
+                                                     (32, 32, 64)])
+def test_group_sizes_and_head_blocks(hq, hkv, head_dim, block_size, dtype):
+    q, k, v, table, sl = make_paged_inputs([300, 77, 1024], hq, hkv, head_dim, block_size, dtype,
+                                           kv_layout="dim_major", seed=23)
+    out = _fd().decode(q, k, v, table, sl, block_size=block_size, kv_layout="dim_major")
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, 16, 40])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_explicit_splits(num_splits, head_dim, dtype):
+    lens = [2049, 1500, 33, 4096]
+    q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, 32, dtype, kv_layout="dim_major", seed=25)
+    out = torch.empty_like(q)
+    _fd().paged_decode_attention_into(q, k, v, table, sl, out, block_size=32, kv_layout="dim_major",
+                                      split_kv_workspace=_workspace(4, 16, 40, head_dim), num_splits=num_splits)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_long_rows_planned_splits(block_size, head_dim, dtype):
+    lens = [8192, 6000, 8191, 3]
+    q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, dtype, kv_layout="dim_major",
+                                           seed=27)
+    out = _fd().decode(q, k, v, table, sl, block_size=block_size, kv_layout="dim_major")
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_non_finite_values_past_row_end_are_masked(block_size, head_dim):
+    lens = [45, 70, 5]
+    q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, torch.bfloat16,
+                                           kv_layout="dim_major", seed=29)
+    ref = _oracle(q, k, v, table, sl)
+    # every token slot past a row's length in its last block holds NaN / Inf
+    for b, n in enumerate(lens):
+        blk = int(table[b, (n - 1) // block_size])
+        tail = n % block_size
+        if tail:
+            k[blk, :, :, tail:] = float("nan")
+            v[blk, :, :, tail:] = float("inf")
+    out = _fd().decode(q, k, v, table, sl, block_size=block_size, kv_layout="dim_major")
+    assert_close_to_oracle(out, ref)
+
+
+def test_table_padding_past_used_range_is_never_read():
+    q, k, v, table, sl = make_paged_inputs([40, 90], 16, 2, 128, 16, torch.float16, kv_layout="dim_major",
+                                           seed=31, table_width=64, pad_value=2**30)
+    out = _fd().decode(q, k, v, table, sl, block_size=16, kv_layout="dim_major")
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_strided_dim_major_view(dtype):
+    # a [blocks, head_dim, kv_heads, block_size] allocation viewed as dim-major:
+    # head stride block_size, dim stride kv_heads * block_size
+    q, k, v, table, sl = make_paged_inputs([130, 61], 16, 2, 128, 32, dtype, kv_layout="dim_major", seed=33)
+    k_view = k.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    v_view = v.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    assert not k_view.is_contiguous() and k_view.stride(3) == 1
+    out = _fd().decode(q, k_view, v_view, table, sl, block_size=32, kv_layout="dim_major")
+    assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+def test_misaligned_view_takes_the_generic_kernel_and_agrees():
+    q, k, v, table, sl = make_paged_inputs([200, 33], 16, 2, 128, 16, torch.bfloat16, kv_layout="dim_major",
+                                           seed=35)
+    # the same values one element into a larger buffer: 2-byte aligned base
+    kb = torch.empty(k.numel() + 1, dtype=k.dtype, device="cuda")
+    vb = torch.empty(v.numel() + 1, dtype=v.dtype, device="cuda")
+    k_off = kb[1:].view(k.shape)
+    v_off = vb[1:].view(v.shape)
+    k_off.copy_(k)
+    v_off.copy_(v)
+    out_fast = _fd().decode(q, k, v, table, sl, block_size=16, kv_layout="dim_major")
+    out_gen = _fd().decode(q, k_off, v_off, table, sl, block_size=16, kv_layout="dim_major")
+    ref = _oracle(q, k, v, table, sl)
+    assert_close_to_oracle(out_fast, ref)
+    assert_close_to_oracle(out_gen, ref)
+
+
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_kv_reuse_is_bit_identical(block_size):
+    q, k, v, table, sl = make_paged_inputs([700, 1300, 64], 16, 2, 128, block_size, torch.bfloat16,
+                                           kv_layout="dim_major", seed=37)
+    a = _fd().decode(q, k, v, table, sl, block_size=block_size, kv_layout="dim_major")
+    b = _fd().paged_decode_attention(q, k, v, table, sl, block_size=block_size, kv_layout="dim_major",
+                                     kv_reuse=True)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert_close_to_oracle(a, _oracle(q, k, v, table, sl))
+
+
+def test_matches_token_major_layout_of_the_same_cache():
+    # one cache in both layouts: both MFMA kernels agree with the oracle and,
+    # within the tolerance, with each other
+    q, k, v, table, sl = make_paged_inputs([511, 1025, 2048], 16, 2, 128, 32, torch.bfloat16, seed=39)
+    kd = k.permute(0, 1, 3, 2).contiguous()
+    vd = v.permute(0, 1, 3, 2).contiguous()
+    tok = _fd().decode(q, k, v, table, sl, block_size=32)
+    dim = _fd().decode(q, kd, vd, table, sl, block_size=32, kv_layout="dim_major")
+    ref = oracle_decode(np32(q), np32(k), np32(v), table.cpu().numpy(), sl.cpu().numpy())
+    assert_close_to_oracle(tok, ref)
+    assert_close_to_oracle(dim, ref)
+    assert np.abs(np32(tok) - np32(dim)).max() <= 2e-2
