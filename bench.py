@@ -491,25 +491,27 @@ def run_prefix_large(torch, dev, args):
 
 def run_formats(torch, dev, args):
     """General-path formats (beyond the C2 shape): head_dim 64, more than 16 query heads per KV
-    head, MHA, and dim-major caches, each B16 x 8192 tokens, bf16, block size 32, through the
-    public API (library-planned splits).  3 rotating pools each."""
+    head, MHA, dim-major caches and 8-token blocks, each B16 x 8192 tokens, bf16, block size 32
+    unless named, through the public API (library-planned splits).  3 rotating pools each."""
     import flashdec_amd as fd
 
-    cases = [  # name, Hq, Hkv, D, layout, kernel the library runs
-        ("d128-g8-token-major", 16, 2, 128, "token_major", "mfma"),
-        ("d64-g8-token-major", 16, 2, 64, "token_major", "mfma"),
-        ("d64-g7-token-major (Qwen2.5-0.5B heads)", 14, 2, 64, "token_major", "mfma"),
-        ("d128-g32-token-major", 64, 2, 128, "token_major", "mfma, 2 head blocks"),
-        ("d64-g71-token-major (MQA)", 71, 1, 64, "token_major", "mfma, 5 head blocks"),
-        ("d128-mha-token-major (B4)", 16, 16, 128, "token_major", "mfma"),
-        ("d128-g8-dim-major", 16, 2, 128, "dim_major", "mfma, K staged through LDS"),
-        ("d64-g8-dim-major", 16, 2, 64, "dim_major", "mfma, K staged through LDS"),
+    cases = [  # name, Hq, Hkv, D, layout, block size, kernel the library runs
+        ("d128-g8-token-major", 16, 2, 128, "token_major", 32, "mfma"),
+        ("d64-g8-token-major", 16, 2, 64, "token_major", 32, "mfma"),
+        ("d64-g7-token-major (Qwen2.5-0.5B heads)", 14, 2, 64, "token_major", 32, "mfma"),
+        ("d128-g32-token-major", 64, 2, 128, "token_major", 32, "mfma, 2 head blocks"),
+        ("d64-g71-token-major (MQA)", 71, 1, 64, "token_major", 32, "mfma, 5 head blocks"),
+        ("d128-mha-token-major (B4)", 16, 16, 128, "token_major", 32, "mfma"),
+        ("d128-g8-dim-major", 16, 2, 128, "dim_major", 32, "mfma dim-major, K staged through LDS"),
+        ("d64-g8-dim-major", 16, 2, 64, "dim_major", 32, "mfma dim-major, K staged through LDS"),
+        ("d128-g8-token-major-bs8", 16, 2, 128, "token_major", 8, "mfma"),
+        ("d128-g8-dim-major-bs8", 16, 2, 128, "dim_major", 8, "mfma dim-major, K staged through LDS"),
     ]
     lines = []
-    for name, hq, hkv, d, layout, kernel in cases:
+    for name, hq, hkv, d, layout, bs, kernel in cases:
         batch = 4 if hq == hkv else 16
         lens = [8192] * batch
-        pools = decode_pools(torch, dev, lens, hq, hkv, d, 32, 3, 31)
+        pools = decode_pools(torch, dev, lens, hq, hkv, d, bs, 3, 31)
         if layout == "dim_major":
             pools = [(q, k.transpose(2, 3).contiguous(), v.transpose(2, 3).contiguous(), t, sl, o)
                      for q, k, v, t, sl, o in pools]
@@ -521,12 +523,12 @@ def run_formats(torch, dev, args):
         ms = graph_ms_per_call(torch, dev, fn, 60)
         kv = sum(lens) * hkv * d * 2 * 2
         log(f"[bench] formats {name}: {ms * 1e3:.2f} us/call, K/V {kv / (ms * 1e-3) / 1e12:.2f} TB/s ({kernel})")
-        lines.append({"case": name, "us_per_call": round(ms * 1e3, 2), "kv_bytes": kv,
+        lines.append({"case": name, "block_size": bs, "us_per_call": round(ms * 1e3, 2), "kv_bytes": kv,
                       "kv_tb_per_s": round(kv / (ms * 1e-3) / 1e12, 3), "kernel": kernel})
         del pools
     out = common_fields(args, "paged-decode us/call over general-path formats, B16 x 8192 tokens bf16",
                         lines[0]["us_per_call"], "us", lines[0]["us_per_call"] * 1e-3, False,
-                        {"workload": "formats-b16-ctx8192", "block_size": 32})
+                        {"workload": "formats-b16-ctx8192", "block_size": "32 unless the case names 8"})
     out["cases"] = lines
     return out
 

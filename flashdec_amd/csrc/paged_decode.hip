@@ -212,24 +212,29 @@ __device__ __forceinline__ V kv_load(const void* a) {
 
 // Physical block ids a unit needs (wave-uniform, so scalar loads); pages are
 // clamped to the table row so the read is in bounds whatever the row's
-// length.  A unit spans one block, or two when the block is half its size.
+// length.  A unit spans one block, or UNIT / BS consecutive ones (at most
+// four: the dim-major kernel's 32-token units on 8-token blocks).
 struct UnitPages {
-  int32_t a, b;
+  int32_t a, b, c, d;
 };
 
 template <int BS, int UNIT>
 __device__ __forceinline__ UnitPages fetch_pages(const DecodeParams& p, int b, int unit) {
-  static_assert(BS >= UNIT / 2, "a unit spans at most two blocks");
-  UnitPages up{0, 0};
+  static_assert(BS >= UNIT / 4, "a unit spans at most four blocks");
+  constexpr int kPages = BS < UNIT ? UNIT / BS : 1;
+  UnitPages up{0, 0, 0, 0};
   const int64_t row = b * p.bts0;
   const int64_t width = p.max_blocks_per_seq;
-  int64_t pa = (static_cast<int64_t>(unit) * UNIT) / BS;
-  pa = pa < width ? pa : width - 1;
-  up.a = load_index(p.bt, row + pa * p.bts1, p.bt_i64);
-  if constexpr (BS < UNIT) {
-    int64_t pb = (static_cast<int64_t>(unit) * UNIT) / BS + 1;
-    pb = pb < width ? pb : width - 1;
-    up.b = load_index(p.bt, row + pb * p.bts1, p.bt_i64);
+  const int64_t first = (static_cast<int64_t>(unit) * UNIT) / BS;
+  auto entry = [&](int i) -> int32_t {
+    const int64_t pg = first + i < width ? first + i : width - 1;
+    return load_index(p.bt, row + pg * p.bts1, p.bt_i64);
+  };
+  up.a = entry(0);
+  if constexpr (kPages >= 2) up.b = entry(1);
+  if constexpr (kPages == 4) {
+    up.c = entry(2);
+    up.d = entry(3);
   }
   return up;
 }
@@ -337,11 +342,12 @@ __device__ __forceinline__ void load_unit_fixed(const DecodeParams& p, const Uni
 // i < 8 (i = 4*mt + r: row 4*g + r of QK row block mt):
 //   K piece i of lane l: dim 16*i + l/4, tokens 8*(l%4) + [0, 8) -- staged
 //     through LDS and read back transposed into the QK A operand
-//   vf[n] of lane 16*g + c: dim (D/16)*c + n, tokens 8*g + [0, 8) -- already
-//     the PV A operand (V^T row (D/16)*c + n, k = the lane's eight tokens)
+//   vf[n] of lane 16*g + c: dim 16*n + c, tokens 8*g + [0, 8) -- already the
+//     PV A operand (V^T row 16*n + c, k = the lane's eight tokens); one load
+//     instruction reads 16 consecutive dim rows
 // (D = 128: K pieces i < 8 and V operands n < 8; D = 64: four of each.)
-// Block sizes 16 and 32: a piece lies in one block (block a, or b for the
-// second half of a unit on 16-token blocks).
+// A piece lies in one block: quarter q of the unit is in page q (8-token
+// blocks), q / 2 (16) or 0 (32).
 constexpr int kDmWaves = 4;
 constexpr int kDmRowBytes = 64;  // one staged dim row: 32 tokens x 2 bytes
 
@@ -357,28 +363,33 @@ template <typename T, int BS, bool NT, int D>
 __device__ __forceinline__ void load_unit_dm(const DecodeParams& p, int kvh, const UnitPages& up, int lane,
                                              DmRegs<D>& t) {
   constexpr int KS = DmRegs<D>::KS;
-  static_assert(BS == 16 || BS == 32, "dim-major units need 16- or 32-token blocks");
+  static_assert(BS == 8 || BS == 16 || BS == 32, "dim-major units need 8-, 16- or 32-token blocks");
   constexpr int64_t E = sizeof(T);
-  const bool oka = up.a >= 0 && up.a < p.num_blocks;
-  const bool okb = BS == 16 ? (up.b >= 0 && up.b < p.num_blocks) : oka;
-  const int32_t blk_a = oka ? up.a : 0;  // invalid blocks read block 0 (masked later)
-  const int32_t blk_b = okb ? up.b : 0;
   const int q = lane & 3;   // K: the lane's eight-token quarter of the unit
   const int g = lane >> 4;  // V: the lane's eight tokens
   const int c = lane & 15;
-  const int32_t kblk = (BS == 16 && q >= 2) ? blk_b : blk_a;
-  const int32_t vblk = (BS == 16 && g >= 2) ? blk_b : blk_a;
+  // the block holding quarter x of the unit; invalid ids read block 0
+  // (masked at compute time)
+  auto page = [&](int x) -> int32_t {
+    if constexpr (BS == 32) return up.a;
+    else if constexpr (BS == 16) return x < 2 ? up.a : up.b;
+    else return x == 0 ? up.a : x == 1 ? up.b : x == 2 ? up.c : up.d;
+  };
+  auto valid = [&](int32_t blk) { return blk >= 0 && blk < p.num_blocks; };
+  const int32_t kpg = page(q);
+  const int32_t vpg = page(g);
+  const int32_t kblk = valid(kpg) ? kpg : 0;
+  const int32_t vblk = valid(vpg) ? vpg : 0;
   const char* kp = static_cast<const char*>(p.k) +
                    (kblk * p.ks0 + kvh * p.ks1 + (lane >> 2) * p.ks3 + (8 * q) % BS) * E;
-  const char* vp =
-      static_cast<const char*>(p.v) + (vblk * p.vs0 + kvh * p.vs1 + (D / 16) * c * p.vs3 + (8 * g) % BS) * E;
+  const char* vp = static_cast<const char*>(p.v) + (vblk * p.vs0 + kvh * p.vs1 + c * p.vs3 + (8 * g) % BS) * E;
   const int64_t kstep = 16 * p.ks3 * E;
-  const int64_t vstep = p.vs3 * E;
+  const int64_t vstep = 16 * p.vs3 * E;
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) t.kf[i / KS][i % KS] = kv_load<NT>(kp + i * kstep);
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) t.vf[n] = kv_load<NT>(vp + n * vstep);
-  t.bmask = ((BS == 16 && g >= 2) ? okb : oka) ? 0xffu : 0u;
+  t.bmask = valid(vpg) ? 0xffu : 0u;
 }
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -1063,13 +1074,19 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       lds.col_h[c] = col_h;
     }
   }
-  // this lane's dims (D/4)*g + (D/16)*rr + n, n < D/16: one or two 16-byte rows
+  if constexpr (DM) {
+    // this lane's dims 16*n + 4*g + rr (load_unit_dm's V rows)
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    float* dst = &lds.acc[wave][c][(D / 4) * g + (D / 16) * rr];
-    *reinterpret_cast<f32x4*>(dst) = f32x4{st.acc[0][rr], st.acc[1][rr], st.acc[2][rr], st.acc[3][rr]};
-    if constexpr (D == 128)
-      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
+    for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f32x4*>(&lds.acc[wave][c][16 * n + 4 * g]) = st.acc[n];
+  } else {
+    // this lane's dims (D/4)*g + (D/16)*rr + n, n < D/16: one or two 16-byte rows
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      float* dst = &lds.acc[wave][c][(D / 4) * g + (D / 16) * rr];
+      *reinterpret_cast<f32x4*>(dst) = f32x4{st.acc[0][rr], st.acc[1][rr], st.acc[2][rr], st.acc[3][rr]};
+      if constexpr (D == 128)
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
+    }
   }
   __syncthreads();
 
@@ -1603,12 +1620,9 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
 }
 
 // Dim-major caches on the MFMA path (decode_dm_kernel): 64- or 128-dim heads,
-// 16- or 32-token blocks, token stride 1, 16-byte aligned dim rows, no fused
-// append.
+// token stride 1, 16-byte aligned dim rows, no fused append.
 bool dm_path_ok(const fd_paged_decode_args& a, int64_t group) {
-  if ((a.head_dim != 128 && a.head_dim != 64) || group > 256 || (a.block_size != 16 && a.block_size != 32) ||
-      a.append_k)
-    return false;
+  if ((a.head_dim != 128 && a.head_dim != 64) || group > 256 || a.append_k) return false;
   if (a.q_stride[2] != 1 || a.k_stride[2] != 1 || a.v_stride[2] != 1) return false;
   const int64_t strides[] = {a.q_stride[0], a.q_stride[1], a.k_stride[0], a.k_stride[1], a.k_stride[3],
                              a.v_stride[0], a.v_stride[1], a.v_stride[3]};
@@ -1681,7 +1695,10 @@ void launch_mfma(const DecodeParams& p, bool nt, dim3 grid, hipStream_t stream, 
 template <typename T, int D>
 void launch_dm(const DecodeParams& p, int64_t block_size, bool nt, dim3 grid, dim3 block, hipStream_t stream,
                void* const* ev) {
-  if (block_size == 16)
+  if (block_size == 8)
+    nt ? dispatch(decode_dm_kernel<T, 8, true, D>, grid, block, stream, ev[0], ev[1], p)
+       : dispatch(decode_dm_kernel<T, 8, false, D>, grid, block, stream, ev[0], ev[1], p);
+  else if (block_size == 16)
     nt ? dispatch(decode_dm_kernel<T, 16, true, D>, grid, block, stream, ev[0], ev[1], p)
        : dispatch(decode_dm_kernel<T, 16, false, D>, grid, block, stream, ev[0], ev[1], p);
   else

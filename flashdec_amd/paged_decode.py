@@ -374,7 +374,7 @@ def paged_decode_attention_into(
             num_splits = max(2, min(balance, -(-max_seq_len // 32)))
         else:
             num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
-            dim_major_mfma = head_dim in (64, 128) and block_size in (16, 32)
+            dim_major_mfma = head_dim in (64, 128)
             if kv_layout == "dim_major" and dim_major_mfma:
                 # the dim-major kernel runs two 4-wave workgroups per CU: twice
                 # the splits, each still >= 4 tiles (one unit per wave)

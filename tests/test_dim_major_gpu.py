@@ -2,7 +2,7 @@
 
 Dim-major caches (``[blocks, kv_heads, head_dim, block_size]``, the
 reference's ``kv_layout="dim_major"``, flashdec/paged_reference.py:19-125)
-with 64- or 128-dim heads and 16- or 32-token blocks run the MFMA kernel that stages
+with 64- or 128-dim heads run the MFMA kernel that stages
 K through LDS.  These cases cover what that kernel adds over the token-major
 one: lengths that end inside a unit, a block or a quarter of a unit, head
 blocks (G > 16), explicit and planned splits, strided views, non-finite
@@ -42,7 +42,7 @@ def _workspace(b, hq, splits, head_dim=128):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
 @pytest.mark.parametrize("lens", [[1, 7, 8, 9], [15, 16, 17, 31], [32, 33, 63, 64], [65, 100, 129, 0]])
 def test_lengths_end_inside_units(lens, block_size, head_dim, dtype):
     q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, dtype, kv_layout="dim_major",
@@ -52,7 +52,7 @@ def test_lengths_end_inside_units(lens, block_size, head_dim, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
 @pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(8, 8, 128), (4, 1, 128), (16, 2, 128), (32, 2, 128),
                                                      (40, 2, 128), (64, 1, 128), (14, 2, 64), (71, 1, 64),
                                                      (32, 32, 64)])
@@ -77,7 +77,7 @@ def test_explicit_splits(num_splits, head_dim, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
 def test_long_rows_planned_splits(block_size, head_dim, dtype):
     lens = [8192, 6000, 8191, 3]
     q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, dtype, kv_layout="dim_major",
@@ -87,7 +87,7 @@ def test_long_rows_planned_splits(block_size, head_dim, dtype):
 
 
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
 def test_non_finite_values_past_row_end_are_masked(block_size, head_dim):
     lens = [45, 70, 5]
     q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, torch.bfloat16,
@@ -140,7 +140,7 @@ def test_misaligned_view_takes_the_generic_kernel_and_agrees():
     assert_close_to_oracle(out_gen, ref)
 
 
-@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
 def test_kv_reuse_is_bit_identical(block_size):
     q, k, v, table, sl = make_paged_inputs([700, 1300, 64], 16, 2, 128, block_size, torch.bfloat16,
                                            kv_layout="dim_major", seed=37)
