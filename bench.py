@@ -65,13 +65,14 @@ def parse_args():
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
     p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine",
-                                          "engine-prefix", "formats"),
+                                          "engine-prefix", "formats", "vllm"),
                    default="decode",
                    help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
                         "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
                         "sharing a 16384-token prefix; engine: C5 36-layer step; engine-prefix: 36-layer steps "
-                        "of 64 rows sharing a 16384-token prefix; formats: head_dim 64, large groups, MHA and "
-                        "dim-major caches")
+                        "of 64 rows sharing a 16384-token prefix; formats: head_dim 64, large groups, MHA, "
+                        "dim-major caches and 8-token blocks; vllm: the vLLM hook's launch at B8 ctx1024/2048, "
+                        "block size 16, fused append")
     p.add_argument("--engine-steps", type=int, default=200, help="timed steps of the engine workload")
     return p.parse_args()
 
@@ -533,6 +534,57 @@ def run_formats(torch, dev, args):
     return out
 
 
+def run_vllm(torch, dev, args):
+    """The vLLM CUSTOM hook's launch at the reference's published vLLM shapes: B8, Hq16/Hkv2/D128
+    bf16, block size 16, vLLM's 5-D NHD cache ``[blocks, 2, 16, kv_heads, 128]``, every row at
+    ctx 1024 or 2048 with its current token appended in the launch (slot of position len - 1),
+    splits as the hook picks them (power of two nearest one workgroup per CU, >= 128 tokens each).
+    8 rotating pools."""
+    import flashdec_amd  # noqa: F401  (loads the library)
+    from flashdec_amd.paged_decode import _vllm_paged_decode_attention_into
+    from flashdec_amd.vllm_splits import _AUTO_MIN_SPLIT_TOKENS, _select_num_splits
+
+    hq, hkv, d, bs, batch = 16, 2, 128, 16, 8
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    lines = []
+    for ctx in (1024, 2048):
+        lens = [ctx] * batch
+        pools = []
+        for q, k, v, table, sl, o in decode_pools(torch, dev, lens, hq, hkv, d, bs, 8, 41 + ctx):
+            kv = torch.empty((k.shape[0], 2, bs, hkv, d), device=dev, dtype=k.dtype)
+            kv[:, 0].copy_(k.permute(0, 2, 1, 3))
+            kv[:, 1].copy_(v.permute(0, 2, 1, 3))
+            del k, v
+            pos = sl.long() - 1
+            slots = table.long().gather(1, (pos // bs).unsqueeze(1)).squeeze(1) * bs + pos % bs
+            ak = torch.randn((batch, hkv, d), device=dev).to(kv.dtype)
+            av = torch.randn((batch, hkv, d), device=dev).to(kv.dtype)
+            pools.append((q, ak, av, kv, table, sl, o, slots))
+        splits = _select_num_splits(0, num_reqs=batch, num_kv_heads=hkv, logical_blocks=ctx // bs,
+                                    target_programs=cus, auto_min_tokens=_AUTO_MIN_SPLIT_TOKENS, block_size=bs)
+        ws = (torch.empty((batch, hq, splits, d), device=dev), torch.empty((batch, hq, splits), device=dev),
+              torch.empty((batch, hq, splits), device=dev))
+
+        def fn(i, pools=pools, ws=ws, splits=splits, ctx=ctx):
+            q, ak, av, kv, table, sl, o, slots = pools[i % len(pools)]
+            _vllm_paged_decode_attention_into(q, ak, av, kv, table, sl, o, slots, *ws, num_reqs=batch,
+                                              num_q_heads=hq, num_kv_heads=hkv, head_dim=d, block_size=bs,
+                                              sm_scale=d ** -0.5, num_splits=splits, max_seq_len=ctx)
+
+        ms = graph_ms_per_call(torch, dev, fn, args.steps)
+        algo = batch * ctx * hkv * d * 2 * 2 + 2 * batch * hq * d * 2 + 4 * batch * (ctx // bs) + 4 * batch
+        log(f"[bench] vllm B8 ctx{ctx} bs16 fused append: {ms * 1e3:.2f} us/call, splits {splits}, "
+            f"{algo / (ms * 1e-3) / 1e9:.1f} GB/s")
+        lines.append({"ctx": ctx, "us_per_call": round(ms * 1e3, 2), "num_splits": splits,
+                      "algorithmic_bytes": algo, "gb_per_s": round(algo / (ms * 1e-3) / 1e9, 1)})
+        del pools
+    out = common_fields(args, "vLLM CUSTOM hook decode us/call, B8 Hq16/Hkv2/D128 bf16 bs16 fused append",
+                        lines[1]["us_per_call"], "us", lines[1]["us_per_call"] * 1e-3, False,
+                        {"workload": "vllm-hook-b8-bs16-fused-append", "block_size": bs})
+    out["cases"] = lines
+    return out
+
+
 def run_engine_prefix(torch, dev, args):
     """36-layer DecodeEngine steps over a shared prefix: B64 rows attached to one resident
     16384-token prefix, private tails ~ U{64..512}, Hq16 Hkv2 D128 bf16.  Two step graphs on the
@@ -775,7 +827,8 @@ def main():
     _lib.load_library()
     if args.workload != "decode":
         run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
-               "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats}[args.workload]
+               "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
+               "vllm": run_vllm}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
         return
     batch, ctx, hq, hkv, d, bs = args.batch, args.ctx, 16, 2, 128, 32

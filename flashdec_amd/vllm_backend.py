@@ -14,7 +14,7 @@ An eligible batch:
 ``FLASHDEC_VLLM_NUM_SPLITS`` picks the split count:
 - 0 = auto; otherwise 1, 2, 4, 8 or 16.
 - A split count of 1 falls back to vLLM's own kernel, as in the reference.
-- Auto uses the reference's policy (power of two nearest the program target, capped by the context). The target is the device's compute-unit count (256 on MI355X) rather than the reference's fixed 128, so one decode layer fills the chip.
+- Auto uses the reference's policy (power of two nearest the program target, capped by the context). The target is the device's compute-unit count (256 on MI355X) rather than the reference's fixed 128, so one decode layer fills the chip, and every automatic split keeps at least 128 tokens (one 32-token unit per wave).
 
 The reference's split-attestation files (benchmark provenance) are not part of this path.
 """
@@ -32,22 +32,16 @@ from vllm.v1.attention.backends.triton_attn import (
 )
 
 from .paged_decode import _vllm_paged_decode_attention_into
+from .vllm_splits import (  # noqa: F401  (re-exported: the hook's policy lives beside it)
+    _AUTO_MIN_SPLIT_TOKENS,
+    _REFERENCE_TARGET_PROGRAMS,
+    _VALID_NUM_SPLITS,
+    _VALID_REQUESTED_SPLITS,
+    _parse_requested_splits,
+    _select_num_splits,
+)
 
-_VALID_REQUESTED_SPLITS = (0, 1, 2, 4, 8, 16)
-_VALID_NUM_SPLITS = _VALID_REQUESTED_SPLITS[1:]
 _MIN_CONTEXT = 512  # below this the split kernel does not pay (vllm_backend.py:254)
-_REFERENCE_TARGET_PROGRAMS = 128
-
-
-def _parse_requested_splits(value: str) -> int:
-    """``FLASHDEC_VLLM_NUM_SPLITS`` -> requested split count (0 = auto)."""
-    try:
-        requested = int(value)
-    except ValueError:
-        requested = -1
-    if requested not in _VALID_REQUESTED_SPLITS:
-        raise ValueError("FLASHDEC_VLLM_NUM_SPLITS must be one of 0, 1, 2, 4, 8, or 16 (0 selects auto)")
-    return requested
 
 
 def _parse_kv_reuse(value: str) -> bool:
@@ -55,16 +49,6 @@ def _parse_kv_reuse(value: str) -> bool:
     if value not in ("0", "1"):
         raise ValueError("FLASHDEC_VLLM_KV_REUSE must be 0 or 1")
     return value == "1"
-
-
-def _select_num_splits(requested_splits: int, *, num_reqs: int, num_kv_heads: int, logical_blocks: int,
-                       target_programs: int = _REFERENCE_TARGET_PROGRAMS) -> int:
-    """Split count: the power of two whose program count is nearest the target, capped by the context."""
-    cap = max(s for s in _VALID_NUM_SPLITS if s <= max(1, logical_blocks))
-    if requested_splits == 0:
-        per_split = max(1, num_reqs * num_kv_heads)
-        requested_splits = min(_VALID_NUM_SPLITS, key=lambda s: (abs(per_split * s - target_programs), s))
-    return min(requested_splits, cap)
 
 
 _TARGETS: dict = {}
@@ -150,7 +134,8 @@ class FlashDecAttentionImpl(TritonAttentionImpl):
         logical_blocks = (attn_metadata.max_seq_len + block_size - 1) // block_size
         num_splits = _select_num_splits(self._requested_splits, num_reqs=num_reqs, num_kv_heads=self.num_kv_heads,
                                         logical_blocks=logical_blocks,
-                                        target_programs=_target_programs(query.device))
+                                        target_programs=_target_programs(query.device),
+                                        auto_min_tokens=_AUTO_MIN_SPLIT_TOKENS, block_size=block_size)
         if num_reqs > attn_metadata.softmax_segm_output.shape[0]:
             num_splits = 1
         if num_splits == 1:

@@ -77,8 +77,8 @@ def test_backend_identity_and_cache_contract(vb):
     assert vb.FlashDecAttentionBackend.get_kv_cache_shape(7, 16, 2, 128) == (7, 2, 16, 2, 128)
 
 
-@pytest.mark.parametrize("max_seq_len", [512, 1024])
-def test_eligible_decode_passes_vllm_tensors_to_the_hip_launcher(vb, monkeypatch, max_seq_len):
+@pytest.mark.parametrize(("max_seq_len", "splits"), [(512, 4), (1024, 8), (2048, 16)])
+def test_eligible_decode_passes_vllm_tensors_to_the_hip_launcher(vb, monkeypatch, max_seq_len, splits):
     calls = record_launches(vb, monkeypatch)
     impl = make_impl(vb)
     q, k, v, cache, out = tensors()
@@ -89,7 +89,7 @@ def test_eligible_decode_passes_vllm_tensors_to_the_hip_launcher(vb, monkeypatch
                      md.softmax_segm_max, md.softmax_segm_expsum)
     assert len(args) == len(expected_args) and all(a is b for a, b in zip(args, expected_args))
     assert kwargs == {"num_reqs": 3, "num_q_heads": 16, "num_kv_heads": 2, "head_dim": 128, "block_size": 16,
-                      "sm_scale": 128 ** -0.5, "num_splits": 16, "max_seq_len": max_seq_len, "kv_reuse": False}
+                      "sm_scale": 128 ** -0.5, "num_splits": splits, "max_seq_len": max_seq_len, "kv_reuse": False}
     assert vllm_fakes.TritonAttentionImpl.fallback_calls == []
 
 
@@ -180,6 +180,16 @@ def test_invalid_kv_reuse_environment_rejected_at_construction(vb, monkeypatch, 
     monkeypatch.setenv("FLASHDEC_VLLM_KV_REUSE", value)
     with pytest.raises(ValueError, match="FLASHDEC_VLLM_KV_REUSE must be 0 or 1"):
         make_impl(vb)
+
+
+def test_automatic_splits_keep_128_tokens_and_requests_keep_the_reference_cap(vb):
+    # auto: 3 rows x 2 heads at 256 programs -> 16, capped to ctx / 128
+    for ctx, expected in [(512, 4), (1024, 8), (1100, 8), (2048, 16), (8192, 16)]:
+        assert vb._select_num_splits(0, num_reqs=3, num_kv_heads=2, logical_blocks=-(-ctx // 16),
+                                     target_programs=256, auto_min_tokens=128, block_size=16) == expected
+    # an explicit request is capped by the logical blocks only, as in the reference
+    assert vb._select_num_splits(16, num_reqs=3, num_kv_heads=2, logical_blocks=32, target_programs=256,
+                                 auto_min_tokens=128, block_size=16) == 16
 
 
 def test_reference_split_policy_is_the_default_target(vb):
