@@ -11,7 +11,7 @@
 //    NHD/HND views too), head_dim 64 or 128, any group size.  QK^T and PV
 //    run on v_mfma_f32_16x16x{32,16}_{bf16,f16}; V is transposed in
 //    registers.  Also the body of the per-row (balanced) and cascade kernels.
-//  * decode_dm_kernel    -- dim-major caches (16/32-token blocks): V loads
+//  * decode_dm_kernel    -- dim-major caches (8/16/32-token blocks): V loads
 //    straight into the PV operand, K goes through LDS and comes back
 //    transposed (ds_read_b64_tr_b16).
 //  * decode_generic_kernel -- any strides; VALU only.
