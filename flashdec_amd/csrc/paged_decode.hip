@@ -658,22 +658,91 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (
   }
 }
 
+// Fused append into a dim-major cache: this lane's elements of the new
+// token in load_unit_dm's layout -- kd(i) = append_k dim 16*i + lane/4 (its K
+// pieces), vd(n) = append_v dim 16*n + c (its V operands), two per register.
+template <int D>
+struct DmAppendRegs {
+  uint32_t k[D / 32];  // element i in bits 16*(i%2) of word i/2
+  uint32_t v[D / 32];
+  __device__ __forceinline__ uint16_t kd(int i) const { return static_cast<uint16_t>(k[i >> 1] >> (16 * (i & 1))); }
+  __device__ __forceinline__ uint16_t vd(int n) const { return static_cast<uint16_t>(v[n >> 1] >> (16 * (n & 1))); }
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void load_append_dm(const DecodeParams& p, int b, int kvh, int lane,
+                                               DmAppendRegs<D>& ar) {
+  const uint16_t* ak = static_cast<const uint16_t*>(p.ak) + b * p.aks0 + kvh * p.aks1;
+  const uint16_t* av = static_cast<const uint16_t*>(p.av) + b * p.avs0 + kvh * p.avs1;
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+    ar.k[j] = ak[(32 * j + (lane >> 2)) * p.aks2] | (static_cast<uint32_t>(ak[(32 * j + 16 + (lane >> 2)) * p.aks2]) << 16);
+    ar.v[j] = av[(32 * j + (lane & 15)) * p.avs2] | (static_cast<uint32_t>(av[(32 * j + 16 + (lane & 15)) * p.avs2]) << 16);
+  }
+}
+
+// The new token's K/V go to slot (block, offset) of the dim-major cache: one
+// element per dim row.  Lanes with lane % 4 == 0 hold every K dim once, lanes
+// with g == 0 every V dim.
+template <typename T, int BS, int D>
+__device__ __forceinline__ void store_append_dm(const DecodeParams& p, int kvh, int32_t slot, int lane,
+                                                const DmAppendRegs<D>& ar) {
+  const int64_t blk = slot / BS, off = slot % BS;
+  if (blk >= p.num_blocks) return;
+  if ((lane & 3) == 0) {
+    uint16_t* dst = static_cast<uint16_t*>(p.k) + blk * p.ks0 + kvh * p.ks1 + off * p.ks2;
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) dst[(16 * i + (lane >> 2)) * p.ks3] = ar.kd(i);
+  }
+  if ((lane >> 4) == 0) {
+    uint16_t* dst = static_cast<uint16_t*>(p.v) + blk * p.vs0 + kvh * p.vs1 + off * p.vs2;
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) dst[(16 * n + lane) * p.vs3] = ar.vd(n);
+  }
+}
+
+// Element e (a token of the lane's eight) of a 16-byte piece replaced by x.
+__device__ __forceinline__ void set_elem16(u32x4& piece, int e, uint16_t x) {
+  const int sh = (e & 1) * 16;
+  const uint32_t keep = ~(0xffffu << sh);
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    piece[w] = (w == (e >> 1)) ? ((piece[w] & keep) | (static_cast<uint32_t>(x) << sh)) : piece[w];
+}
+
 // process_unit for a dim-major unit (load_unit_dm's layout): the lane's
 // scores and V columns are tokens 8*g + i, and V needs no transposes.
-template <typename T, int D>
+template <typename T, bool FUSE, int D>
 __device__ __forceinline__ void process_unit_dm(DmRegs<D>& t, const u32x4 (&qf)[D / 32], float scale_log2,
-                                                int tok0, int first, int last, int lane, uint8_t* stage,
+                                                int tok0, int first, int last, int app,
+                                                const DmAppendRegs<D>& ar, int lane, uint8_t* stage,
                                                 WaveState<D>& st) {
   constexpr int KS = DmRegs<D>::KS;
   constexpr int NTILE = D / 16;
   const int g = lane >> 4;
-  stage_k_dm<D>(t, stage, lane);
   uint32_t vmask = t.bmask;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int tok = tok0 + 8 * g + i;
     vmask &= (tok <= last && (first == 0 || tok >= first)) ? ~0u : ~(1u << i);
   }
+  if constexpr (FUSE) {
+    // the new token comes from registers: token at = 8*qa + e of this unit
+    const int at = app - tok0;
+    if (at >= 0 && at < 32) {
+      const int qa = at >> 3, e = at & 7;
+      if ((lane & 3) == qa) {
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) set_elem16(t.kf[i / KS][i % KS], e, ar.kd(i));
+      }
+      if (g == qa) {
+#pragma unroll
+        for (int n = 0; n < NTILE; ++n) set_elem16(t.vf[n], e, ar.vd(n));
+        vmask |= 1u << e;
+      }
+    }
+  }
+  stage_k_dm<D>(t, stage, lane);
   float sc[8];
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
@@ -859,7 +928,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
                 "cascade and balanced roles have no fused append or in-launch merge");
   static_assert(D == 128 || (ROLE == Role::kRow && FUSE != 2 && !MERGE),
                 "head_dim 64 runs the row role without RoPE or in-launch merge");
-  static_assert(!DM || (ROLE == Role::kRow && FUSE == 0 && !MERGE && UNIT == 32),
+  static_assert(!DM || (ROLE == Role::kRow && FUSE != 2 && !MERGE && UNIT == 32),
                 "dim-major caches run the row role on 32-token units");
   constexpr int KS = D / 32;  // 32-dim pieces of q / K rows
   constexpr int kWaves = WAVES;
@@ -954,7 +1023,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     }
   }
   AppendRegs<D> ar;
-  if constexpr (FUSE) {
+  [[maybe_unused]] DmAppendRegs<D> dar;
+  if constexpr (FUSE && DM) {
+    load_append_dm<T, D>(p, b, kvh, lane, dar);
+  } else if constexpr (FUSE) {
     const T* ak = static_cast<const T*>(p.ak) + b * p.aks0 + kvh * p.aks1;
     const T* av = static_cast<const T*>(p.av) + b * p.avs0 + kvh * p.avs1;
 #pragma unroll
@@ -1041,10 +1113,15 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, trow, next + kWaves);
       }
       if constexpr (FUSE)
-        if (app >= 0 && app / UNIT == unit && hb == 0) store_append<T, BS, D>(p, kvh, slot, c, g, ar);
+        if (app >= 0 && app / UNIT == unit && hb == 0) {
+          if constexpr (DM)
+            store_append_dm<T, BS, D>(p, kvh, slot, lane, dar);
+          else
+            store_append<T, BS, D>(p, kvh, slot, c, g, ar);
+        }
       if constexpr (DM)
-        process_unit_dm<T, D>(now, qf, p.scale_log2, unit * UNIT, first, last, lane,
-                              kstage + wave * D * kDmRowBytes, st);
+        process_unit_dm<T, (FUSE != 0), D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, dar, lane,
+                                           kstage + wave * D * kDmRowBytes, st);
       else
         process_unit<T, (FUSE != 0), UNIT, D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
       unit = next;
@@ -1237,11 +1314,14 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
 // workgroup per CU at its best split count.
 constexpr int kDmPerCU = 2;
 
-template <typename T, int BS, bool NT, int D>
-__global__ __launch_bounds__(64 * kDmWaves, kDmPerCU) void decode_dm_kernel(DecodeParams p) {
+// FUSE: fused current-token append.  Its variant runs one workgroup per CU:
+// within two per CU (256 registers a wave) the 128-dim variant spilled.
+template <typename T, int BS, bool NT, int D, int FUSE>
+__global__ __launch_bounds__(64 * kDmWaves, FUSE ? 1 : kDmPerCU) void decode_dm_kernel(DecodeParams p) {
   __shared__ DecodeLds<kDmWaves> lds;
   __shared__ __attribute__((aligned(16))) uint8_t stage[kDmWaves * D * kDmRowBytes];
-  decode_role<T, BS, 0, false, 32, Role::kRow, NT, D, kDmWaves, true>(p, CascadeParams{}, blockIdx.x, lds, stage);
+  decode_role<T, BS, FUSE, false, 32, Role::kRow, NT, D, kDmWaves, true>(p, CascadeParams{}, blockIdx.x, lds,
+                                                                         stage);
 }
 
 // Balanced splits (ragged batches): the row and split of each workgroup come
@@ -1620,9 +1700,10 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
 }
 
 // Dim-major caches on the MFMA path (decode_dm_kernel): 64- or 128-dim heads,
-// token stride 1, 16-byte aligned dim rows, no fused append.
+// token stride 1, 16-byte aligned dim rows (the fused append's rows may have
+// any strides: they are read and stored one element at a time).
 bool dm_path_ok(const fd_paged_decode_args& a, int64_t group) {
-  if ((a.head_dim != 128 && a.head_dim != 64) || group > 256 || a.append_k) return false;
+  if ((a.head_dim != 128 && a.head_dim != 64) || group > 256) return false;
   if (a.q_stride[2] != 1 || a.k_stride[2] != 1 || a.v_stride[2] != 1) return false;
   const int64_t strides[] = {a.q_stride[0], a.q_stride[1], a.k_stride[0], a.k_stride[1], a.k_stride[3],
                              a.v_stride[0], a.v_stride[1], a.v_stride[3]};
@@ -1692,18 +1773,18 @@ void launch_mfma(const DecodeParams& p, bool nt, dim3 grid, hipStream_t stream, 
     launch_mfma<T, BS, false>(p, grid, stream, ev);
 }
 
-template <typename T, int D>
+template <typename T, int D, int FUSE>
 void launch_dm(const DecodeParams& p, int64_t block_size, bool nt, dim3 grid, dim3 block, hipStream_t stream,
                void* const* ev) {
   if (block_size == 8)
-    nt ? dispatch(decode_dm_kernel<T, 8, true, D>, grid, block, stream, ev[0], ev[1], p)
-       : dispatch(decode_dm_kernel<T, 8, false, D>, grid, block, stream, ev[0], ev[1], p);
+    nt ? dispatch(decode_dm_kernel<T, 8, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p)
+       : dispatch(decode_dm_kernel<T, 8, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p);
   else if (block_size == 16)
-    nt ? dispatch(decode_dm_kernel<T, 16, true, D>, grid, block, stream, ev[0], ev[1], p)
-       : dispatch(decode_dm_kernel<T, 16, false, D>, grid, block, stream, ev[0], ev[1], p);
+    nt ? dispatch(decode_dm_kernel<T, 16, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p)
+       : dispatch(decode_dm_kernel<T, 16, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p);
   else
-    nt ? dispatch(decode_dm_kernel<T, 32, true, D>, grid, block, stream, ev[0], ev[1], p)
-       : dispatch(decode_dm_kernel<T, 32, false, D>, grid, block, stream, ev[0], ev[1], p);
+    nt ? dispatch(decode_dm_kernel<T, 32, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p)
+       : dispatch(decode_dm_kernel<T, 32, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p);
 }
 
 ReduceParams reduce_params(const DecodeParams& p) {
@@ -1810,9 +1891,11 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
     const dim3 block(64 * kDmWaves);
     void* const* ev = a.timing_events;
     if (a.head_dim == 64)
-      launch_dm<T, 64>(p, a.block_size, nt, grid, block, stream, ev);
+      p.fuse ? launch_dm<T, 64, 1>(p, a.block_size, nt, grid, block, stream, ev)
+             : launch_dm<T, 64, 0>(p, a.block_size, nt, grid, block, stream, ev);
     else
-      launch_dm<T, 128>(p, a.block_size, nt, grid, block, stream, ev);
+      p.fuse ? launch_dm<T, 128, 1>(p, a.block_size, nt, grid, block, stream, ev)
+             : launch_dm<T, 128, 0>(p, a.block_size, nt, grid, block, stream, ev);
   } else {
     const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
     const dim3 grid(static_cast<unsigned>(pairs * hg), static_cast<unsigned>(p.splits));

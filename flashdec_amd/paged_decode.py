@@ -376,9 +376,10 @@ def paged_decode_attention_into(
             num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max_seq_len)
             dim_major_mfma = head_dim in (64, 128)
             if kv_layout == "dim_major" and dim_major_mfma:
-                # the dim-major kernel runs two 4-wave workgroups per CU: twice
-                # the splits, each still >= 4 tiles (one unit per wave)
-                num_splits = max(1, min(2 * num_splits, -(-max_seq_len // 128)))
+                if not fuse_kv_append:
+                    # the dim-major kernel runs two 4-wave workgroups per CU:
+                    # twice the splits, each still >= 4 tiles (one unit per wave)
+                    num_splits = max(1, min(2 * num_splits, -(-max_seq_len // 128)))
             elif kv_layout == "dim_major" or head_dim not in (64, 128):
                 # the generic kernel runs one wave per workgroup: 8x the splits
                 # keeps ~8 waves per CU (dim-major B16 ctx8192: 515 -> 128 us),

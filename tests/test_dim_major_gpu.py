@@ -6,8 +6,9 @@ with 64- or 128-dim heads run the MFMA kernel that stages
 K through LDS.  These cases cover what that kernel adds over the token-major
 one: lengths that end inside a unit, a block or a quarter of a unit, head
 blocks (G > 16), explicit and planned splits, strided views, non-finite
-values past a row's end, table padding past the used range, and streamed
-against cached K/V loads (bit-identical).  Views whose strides or alignment
+values past a row's end, table padding past the used range, streamed
+against cached K/V loads (bit-identical), and the fused current-token append
+(output against the oracle, cache bytes bit-exact, inert rows).  Views whose strides or alignment
 the kernel does not take run the generic kernel and must agree as well.
 Tolerance: atol 2e-2 / rtol 1e-2 against the fp32 oracle.
 """
@@ -163,3 +164,72 @@ def test_matches_token_major_layout_of_the_same_cache():
     assert_close_to_oracle(tok, ref)
     assert_close_to_oracle(dim, ref)
     assert np.abs(np32(tok) - np32(dim)).max() <= 2e-2
+
+
+def _slots(table, lens, block_size):
+    slots = []
+    for b, n in enumerate(lens.tolist()):
+        if n == 0:
+            slots.append(-1)
+            continue
+        blk = int(table[b, (n - 1) // block_size])
+        slots.append(blk * block_size + (n - 1) % block_size)
+    return slots
+
+
+@pytest.mark.parametrize("num_splits", [0, 1, 8])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("prior", [(0, 17, 31), (256, 193, 1000), (31, 63, 8)])
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_fused_current_token_append(prior, num_splits, dtype, block_size):
+    # the new token's K/V come from append_k/v (its cache slot holds NaN before
+    # the call); the cache afterwards holds them at that slot, bit for bit
+    lens_after = [p + 1 for p in prior]
+    q, k, v, table, lens = make_paged_inputs(lens_after, 16, 2, 128, block_size, dtype, kv_layout="dim_major",
+                                             seed=41)
+    expected = _oracle(q, k, v, table, lens)
+    slots = _slots(table, lens.cpu(), block_size)
+    append_k = torch.empty((3, 2, 128), device="cuda", dtype=dtype)
+    append_v = torch.empty_like(append_k)
+    k_expected = k.clone()
+    v_expected = v.clone()
+    for b, s in enumerate(slots):
+        blk, off = divmod(s, block_size)
+        append_k[b] = k[blk, :, :, off]
+        append_v[b] = v[blk, :, :, off]
+        k[blk, :, :, off] = float("nan")
+        v[blk, :, :, off] = float("nan")
+    out = torch.empty_like(q)
+    kwargs = {}
+    if num_splits:
+        kwargs = {"split_kv_workspace": _workspace(3, 16, 8), "num_splits": num_splits}
+    _fd().paged_decode_attention_into(q, k, v, table, lens, out, block_size=block_size, kv_layout="dim_major",
+                                      append_k=append_k, append_v=append_v,
+                                      slot_mapping=torch.tensor(slots, device="cuda", dtype=torch.int64), **kwargs)
+    assert_close_to_oracle(out, expected)
+    assert torch.equal(k.view(torch.int16), k_expected.view(torch.int16))
+    assert torch.equal(v.view(torch.int16), v_expected.view(torch.int16))
+
+
+def test_fused_append_inert_rows():
+    # slot -1 and seq_len 0 rows: zero output, no cache write
+    q, k, v, table, lens = make_paged_inputs([40, 0, 70], 16, 2, 128, 32, torch.bfloat16, kv_layout="dim_major",
+                                             seed=43)
+    slots = _slots(table, lens.cpu(), 32)
+    slots[2] = -1
+    before_k, before_v = k.clone(), v.clone()
+    append_k = torch.randn((3, 2, 128), device="cuda").to(torch.bfloat16)
+    append_v = torch.randn((3, 2, 128), device="cuda").to(torch.bfloat16)
+    blk, off = divmod(slots[0], 32)
+    exp_k, exp_v = before_k.clone(), before_v.clone()
+    exp_k[blk, :, :, off] = append_k[0]
+    exp_v[blk, :, :, off] = append_v[0]
+    out = torch.empty_like(q)
+    _fd().paged_decode_attention_into(q, k, v, table, lens, out, block_size=32, kv_layout="dim_major",
+                                      append_k=append_k, append_v=append_v,
+                                      slot_mapping=torch.tensor(slots, device="cuda", dtype=torch.int32))
+    assert torch.count_nonzero(out[1]) == 0 and torch.count_nonzero(out[2]) == 0
+    assert torch.equal(k.view(torch.int16), exp_k.view(torch.int16))
+    assert torch.equal(v.view(torch.int16), exp_v.view(torch.int16))
+    ref = _oracle(q[:1], exp_k, exp_v, table[:1], lens[:1])
+    assert_close_to_oracle(out[:1], ref)
