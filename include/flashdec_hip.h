@@ -8,7 +8,11 @@
  *
  * Tensors are passed as raw device pointers plus element strides, so strided
  * views (vLLM's [block, plane, token, head, dim] cache, NHD/HND permutations,
- * dim-major caches) are consumed in place without copies.
+ * dim-major caches) are consumed in place without copies.  fd_paged_decode
+ * runs an MFMA kernel (head_dim 64 or 128, any group size, strides
+ * multiples of 8 and 16-byte aligned bases) for token-major caches with unit
+ * dim stride and for dim-major caches with unit token stride; other views run
+ * a VALU kernel with the same results within rounding.
  *
  * Reference interfaces replaced (paths relative to cysong2025/flashdec):
  *   fd_paged_decode          flashdec/kernels/paged_decode.py:972-1264
@@ -158,8 +162,9 @@ typedef struct fd_paged_decode_args {
    * at most T tiles.  The launch has num_kv_heads * (V + num_seqs)
    * workgroups, the ones past the batch's Σ S_b exit at once.  S_b <= V, so
    * a workspace of num_splits = min(V, ceil(max_len / 32)) splits suffices.
-   * Needs the MFMA path, num_splits > 1 and no fused append (otherwise
-   * ignored); costs one extra round trip (the lengths) per workgroup.  No
+   * Needs the token-major MFMA path with head_dim 128 and <= 16 query heads
+   * per KV head, num_splits > 1 and no fused append (otherwise ignored);
+   * costs one extra round trip (the lengths) per workgroup.  No
    * counterpart in the reference, whose split count is per launch
    * (flashdec/kernels/paged_decode.py:408-411). */
   int32_t balance_target;
@@ -209,8 +214,8 @@ int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
  * [0, num_splits); the reducer merges them (tail splits only for rows with
  * no prefix).
  *
- * Needs the MFMA path (head_dim 128, <= 16 query heads per KV head, unit
- * dim stride, 16-byte aligned rows), a split workspace of num_splits +
+ * Needs the token-major MFMA path (head_dim 128, <= 16 query heads per KV
+ * head, unit dim stride, 16-byte aligned rows), a split workspace of num_splits +
  * prefix_splits splits and no fused append (append first).  max_prefix_len
  * is a hint (the longest group prefix) for where each split starts.  The
  * timing events [0]/[1] bracket the attention launch, [2]/[3] the reducer.
