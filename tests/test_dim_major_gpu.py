@@ -7,8 +7,9 @@ K through LDS.  These cases cover what that kernel adds over the token-major
 one: lengths that end inside a unit, a block or a quarter of a unit, head
 blocks (G > 16), explicit and planned splits, strided views, non-finite
 values past a row's end, table padding past the used range, streamed
-against cached K/V loads (bit-identical), and the fused current-token append
-(output against the oracle, cache bytes bit-exact, inert rows).  Views whose strides or alignment
+against cached K/V loads (bit-identical), the fused current-token append
+(output against the oracle, cache bytes bit-exact, inert rows), and hipGraph
+replays with new inputs against eager calls.  Views whose strides or alignment
 the kernel does not take run the generic kernel and must agree as well.
 Tolerance: atol 2e-2 / rtol 1e-2 against the fp32 oracle.
 """
@@ -233,3 +234,42 @@ def test_fused_append_inert_rows():
     assert torch.equal(v.view(torch.int16), exp_v.view(torch.int16))
     ref = _oracle(q[:1], exp_k, exp_v, table[:1], lens[:1])
     assert_close_to_oracle(out[:1], ref)
+
+
+@pytest.mark.parametrize("block_size", [8, 32])
+def test_graph_replays_match_eager_with_new_inputs(block_size):
+    # one captured dim-major launch replayed with new q and lengths written
+    # into its buffers between replays (eager work and synchronisations in
+    # between), each replay checked against an eager call on the same inputs
+    q, k, v, table, lens = make_paged_inputs([600, 900, 64], 16, 2, 128, block_size, torch.bfloat16,
+                                             kv_layout="dim_major", seed=47)
+    fd = _fd()
+    ws = _workspace(3, 16, 8)
+    out = torch.empty_like(q)
+
+    def call(o):
+        fd.paged_decode_attention_into(q, k, v, table, lens, o, block_size=block_size, kv_layout="dim_major",
+                                       split_kv_workspace=ws, num_splits=8)
+
+    call(out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph):
+            call(out)
+    torch.cuda.current_stream().wait_stream(stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    for step in range(3):
+        q.copy_(torch.randn(q.shape, device="cuda", generator=gen).to(q.dtype))
+        lens.copy_(torch.tensor([600 - 100 * step, 900 - step, 64 - 3 * step], device="cuda", dtype=lens.dtype))
+        expected = torch.empty_like(q)
+        call(expected)
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), step
+        assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
