@@ -24,6 +24,7 @@ FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
 ABI_VERSION = 6
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
+NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024  # FD_NOALLOC_SCRATCH_BYTES: per-GPU scratch of fd_paged_decode_noalloc
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -119,6 +120,7 @@ class RopeAppendArgs(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "fd_paged_decode",
+    "fd_paged_decode_noalloc",
     "fd_paged_decode_cascade",
     "fd_paged_decode_plan",
     "fd_paged_decode_balance_target",
@@ -157,6 +159,8 @@ def load_library():
             raise RuntimeError(f"failed to load {path}: {exc}") from exc
         lib.fd_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), _vp]
         lib.fd_paged_decode.restype = ctypes.c_int
+        lib.fd_paged_decode_noalloc.argtypes = [ctypes.POINTER(PagedDecodeArgs), _vp]
+        lib.fd_paged_decode_noalloc.restype = ctypes.c_int
         lib.fd_paged_decode_cascade.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(CascadeArgs), _vp]
         lib.fd_paged_decode_cascade.restype = ctypes.c_int
         lib.fd_paged_decode_balance_target.argtypes = [_i64, _i64]
@@ -217,6 +221,13 @@ def paged_decode(args: PagedDecodeArgs, stream: int) -> None:
     lib = load_library()
     args.struct_size = ctypes.sizeof(PagedDecodeArgs)
     check(lib.fd_paged_decode(ctypes.byref(args), stream), "fd_paged_decode")
+
+
+def paged_decode_noalloc(args: PagedDecodeArgs, stream: int) -> None:
+    """``fd_paged_decode_noalloc``: the split partials live in the library's per-GPU scratch."""
+    lib = load_library()
+    args.struct_size = ctypes.sizeof(PagedDecodeArgs)
+    check(lib.fd_paged_decode_noalloc(ctypes.byref(args), stream), "fd_paged_decode_noalloc")
 
 
 def paged_decode_cascade(args: PagedDecodeArgs, cascade: CascadeArgs, stream: int) -> None:

@@ -25,6 +25,7 @@
 //                                             seq_len == 0 / slot < 0
 #include <hip/hip_ext.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "fd_common.h"
@@ -2159,6 +2160,107 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
   const fd_paged_decode_args& a = *args;
 
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (a.dtype == FD_DTYPE_BF16) return launch_decode<__bf16>(a, p, stream);
+  return launch_decode<_Float16>(a, p, stream);
+}
+
+// ------------------------------------------------ no-allocation entry ----
+// Split partials of fd_paged_decode_noalloc live in this file-scope array:
+// one copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol):
+// the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) float scratch[FD_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the stream's device (the current device for
+// the null stream); looked up on the first call on that device, with it
+// current.
+int scratch_address(hipStream_t stream, const char* fn, float** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return set_error(FD_E_LAUNCH, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+  int dev = cur;
+  if (stream != nullptr) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) return set_error(FD_E_LAUNCH, "%s: hipStreamGetDevice failed: %s", fn, hipGetErrorString(e));
+  }
+  if (dev < 0 || dev >= kMaxDevices) return set_error(FD_E_UNSUPPORTED, "%s: device %d >= %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return set_error(FD_E_LAUNCH, "%s: hipSetDevice(%d) failed: %s", fn, dev, hipGetErrorString(e));
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) hipSetDevice(cur);
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(FD_E_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return FD_OK;
+}
+}  // namespace
+
+extern "C" int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream_) {
+  static const char* fn = "fd_paged_decode_noalloc";
+  if (args == nullptr) return set_error(FD_E_INVALID, "%s: args is NULL", fn);
+  if (args->struct_size != sizeof(fd_paged_decode_args))
+    return set_error(FD_E_INVALID, "%s: struct_size %u != %zu (ABI mismatch)", fn, args->struct_size,
+                     sizeof(fd_paged_decode_args));
+  if (args->split_acc || args->split_max || args->split_sum || args->split_counters)
+    return set_error(FD_E_INVALID,
+                     "%s: split_acc, split_max, split_sum and split_counters must be NULL (the library's scratch "
+                     "holds the split partials)",
+                     fn);
+  fd_paged_decode_args a = *args;
+  const bool split = a.num_splits > 1;
+  int64_t rows = 0;
+  if (split) {
+    // stand-in pointers so the shared validation below passes; the scratch
+    // address replaces them after it
+    a.split_acc = a.split_max = a.split_sum = reinterpret_cast<float*>(alignof(float));
+    // fp32 partials: acc [B, Hq, S, D], then max and sum planes [B, Hq, S]
+    // (shapes that fail here are reported by the shared validation)
+    if (a.num_seqs > 0 && a.num_q_heads > 0 && a.num_seqs < (int64_t{1} << 31) && a.num_q_heads < (int64_t{1} << 31) &&
+        a.num_seqs * a.num_q_heads <= 0x7fffffffLL && (a.head_dim == 64 || a.head_dim == 128) &&
+        a.num_splits <= 4096) {
+      rows = a.num_seqs * a.num_q_heads * a.num_splits;
+      const int64_t bytes = rows * (a.head_dim + 2) * static_cast<int64_t>(sizeof(float));
+      if (bytes > static_cast<int64_t>(FD_NOALLOC_SCRATCH_BYTES))
+        return set_error(FD_E_INVALID,
+                         "%s: %lld sequences x %lld query heads x %d splits x (head_dim %lld + 2) fp32 partials "
+                         "(%lld bytes) exceed the %lld-byte scratch; use fewer splits or fd_paged_decode",
+                         fn, static_cast<long long>(a.num_seqs), static_cast<long long>(a.num_q_heads), a.num_splits,
+                         static_cast<long long>(a.head_dim), static_cast<long long>(bytes),
+                         static_cast<long long>(FD_NOALLOC_SCRATCH_BYTES));
+    }
+  }
+  DecodeParams p;
+  const int rc = fill_decode_params(&a, fn, p);
+  if (rc != FD_OK) return rc;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (split) {
+    float* base = nullptr;
+    const int rs = scratch_address(stream, fn, &base);
+    if (rs != FD_OK) return rs;
+    const int64_t S = a.num_splits, D = a.head_dim;
+    p.acc = base;
+    p.as0 = a.num_q_heads * S * D;
+    p.as1 = S * D;
+    p.as2 = D;
+    p.as3 = 1;
+    p.mx = base + rows * D;
+    p.sm = p.mx + rows;
+    p.ss0 = a.num_q_heads * S;
+    p.ss1 = S;
+    p.ss2 = 1;
+  }
+  p.counters = nullptr;  // the reducer kernel merges the splits
   if (a.dtype == FD_DTYPE_BF16) return launch_decode<__bf16>(a, p, stream);
   return launch_decode<_Float16>(a, p, stream);
 }

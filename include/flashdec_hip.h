@@ -1,9 +1,10 @@
 /*
  * flashdec_hip.h -- C ABI of the MI355X (gfx950) paged-decode data path.
  *
- * Every entry point is stateless and re-entrant, allocates no device memory,
- * never synchronises, launches on the caller's hipStream_t and returns an int
- * status (FD_OK or a negative FD_E* code).  On error, fd_last_error() returns
+ * Every entry point allocates no device memory, never synchronises, launches
+ * on the caller's hipStream_t and returns an int status (FD_OK or a negative
+ * FD_E* code).  All are stateless and re-entrant except
+ * fd_paged_decode_noalloc, whose calls share one scratch array per GPU.  On error, fd_last_error() returns
  * a thread-local, human-readable message.  Nothing here throws across the ABI.
  *
  * Tensors are passed as raw device pointers plus element strides, so strided
@@ -190,6 +191,31 @@ typedef struct fd_paged_decode_args {
 } fd_paged_decode_args;
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
+
+/* bytes of the per-GPU scratch array behind fd_paged_decode_noalloc (8 MiB) */
+#define FD_NOALLOC_SCRATCH_BYTES 8388608
+
+/*
+ * fd_paged_decode without a caller workspace and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).
+ *
+ * Same arguments, kernels and results as fd_paged_decode, except that
+ * split_acc, split_max, split_sum and split_counters must be NULL: the split
+ * partials go to a file-scope device array of FD_NOALLOC_SCRATCH_BYTES per
+ * GPU, which each GPU the library runs on holds until the process ends.  A
+ * launch with num_splits > 1 needs
+ *   num_seqs * num_q_heads * num_splits * (head_dim + 2) * 4 bytes
+ * of it (B8 Hq16 D128: up to 126 splits; B64 Hq16: up to 15); larger launches
+ * are rejected with FD_E_INVALID before anything runs.  The splits are
+ * merged by the reducer kernel (no in-launch merge).  Nothing in the array
+ * needs to start at zero.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller.  The first call on a device looks the array's
+ * address up once (hipGetSymbolAddress); no call allocates or frees memory.
+ */
+int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream);
 
 /*
  * Shared-prefix (cascade) decode: the result of fd_paged_decode, with the

@@ -103,3 +103,39 @@ def test_header_constants_match_binding():
     assert int(consts["FD_DTYPE_BF16"]) == _lib.FD_DTYPE_BF16
     assert int(consts["FD_DTYPE_F32"]) == _lib.FD_DTYPE_F32
     assert int(consts["FD_INDEX_I64"]) == _lib.FD_INDEX_I64
+    assert int(consts["FD_NOALLOC_SCRATCH_BYTES"]) == _lib.NOALLOC_SCRATCH_BYTES
+
+
+def _noalloc_args(num_seqs, num_q_heads, head_dim, num_splits):
+    args = _lib.PagedDecodeArgs()
+    args.struct_size = ctypes.sizeof(args)
+    args.dtype = _lib.FD_DTYPE_BF16
+    args.num_seqs, args.num_q_heads, args.num_kv_heads = num_seqs, num_q_heads, 2
+    args.head_dim, args.block_size, args.num_blocks, args.max_blocks_per_seq = head_dim, 32, 1, 1
+    args.num_splits = num_splits
+    return args
+
+
+def test_noalloc_rejects_a_workspace_and_oversized_launches_before_any_hip_call():
+    lib = _lib.load_library()
+    args = _noalloc_args(8, 16, 128, 16)
+    args.split_acc = 0x1000  # never dereferenced: the call is refused first
+    assert lib.fd_paged_decode_noalloc(ctypes.byref(args), None) == -1
+    assert b"must be NULL" in lib.fd_last_error()
+    args = _noalloc_args(8, 16, 128, 16)
+    args.split_counters = 0x1000
+    assert lib.fd_paged_decode_noalloc(ctypes.byref(args), None) == -1
+    assert b"must be NULL" in lib.fd_last_error()
+    # B64 Hq16 D128 S16: 64*16*16*130*4 bytes of partials > 8 MiB
+    args = _noalloc_args(64, 16, 128, 16)
+    assert lib.fd_paged_decode_noalloc(ctypes.byref(args), None) == -1
+    msg = lib.fd_last_error()
+    assert b"exceed" in msg and str(_lib.NOALLOC_SCRATCH_BYTES).encode() in msg
+    # one split more than fits at B8 Hq16 D128 (126 fit)
+    args = _noalloc_args(8, 16, 128, 127)
+    assert lib.fd_paged_decode_noalloc(ctypes.byref(args), None) == -1
+    assert b"exceed" in lib.fd_last_error()
+    args.struct_size -= 8
+    assert lib.fd_paged_decode_noalloc(ctypes.byref(args), None) == -1
+    assert b"struct_size" in lib.fd_last_error()
+    assert lib.fd_paged_decode_noalloc(None, None) == -1

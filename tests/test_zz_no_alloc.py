@@ -1,0 +1,129 @@
+"""fd_paged_decode_noalloc against fd_paged_decode, through the C ABI.
+
+The no-allocation entry point runs the same kernels with the split partials
+in the library's per-GPU scratch array instead of a caller workspace, so its
+output must equal fd_paged_decode's bit for bit (and the oracle within the
+attention tolerance).  Two calls in a row, the second smaller, check that a
+call never depends on what the previous one left in the scratch; the largest
+launch the scratch holds runs too.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import paged_decode_attention as oracle_decode
+from tests.helpers import assert_close_to_oracle, bits16, make_paged_inputs, np32
+
+pytestmark = pytest.mark.gpu
+
+
+def _args(q, k, v, table, lens, out, bs, hkv, splits, ws=None, append=None):
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    args = _lib.PagedDecodeArgs()
+    pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out, hkv, bs,
+                    1.0 / math.sqrt(q.shape[2]))
+    args.num_blocks = k.shape[0]
+    args.max_seq_len = int(lens.max())
+    if ws is not None:
+        pd._fill_workspace(args, *ws, splits)
+    else:
+        args.num_splits = splits
+    if append is not None:
+        pd._fill_append(args, *append)
+    return args
+
+
+def _workspace(b, hq, splits, d):
+    return (torch.empty((b, hq, splits, d), device="cuda"), torch.empty((b, hq, splits), device="cuda"),
+            torch.empty((b, hq, splits), device="cuda"))
+
+
+def _both(q, k, v, table, lens, bs, hkv, splits):
+    """(fd_paged_decode output, fd_paged_decode_noalloc output) on the same inputs."""
+    from flashdec_amd import _lib
+
+    stream = _lib.current_stream_handle(q.device)
+    ref = torch.empty_like(q)
+    _lib.paged_decode(_args(q, k, v, table, lens, ref, bs, hkv, splits, _workspace(*q.shape[:2], splits, q.shape[2])),
+                      stream)
+    out = torch.full_like(q, float("nan"))
+    _lib.paged_decode_noalloc(_args(q, k, v, table, lens, out, bs, hkv, splits), stream)
+    torch.cuda.synchronize()
+    return ref, out
+
+
+def _oracle(q, k, v, table, lens):
+    return oracle_decode(np32(q), np32(k), np32(v), table.cpu().numpy(), lens.cpu().numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_two_calls_in_a_row_match_the_workspace_entry_point(dtype):
+    from flashdec_amd import _lib
+
+    # C2's shape with the library's split plan, then a smaller ragged batch
+    lens_big = [2048] * 8
+    splits = _lib.paged_decode_plan(8, 16, 2, 128, 2048)
+    assert splits > 1
+    q, k, v, table, lens = make_paged_inputs(lens_big, 16, 2, 128, 32, dtype, seed=20260830 + 8 + 2048)
+    ref, out = _both(q, k, v, table, lens, 32, 2, splits)
+    assert torch.equal(ref, out)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+    q, k, v, table, lens = make_paged_inputs([700, 1, 333], 16, 2, 128, 16, dtype, seed=5)
+    ref, out = _both(q, k, v, table, lens, 16, 2, 8)
+    assert torch.equal(ref, out)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+def test_largest_launch_the_scratch_holds():
+    from flashdec_amd import _lib
+
+    b, hq, d = 8, 16, 128
+    splits = _lib.NOALLOC_SCRATCH_BYTES // (b * hq * (d + 2) * 4)
+    assert b * hq * splits * (d + 2) * 4 <= _lib.NOALLOC_SCRATCH_BYTES < b * hq * (splits + 1) * (d + 2) * 4
+    q, k, v, table, lens = make_paged_inputs([4000, 37, 2048, 0, 1, 3999, 100, 64], hq, 2, d, 32, seed=17)
+    ref, out = _both(q, k, v, table, lens, 32, 2, splits)
+    assert torch.equal(ref, out)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+    # and a smaller call right after it
+    q, k, v, table, lens = make_paged_inputs([5, 90], 8, 2, 64, 8, seed=19)
+    ref, out = _both(q, k, v, table, lens, 8, 2, 3)
+    assert torch.equal(ref, out)
+    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+def test_fused_append_writes_the_same_cache_bytes():
+    from flashdec_amd import _lib
+
+    bs, hkv, splits = 32, 2, 8
+    lens_l = [517, 64, 1]
+    q, k, v, table, lens = make_paged_inputs(lens_l, 16, hkv, 128, bs, seed=23)
+    gen = torch.Generator().manual_seed(29)
+    ak = torch.randn((3, hkv, 128), generator=gen).to(torch.bfloat16).cuda()
+    av = torch.randn((3, hkv, 128), generator=gen).to(torch.bfloat16).cuda()
+    slots = []
+    for b, n in enumerate(lens_l):
+        blk = int(table[b, (n - 1) // bs])
+        slots.append(blk * bs + (n - 1) % bs)
+    slot = torch.tensor(slots, device="cuda", dtype=torch.int64)
+    for b, s in enumerate(slots):  # poison the slots: the kernels must take the new token from registers
+        k[s // bs, :, s % bs] = float("nan")
+        v[s // bs, :, s % bs] = float("nan")
+    stream = _lib.current_stream_handle(q.device)
+    k1, v1, k2, v2 = k.clone(), v.clone(), k.clone(), v.clone()
+    ref = torch.empty_like(q)
+    out = torch.empty_like(q)
+    _lib.paged_decode(_args(q, k1, v1, table, lens, ref, bs, hkv, splits, _workspace(3, 16, splits, 128),
+                            (ak, av, slot)), stream)
+    _lib.paged_decode_noalloc(_args(q, k2, v2, table, lens, out, bs, hkv, splits, None, (ak, av, slot)), stream)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, out)
+    assert np.array_equal(bits16(k1), bits16(k2)) and np.array_equal(bits16(v1), bits16(v2))
+    for b, s in enumerate(slots):
+        assert torch.equal(k2[s // bs, :, s % bs], ak[b]) and torch.equal(v2[s // bs, :, s % bs], av[b])
+    assert_close_to_oracle(out, _oracle(q, k2, v2, table, lens))
