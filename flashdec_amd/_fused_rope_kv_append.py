@@ -100,6 +100,20 @@ def _validate_index_values(block_ids, block_offsets, positions, num_blocks, bloc
         raise ValueError("positions must be non-negative")
 
 
+def _check_cos_sin_table(table, rotary_dim, device):
+    """A cos/sin table from :func:`flashdec_amd.rope.rope_cos_sin_table` for this rotary width."""
+    if not isinstance(table, torch.Tensor):
+        raise TypeError("cos_sin_table must be a torch.Tensor")
+    if table.device != device:
+        raise ValueError("cos_sin_table must be on the inputs' device")
+    if table.dtype != torch.float32:
+        raise ValueError("cos_sin_table must be float32")
+    if table.dim() != 3 or table.shape[0] != 2 or table.shape[1] < 1 or table.shape[2] != rotary_dim // 2:
+        raise ValueError("cos_sin_table must have shape [2, num_positions, rotary_dim // 2]")
+    if not table.is_contiguous():
+        raise ValueError("cos_sin_table must be contiguous")
+
+
 def _prepare(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base):
     if rotary_dim is None:
         if not isinstance(q, torch.Tensor):
@@ -109,7 +123,8 @@ def _prepare(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rot
     return rotary_dim, base
 
 
-def _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base, q_out=None):
+def _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base, q_out=None,
+            cos_sin_table=None):
     """One ``fd_fused_rope_kv_append`` launch; the three index tensors share a dtype."""
     if q_out is None:
         q_out = torch.empty_like(q)
@@ -139,27 +154,47 @@ def _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rota
     args.block_offsets = block_offsets.data_ptr()
     args.positions = positions.data_ptr()
     args.index_dtype = _lib.index_code(idx_dtype)
+    if cos_sin_table is not None:
+        args.cos_sin_table = cos_sin_table.data_ptr()
+        args.table_rows = cos_sin_table.shape[1]
     _lib.rope_append(args, _lib.current_stream_handle(q.device), rotate=True)
     return q_out
 
 
 def fused_rope_kv_append(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim=None,
-                         base=10_000.0):
+                         base=10_000.0, cos_sin_table=None):
     """Rotate Q/K and append rotated K / raw V through one HIP kernel.
 
     The caller supplies allocated physical ``block_ids`` and ``block_offsets``
     (one per row).  Returns the rotated Q (new tensor, same shape/dtype); the
     caches are written in place.  Allocator state is not touched.
+
+    ``cos_sin_table`` (no counterpart in the reference): a table from
+    :func:`flashdec_amd.rope.rope_cos_sin_table` for this ``rotary_dim`` and
+    ``base``; the kernel then reads cos/sin instead of evaluating them, and
+    q_out and the K bytes equal :func:`flashdec_amd.rope.apply_rope` on the
+    same device bit for bit.  Every position must be below its row count.
     """
     rotary_dim, base = _prepare(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base)
     _validate_index_values(block_ids, block_offsets, positions, k_cache.shape[0], k_cache.shape[2])
-    return _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base)
+    if cos_sin_table is not None:
+        _check_cos_sin_table(cos_sin_table, rotary_dim, q.device)
+        if bool(torch.any(positions >= cos_sin_table.shape[1]).item()):
+            raise ValueError("positions must be below the cos_sin_table's rows")
+    return _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base,
+                   cos_sin_table=cos_sin_table)
 
 
 def _fused_rope_kv_append_trusted(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions,
-                                  rotary_dim=None, base=10_000.0, q_out=None):
-    """Launch with cache-owned transaction metadata: no device reductions, no syncs."""
+                                  rotary_dim=None, base=10_000.0, q_out=None, cos_sin_table=None):
+    """Launch with cache-owned transaction metadata: no device reductions, no syncs.
+
+    A ``cos_sin_table`` must cover every position (the caller's contract here).
+    """
     rotary_dim, base = _prepare(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base)
     if any(t.dtype != torch.int64 for t in (block_ids, block_offsets, positions)):
         raise ValueError("trusted transaction metadata must use int64")
-    return _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base, q_out=q_out)
+    if cos_sin_table is not None:
+        _check_cos_sin_table(cos_sin_table, rotary_dim, q.device)
+    return _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base, q_out=q_out,
+                   cos_sin_table=cos_sin_table)

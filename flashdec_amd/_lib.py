@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 6
+ABI_VERSION = 7
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024  # FD_NOALLOC_SCRATCH_BYTES: per-GPU scratch of fd_paged_decode_noalloc
 
@@ -77,6 +77,8 @@ class PagedDecodeArgs(ctypes.Structure):
         ("kv_reuse", _i32),
         ("rotary_dim", _i32),
         ("rope_base", ctypes.c_double),
+        ("rope_cos_sin_table", _vp),
+        ("rope_table_rows", _i64),
     ]
 
 
@@ -115,6 +117,8 @@ class RopeAppendArgs(ctypes.Structure):
         ("block_offsets", _vp),
         ("positions", _vp),
         ("index_dtype", _i32),
+        ("cos_sin_table", _vp),
+        ("table_rows", _i64),
     ]
 
 

@@ -597,12 +597,14 @@ class PagedKVCache:
         return self._record_transaction_layer_write(state, layer_idx)
 
     def write_token_layer_fused_cuda(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0,
-                                     q_out=None):
+                                     q_out=None, cos_sin_table=None):
         """Fused RoPE + K/V write of one layer at the transaction's reserved slots (HIP).
 
         The launch reads the allocator's own device copy of the reserved
         locations (resolved from the transaction id, never from the caller's
-        view).  Returns ``(q_rotated, view)``.
+        view).  Returns ``(q_rotated, view)``.  ``cos_sin_table``: see
+        :func:`flashdec_amd.rope.rope_cos_sin_table` (rows must cover the
+        transaction's positions).
         """
         state = self._require_open_transaction(transaction)
         try:
@@ -625,7 +627,8 @@ class PagedKVCache:
             meta = state.meta
             q_rot = _fused_rope_kv_append_trusted(q, k, v, self.k_cache[layer_idx], self.v_cache[layer_idx],
                                                   meta.block_ids, meta.offsets, meta.positions,
-                                                  rotary_dim=rotary_dim, base=base, q_out=q_out)
+                                                  rotary_dim=rotary_dim, base=base, q_out=q_out,
+                                                  cos_sin_table=cos_sin_table)
         except Exception:
             self._transaction_failure_count += 1
             raise

@@ -77,6 +77,8 @@ struct DecodeParams {
   // arrive unrotated and are rotated at position seq_len - 1
   int rope_dim;
   float rope_base;
+  const float* rope_tab;  // optional cos/sin table [2, rope_tab_rows, rope_dim / 2]
+  int64_t rope_tab_rows;
 };
 
 // Row-level bookkeeping shared by the decode kernels.
@@ -463,14 +465,18 @@ __device__ __forceinline__ void store_append(const DecodeParams& p, int kvh, int
 // s of a lane holds dims [32*s + 8*g, +8); with half = rope_dim / 2 its
 // rotation partner is piece s + half / 32 (rope_dim 64: 0 <-> 1, dims 64-127
 // unrotated; 128: 0 <-> 2 and 1 <-> 3).  Lane l evaluates frequency l in
-// float64, and ds_bpermute hands each lane the 8 frequencies of a piece.
+// float64 (or reads it from the caller's cos/sin table), and ds_bpermute
+// hands each lane the 8 frequencies of a piece.
 template <typename T>
 __device__ __forceinline__ void rope_operands(const DecodeParams& p, int32_t seq_len, int lane, int g,
                                               u32x4 (&qf)[4], AppendRegs<128>& ar) {
   const int half = p.rope_dim / 2;  // 32 or 64, checked on the host
   const int64_t pos = seq_len > 0 ? seq_len - 1 : 0;
   float cl, sl;
-  rope_cos_sin(p.rope_base, p.rope_dim, pos, lane < half ? lane : 0, cl, sl);
+  if (p.rope_tab != nullptr)
+    rope_table_cos_sin(p.rope_tab, p.rope_tab_rows, half, pos, lane < half ? lane : 0, cl, sl);
+  else
+    rope_cos_sin(p.rope_base, p.rope_dim, pos, lane < half ? lane : 0, cl, sl);
   const int ci = __builtin_bit_cast(int, cl), si = __builtin_bit_cast(int, sl);
   auto rotate = [&](u32x4& lo_w, u32x4& hi_w, const float (&c)[8], const float (&sn)[8]) {
     u32x4 a = lo_w, b = hi_w;
@@ -2140,6 +2146,14 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
       return set_error(FD_E_UNSUPPORTED, "%s: fused RoPE does not combine with the in-launch merge", fn);
     p.rope_dim = static_cast<int>(a.rotary_dim);
     p.rope_base = static_cast<float>(a.rope_base);  // the reference's pow runs on an fp32 base
+    if (a.rope_cos_sin_table != nullptr) {
+      if (a.rope_table_rows <= 0 || (reinterpret_cast<uintptr_t>(a.rope_cos_sin_table) & 3u))
+        return set_error(FD_E_INVALID, "%s: rope_cos_sin_table needs rope_table_rows > 0 and 4-byte alignment", fn);
+      p.rope_tab = a.rope_cos_sin_table;
+      p.rope_tab_rows = a.rope_table_rows;
+    }
+  } else if (a.rope_cos_sin_table != nullptr) {
+    return set_error(FD_E_INVALID, "%s: rope_cos_sin_table needs rotary_dim (fused RoPE)", fn);
   }
   {
     // first-tile guess of the MFMA kernel: from max_seq_len when given, else

@@ -8,6 +8,11 @@
 //                                       V written to ((blk*Hkv+h)*bs+off)*D+d
 //   flashdec/csrc/kv_append_kernel.cu:10-42   K/V scatter only
 //
+// Table mode (cos_sin_table): cos/sin come from the caller's fp32 table, row =
+// position; built with the reference's torch expression on the same device,
+// the output equals apply_rope there bit for bit (the rotation below is the
+// same unfused arithmetic torch's elementwise ops perform).
+//
 // Bit-exactness: per request, the R/2 angles are formed exactly as
 // rope.py:66-68 does in fp32 (e = fp32(-2i / R), angle = fp32(pos) * inv),
 // while the two transcendental steps -- inv = base^e and cos/sin(angle) --
@@ -40,7 +45,18 @@ struct RopeParams {
   int hq, hkv, head_dim, block_size, rotary_dim;
   int64_t num_blocks;
   float base;  // fp32(base): the reference's pow runs on an fp32 base
+  const float* tab;  // optional cos/sin table [2, tab_rows, rotary_dim / 2]
+  int64_t tab_rows;
 };
+
+// cos/sin of frequency i at position pos: from the caller's table when given,
+// else the correctly rounded evaluation
+__device__ __forceinline__ void rope_angle(const RopeParams& p, int64_t pos, int i, float& c, float& s) {
+  if (p.tab != nullptr)
+    rope_table_cos_sin(p.tab, p.tab_rows, p.rotary_dim / 2, pos, i, c, s);
+  else
+    rope_cos_sin(p.base, p.rotary_dim, pos, i, c, s);
+}
 
 constexpr int kMaxHalf = 512;  // rotary_dim <= 1024
 
@@ -56,7 +72,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeParams p) {
   const int64_t pos = load_index(p.positions, b, p.idx_i64);
   for (int i = tid; i < half; i += blockDim.x) {
     // e = -(2i) / R in fp32, as torch evaluates -arange(0, R, 2) / R
-    rope_cos_sin(p.base, R, pos, i, s_cos[i], s_sin[i]);
+    rope_angle(p, pos, i, s_cos[i], s_sin[i]);
   }
   __syncthreads();
 
@@ -272,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void rope_append_vec_kernel(RopeParams p)
     }
   }
   for (int i = tid; i < half; i += kThreads) {
-    rope_cos_sin(p.base, R, pos, i, s_cos[i], s_sin[i]);
+    rope_angle(p, pos, i, s_cos[i], s_sin[i]);
   }
   __syncthreads();
 #pragma unroll
@@ -332,6 +348,8 @@ int fill_params(const fd_rope_append_args* args, RopeParams& p, bool need_rope, 
       return set_error(FD_E_INVALID, "%s: rotary_dim must be positive, even and <= head_dim", who);
     if (!(a.base > 0.0) || a.base > 3.4e38)
       return set_error(FD_E_INVALID, "%s: base must be a positive finite number", who);
+    if (a.cos_sin_table != nullptr && (a.table_rows <= 0 || (reinterpret_cast<uintptr_t>(a.cos_sin_table) & 3u)))
+      return set_error(FD_E_INVALID, "%s: cos_sin_table needs table_rows > 0 and 4-byte alignment", who);
   }
   p.q_out = a.q_out;
   p.q = a.q;
@@ -350,6 +368,8 @@ int fill_params(const fd_rope_append_args* args, RopeParams& p, bool need_rope, 
   p.rotary_dim = static_cast<int>(a.rotary_dim);
   p.num_blocks = a.num_blocks;
   p.base = static_cast<float>(a.base);
+  p.tab = need_rope ? a.cos_sin_table : nullptr;
+  p.tab_rows = a.table_rows;
   return FD_OK;
 }
 

@@ -9,6 +9,11 @@
 // reference's fp32 expressions.  The rotation of a pair (x1, x2) is
 //   lo = rn(rn(x1 * c) - rn(x2 * s)),  hi = rn(rn(x2 * c) + rn(x1 * s))
 // with contraction into FMAs switched off, then rounded to the element type.
+//
+// Table mode: the caller passes cos/sin already evaluated (e.g. by the
+// reference's own torch expression on the same device, flashdec/rope.py:
+// 66-70), and only the rotation above runs here, so the result equals that
+// expression's rotation bit for bit.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -24,6 +29,18 @@ __device__ __forceinline__ void rope_cos_sin(float base, int rotary_dim, int64_t
   sincos(static_cast<double>(ang), &sd, &cd);
   c = static_cast<float>(cd);
   s = static_cast<float>(sd);
+}
+
+// cos/sin of frequency i at position pos from a caller-built fp32 table
+// [2, rows, half] (plane 0 cos, plane 1 sin, row = position).  Positions
+// outside [0, rows) read the nearest row, which keeps the loads in bounds;
+// callers keep positions below rows (the checked Python entry points
+// verify it).
+__device__ __forceinline__ void rope_table_cos_sin(const float* tab, int64_t rows, int half, int64_t pos, int i,
+                                                   float& c, float& s) {
+  const int64_t r = pos < 0 ? 0 : (pos < rows ? pos : rows - 1);
+  c = tab[r * half + i];
+  s = tab[(rows + r) * half + i];
 }
 
 __device__ __forceinline__ void rope_rotate(float x1, float x2, float c, float s, float& lo, float& hi) {

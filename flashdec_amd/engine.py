@@ -126,6 +126,7 @@ class DecodeStepGraph:
     kv_reuse: bool = False  # rows shared prefix blocks at capture: plain (cached) K/V loads
     fused_rope: bool = False  # RoPE + append inside the decode launch (q_rot unused)
     cascade: Any = None  # _GraphCascade: shared-prefix decode with per-replay group tables
+    cos_sin_table: Any = None  # RoPE cos/sin table every launch reads (None: evaluated in the kernels)
 
 
 @dataclass
@@ -400,8 +401,14 @@ class DecodeEngine:
         tails = [max(0, n + 1 - p) for n, p in zip(lengths, row_prefix)]  # the new token included
         return dataclasses.replace(cached, max_tail_len=max(tails), total_tail_len=sum(tails))
 
-    def step_layer(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0):
-        """RoPE + KV write + paged decode for one layer; any error aborts the whole token."""
+    def step_layer(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0, cos_sin_table=None):
+        """RoPE + KV write + paged decode for one layer; any error aborts the whole token.
+
+        ``cos_sin_table`` (HIP append backend; no counterpart in the reference):
+        a :func:`flashdec_amd.rope.rope_cos_sin_table` covering the step's
+        positions, so q and the appended K are rotated exactly as
+        :func:`flashdec_amd.rope.apply_rope` does on this device.
+        """
         state = self._require_open_step(transaction)
         try:
             layer_idx = int(layer_idx)
@@ -414,11 +421,12 @@ class DecodeEngine:
             if v.dim() == 2:
                 v = v.unsqueeze(0)
             if self._range is None:
-                q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base)
+                q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table)
                 output = self._decode_layer(q_rot, view, meta, layer_idx)
             else:
                 with self._range(PROFILE_RANGE_APPEND):
-                    q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base)
+                    q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base,
+                                                          cos_sin_table)
                 with self._range(PROFILE_RANGE_DECODE):
                     output = self._decode_layer(q_rot, view, meta, layer_idx)
         except Exception:
@@ -467,7 +475,7 @@ class DecodeEngine:
         return self._abort_open_step(self._require_open_step(transaction))
 
     def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None,
-                           merge=False, kv_reuse=None, fuse_rope=None, cascade=None):
+                           merge=False, kv_reuse=None, fuse_rope=None, cascade=None, cos_sin_table=None):
         """Capture every layer's launches of one token step into a hipGraph.
 
         Needs the HIP backends, a GPU cache and its graph-metadata arena
@@ -489,6 +497,9 @@ class DecodeEngine:
         threshold asks) decodes each layer with the shared-prefix launch; the
         group count and size of the active batch at capture bound every later
         step's prefix groups, which each replay reads from the graph's tables.
+        ``cos_sin_table``: a :func:`flashdec_amd.rope.rope_cos_sin_table` with a
+        row for every position the arena's table width allows; every launch
+        then rotates with it (bit-identical to ``apply_rope`` on this device).
         """
         torch = _torch()
         from . import _lib
@@ -507,6 +518,12 @@ class DecodeEngine:
         meta = cache.graph_metadata(batch_size)
         if rotary_dim is None:
             rotary_dim = cache.head_dim
+        if cos_sin_table is not None:
+            from ._fused_rope_kv_append import _check_cos_sin_table
+
+            _check_cos_sin_table(cos_sin_table, int(rotary_dim), cache.device)
+            if cos_sin_table.shape[1] < meta.block_tables.shape[1] * cache.block_size:
+                raise ValueError("cos_sin_table needs a row for every position of the metadata arena's table width")
         shape_q = (cache.num_layers, batch_size, num_q_heads, cache.head_dim)
         shape_kv = (cache.num_layers, batch_size, cache.num_kv_heads, cache.head_dim)
         dev, dt = cache.device, cache.dtype
@@ -615,7 +632,7 @@ class DecodeEngine:
                         _fused_rope_kv_append_trusted(q[layer], k[layer], v[layer], cache.k_cache[layer],
                                                       cache.v_cache[layer], meta.block_ids, meta.offsets,
                                                       meta.positions, rotary_dim=rotary_dim, base=base,
-                                                      q_out=q_rot[layer])
+                                                      q_out=q_rot[layer], cos_sin_table=cos_sin_table)
                         paged_decode_attention_cascade_into(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
                                                             meta.block_tables, meta.eff_lens, out[layer],
                                                             gc.groups, sm_scale=self.sm_scale,
@@ -628,11 +645,12 @@ class DecodeEngine:
                                                cache.block_size, splits, workspace[:3] if workspace else None,
                                                cache.max_blocks, kv_reuse=kv_reuse,
                                                append=(k[layer], v[layer], meta.slots),
-                                               rope=(int(rotary_dim), float(base)))
+                                               rope=(int(rotary_dim), float(base), cos_sin_table))
                         continue
                     _fused_rope_kv_append_trusted(q[layer], k[layer], v[layer], cache.k_cache[layer],
                                                   cache.v_cache[layer], meta.block_ids, meta.offsets, meta.positions,
-                                                  rotary_dim=rotary_dim, base=base, q_out=q_rot[layer])
+                                                  rotary_dim=rotary_dim, base=base, q_out=q_rot[layer],
+                                                  cos_sin_table=cos_sin_table)
                     _decode_with_workspace(q_rot[layer], cache.k_cache[layer], cache.v_cache[layer],
                                            meta.block_tables, meta.eff_lens, out[layer], self.sm_scale,
                                            cache.block_size, splits, workspace[:3] if workspace else None,
@@ -642,7 +660,7 @@ class DecodeEngine:
         return DecodeStepGraph(graph=graph, batch_size=batch_size, q=q, k=k, v=v, q_rot=q_rot, out=out,
                                num_splits=splits, rotary_dim=int(rotary_dim), base=float(base), metadata=meta,
                                workspace=workspace, balance_target=balance, kv_reuse=kv_reuse,
-                               fused_rope=fuse_rope, cascade=gc)
+                               fused_rope=fuse_rope, cascade=gc, cos_sin_table=cos_sin_table)
 
     def step_graph(self, transaction, step_graph):
         """Run every layer of the open step by replaying ``step_graph``; returns ``out [L, B, Hq, D]``.
@@ -768,13 +786,16 @@ class DecodeEngine:
         return True
 
     # ------------------------------------------------------------ internals
-    def _write_layer(self, state, layer_idx, q, k, v, rotary_dim, base):
+    def _write_layer(self, state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table=None):
         """Returns (q_rotated, caller view, allocator device metadata or None)."""
         tx = state.cache_transaction
         if self._append == "fused_hip":
             meta = self.cache.transaction_device_metadata(tx)
+            # the table keyword goes only where it is used: the call keeps the
+            # reference's signature otherwise
+            extra = {} if cos_sin_table is None else {"cos_sin_table": cos_sin_table}
             q_rot, view = self.cache.write_token_layer_fused_cuda(tx, layer_idx, q, k, v, rotary_dim=rotary_dim,
-                                                                  base=base)
+                                                                  base=base, **extra)
             return q_rot, view, meta
         from .rope import apply_rope
 

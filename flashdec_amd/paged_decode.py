@@ -428,10 +428,11 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     merge: one dispatch, no reducer kernel.  ``kv_reuse``: plain instead of
     non-temporal K/V loads (rows share blocks).  ``append`` = ``(append_k,
     append_v, slot_mapping)`` fuses the current token's cache write; with it,
-    ``rope`` = ``(rotary_dim, base)`` (rotary_dim 64 or 128, head_dim 128)
-    takes ``q`` and ``append_k`` unrotated and rotates both at position
-    ``seq_len - 1`` inside the launch -- the same bits as the RoPE + append
-    kernel followed by this decode on the rotated q.  No counterpart in the
+    ``rope`` = ``(rotary_dim, base)`` or ``(rotary_dim, base, cos_sin_table)``
+    (rotary_dim 64 or 128, head_dim 128) takes ``q`` and ``append_k``
+    unrotated and rotates both at position ``seq_len - 1`` inside the launch
+    -- the same bits as the RoPE + append kernel (with the same table, if
+    any) followed by this decode on the rotated q.  No counterpart in the
     reference.
     """
     num_kv_heads = k_cache.shape[1]
@@ -451,6 +452,9 @@ def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_
     if rope is not None:
         args.rotary_dim = int(rope[0])
         args.rope_base = float(rope[1])
+        if len(rope) > 2 and rope[2] is not None:
+            args.rope_cos_sin_table = rope[2].data_ptr()
+            args.rope_table_rows = rope[2].shape[1]
     _lib.paged_decode(args, _lib.current_stream_handle(q.device))
     return out
 

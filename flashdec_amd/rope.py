@@ -91,6 +91,32 @@ def apply_rope(x, positions, rotary_dim=None, base=10_000.0):
     return torch.cat((rotated, x[..., rotary_dim:]), dim=-1)
 
 
+def rope_cos_sin_table(num_positions, rotary_dim, base=10_000.0, device="cuda"):
+    """fp32 ``[2, num_positions, rotary_dim // 2]``: cos (plane 0) and sin (plane 1) of positions
+    ``0 .. num_positions - 1``.
+
+    Evaluated with :func:`apply_rope`'s own torch expression (flashdec/rope.py:
+    66-70) on ``device``, so the HIP kernels that read it
+    (``fused_rope_kv_append(..., cos_sin_table=...)`` and the engine's fused
+    decode launch) rotate exactly as :func:`apply_rope` does there, bit for
+    bit.  No counterpart in the reference.
+    """
+    torch = _torch()
+    num_positions = int(num_positions)
+    if num_positions <= 0:
+        raise ValueError("num_positions must be positive")
+    if isinstance(rotary_dim, bool) or not isinstance(rotary_dim, int) or rotary_dim <= 0 or rotary_dim % 2:
+        raise ValueError("rotary_dim must be a positive even integer")
+    base = float(base)
+    if not math.isfinite(base) or base <= 0.0:
+        raise ValueError("base must be a positive finite number")
+    steps = torch.arange(0, rotary_dim, 2, device=device, dtype=torch.float32)
+    inv_freq = torch.pow(base, -steps / rotary_dim)
+    positions = torch.arange(num_positions, device=device, dtype=torch.int64)
+    angles = positions.to(torch.float32)[:, None] * inv_freq[None, :]
+    return torch.stack((torch.cos(angles), torch.sin(angles))).contiguous()
+
+
 def _prepare_inputs(cache, request_ids, q, k, v):
     """Validate one RoPE + paged append batch (rope.py:88-124, same messages)."""
     from .cache import PagedKVCache

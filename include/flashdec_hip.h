@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 6
+#define FD_ABI_VERSION 7
 
 /* status codes */
 #define FD_OK 0
@@ -188,6 +188,12 @@ typedef struct fd_paged_decode_args {
    * append as its own kernel. */
   int32_t rotary_dim;
   double rope_base;
+  /* Optional with fused RoPE: fp32 cos/sin table [2, rope_table_rows,
+   * rotary_dim / 2], contiguous (plane 0 cos, plane 1 sin, row = position),
+   * used instead of the kernel's own evaluation -- see cos_sin_table of
+   * fd_rope_append_args.  NULL = off.  Needs rotary_dim != 0. */
+  const float* rope_cos_sin_table;
+  int64_t rope_table_rows;
 } fd_paged_decode_args;
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
@@ -321,6 +327,17 @@ typedef struct fd_rope_append_args {
   const void* block_offsets;
   const void* positions;
   int32_t index_dtype; /* FD_INDEX_I32 / FD_INDEX_I64, shared by the three */
+  /* Optional fp32 cos/sin table [2, table_rows, rotary_dim / 2], contiguous:
+   * plane 0 cos, plane 1 sin, row p = the angles of position p.  When given,
+   * cos/sin are read from it instead of being evaluated, and only the
+   * rotation above runs: a table built with flashdec/rope.py:66-70's torch
+   * expression on the same device makes q_out and the K bytes equal that
+   * apply_rope bit for bit.  Positions must be < table_rows (a position
+   * outside reads the nearest row; nothing is read out of bounds).  NULL =
+   * off (the correctly rounded evaluation).  fd_kv_append ignores it.
+   * No counterpart in the reference. */
+  const float* cos_sin_table;
+  int64_t table_rows;
 } fd_rope_append_args;
 
 int fd_fused_rope_kv_append(const fd_rope_append_args* args, fd_stream_t stream);

@@ -71,3 +71,19 @@ def assert_close_to_oracle(actual, expected, atol=ATOL, rtol=RTOL):
 def bits16(t):
     """Bit patterns of a 16-bit float tensor (for bit-exact comparisons)."""
     return t.detach().contiguous().view(torch.int16).cpu().numpy()
+
+
+def rope_pair_bound(x, pos, rotary_dim, base):
+    """Per-element bound on how far two fp32 evaluations of split-half RoPE may differ when each
+    one's inv_freq is within an ulp of the correctly rounded value (cos/sin within an ulp too).
+
+    Frequency i's angle error is at most (pos + 1) * ulp(inv_i) <= (pos + 1) * inv_i * 2^-23 per
+    evaluation; each rotated element moves by at most (|x_lo| + |x_hi|) times the angle error plus
+    the products' and sum's rounding (2^-21 relative).  Low frequencies (inv_i << 1) therefore get
+    a bound far below the position-independent 2^-23 * pos * max|x|.
+    """
+    half = rotary_dim // 2
+    inv = np.array([base ** (-2.0 * i / rotary_dim) for i in range(half)])
+    pair = np.abs(x[..., :half]) + np.abs(x[..., half:rotary_dim])
+    per = pair * (2.0 * (np.asarray(pos, dtype=np.float64)[:, None, None] + 1) * inv * 2.0**-23 + 2.0**-21)
+    return np.concatenate([per, per], axis=-1)

@@ -18,6 +18,7 @@ import torch
 from oracle import attention as oa
 from oracle import rope as orope
 from oracle import split_policy as osp
+from tests.helpers import rope_pair_bound
 
 KATS = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
@@ -221,7 +222,7 @@ def test_rope_invariants():
         orope.apply_rope(x, -pos - 1)
 
 
-def test_rope_within_one_ulp_of_torch_reference_order():
+def test_rope_matches_torch_reference_order_per_frequency():
     from flashdec_amd.rope import apply_rope as torch_rope
 
     rng = np.random.default_rng(9)
@@ -229,16 +230,51 @@ def test_rope_within_one_ulp_of_torch_reference_order():
     pos = rng.integers(0, 32768, 8)
     ours = orope.apply_rope(x, pos, base=1e6)
     theirs = torch_rope(torch.from_numpy(x), torch.from_numpy(pos), base=1e6).numpy()
-    # torch's fp32 pow may be one ulp off the correctly rounded inv_freq (<= eps since inv <= 1); that
-    # error is multiplied by the position inside the angle, so |d angle| <= pos * eps and each output
-    # moves by at most |x| * 2 * (pos + 1) * eps (plus rounding); a wrong formula moves it by O(|x|).
-    eps = np.finfo(np.float32).eps
-    tol = 8 * eps * np.abs(x).max() * (1 + pos.astype(np.float64))
-    assert (np.abs(ours - theirs).max(axis=(1, 2)) <= tol).all()
+    assert (np.abs(ours - theirs) <= rope_pair_bound(x, pos, 64, 1e6)).all()
     steps = torch.arange(0, 64, 2, dtype=torch.float32)
     torch_inv = torch.pow(1e6, -steps / 64).numpy()
     oracle_inv = np.array([np.float32(math.pow(1e6, float(np.float32(-s / np.float32(64))))) for s in steps.numpy()])
     assert (np.abs(torch_inv - oracle_inv) <= np.spacing(oracle_inv)).all()
+
+
+def test_rope_frequencies_match_the_closed_form():
+    """Rotating unit vectors recovers each frequency's angle; against theta_i = exp(-2i/R * ln base)
+    (float64), it is off by no more than the fp32 algorithm's own rounding: (pos + 1) * theta_i *
+    2^-22 + 2^-22.  A wrong frequency (index off by one, a different base, a dropped factor 2)
+    changes the angle by a fraction of pos * theta_i and fails at every position tested."""
+    def angles(fn, pos, rotary_dim, base):
+        half = rotary_dim // 2
+        x = np.zeros((len(pos), 1, rotary_dim), dtype=np.float32)
+        x[..., :half] = 1.0  # lo = cos(angle), hi = sin(angle)
+        out = fn(x, pos, rotary_dim, base)
+        return np.arctan2(out[:, 0, half:].astype(np.float64), out[:, 0, :half].astype(np.float64))
+
+    pos = np.array([1, 2, 3, 17, 100, 1000, 8191, 32767])
+    for rotary_dim, base in ((128, 1e6), (64, 1e4), (128, 10000.0)):
+        half = rotary_dim // 2
+        theta = np.exp(-2.0 * np.arange(half) / rotary_dim * math.log(base))
+        exact = np.mod(pos[:, None] * theta[None, :] + math.pi, 2 * math.pi) - math.pi
+        tol = (pos[:, None] + 1) * theta[None, :] * 2.0**-22 + 2.0**-22
+
+        def wrapped(a, b):
+            return np.abs(np.mod(a - b + math.pi, 2 * math.pi) - math.pi)
+
+        def oracle(x, p, r, bs):
+            return orope.apply_rope(x, p, rotary_dim=r, base=bs)
+
+        assert (wrapped(angles(oracle, pos, rotary_dim, base), exact) <= tol).all()
+        # planted mistakes in the frequency formula: each must fail the same check
+        for wrong_base, wrong_shift, wrong_scale in ((base * 10, 0, 1.0), (base, 1, 1.0), (base, 0, 0.5)):
+            theta_w = np.exp(-2.0 * (np.arange(half) + wrong_shift) / rotary_dim * math.log(wrong_base)) * wrong_scale
+            cos_w, sin_w = np.cos(pos[:, None] * theta_w), np.sin(pos[:, None] * theta_w)
+
+            def planted(x, p, r, bs, cos_w=cos_w, sin_w=sin_w):
+                out = x.copy()
+                out[..., :half] = x[..., :half] * cos_w[:, None] - x[..., half:r] * sin_w[:, None]
+                out[..., half:r] = x[..., half:r] * cos_w[:, None] + x[..., :half] * sin_w[:, None]
+                return out
+
+            assert (wrapped(angles(planted, pos, rotary_dim, base), exact) > tol).any()
 
 
 def test_planted_rope_mistakes_are_detected():
