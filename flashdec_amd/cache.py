@@ -1,19 +1,34 @@
-"""Paged KV cache runtime: block allocator, multi-layer token transactions,
+"""Paged KV cache runtime: block pool, multi-layer token transactions and
 refcounted shared prefixes -- host-side state with device-resident tables.
 
-Semantics follow cysong2025/flashdec ``flashdec/cache.py`` (``PagedKVCache``,
-:74-1409): the physical pool ``[num_layers, max_blocks, num_kv_heads,
-block_size, head_dim]`` for K and V (:136-145), a deterministic free list
-(``popleft`` to allocate, released blocks pushed back to the front in
-reverse, :146, 1245-1255, 1269-1270), one open token transaction at a time
-(:438-648), shared-prefix registry with LRU eviction (:192-276, 1365-1397),
-the 45-key ``metrics()`` (:705-803) and ``validate_invariants()``
-(:805-943).  Method names, arguments and error messages are the reference's
-so callers drop in.
+Public surface and observable behaviour follow cysong2025/flashdec
+``flashdec/cache.py`` (``PagedKVCache``, :74-1409): the physical pool
+``[num_layers, max_blocks, num_kv_heads, block_size, head_dim]`` for K and V
+(:136-145), the order in which block ids are handed out and returned
+(:146, 1245-1255, 1269-1270), one open token transaction at a time
+(:438-648), the shared-prefix registry with LRU eviction (:192-276,
+1365-1397), the 45-key ``metrics()`` (:705-803), ``validate_invariants()``
+(:805-943), method names, arguments, error types and messages, and where the
+state version advances.  Reference-recorded operation traces
+(``tests/golden/cache_traces.json``) pin all of it.
+
+Internal organisation (this module's own):
+
+* :class:`_Pool` -- the free list and its allocation statistics; the only
+  code that moves block ids in or out of it.
+* :class:`_Seq` -- one request: status, committed length, page list (logical
+  block -> physical block), the leading pages it borrows from a prefix, and
+  the open transaction it belongs to.
+* :class:`_PrefixBook` -- resident shared prefixes in LRU order.
+* :class:`_Journal` -- the open transaction (:class:`_Txn`, at most one) and
+  a bounded, tensor-free history of closed ones (:class:`_Closed`).
+* :class:`_Tally` -- event counters reported by ``metrics()``.
+* Argument contracts are rule tables (``_rules``) checked in order, and the
+  ownership invariants are one rule list over a snapshot of the ledger.
 
 MI355X-specific: a transaction's metadata (positions, physical block ids,
-offsets, padded block tables, effective lengths) is packed on the host into
-one pinned staging buffer and sent with a single H2D copy when the
+offsets, slots, padded block tables, effective lengths) is packed on the host
+into one pinned staging buffer and sent with a single H2D copy when the
 transaction opens; each layer's fused RoPE + append launch reads that
 resident buffer directly.  Views handed to callers are device-side clones, so
 a caller mutating them cannot reach the allocator's copy.
@@ -27,22 +42,6 @@ from dataclasses import dataclass, field, replace
 from typing import Hashable
 
 import numpy as np
-
-
-@dataclass
-class _RequestState:
-    status: str = "active"
-    seq_len: int = 0
-    block_ids: list = field(default_factory=list)
-    transaction_id: int | None = None
-    prefix_id: Hashable | None = None
-    shared_block_count: int = 0
-
-
-@dataclass
-class _PrefixState:
-    block_ids: tuple
-    active_refcount: int = 0
 
 
 @dataclass(frozen=True)
@@ -167,32 +166,6 @@ class _StagingRing:
         self.events[i] = ev
 
 
-@dataclass
-class _KVTokenTransactionState:
-    transaction_id: int
-    cache_version: int
-    request_ids: tuple
-    positions: tuple
-    locations: tuple
-    block_tables: object
-    newly_allocated_by_request: dict
-    allocation_order: tuple
-    meta: object = None
-    next_layer_idx: int = 0
-    written_layers: set = field(default_factory=set)
-    state: str = "open"
-
-
-@dataclass(frozen=True)
-class _TerminalTransactionState:
-    """Metadata-only tombstone for a recently closed transaction."""
-
-    transaction_id: int
-    cache_version: int
-    request_ids: tuple
-    state: str
-
-
 def _torch():
     import torch
 
@@ -216,6 +189,283 @@ def _host_to_device(data, dtype, device):
     return host.pin_memory().to(device, non_blocking=True)
 
 
+# ------------------------------------------------------------------ ledger --
+OUT_OF_BLOCKS = "PagedKVCache is out of physical blocks"
+
+
+class _Pool:
+    """Free physical blocks (a deque: taken from the front; returned blocks go
+    back to the front, last one first, so they are the next handed out) and
+    allocation statistics."""
+
+    __slots__ = ("free", "seen", "taken", "fresh", "reused", "released")
+
+    def __init__(self, size):
+        self.free = deque(range(size))
+        self.seen = bytearray(size)  # 1 once a block has ever been handed out
+        self.taken = 0
+        self.fresh = 0
+        self.reused = 0
+        self.released = 0  # blocks given back by closed requests and evicted prefixes
+
+    def __len__(self):
+        return len(self.free)
+
+    def take(self):
+        if not self.free:
+            raise RuntimeError(OUT_OF_BLOCKS)
+        blk = self.free.popleft()
+        self.taken += 1
+        if self.seen[blk]:
+            self.reused += 1
+        else:
+            self.seen[blk] = 1
+            self.fresh += 1
+        return blk
+
+    def give_back(self, blocks, *, released):
+        """Return ``blocks`` to the front so that ``blocks[0]`` is the next one
+        taken; ``released`` counts them as freed (closing and eviction do,
+        transaction rollback does not)."""
+        for blk in reversed(blocks):
+            self.free.appendleft(blk)
+        if released:
+            self.released += len(blocks)
+
+
+@dataclass(eq=False)
+class _Seq:
+    """One request's ledger entry."""
+
+    __slots__ = ("status", "length", "pages", "txn", "prefix", "shared")
+    status: str
+    length: int  # committed tokens
+    pages: list  # physical block of each logical block
+    txn: int | None  # id of the open transaction holding a reserved token
+    prefix: Hashable | None
+    shared: int  # leading pages that belong to the prefix
+
+    @classmethod
+    def empty(cls):
+        return cls("active", 0, [], None, None, 0)
+
+    def private_pages(self):
+        return self.pages[self.shared:]
+
+
+@dataclass(eq=False)
+class _PrefixEntry:
+    __slots__ = ("pages", "refs")
+    pages: tuple
+    refs: int
+
+
+class _PrefixBook:
+    """Resident prefixes, least recently used first."""
+
+    __slots__ = ("entries",)
+
+    def __init__(self):
+        self.entries: OrderedDict = OrderedDict()
+
+    def __contains__(self, pid):
+        return pid in self.entries
+
+    def get(self, pid):
+        return self.entries.get(pid)
+
+    def touch(self, pid):
+        self.entries.move_to_end(pid)
+
+    def resident_blocks(self):
+        return sum(len(e.pages) for e in self.entries.values())
+
+    def room_plan(self, blocks, capacity, free):
+        """Idle prefixes to evict (LRU first) so that ``blocks`` more fit both
+        the prefix capacity and the free pool: ``()`` if none need to go,
+        None if even evicting every idle prefix would not do."""
+        if blocks > capacity:
+            return None
+        short = max(0, self.resident_blocks() + blocks - capacity, blocks - free)
+        plan, gained = [], 0
+        for pid, entry in self.entries.items():
+            if gained >= short:
+                break
+            if not entry.refs:
+                plan.append(pid)
+                gained += len(entry.pages)
+        return tuple(plan) if gained >= short else None
+
+    def drop(self, pid):
+        entry = self.entries[pid]
+        if entry.refs:
+            raise RuntimeError("cannot evict a prefix with active request references")
+        del self.entries[pid]
+        return entry.pages
+
+
+@dataclass(eq=False)
+class _Txn:
+    """The open token transaction."""
+
+    __slots__ = ("tid", "version", "rids", "positions", "slots", "grown", "meta", "layers", "phase")
+    tid: int
+    version: int  # the state version its opening published
+    rids: tuple
+    positions: tuple  # pre-append length of each row
+    slots: tuple  # (block, offset) of each row's reserved token
+    grown: tuple  # (request id, block) of each page this transaction appended, in allocation order
+    meta: object  # _DeviceMeta
+    layers: int  # layers written so far (always 0 .. layers-1, in order)
+    phase: str
+
+
+@dataclass(frozen=True)
+class _Closed:
+    """Tensor-free record of a committed or aborted transaction."""
+
+    __slots__ = ("tid", "version", "rids", "phase")
+    tid: int
+    version: int
+    rids: tuple
+    phase: str
+
+
+class _Journal:
+    """At most one open transaction plus the last ``limit`` closed ones."""
+
+    __slots__ = ("open", "history", "limit", "next_id")
+
+    def __init__(self, limit):
+        self.open: _Txn | None = None
+        self.history: OrderedDict = OrderedDict()
+        self.limit = limit
+        self.next_id = 1
+
+    def find(self, handle):
+        if not isinstance(handle, KVTokenTransactionView):
+            raise TypeError("transaction must be a KVTokenTransactionView")
+        tid = handle.transaction_id
+        rec = self.open if self.open is not None and self.open.tid == tid else self.history.get(tid)
+        if rec is None:
+            raise RuntimeError("unknown token transaction")
+        if handle.cache_version != rec.version or handle.request_ids != rec.rids:
+            raise RuntimeError("stale or invalid token transaction handle")
+        return rec
+
+    def find_open(self, handle):
+        rec = self.find(handle)
+        if rec.phase != "open":
+            raise RuntimeError(f"token transaction is already {rec.phase}")
+        if self.open is not rec:
+            raise RuntimeError("token transaction is not the current open transaction")
+        return rec
+
+    def close(self, txn, phase):
+        if self.open is not txn:
+            raise RuntimeError("token transaction retention state is inconsistent")
+        txn.phase = phase
+        self.open = None
+        self.history[txn.tid] = _Closed(txn.tid, txn.version, txn.rids, phase)
+        while len(self.history) > self.limit:
+            self.history.popitem(last=False)
+
+
+class _Tally:
+    """Event counters (the pool keeps its own allocation statistics)."""
+
+    __slots__ = ("capacity_failures", "begins", "commits", "aborts", "layer_writes", "rollback_blocks", "failures",
+                 "prefix_registrations", "prefix_hits", "prefix_misses", "prefix_evictions",
+                 "prefix_capacity_failures")
+
+    def __init__(self):
+        for name in self.__slots__:
+            setattr(self, name, 0)
+
+
+def _rules(*checks):
+    """An argument contract: ``(predicate, exception type, message)`` rows, checked in order."""
+
+    def check(*args):
+        for ok, exc, msg in checks:
+            if not ok(*args):
+                raise exc(msg)
+
+    return check
+
+
+def _require_hashable(x, what="request ids"):
+    try:
+        hash(x)
+    except TypeError as exc:
+        raise ValueError(f"{what} must be hashable") from exc
+
+
+# per-token K/V rows [num_requests, num_kv_heads, head_dim] for one layer
+# (args: cache, row count, k, v)
+_check_kv_rows = _rules(
+    (lambda c, n, k, v: k.dim() == 3 and v.dim() == 3, ValueError,
+     "k and v must have shape [num_requests, num_kv_heads, head_dim]"),
+    (lambda c, n, k, v: k.shape == v.shape, ValueError, "k and v must have the same shape"),
+    (lambda c, n, k, v: k.shape == (n, c.num_kv_heads, c.head_dim), ValueError,
+     "k and v shapes must match request count, num_kv_heads, and head_dim"),
+    (lambda c, n, k, v: k.device == c.device and v.device == c.device, ValueError,
+     "k and v must be on the cache device"),
+    (lambda c, n, k, v: k.dtype == c.dtype and v.dtype == c.dtype, ValueError, "k and v must use the cache dtype"),
+    (lambda c, n, k, v: k.is_floating_point() and v.is_floating_point(), ValueError,
+     "k and v must be floating point tensors"),
+)
+
+# shared-prefix blocks [num_layers, n, num_kv_heads, block_size, head_dim] (args: cache, k, v)
+_check_prefix_blocks = _rules(
+    (lambda c, k, v: isinstance(k, _torch().Tensor) and isinstance(v, _torch().Tensor), TypeError,
+     "k_blocks and v_blocks must be torch tensors"),
+    (lambda c, k, v: k.dim() == 5 and v.dim() == 5, ValueError,
+     "prefix K/V must have shape [num_layers, num_prefix_blocks, num_kv_heads, block_size, head_dim]"),
+    (lambda c, k, v: k.shape == v.shape, ValueError, "prefix k_blocks and v_blocks must have the same shape"),
+    (lambda c, k, v: k.shape[0] == c.num_layers and tuple(k.shape[2:]) == (c.num_kv_heads, c.block_size, c.head_dim),
+     ValueError, "prefix K/V shape does not match the PagedKVCache layout"),
+    (lambda c, k, v: k.shape[1] > 0, ValueError, "prefix must contain at least one full block"),
+    (lambda c, k, v: k.device == c.device and v.device == c.device, ValueError,
+     "prefix K/V must be on the cache device"),
+    (lambda c, k, v: k.dtype == c.dtype and v.dtype == c.dtype, ValueError, "prefix K/V must use the cache dtype"),
+)
+
+# q of a fused RoPE + append [num_requests, num_q_heads, head_dim] (args: cache, row count, q)
+_check_fused_q = _rules(
+    (lambda c, n, q: q.dim() == 3 and q.shape[0] == n and q.shape[1] > 0 and q.shape[2] == c.head_dim, ValueError,
+     "q shape must match request count and cache head_dim"),
+    (lambda c, n, q: q.device == c.device and q.dtype == c.dtype, ValueError, "q must use the cache device and dtype"),
+)
+
+_check_transaction_q = _rules(
+    (lambda c, n, q: q.dim() == 3 and q.shape[0] == n and q.shape[1] > 0 and q.shape[2] == c.head_dim, ValueError,
+     "q shape must match transaction request count and cache head_dim"),
+    (lambda c, n, q: q.device == c.device and q.dtype == c.dtype, ValueError, "q must use the cache device and dtype"),
+)
+
+
+def _rotary_dim_and_base(head_dim, rotary_dim, base):
+    if rotary_dim is None:
+        rotary_dim = head_dim
+    if isinstance(rotary_dim, bool) or not isinstance(rotary_dim, int):
+        raise ValueError("rotary_dim must be an even integer")
+    if not 0 < rotary_dim <= head_dim or rotary_dim % 2:
+        raise ValueError("rotary_dim must be positive, even, and no larger than head_dim")
+    base = float(base)
+    if not math.isfinite(base) or base <= 0.0:
+        raise ValueError("base must be a positive finite number")
+    return rotary_dim, base
+
+
+def _rows_unique(ids, message):
+    if not ids:
+        raise ValueError("request_ids must be non-empty")
+    if len(set(ids)) != len(ids):
+        raise ValueError(message)
+
+
+# ------------------------------------------------------------------ facade --
 class PagedKVCache:
     """Fixed-block KV cache runtime for single-token decode.
 
@@ -235,26 +485,17 @@ class PagedKVCache:
     def __init__(self, num_layers, num_kv_heads, head_dim, block_size, max_blocks, dtype=None, device=None,
                  prefix_cache_capacity_blocks=0):
         torch = _torch()
-        if dtype is None:
-            dtype = torch.float16
-        if device is None:
-            device = "cuda" if torch.cuda.is_available() else "cpu"
-        for name, value in [
-            ("num_layers", num_layers),
-            ("num_kv_heads", num_kv_heads),
-            ("head_dim", head_dim),
-            ("block_size", block_size),
-            ("max_blocks", max_blocks),
-        ]:
+        dtype = torch.float16 if dtype is None else dtype
+        device = ("cuda" if torch.cuda.is_available() else "cpu") if device is None else device
+        dims = {"num_layers": num_layers, "num_kv_heads": num_kv_heads, "head_dim": head_dim,
+                "block_size": block_size, "max_blocks": max_blocks}
+        for name, value in dims.items():
             if int(value) <= 0:
                 raise ValueError(f"{name} must be positive")
         if not torch.empty((), dtype=dtype).is_floating_point():
             raise ValueError("dtype must be a floating point torch dtype")
-        self.num_layers = int(num_layers)
-        self.num_kv_heads = int(num_kv_heads)
-        self.head_dim = int(head_dim)
-        self.block_size = int(block_size)
-        self.max_blocks = int(max_blocks)
+        for name, value in dims.items():
+            setattr(self, name, int(value))
         self.prefix_cache_capacity_blocks = int(prefix_cache_capacity_blocks)
         if self.prefix_cache_capacity_blocks < 0:
             raise ValueError("prefix_cache_capacity_blocks must be non-negative")
@@ -265,56 +506,87 @@ class PagedKVCache:
         self.k_cache = torch.zeros(shape, device=device, dtype=dtype)
         self.device = self.k_cache.device
         self.v_cache = torch.zeros_like(self.k_cache)
-        self._free_blocks = deque(range(self.max_blocks))
-        self._requests: dict = {}
-        self._prefixes: OrderedDict = OrderedDict()
-        self._ever_allocated_blocks: set = set()
-        self._allocation_count = 0
-        self._fresh_allocation_count = 0
-        self._free_count = 0
-        self._reuse_count = 0
-        self._capacity_failure_count = 0
-        self._state_version = 0
-        self._next_transaction_id = 1
-        self._open_transaction_id = None
-        self._transactions: dict = {}
-        self._terminal_transactions: OrderedDict = OrderedDict()
-        self._terminal_transaction_history_limit = self._TERMINAL_TRANSACTION_HISTORY_LIMIT
-        self._transaction_begin_count = 0
-        self._transaction_commit_count = 0
-        self._transaction_abort_count = 0
-        self._transaction_layer_write_count = 0
-        self._transaction_rollback_block_count = 0
-        self._transaction_failure_count = 0
-        self._prefix_registration_count = 0
-        self._prefix_hit_count = 0
-        self._prefix_miss_count = 0
-        self._prefix_eviction_count = 0
-        self._prefix_capacity_failure_count = 0
+        self._pool = _Pool(self.max_blocks)
+        self._seqs: dict = {}  # request id -> _Seq, in first-seen order
+        self._prefix_book = _PrefixBook()
+        self._journal = _Journal(self._TERMINAL_TRANSACTION_HISTORY_LIMIT)
+        self._tally = _Tally()
+        self._version = 0
         self._meta_arena = None  # (device buffer, capacity rows, table width) once enabled
         self._meta_staging = None  # pinned staging ring of the arena copies
+
+    # ---------------------------------------------------------- state guards
+    def _no_transaction(self, message):
+        if self._journal.open is not None:
+            raise RuntimeError(message)
+
+    def _publish(self):
+        """Advance the state version (every successful mutation does, once)."""
+        self._version += 1
+
+    def _seq(self, request_id):
+        seq = self._seqs.get(request_id)
+        if seq is None:
+            raise KeyError(f"unknown request_id: {request_id!r}")
+        return seq
+
+    def _active_seq(self, request_id):
+        seq = self._seq(request_id)
+        if seq.status != self.ACTIVE:
+            raise RuntimeError(f"request_id {request_id!r} is {seq.status}, not active")
+        return seq
+
+    def _prefix_entry(self, prefix_id):
+        if prefix_id is None:
+            raise ValueError("prefix_id must not be None")
+        _require_hashable(prefix_id, "prefix ids")
+        return self._prefix_book.get(prefix_id)
+
+    def _pages_for(self, length):
+        return -(-length // self.block_size)
 
     # ------------------------------------------------------------ lifecycle
     def add_request(self, request_id):
         """Register an empty request if it does not already exist."""
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot add a request during an open token transaction")
-        self._check_request_id(request_id)
-        state = self._requests.get(request_id)
-        if state is None:
-            self._requests[request_id] = _RequestState()
-            self._state_version += 1
-        elif state.status != self.ACTIVE:
-            raise RuntimeError(f"request_id {request_id!r} is {state.status} and cannot be reactivated")
+        self._no_transaction("cannot add a request during an open token transaction")
+        _require_hashable(request_id)
+        seq = self._seqs.get(request_id)
+        if seq is None:
+            self._seqs[request_id] = _Seq.empty()
+            self._publish()
+        elif seq.status != self.ACTIVE:
+            raise RuntimeError(f"request_id {request_id!r} is {seq.status} and cannot be reactivated")
         return self
 
     def finish_request(self, request_id):
         """Mark an active request finished and release its private blocks."""
-        return self._close_request(request_id, self.FINISHED)
+        return self._retire_request(request_id, self.FINISHED)
 
     def cancel_request(self, request_id):
         """Mark an active request cancelled and release its private blocks."""
-        return self._close_request(request_id, self.CANCELLED)
+        return self._retire_request(request_id, self.CANCELLED)
+
+    def _retire_request(self, request_id, status):
+        self._no_transaction("cannot close a request during an open token transaction")
+        seq = self._active_seq(request_id)
+        entry = self._prefix_book.get(seq.prefix) if seq.prefix is not None else None
+        if seq.prefix is not None and (entry is None or entry.refs <= 0):
+            raise RuntimeError("shared prefix reference accounting is inconsistent")
+        # the K/V bytes stay: ownership and the next owner's length mask them
+        released = tuple(seq.private_pages())
+        self._pool.give_back(released, released=True)
+        if entry is not None:
+            entry.refs -= 1
+            self._prefix_book.touch(seq.prefix)
+        seq.pages, seq.prefix, seq.shared, seq.status = [], None, 0, status
+        self._publish()
+        return released
+
+    def request_state(self, request_id):
+        """Detached snapshot of one request's lifecycle state."""
+        seq = self._seq(request_id)
+        return {"request_id": request_id, "status": seq.status, "seq_len": seq.length,
+                "block_ids": tuple(seq.pages), "prefix_id": seq.prefix, "shared_block_count": seq.shared}
 
     def _prefix_groups(self, request_ids):
         """Rows of ``request_ids`` attached to the same resident prefix, from
@@ -322,26 +594,14 @@ class PagedKVCache:
         of them (the rows' tables all lead with the prefix's blocks)."""
         by_prefix = {}
         for row, rid in enumerate(request_ids):
-            state = self._require_request(rid)
-            if state.prefix_id is not None and state.shared_block_count > 0:
-                by_prefix.setdefault(state.prefix_id, (state.shared_block_count, []))[1].append(row)
+            seq = self._seq(rid)
+            if seq.prefix is not None and seq.shared > 0:
+                by_prefix.setdefault(seq.prefix, (seq.shared, []))[1].append(row)
         return [(rows, blocks) for blocks, rows in by_prefix.values() if len(rows) >= 2]
 
     def _host_seq_lens(self, request_ids):
         """Current lengths of known requests, from host state (no device access)."""
-        return [self._require_request(rid).seq_len for rid in request_ids]
-
-    def request_state(self, request_id):
-        """Detached snapshot of one request's lifecycle state."""
-        state = self._require_request(request_id)
-        return {
-            "request_id": request_id,
-            "status": state.status,
-            "seq_len": state.seq_len,
-            "block_ids": tuple(state.block_ids),
-            "prefix_id": state.prefix_id,
-            "shared_block_count": state.shared_block_count,
-        }
+        return [self._seq(rid).length for rid in request_ids]
 
     # -------------------------------------------------------- shared prefix
     def register_prefix(self, prefix_id, k_blocks, v_blocks):
@@ -350,159 +610,181 @@ class PagedKVCache:
         Inactive least-recently-used prefixes are evicted when the prefix
         capacity or the shared physical pool needs room.
         """
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot register a prefix during an open token transaction")
-        self._check_prefix_id(prefix_id)
-        if prefix_id in self._prefixes:
+        self._no_transaction("cannot register a prefix during an open token transaction")
+        self._prefix_entry(prefix_id)
+        if prefix_id in self._prefix_book:
             raise RuntimeError(f"prefix_id {prefix_id!r} is already registered")
-        k_blocks, v_blocks = self._prepare_prefix_blocks(k_blocks, v_blocks)
-        num_blocks = int(k_blocks.shape[1])
-        plan = self._prefix_eviction_plan(num_blocks)
+        _check_prefix_blocks(self, k_blocks, v_blocks)
+        count = int(k_blocks.shape[1])
+        plan = self._prefix_book.room_plan(count, self.prefix_cache_capacity_blocks, len(self._pool))
         if plan is None:
-            self._capacity_failure_count += 1
-            self._prefix_capacity_failure_count += 1
+            self._tally.capacity_failures += 1
+            self._tally.prefix_capacity_failures += 1
             raise RuntimeError("PagedKVCache has insufficient evictable prefix capacity")
-        for evicted in plan:
-            self._evict_prefix_entry(evicted)
-        block_ids = tuple(self._allocate_block() for _ in range(num_blocks))
-        index = _torch().tensor(block_ids, device=self.device, dtype=_torch().long)
+        for victim in plan:
+            self._evict(victim)
+        pages = tuple(self._pool.take() for _ in range(count))
+        index = _torch().tensor(pages, device=self.device, dtype=_torch().long)
         self.k_cache.index_copy_(1, index, k_blocks)
         self.v_cache.index_copy_(1, index, v_blocks)
-        self._prefixes[prefix_id] = _PrefixState(block_ids=block_ids)
-        self._prefix_registration_count += 1
-        self._state_version += 1
+        self._prefix_book.entries[prefix_id] = _PrefixEntry(pages, 0)
+        self._tally.prefix_registrations += 1
+        self._publish()
         return self.prefix_state(prefix_id)
 
     def attach_prefix(self, request_id, prefix_id):
         """Attach a resident prefix to an empty active request."""
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot attach a prefix during an open token transaction")
-        self._check_prefix_id(prefix_id)
-        state = self._require_active_request(request_id)
-        if state.transaction_id is not None:
+        self._no_transaction("cannot attach a prefix during an open token transaction")
+        self._prefix_entry(prefix_id)
+        seq = self._active_seq(request_id)
+        if seq.txn is not None:
             raise RuntimeError("cannot attach a prefix to a request in a token transaction")
-        if state.seq_len or state.block_ids or state.prefix_id is not None:
+        if seq.length or seq.pages or seq.prefix is not None:
             raise RuntimeError("shared prefixes can only attach to an empty active request")
-        prefix = self._prefixes.get(prefix_id)
-        if prefix is None:
-            self._prefix_miss_count += 1
+        entry = self._prefix_book.get(prefix_id)
+        if entry is None:
+            self._tally.prefix_misses += 1
             raise KeyError(f"unknown prefix_id: {prefix_id!r}")
-        state.block_ids.extend(prefix.block_ids)
-        state.seq_len = len(prefix.block_ids) * self.block_size
-        state.prefix_id = prefix_id
-        state.shared_block_count = len(prefix.block_ids)
-        prefix.active_refcount += 1
-        self._prefixes.move_to_end(prefix_id)
-        self._prefix_hit_count += 1
-        self._state_version += 1
-        return tuple(prefix.block_ids)
+        seq.pages.extend(entry.pages)
+        seq.length = len(entry.pages) * self.block_size
+        seq.prefix, seq.shared = prefix_id, len(entry.pages)
+        entry.refs += 1
+        self._prefix_book.touch(prefix_id)
+        self._tally.prefix_hits += 1
+        self._publish()
+        return tuple(entry.pages)
 
     def evict_prefix(self, prefix_id):
         """Evict one inactive prefix and return its blocks to the free list."""
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot evict a prefix during an open token transaction")
-        self._check_prefix_id(prefix_id)
-        prefix = self._prefixes.get(prefix_id)
-        if prefix is None:
+        self._no_transaction("cannot evict a prefix during an open token transaction")
+        entry = self._prefix_entry(prefix_id)
+        if entry is None:
             raise KeyError(f"unknown prefix_id: {prefix_id!r}")
-        if prefix.active_refcount:
+        if entry.refs:
             raise RuntimeError("cannot evict a prefix with active request references")
-        released = self._evict_prefix_entry(prefix_id)
-        self._state_version += 1
+        released = self._evict(prefix_id)
+        self._publish()
         return released
+
+    def _evict(self, prefix_id):
+        pages = self._prefix_book.drop(prefix_id)
+        self._pool.give_back(pages, released=True)
+        self._tally.prefix_evictions += 1
+        return tuple(pages)
 
     def prefix_state(self, prefix_id):
         """Detached snapshot of one resident shared prefix."""
-        self._check_prefix_id(prefix_id)
-        prefix = self._prefixes.get(prefix_id)
-        if prefix is None:
+        entry = self._prefix_entry(prefix_id)
+        if entry is None:
             raise KeyError(f"unknown prefix_id: {prefix_id!r}")
-        return {
-            "prefix_id": prefix_id,
-            "block_ids": tuple(prefix.block_ids),
-            "num_blocks": len(prefix.block_ids),
-            "token_count": len(prefix.block_ids) * self.block_size,
-            "active_refcount": prefix.active_refcount,
-        }
+        return {"prefix_id": prefix_id, "block_ids": tuple(entry.pages), "num_blocks": len(entry.pages),
+                "token_count": len(entry.pages) * self.block_size, "active_refcount": entry.refs}
 
     # ------------------------------------------------ single-layer appends
+    def _single_layer_rows(self, layer_idx, request_ids, k, v):
+        """Common contract of the single-layer appends: returns (layer, ids, k, v)."""
+        if self.num_layers != 1:
+            raise RuntimeError("multi-layer cache writes require the token transaction API")
+        self._no_transaction("legacy append is not allowed during an open token transaction")
+        return self._kv_rows(layer_idx, request_ids, k, v, "request_ids must be unique within one append call")
+
+    def _kv_rows(self, layer_idx, request_ids, k, v, duplicate_message):
+        layer_idx = self._validate_layer_idx(layer_idx)
+        ids = self._normalize_request_ids(request_ids)
+        _rows_unique(ids, duplicate_message)
+        if len(ids) == 1:
+            k = k.unsqueeze(0) if k.dim() == 2 else k
+            v = v.unsqueeze(0) if v.dim() == 2 else v
+        _check_kv_rows(self, len(ids), k, v)
+        return layer_idx, ids, k, v
+
+    def _reserve_single_layer(self, ids):
+        """Allocate each request's next slot (implicitly adding unknown ids);
+        all-or-nothing: capacity is checked before anything changes."""
+        grow = 0
+        for rid in ids:
+            seq = self._seqs.get(rid)
+            if seq is not None and seq.status != self.ACTIVE:
+                raise RuntimeError(f"request_id {rid!r} is {seq.status} and cannot accept append")
+            grow += (seq.length if seq is not None else 0) % self.block_size == 0
+        if grow > len(self._pool):
+            self._tally.capacity_failures += 1
+            raise RuntimeError(OUT_OF_BLOCKS)
+        slots = []
+        for rid in ids:
+            seq = self._seqs.setdefault(rid, _Seq.empty())
+            if seq.length % self.block_size == 0:
+                seq.pages.append(self._pool.take())
+            slots.append((seq.pages[seq.length // self.block_size], seq.length % self.block_size))
+        return slots
+
+    def _commit_single_layer(self, ids):
+        for rid in ids:
+            self._seqs[rid].length += 1
+        self._publish()
+
     def append(self, layer_idx, request_ids, k, v):
         """Append one K/V token per request (single-layer caches); returns block tables."""
-        self._require_legacy_append_available()
-        layer_idx, ids, k, v = self._prepare_append_inputs(layer_idx, request_ids, k, v)
-        self._preflight_append(ids)
-        locations = self._allocate_append_locations(ids)
-        for row, (blk, off) in enumerate(locations):
+        layer_idx, ids, k, v = self._single_layer_rows(layer_idx, request_ids, k, v)
+        for row, (blk, off) in enumerate(self._reserve_single_layer(ids)):
             self.k_cache[layer_idx, blk, :, off, :] = k[row]
             self.v_cache[layer_idx, blk, :, off, :] = v[row]
-        self._advance_request_lengths(ids)
-        self._state_version += 1
+        self._commit_single_layer(ids)
         return self.block_tables(ids)
+
+    def _require_gpu_cache(self, what):
+        torch = _torch()
+        if self.device.type != "cuda":
+            raise ValueError(f"{what} requires a CUDA-resident PagedKVCache")
+        if self.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError(f"{what} supports cache dtype float16, bfloat16, or float32")
 
     def append_cuda(self, layer_idx, request_ids, k, v):
         """Append through the HIP K/V scatter (``fd_kv_append``); allocator stays on the host."""
-        self._require_legacy_append_available()
-        torch = _torch()
-        layer_idx, ids, k, v = self._prepare_append_inputs(layer_idx, request_ids, k, v)
-        if self.device.type != "cuda":
-            raise ValueError("append_cuda requires a CUDA-resident PagedKVCache")
-        if self.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            raise ValueError("append_cuda supports cache dtype float16, bfloat16, or float32")
+        layer_idx, ids, k, v = self._single_layer_rows(layer_idx, request_ids, k, v)
+        self._require_gpu_cache("append_cuda")
         if not k.is_contiguous() or not v.is_contiguous():
             raise ValueError("append_cuda requires contiguous k and v tensors")
         from ._kv_append import _launch_kv_append, load_cuda_kv_append_extension
 
         load_cuda_kv_append_extension()  # fail before any allocator mutation
-        self._preflight_append(ids)
-        locations = self._allocate_append_locations(ids)
-        blk, off = self._location_tensors(locations)
+        blk, off = self._slot_tensors(self._reserve_single_layer(ids))
         _launch_kv_append(self.k_cache[layer_idx], self.v_cache[layer_idx], blk, off, k, v)
-        self._advance_request_lengths(ids)
-        self._state_version += 1
+        self._commit_single_layer(ids)
         return self.block_tables(ids)
 
     append_hip = append_cuda
 
-    def append_fused_cuda(self, layer_idx, request_ids, q, k, v, positions, rotary_dim=None, base=10_000.0):
-        """Fused RoPE + K/V append via ``fd_fused_rope_kv_append``; returns ``(q_rot, tables)``."""
-        self._require_legacy_append_available()
+    def append_fused_cuda(self, layer_idx, request_ids, q, k, v, positions, rotary_dim=None, base=10_000.0,
+                          cos_sin_table=None):
+        """Fused RoPE + K/V append via ``fd_fused_rope_kv_append``; returns ``(q_rot, tables)``.
+
+        ``cos_sin_table``: see :func:`flashdec_amd.rope.rope_cos_sin_table`.
+        """
         torch = _torch()
-        layer_idx, ids, k, v = self._prepare_append_inputs(layer_idx, request_ids, k, v)
-        if self.device.type != "cuda":
-            raise ValueError("append_fused_cuda requires a CUDA-resident PagedKVCache")
-        if self.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-            raise ValueError("append_fused_cuda supports cache dtype float16, bfloat16, or float32")
-        if q.dim() != 3 or q.shape[0] != len(ids) or q.shape[1] <= 0 or q.shape[2] != self.head_dim:
-            raise ValueError("q shape must match request count and cache head_dim")
-        if q.device != self.device or q.dtype != self.dtype:
-            raise ValueError("q must use the cache device and dtype")
+        layer_idx, ids, k, v = self._single_layer_rows(layer_idx, request_ids, k, v)
+        self._require_gpu_cache("append_fused_cuda")
+        _check_fused_q(self, len(ids), q)
         if positions.dim() != 1 or positions.numel() != len(ids):
             raise ValueError("positions must have shape [num_requests]")
         if positions.device != self.device or positions.dtype not in (torch.int32, torch.int64):
             raise ValueError("positions must use int32/int64 on the cache device")
         if bool(torch.any(positions < 0).item()):
             raise ValueError("positions must be non-negative")
-        if rotary_dim is None:
-            rotary_dim = self.head_dim
-        if isinstance(rotary_dim, bool) or not isinstance(rotary_dim, int):
-            raise ValueError("rotary_dim must be an even integer")
-        if rotary_dim <= 0 or rotary_dim > self.head_dim or rotary_dim % 2 != 0:
-            raise ValueError("rotary_dim must be positive, even, and no larger than head_dim")
-        base = float(base)
-        if not math.isfinite(base) or base <= 0.0:
-            raise ValueError("base must be a positive finite number")
+        rotary_dim, base = _rotary_dim_and_base(self.head_dim, rotary_dim, base)
         if not q.is_contiguous() or not k.is_contiguous() or not v.is_contiguous():
             raise ValueError("append_fused_cuda requires contiguous q, k, and v tensors")
-        from ._fused_rope_kv_append import _launch, load_fused_rope_kv_append_extension
+        from ._fused_rope_kv_append import _check_cos_sin_table, _launch, load_fused_rope_kv_append_extension
 
+        if cos_sin_table is not None:
+            _check_cos_sin_table(cos_sin_table, rotary_dim, self.device)
+            if bool(torch.any(positions >= cos_sin_table.shape[1]).item()):
+                raise ValueError("positions must be below the cos_sin_table's rows")
         load_fused_rope_kv_append_extension()
-        self._preflight_append(ids)
-        locations = self._allocate_append_locations(ids)
-        blk, off = self._location_tensors(locations)
+        blk, off = self._slot_tensors(self._reserve_single_layer(ids))
         q_rot = _launch(q, k, v, self.k_cache[layer_idx], self.v_cache[layer_idx], blk, off,
-                        positions.to(torch.int64), rotary_dim, base)
-        self._advance_request_lengths(ids)
-        self._state_version += 1
+                        positions.to(torch.int64), rotary_dim, base, cos_sin_table=cos_sin_table)
+        self._commit_single_layer(ids)
         return q_rot, self.block_tables(ids)
 
     append_fused_hip = append_fused_cuda
@@ -510,91 +792,107 @@ class PagedKVCache:
     # ---------------------------------------------- multi-layer transactions
     def begin_token(self, request_ids):
         """Reserve one token location (all layers) per request; blocks are allocated at boundaries."""
-        if self._open_transaction_id is not None:
-            raise RuntimeError("PagedKVCache already has an open token transaction")
+        self._no_transaction("PagedKVCache already has an open token transaction")
         ids = tuple(self._normalize_request_ids(request_ids))
-        if not ids:
-            raise ValueError("request_ids must be non-empty")
-        if len(set(ids)) != len(ids):
-            raise ValueError("request_ids must be unique within one token transaction")
-        states = [self._require_active_request(rid) for rid in ids]
-        if any(s.transaction_id is not None for s in states):
+        _rows_unique(ids, "request_ids must be unique within one token transaction")
+        seqs = [self._active_seq(rid) for rid in ids]
+        if any(seq.txn is not None for seq in seqs):
             raise RuntimeError("request already belongs to an open token transaction")
-        needed = sum(s.seq_len % self.block_size == 0 for s in states)
-        if needed > len(self._free_blocks):
-            self._capacity_failure_count += 1
-            self._transaction_failure_count += 1
-            raise RuntimeError("PagedKVCache is out of physical blocks")
-
-        transaction_id = self._next_transaction_id
-        positions = tuple(s.seq_len for s in states)
-        locations = []
-        newly_allocated = {}
-        allocation_order = []
+        if sum(seq.length % self.block_size == 0 for seq in seqs) > len(self._pool):
+            self._tally.capacity_failures += 1
+            self._tally.failures += 1
+            raise RuntimeError(OUT_OF_BLOCKS)
+        tid = self._journal.next_id
+        positions = tuple(seq.length for seq in seqs)
+        grown = []
         try:
-            for rid, s, pos in zip(ids, states, positions):
-                off = pos % self.block_size
-                if off == 0:
-                    blk = self._allocate_block()
-                    s.block_ids.append(blk)
-                    newly_allocated[rid] = blk
-                    allocation_order.append(blk)
-                locations.append((s.block_ids[pos // self.block_size], off))
-            self._validate_reserved_transaction_locations(ids, states, positions, locations)
-            width = max(1, max(len(s.block_ids) for s in states))
-            arena = self._meta_arena
-            if arena is not None:
-                if len(ids) > arena[1] or width > arena[2]:
-                    raise RuntimeError("transaction exceeds the graph metadata arena "
-                                       f"({len(ids)} rows x {width} blocks > {arena[1]} x {arena[2]})")
-                width = arena[2]
-            rows = self._table_rows(states, width)
-            meta = _DeviceMeta.build(self.device, positions, locations, rows, width, self.block_size, arena,
-                                     self._meta_staging)
-            for s in states:
-                s.transaction_id = transaction_id
+            for rid, seq in zip(ids, seqs):
+                if seq.length % self.block_size == 0:
+                    blk = self._pool.take()
+                    seq.pages.append(blk)
+                    grown.append((rid, blk))
+            slots = tuple((seq.pages[p // self.block_size], p % self.block_size) for seq, p in zip(seqs, positions))
+            self._validate_reserved_transaction_locations(ids, seqs, positions, slots)
+            meta = self._pack_metadata(seqs, positions, slots)
+            for seq in seqs:
+                seq.txn = tid
         except Exception:
-            for rid, blk in newly_allocated.items():
-                s = self._requests[rid]
-                if s.block_ids and s.block_ids[-1] == blk:
-                    s.block_ids.pop()
-                s.transaction_id = None
-            for blk in reversed(allocation_order):
-                self._free_blocks.appendleft(blk)
-            self._transaction_failure_count += 1
+            self._undo_growth(grown)
+            for seq in seqs:
+                seq.txn = None
+            self._tally.failures += 1
             raise
+        self._publish()
+        txn = _Txn(tid, self._version, ids, positions, slots, tuple(grown), meta, 0, "open")
+        self._journal.open = txn
+        self._journal.next_id += 1
+        self._tally.begins += 1
+        return self._snapshot(txn)
 
-        cache_version = self._state_version + 1
-        state = _KVTokenTransactionState(
-            transaction_id=transaction_id,
-            cache_version=cache_version,
-            request_ids=ids,
-            positions=positions,
-            locations=tuple(locations),
-            block_tables=meta.block_tables,
-            newly_allocated_by_request=newly_allocated,
-            allocation_order=tuple(allocation_order),
-            meta=meta,
-        )
-        self._transactions[transaction_id] = state
-        self._open_transaction_id = transaction_id
-        self._next_transaction_id += 1
-        self._transaction_begin_count += 1
-        self._state_version = cache_version
-        return self._transaction_view(state)
+    def _pack_metadata(self, seqs, positions, slots):
+        """The transaction's device metadata: in the graph arena when enabled."""
+        width = max(1, max(len(seq.pages) for seq in seqs))
+        arena = self._meta_arena
+        if arena is not None:
+            if len(seqs) > arena[1] or width > arena[2]:
+                raise RuntimeError("transaction exceeds the graph metadata arena "
+                                   f"({len(seqs)} rows x {width} blocks > {arena[1]} x {arena[2]})")
+            width = arena[2]
+        return _DeviceMeta.build(self.device, positions, slots, self._table_rows(seqs, width), width,
+                                 self.block_size, arena, self._meta_staging)
+
+    def _undo_growth(self, grown):
+        """Take back the pages a reservation appended (newest first) and return
+        them to the front of the pool in allocation order."""
+        for rid, blk in reversed(grown):
+            pages = self._seqs[rid].pages
+            if pages and pages[-1] == blk:
+                pages.pop()
+        self._pool.give_back([blk for _, blk in grown], released=False)
+
+    def _validate_reserved_transaction_locations(self, request_ids, seqs, positions, slots):
+        """Check every reserved (block, offset) against the ledger before any kernel sees it."""
+        if not len(request_ids) == len(seqs) == len(positions) == len(slots):
+            raise RuntimeError("transaction location metadata has inconsistent rows")
+        for rid, seq, pos, (blk, off) in zip(request_ids, seqs, positions, slots):
+            problem = (
+                "transaction position must be non-negative" if pos < 0 else
+                "transaction physical block id is out of range" if not 0 <= blk < self.max_blocks else
+                "transaction block offset is out of range" if not 0 <= off < self.block_size else
+                "transaction block offset does not match position" if off != pos % self.block_size else
+                "transaction logical block is not allocated" if pos // self.block_size >= len(seq.pages) else
+                f"transaction physical block does not match request {rid!r}"
+                if seq.pages[pos // self.block_size] != blk else None)
+            if problem is not None:
+                raise RuntimeError(problem)
+
+    def _layer_rows(self, txn, layer_idx, k, v):
+        """One transaction layer write's contract: returns (layer, k, v)."""
+        layer_idx = self._validate_layer_idx(layer_idx)
+        if layer_idx != txn.layers:
+            raise RuntimeError(f"transaction requires layer {txn.layers}, got layer {layer_idx}")
+        _, ids, k, v = self._kv_rows(layer_idx, txn.rids, k, v, "request_ids must be unique within one append call")
+        if tuple(ids) != txn.rids:
+            raise RuntimeError("transaction request order changed unexpectedly")
+        return layer_idx, k, v
+
+    def _layer_written(self, txn):
+        txn.layers += 1
+        self._tally.layer_writes += 1
+        return self._snapshot(txn)
 
     def write_token_layer(self, transaction, layer_idx, k, v):
         """Write one layer's K/V at the locations reserved by ``begin_token`` (torch path)."""
-        state = self._require_open_transaction(transaction)
+        txn = self._journal.find_open(transaction)
         try:
-            layer_idx, k, v = self._prepare_transaction_layer_write(state, layer_idx, k, v)
-            for row, (blk, off) in enumerate(state.locations):
+            layer_idx, k, v = self._layer_rows(txn, layer_idx, k, v)
+            for row, (blk, off) in enumerate(txn.slots):
                 self.k_cache[layer_idx, blk, :, off, :] = k[row]
                 self.v_cache[layer_idx, blk, :, off, :] = v[row]
         except Exception:
-            self._transaction_failure_count += 1
+            self._tally.failures += 1
             raise
-        return self._record_transaction_layer_write(state, layer_idx)
+        return self._layer_written(txn)
 
     def write_token_layer_fused_cuda(self, transaction, layer_idx, q, k, v, *, rotary_dim=None, base=10_000.0,
                                      q_out=None, cos_sin_table=None):
@@ -606,91 +904,77 @@ class PagedKVCache:
         :func:`flashdec_amd.rope.rope_cos_sin_table` (rows must cover the
         transaction's positions).
         """
-        state = self._require_open_transaction(transaction)
+        txn = self._journal.find_open(transaction)
         try:
             torch = _torch()
-            layer_idx, k, v = self._prepare_transaction_layer_write(state, layer_idx, k, v)
+            layer_idx, k, v = self._layer_rows(txn, layer_idx, k, v)
             if self.device.type != "cuda":
                 raise ValueError("write_token_layer_fused_cuda requires a CUDA-resident PagedKVCache")
             if self.dtype not in (torch.float16, torch.bfloat16, torch.float32):
                 raise ValueError("write_token_layer_fused_cuda supports float16, bfloat16, or float32")
-            if q.dim() != 3 or q.shape[0] != len(state.request_ids):
-                raise ValueError("q shape must match transaction request count and cache head_dim")
-            if q.shape[1] <= 0 or q.shape[2] != self.head_dim:
-                raise ValueError("q shape must match transaction request count and cache head_dim")
-            if q.device != self.device or q.dtype != self.dtype:
-                raise ValueError("q must use the cache device and dtype")
+            _check_transaction_q(self, len(txn.rids), q)
             if not q.is_contiguous() or not k.is_contiguous() or not v.is_contiguous():
                 raise ValueError("write_token_layer_fused_cuda requires contiguous q, k, and v tensors")
             from ._fused_rope_kv_append import _fused_rope_kv_append_trusted
 
-            meta = state.meta
+            meta = txn.meta
             q_rot = _fused_rope_kv_append_trusted(q, k, v, self.k_cache[layer_idx], self.v_cache[layer_idx],
                                                   meta.block_ids, meta.offsets, meta.positions,
                                                   rotary_dim=rotary_dim, base=base, q_out=q_out,
                                                   cos_sin_table=cos_sin_table)
         except Exception:
-            self._transaction_failure_count += 1
+            self._tally.failures += 1
             raise
-        return q_rot, self._record_transaction_layer_write(state, layer_idx)
+        return q_rot, self._layer_written(txn)
 
     write_token_layer_fused_hip = write_token_layer_fused_cuda
 
     def _record_graph_layers(self, transaction):
         """Record every layer as written by a replayed step graph (see DecodeEngine.step_graph)."""
-        state = self._require_open_transaction(transaction)
-        if state.next_layer_idx != 0:
+        txn = self._journal.find_open(transaction)
+        if txn.layers != 0:
             raise RuntimeError("a step graph writes every layer; this transaction already wrote some")
-        for layer in range(self.num_layers):
-            state.written_layers.add(layer)
-        state.next_layer_idx = self.num_layers
-        self._transaction_layer_write_count += self.num_layers
+        txn.layers = self.num_layers
+        self._tally.layer_writes += self.num_layers
 
     def commit_token(self, transaction):
         """Publish the token after every layer has been written."""
-        state = self._require_open_transaction(transaction)
-        if state.next_layer_idx != self.num_layers:
+        txn = self._journal.find_open(transaction)
+        if txn.layers != self.num_layers:
             raise RuntimeError("cannot commit token before all layers are written")
-        view = replace(self._transaction_view(state), state="committed")
-        for rid in state.request_ids:
-            r = self._requests[rid]
-            r.seq_len += 1
-            r.transaction_id = None
-        state.state = "committed"
-        self._open_transaction_id = None
-        self._transaction_commit_count += 1
-        self._state_version += 1
-        self._retire_transaction(state)
+        view = replace(self._snapshot(txn), state="committed")  # before any change: a failure leaves it open
+        for rid in txn.rids:
+            seq = self._seqs[rid]
+            seq.length += 1
+            seq.txn = None
+        self._tally.commits += 1
+        self._publish()
+        self._journal.close(txn, "committed")
         return view
 
     def abort_token(self, transaction):
         """Abort the open token and return the boundary blocks it reserved."""
-        state = self._require_open_transaction(transaction)
-        for rid, blk in state.newly_allocated_by_request.items():
-            r = self._requests[rid]
-            if not r.block_ids or r.block_ids[-1] != blk:
+        txn = self._journal.find_open(transaction)
+        for rid, blk in txn.grown:
+            pages = self._seqs[rid].pages
+            if not pages or pages[-1] != blk:
                 raise RuntimeError("transaction rollback block ownership is inconsistent")
-        view = replace(self._transaction_view(state), state="aborted")
-        for rid in state.newly_allocated_by_request:
-            self._requests[rid].block_ids.pop()
-        for blk in reversed(state.allocation_order):
-            self._free_blocks.appendleft(blk)
-        for rid in state.request_ids:
-            self._requests[rid].transaction_id = None
-        state.state = "aborted"
-        self._open_transaction_id = None
-        self._transaction_abort_count += 1
-        self._transaction_rollback_block_count += len(state.allocation_order)
-        self._state_version += 1
-        self._retire_transaction(state)
+        view = replace(self._snapshot(txn), state="aborted")  # before any change: a failure leaves it open
+        self._undo_growth(txn.grown)
+        for rid in txn.rids:
+            self._seqs[rid].txn = None
+        self._tally.aborts += 1
+        self._tally.rollback_blocks += len(txn.grown)
+        self._publish()
+        self._journal.close(txn, "aborted")
         return view
 
     def transaction_view(self, transaction):
         """Latest detached snapshot of an open transaction."""
-        state = self._require_transaction(transaction)
-        if isinstance(state, _TerminalTransactionState):
-            raise RuntimeError(f"token transaction is already {state.state}")
-        return self._transaction_view(state)
+        rec = self._journal.find(transaction)
+        if isinstance(rec, _Closed):
+            raise RuntimeError(f"token transaction is already {rec.phase}")
+        return self._snapshot(rec)
 
     def transaction_device_metadata(self, transaction):
         """The allocator's device-resident metadata of the open transaction.
@@ -699,7 +983,14 @@ class PagedKVCache:
         (int64), ``eff_lens`` and ``block_tables`` (int32).  For launch paths (e.g.
         graph capture) that must not allocate per layer.
         """
-        return self._require_open_transaction(transaction).meta
+        return self._journal.find_open(transaction).meta
+
+    def _snapshot(self, txn):
+        meta = txn.meta.clone()
+        return KVTokenTransactionView(
+            transaction_id=txn.tid, cache_version=txn.version, request_ids=txn.rids, positions=meta.positions,
+            physical_block_ids=meta.block_ids, block_offsets=meta.offsets, block_tables=meta.block_tables,
+            effective_seq_lens=meta.eff_lens, next_layer_idx=txn.layers, state=txn.phase)
 
     def enable_graph_metadata(self, max_batch, max_blocks_per_seq):
         """Give every later transaction's metadata one fixed device address.
@@ -712,8 +1003,7 @@ class PagedKVCache:
         on the current stream after any earlier replay that reads it.
         """
         torch = _torch()
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot change the metadata arena during an open token transaction")
+        self._no_transaction("cannot change the metadata arena during an open token transaction")
         max_batch, width = int(max_batch), int(max_blocks_per_seq)
         if max_batch <= 0 or width <= 0:
             raise ValueError("max_batch and max_blocks_per_seq must be positive")
@@ -743,15 +1033,14 @@ class PagedKVCache:
         synthetic benchmark data).  Transaction counters are not advanced.
         """
         torch = _torch()
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot seed context during an open token transaction")
+        self._no_transaction("cannot seed context during an open token transaction")
         ids = tuple(self._normalize_request_ids(request_ids))
         if not ids or len(set(ids)) != len(ids):
             raise ValueError("request_ids must be non-empty and unique")
         num_tokens = int(num_tokens)
         if num_tokens <= 0:
             raise ValueError("num_tokens must be positive")
-        states = [self._require_active_request(rid) for rid in ids]
+        seqs = [self._active_seq(rid) for rid in ids]
         if (k is None) != (v is None):
             raise ValueError("k and v must be provided together")
         if k is not None:
@@ -760,497 +1049,283 @@ class PagedKVCache:
                 raise ValueError("seed K/V must have shape [num_layers, num_requests, num_tokens, Hkv, D]")
             if k.device != self.device or v.device != self.device or k.dtype != self.dtype or v.dtype != self.dtype:
                 raise ValueError("seed K/V must use the cache device and dtype")
-        bs = self.block_size
-        starts = [s.seq_len for s in states]
-        needed = [(p + num_tokens + bs - 1) // bs - (p + bs - 1) // bs for p in starts]
-        if sum(needed) > len(self._free_blocks):
-            self._capacity_failure_count += 1
-            raise RuntimeError("PagedKVCache is out of physical blocks")
-        # block boundaries in token order, requests in order at each token
+        starts = [seq.length for seq in seqs]
+        grow = [self._pages_for(p + num_tokens) - self._pages_for(p) for p in starts]
+        if sum(grow) > len(self._pool):
+            self._tally.capacity_failures += 1
+            raise RuntimeError(OUT_OF_BLOCKS)
+        # new pages in the order token-by-token appends would take them: at
+        # each token index, every request that crosses a block boundary
         for t in range(num_tokens):
-            for s, p in zip(states, starts):
-                if (p + t) % bs == 0:
-                    s.block_ids.append(self._allocate_block())
+            for seq, p in zip(seqs, starts):
+                if (p + t) % self.block_size == 0:
+                    seq.pages.append(self._pool.take())
         if k is not None:
-            for row, (s, p) in enumerate(zip(states, starts)):
+            for row, (seq, p) in enumerate(zip(seqs, starts)):
                 pos = torch.arange(p, p + num_tokens, device=self.device)
-                blk = torch.tensor(s.block_ids, device=self.device)[pos // bs]
-                off = pos % bs
+                blk = torch.tensor(seq.pages, device=self.device)[pos // self.block_size]
+                off = pos % self.block_size
                 # non-adjacent advanced indices put the token axis first: [T, L, Hkv, D]
                 self.k_cache[:, blk, :, off, :] = k[:, row].permute(1, 0, 2, 3)
                 self.v_cache[:, blk, :, off, :] = v[:, row].permute(1, 0, 2, 3)
-        for s in states:
-            s.seq_len += num_tokens
-        self._state_version += 1
+        for seq in seqs:
+            seq.length += num_tokens
+        self._publish()
         return self.seq_lens_tensor(ids)
 
     # -------------------------------------------------------------- queries
     def next_positions(self, request_ids, device=None):
         """Each request's pre-append token position, without mutation."""
-        torch = _torch()
         ids = self._normalize_request_ids(request_ids)
-        if not ids:
-            raise ValueError("request_ids must be non-empty")
-        if len(set(ids)) != len(ids):
-            raise ValueError("request_ids must be unique")
+        _rows_unique(ids, "request_ids must be unique")
         positions = []
         for rid in ids:
-            s = self._requests.get(rid)
-            if s is None:
-                positions.append(0)
-            elif s.status != self.ACTIVE:
-                raise RuntimeError(f"request_id {rid!r} is {s.status} and cannot accept append")
-            elif s.transaction_id is not None:
+            seq = self._seqs.get(rid)
+            if seq is not None and seq.status != self.ACTIVE:
+                raise RuntimeError(f"request_id {rid!r} is {seq.status} and cannot accept append")
+            if seq is not None and seq.txn is not None:
                 raise RuntimeError(f"request_id {rid!r} belongs to an open token transaction")
-            else:
-                positions.append(s.seq_len)
-        return _host_to_device(positions, torch.int64, self.device if device is None else device)
+            positions.append(0 if seq is None else seq.length)
+        return _host_to_device(positions, _torch().int64, self.device if device is None else device)
 
     def block_tables(self, request_ids=None, max_blocks_per_seq=None, pad_value=-1):
         """Padded physical block ids ``[num_requests, max_blocks_per_seq]`` (int32)."""
-        torch = _torch()
-        ids = self._normalize_active_request_ids(request_ids)
-        if max_blocks_per_seq is None:
-            max_blocks_per_seq = max(1, max((len(self._requests[r].block_ids) for r in ids), default=0))
-        max_blocks_per_seq = int(max_blocks_per_seq)
-        if max_blocks_per_seq <= 0:
+        seqs = [self._seqs[rid] for rid in self._normalize_active_request_ids(request_ids)]
+        width = max(1, max((len(seq.pages) for seq in seqs), default=0)) if max_blocks_per_seq is None \
+            else int(max_blocks_per_seq)
+        if width <= 0:
             raise ValueError("max_blocks_per_seq must be positive")
-        states = [self._requests[r] for r in ids]
-        if any(len(s.block_ids) > max_blocks_per_seq for s in states):
+        if any(len(seq.pages) > width for seq in seqs):
             raise ValueError("max_blocks_per_seq is smaller than a request's block count")
-        rows = self._table_rows(states, max_blocks_per_seq, int(pad_value))
-        return _host_to_device(rows, torch.int32, self.device)
+        return _host_to_device(self._table_rows(seqs, width, int(pad_value)), _torch().int32, self.device)
 
     def seq_lens_tensor(self, request_ids=None, device=None):
         """Sequence lengths (int32) for the requested rows."""
-        torch = _torch()
-        ids = self._normalize_active_request_ids(request_ids)
-        lens = [self._requests[r].seq_len for r in ids]
-        return _host_to_device(lens, torch.int32, self.device if device is None else device)
+        lens = [self._seqs[rid].length for rid in self._normalize_active_request_ids(request_ids)]
+        return _host_to_device(lens, _torch().int32, self.device if device is None else device)
 
     def request_block_ids(self, request_id):
         """Logical-to-physical block list of one request."""
-        return tuple(self._require_request(request_id).block_ids)
+        return tuple(self._seq(request_id).pages)
 
     def to_dense(self, layer_idx=0, request_ids=None, max_seq_len=None):
         """Materialise ``(k_dense, v_dense, seq_lens)`` with K/V ``[B, L, Hkv, D]``."""
         torch = _torch()
         layer_idx = self._validate_layer_idx(layer_idx)
         ids = self._normalize_active_request_ids(request_ids)
-        longest = max((self._requests[r].seq_len for r in ids), default=0)
-        if max_seq_len is None:
-            max_seq_len = max(1, longest)
-        max_seq_len = int(max_seq_len)
+        longest = max((self._seqs[rid].length for rid in ids), default=0)
+        max_seq_len = max(1, longest) if max_seq_len is None else int(max_seq_len)
         if max_seq_len < longest:
             raise ValueError("max_seq_len is smaller than an existing request length")
-        shape = (len(ids), max_seq_len, self.num_kv_heads, self.head_dim)
-        k_dense = torch.zeros(shape, device=self.device, dtype=self.dtype)
+        k_dense = torch.zeros((len(ids), max_seq_len, self.num_kv_heads, self.head_dim), device=self.device,
+                              dtype=self.dtype)
         v_dense = torch.zeros_like(k_dense)
         for row, rid in enumerate(ids):
-            s = self._requests[rid]
-            if s.seq_len == 0:
+            seq = self._seqs[rid]
+            if not seq.length:
                 continue
-            index = torch.tensor(s.block_ids, device=self.device, dtype=torch.long)
-            kt = self.k_cache[layer_idx].index_select(0, index).permute(0, 2, 1, 3)
-            vt = self.v_cache[layer_idx].index_select(0, index).permute(0, 2, 1, 3)
-            k_dense[row, : s.seq_len] = kt.reshape(-1, self.num_kv_heads, self.head_dim)[: s.seq_len]
-            v_dense[row, : s.seq_len] = vt.reshape(-1, self.num_kv_heads, self.head_dim)[: s.seq_len]
+            index = torch.tensor(seq.pages, device=self.device, dtype=torch.long)
+            for dense, pool in ((k_dense, self.k_cache), (v_dense, self.v_cache)):
+                tokens = pool[layer_idx].index_select(0, index).permute(0, 2, 1, 3)
+                dense[row, : seq.length] = tokens.reshape(-1, self.num_kv_heads, self.head_dim)[: seq.length]
         return k_dense, v_dense, self.seq_lens_tensor(ids)
 
     @property
     def num_free_blocks(self):
-        return len(self._free_blocks)
+        return len(self._pool)
 
     @property
     def num_used_blocks(self):
-        return self.max_blocks - len(self._free_blocks)
+        return self.max_blocks - len(self._pool)
 
     @property
     def state_version(self):
-        return self._state_version
+        return self._version
 
     @property
     def has_open_transaction(self):
-        return self._open_transaction_id is not None
+        return self._journal.open is not None
 
     def metrics(self):
         """Block-pool, fragmentation, lifecycle, transaction and prefix counters (45 keys)."""
-        states = list(self._requests.values())
-        active = [s for s in states if s.status == self.ACTIVE]
+        pool, tally, book, txn = self._pool, self._tally, self._prefix_book, self._journal.open
+        seqs = list(self._seqs.values())
+        live = [seq for seq in seqs if seq.status == self.ACTIVE]
+        by_status = {s: sum(seq.status == s for seq in seqs) for s in (self.ACTIVE, self.FINISHED, self.CANCELLED)}
         used = self.num_used_blocks
-        resident_prefix_blocks = self._resident_prefix_blocks()
-        refs = sum(p.active_refcount for p in self._prefixes.values())
-        shared_prefix_blocks = sum(len(p.block_ids) for p in self._prefixes.values() if p.active_refcount >= 2)
-        saved_prefix_blocks = sum(max(0, p.active_refcount - 1) * len(p.block_ids) for p in self._prefixes.values())
-        bytes_per_block = (self.num_layers * 2 * self.num_kv_heads * self.block_size * self.head_dim
-                           * self.k_cache.element_size())
-        open_tx = self._transactions.get(self._open_transaction_id) if self._open_transaction_id is not None else None
-        reserved_tx_blocks = len(open_tx.allocation_order) if open_tx is not None else 0
+        entries = list(book.entries.values())
+        resident = book.resident_blocks()
+        block_bytes = (self.num_layers * 2 * self.num_kv_heads * self.block_size * self.head_dim
+                       * self.k_cache.element_size())
+        reserving = len(txn.grown) if txn is not None else 0
         reserved_tokens = used * self.block_size
-        active_tokens = sum(s.seq_len for s in active)
-        physical_tokens = resident_prefix_blocks * self.block_size + sum(
-            max(0, s.seq_len - s.shared_block_count * self.block_size) for s in active
-        )
-        frag = reserved_tokens - physical_tokens
-        lookups = self._prefix_hit_count + self._prefix_miss_count
+        data_tokens = resident * self.block_size + sum(
+            max(0, seq.length - seq.shared * self.block_size) for seq in live)
+        frag = reserved_tokens - data_tokens
+        saved = sum(max(0, e.refs - 1) * len(e.pages) for e in entries)
+        lookups = tally.prefix_hits + tally.prefix_misses
         return {
             "max_blocks": self.max_blocks,
             "used_blocks": used,
-            "free_blocks": self.num_free_blocks,
+            "free_blocks": len(pool),
             "block_utilization": used / self.max_blocks,
-            "active_tokens": active_tokens,
-            "physical_data_tokens": physical_tokens,
+            "active_tokens": sum(seq.length for seq in live),
+            "physical_data_tokens": data_tokens,
             "reserved_tokens": reserved_tokens,
             "internal_fragmentation_tokens": frag,
             "internal_fragmentation_ratio": frag / reserved_tokens if reserved_tokens else 0.0,
-            "allocation_count": self._allocation_count,
-            "fresh_allocation_count": self._fresh_allocation_count,
-            "free_count": self._free_count,
-            "reuse_count": self._reuse_count,
-            "capacity_failure_count": self._capacity_failure_count,
-            "active_requests": sum(s.status == self.ACTIVE for s in states),
-            "finished_requests": sum(s.status == self.FINISHED for s in states),
-            "cancelled_requests": sum(s.status == self.CANCELLED for s in states),
-            "transaction_begin_count": self._transaction_begin_count,
-            "transaction_commit_count": self._transaction_commit_count,
-            "transaction_abort_count": self._transaction_abort_count,
-            "open_transaction_count": int(open_tx is not None),
-            "retained_transaction_state_count": len(self._transactions),
-            "terminal_transaction_history_count": len(self._terminal_transactions),
-            "terminal_transaction_history_limit": self._terminal_transaction_history_limit,
-            "pending_request_count": len(open_tx.request_ids) if open_tx is not None else 0,
-            "reserved_transaction_blocks": reserved_tx_blocks,
-            "transaction_layer_write_count": self._transaction_layer_write_count,
-            "transaction_rollback_block_count": self._transaction_rollback_block_count,
-            "transaction_failure_count": self._transaction_failure_count,
-            "bytes_per_block": bytes_per_block,
-            "allocated_kv_bytes": used * bytes_per_block,
-            "reserved_transaction_bytes": reserved_tx_blocks * bytes_per_block,
+            "allocation_count": pool.taken,
+            "fresh_allocation_count": pool.fresh,
+            "free_count": pool.released,
+            "reuse_count": pool.reused,
+            "capacity_failure_count": tally.capacity_failures,
+            "active_requests": by_status[self.ACTIVE],
+            "finished_requests": by_status[self.FINISHED],
+            "cancelled_requests": by_status[self.CANCELLED],
+            "transaction_begin_count": tally.begins,
+            "transaction_commit_count": tally.commits,
+            "transaction_abort_count": tally.aborts,
+            "open_transaction_count": int(txn is not None),
+            "retained_transaction_state_count": int(txn is not None),
+            "terminal_transaction_history_count": len(self._journal.history),
+            "terminal_transaction_history_limit": self._journal.limit,
+            "pending_request_count": len(txn.rids) if txn is not None else 0,
+            "reserved_transaction_blocks": reserving,
+            "transaction_layer_write_count": tally.layer_writes,
+            "transaction_rollback_block_count": tally.rollback_blocks,
+            "transaction_failure_count": tally.failures,
+            "bytes_per_block": block_bytes,
+            "allocated_kv_bytes": used * block_bytes,
+            "reserved_transaction_bytes": reserving * block_bytes,
             "prefix_cache_capacity_blocks": self.prefix_cache_capacity_blocks,
-            "resident_prefix_count": len(self._prefixes),
-            "resident_prefix_blocks": resident_prefix_blocks,
-            "active_prefix_references": refs,
-            "shared_prefix_blocks": shared_prefix_blocks,
-            "saved_prefix_blocks": saved_prefix_blocks,
-            "saved_prefix_bytes": saved_prefix_blocks * bytes_per_block,
-            "prefix_registration_count": self._prefix_registration_count,
-            "prefix_hit_count": self._prefix_hit_count,
-            "prefix_miss_count": self._prefix_miss_count,
-            "prefix_hit_ratio": self._prefix_hit_count / lookups if lookups else 0.0,
-            "prefix_eviction_count": self._prefix_eviction_count,
-            "prefix_capacity_failure_count": self._prefix_capacity_failure_count,
+            "resident_prefix_count": len(entries),
+            "resident_prefix_blocks": resident,
+            "active_prefix_references": sum(e.refs for e in entries),
+            "shared_prefix_blocks": sum(len(e.pages) for e in entries if e.refs >= 2),
+            "saved_prefix_blocks": saved,
+            "saved_prefix_bytes": saved * block_bytes,
+            "prefix_registration_count": tally.prefix_registrations,
+            "prefix_hit_count": tally.prefix_hits,
+            "prefix_miss_count": tally.prefix_misses,
+            "prefix_hit_ratio": tally.prefix_hits / lookups if lookups else 0.0,
+            "prefix_eviction_count": tally.prefix_evictions,
+            "prefix_capacity_failure_count": tally.prefix_capacity_failures,
         }
 
     def validate_invariants(self):
         """Raise RuntimeError if ownership, free list and transactions disagree."""
-        free = list(self._free_blocks)
-        if len(free) != len(set(free)):
-            raise RuntimeError("PagedKVCache free list contains duplicate blocks")
-        prefix_blocks = []
-        expected_refs = {pid: 0 for pid in self._prefixes}
-        for prefix in self._prefixes.values():
-            if not prefix.block_ids:
-                raise RuntimeError("resident prefix must own at least one block")
-            if prefix.active_refcount < 0:
-                raise RuntimeError("prefix active_refcount must be non-negative")
-            prefix_blocks.extend(prefix.block_ids)
-        if len(prefix_blocks) != len(set(prefix_blocks)):
-            raise RuntimeError("a physical block belongs to multiple prefixes")
-        if len(prefix_blocks) > self.prefix_cache_capacity_blocks:
-            raise RuntimeError("resident prefixes exceed configured prefix capacity")
-        private = []
-        for s in self._requests.values():
-            if s.status == self.ACTIVE:
-                pending = int(s.transaction_id is not None)
-                if len(s.block_ids) != (s.seq_len + pending + self.block_size - 1) // self.block_size:
-                    raise RuntimeError("active request block count does not match seq_len")
-                if s.prefix_id is None:
-                    if s.shared_block_count:
-                        raise RuntimeError("request without prefix has shared blocks")
-                else:
-                    prefix = self._prefixes.get(s.prefix_id)
-                    if prefix is None:
-                        raise RuntimeError("request references a non-resident prefix")
-                    if s.shared_block_count != len(prefix.block_ids):
-                        raise RuntimeError("request shared block count does not match prefix")
-                    if tuple(s.block_ids[: s.shared_block_count]) != prefix.block_ids:
-                        raise RuntimeError("request shared block ids do not match prefix")
-                    if s.seq_len < s.shared_block_count * self.block_size:
-                        raise RuntimeError("request seq_len is shorter than its shared prefix")
-                    expected_refs[s.prefix_id] += 1
-                private.extend(s.block_ids[s.shared_block_count :])
-            else:
-                if s.block_ids:
-                    raise RuntimeError("terminal request still owns physical blocks")
-                if s.transaction_id is not None:
-                    raise RuntimeError("terminal request belongs to a token transaction")
-                if s.prefix_id is not None or s.shared_block_count:
-                    raise RuntimeError("terminal request still references a shared prefix")
-        for pid, prefix in self._prefixes.items():
-            if prefix.active_refcount != expected_refs[pid]:
-                raise RuntimeError("prefix active_refcount does not match attached requests")
-        if len(private) != len(set(private)):
-            raise RuntimeError("a private physical block is owned by multiple requests")
-        if set(private) & set(prefix_blocks):
-            raise RuntimeError("a physical block is both private and prefix-owned")
-        owned = prefix_blocks + private
-        if set(owned) & set(free):
-            raise RuntimeError("a physical block is both owned and free")
-        if set(owned) | set(free) != set(range(self.max_blocks)):
-            raise RuntimeError("physical block accounting does not cover the cache")
-        if len(self._transactions) > 1:
-            raise RuntimeError("PagedKVCache retains more than one transaction state")
-        if any(t.state != "open" for t in self._transactions.values()):
-            raise RuntimeError("terminal transaction retained device-backed state")
-        if self._terminal_transaction_history_limit < 0:
-            raise RuntimeError("terminal transaction history limit is negative")
-        if len(self._terminal_transactions) > self._terminal_transaction_history_limit:
-            raise RuntimeError("terminal transaction history exceeds its limit")
-        if set(self._transactions) & set(self._terminal_transactions):
-            raise RuntimeError("transaction appears in both open and terminal state")
-        if any(t.state not in {"committed", "aborted"} for t in self._terminal_transactions.values()):
-            raise RuntimeError("terminal transaction history contains an open state")
-        terminal_ids = tuple(self._terminal_transactions)
-        if any(tid != t.transaction_id for tid, t in self._terminal_transactions.items()):
-            raise RuntimeError("terminal transaction history key does not match its state")
-        if any(tid <= 0 or tid >= self._next_transaction_id for tid in terminal_ids):
-            raise RuntimeError("terminal transaction history contains an invalid id")
-        if any(t.cache_version <= 0 or t.cache_version > self._state_version
-               for t in self._terminal_transactions.values()):
-            raise RuntimeError("terminal transaction history contains an invalid version")
-        if terminal_ids != tuple(sorted(terminal_ids)):
-            raise RuntimeError("terminal transaction history is not ordered by id")
-        open_states = list(self._transactions.values())
-        if self._open_transaction_id is None:
-            if open_states:
-                raise RuntimeError("open transaction is missing from cache state")
-            if any(s.transaction_id is not None for s in self._requests.values()):
-                raise RuntimeError("request has an in-flight marker without an open transaction")
-        else:
-            if len(open_states) != 1:
-                raise RuntimeError("PagedKVCache must have exactly one open transaction")
-            tx = open_states[0]
-            if tx.transaction_id != self._open_transaction_id:
-                raise RuntimeError("open transaction id does not match cache state")
-            if tx.written_layers != set(range(tx.next_layer_idx)):
-                raise RuntimeError("transaction written layers are not sequential")
-            if not 0 <= tx.next_layer_idx <= self.num_layers:
-                raise RuntimeError("transaction next layer is out of range")
-            for rid, pos, loc in zip(tx.request_ids, tx.positions, tx.locations):
-                r = self._require_active_request(rid)
-                if r.transaction_id != tx.transaction_id:
-                    raise RuntimeError("request transaction marker does not match")
-                if pos != r.seq_len:
-                    raise RuntimeError("transaction position is not the committed seq_len")
-                if loc != (r.block_ids[pos // self.block_size], pos % self.block_size):
-                    raise RuntimeError("transaction physical location does not match ownership")
+        for ok, message in self._invariant_rules():
+            if not ok():
+                raise RuntimeError(message)
         return True
 
+    def _invariant_rules(self):
+        """(check, message) in the order they are reported; each check is lazy
+        and may rely on the ones before it having passed."""
+        free = list(self._pool.free)
+        book = self._prefix_book.entries
+        seqs = list(self._seqs.values())
+        live = [seq for seq in seqs if seq.status == self.ACTIVE]
+        closed = [seq for seq in seqs if seq.status != self.ACTIVE]
+        attached = [seq for seq in live if seq.prefix is not None]
+        prefix_pages = [blk for e in book.values() for blk in e.pages]
+        private = [blk for seq in live for blk in seq.private_pages()]
+        txn, history = self._journal.open, self._journal.history
+        hist_ids = tuple(history)
+
+        def each(items, pred):
+            return lambda: all(pred(x) for x in items)
+
+        def refs_match():
+            want = {pid: 0 for pid in book}
+            for seq in attached:
+                want[seq.prefix] += 1
+            return all(e.refs == want[pid] for pid, e in book.items())
+
+        def txn_rows():
+            for rid in txn.rids:
+                self._active_seq(rid)  # raises as a lookup of that request would
+            return True
+
+        rules = [
+            (lambda: len(free) == len(set(free)), "PagedKVCache free list contains duplicate blocks"),
+            (each(book.values(), lambda e: len(e.pages) > 0), "resident prefix must own at least one block"),
+            (each(book.values(), lambda e: e.refs >= 0), "prefix active_refcount must be non-negative"),
+            (lambda: len(prefix_pages) == len(set(prefix_pages)), "a physical block belongs to multiple prefixes"),
+            (lambda: len(prefix_pages) <= self.prefix_cache_capacity_blocks,
+             "resident prefixes exceed configured prefix capacity"),
+            (each(live, lambda s: len(s.pages) == self._pages_for(s.length + (s.txn is not None))),
+             "active request block count does not match seq_len"),
+            (each(live, lambda s: s.prefix is not None or not s.shared), "request without prefix has shared blocks"),
+            (each(attached, lambda s: s.prefix in book), "request references a non-resident prefix"),
+            (each(attached, lambda s: s.shared == len(book[s.prefix].pages)),
+             "request shared block count does not match prefix"),
+            (each(attached, lambda s: tuple(s.pages[: s.shared]) == book[s.prefix].pages),
+             "request shared block ids do not match prefix"),
+            (each(attached, lambda s: s.length >= s.shared * self.block_size),
+             "request seq_len is shorter than its shared prefix"),
+            (each(closed, lambda s: not s.pages), "terminal request still owns physical blocks"),
+            (each(closed, lambda s: s.txn is None), "terminal request belongs to a token transaction"),
+            (each(closed, lambda s: s.prefix is None and not s.shared),
+             "terminal request still references a shared prefix"),
+            (refs_match, "prefix active_refcount does not match attached requests"),
+            (lambda: len(private) == len(set(private)), "a private physical block is owned by multiple requests"),
+            (lambda: not set(private) & set(prefix_pages), "a physical block is both private and prefix-owned"),
+            (lambda: not set(private + prefix_pages) & set(free), "a physical block is both owned and free"),
+            (lambda: set(private + prefix_pages) | set(free) == set(range(self.max_blocks)),
+             "physical block accounting does not cover the cache"),
+            (lambda: txn is None or txn.phase == "open", "terminal transaction retained device-backed state"),
+            (lambda: self._journal.limit >= 0, "terminal transaction history limit is negative"),
+            (lambda: len(history) <= self._journal.limit, "terminal transaction history exceeds its limit"),
+            (lambda: txn is None or txn.tid not in history, "transaction appears in both open and terminal state"),
+            (each(history.values(), lambda c: c.phase in ("committed", "aborted")),
+             "terminal transaction history contains an open state"),
+            (each(history.items(), lambda kv: kv[0] == kv[1].tid), "terminal transaction history key does not match its state"),
+            (each(hist_ids, lambda tid: 0 < tid < self._journal.next_id),
+             "terminal transaction history contains an invalid id"),
+            (each(history.values(), lambda c: 0 < c.version <= self._version),
+             "terminal transaction history contains an invalid version"),
+            (lambda: hist_ids == tuple(sorted(hist_ids)), "terminal transaction history is not ordered by id"),
+            (lambda: txn is not None or all(s.txn is None for s in seqs),
+             "request has an in-flight marker without an open transaction"),
+        ]
+        if txn is not None:
+            rules += [
+                (lambda: 0 <= txn.layers <= self.num_layers, "transaction next layer is out of range"),
+                (txn_rows, "request_id is not active"),
+                (lambda: all(self._seqs[rid].txn == txn.tid for rid in txn.rids),
+                 "request transaction marker does not match"),
+                (lambda: all(self._seqs[rid].length == pos for rid, pos in zip(txn.rids, txn.positions)),
+                 "transaction position is not the committed seq_len"),
+                (lambda: all(slot == (self._seqs[rid].pages[pos // self.block_size], pos % self.block_size)
+                             for rid, pos, slot in zip(txn.rids, txn.positions, txn.slots)),
+                 "transaction physical location does not match ownership"),
+            ]
+        return rules
+
     # ------------------------------------------------------------ internals
-    def _table_rows(self, states, width, pad=-1):
-        rows = np.full((len(states), width), pad, dtype=np.int32)
-        for i, s in enumerate(states):
-            if s.block_ids:
-                rows[i, : len(s.block_ids)] = s.block_ids
+    @staticmethod
+    def _table_rows(seqs, width, pad=-1):
+        rows = np.full((len(seqs), width), pad, dtype=np.int32)
+        for i, seq in enumerate(seqs):
+            rows[i, : len(seq.pages)] = seq.pages
         return rows
 
-    def _location_tensors(self, locations):
-        torch = _torch()
-        arr = np.asarray(locations, dtype=np.int64).reshape(-1, 2)
-        both = _host_to_device(np.ascontiguousarray(arr.T), torch.int64, self.device)
+    def _slot_tensors(self, slots):
+        both = np.ascontiguousarray(np.asarray(slots, dtype=np.int64).reshape(-1, 2).T)
+        both = _host_to_device(both, _torch().int64, self.device)
         return both[0], both[1]
-
-    def _transaction_view(self, transaction):
-        meta = transaction.meta.clone()
-        return KVTokenTransactionView(
-            transaction_id=transaction.transaction_id,
-            cache_version=transaction.cache_version,
-            request_ids=transaction.request_ids,
-            positions=meta.positions,
-            physical_block_ids=meta.block_ids,
-            block_offsets=meta.offsets,
-            block_tables=meta.block_tables,
-            effective_seq_lens=meta.eff_lens,
-            next_layer_idx=transaction.next_layer_idx,
-            state=transaction.state,
-        )
-
-    def _require_transaction(self, transaction):
-        if not isinstance(transaction, KVTokenTransactionView):
-            raise TypeError("transaction must be a KVTokenTransactionView")
-        state = self._transactions.get(transaction.transaction_id)
-        if state is None:
-            state = self._terminal_transactions.get(transaction.transaction_id)
-        if state is None:
-            raise RuntimeError("unknown token transaction")
-        if transaction.cache_version != state.cache_version or transaction.request_ids != state.request_ids:
-            raise RuntimeError("stale or invalid token transaction handle")
-        return state
-
-    def _retire_transaction(self, transaction):
-        retained = self._transactions.pop(transaction.transaction_id, None)
-        if retained is not transaction:
-            raise RuntimeError("token transaction retention state is inconsistent")
-        self._terminal_transactions[transaction.transaction_id] = _TerminalTransactionState(
-            transaction_id=transaction.transaction_id,
-            cache_version=transaction.cache_version,
-            request_ids=transaction.request_ids,
-            state=transaction.state,
-        )
-        while len(self._terminal_transactions) > self._terminal_transaction_history_limit:
-            self._terminal_transactions.popitem(last=False)
-
-    def _require_open_transaction(self, transaction):
-        state = self._require_transaction(transaction)
-        if state.state != "open":
-            raise RuntimeError(f"token transaction is already {state.state}")
-        if self._open_transaction_id != state.transaction_id:
-            raise RuntimeError("token transaction is not the current open transaction")
-        return state
-
-    def _require_legacy_append_available(self):
-        if self.num_layers != 1:
-            raise RuntimeError("multi-layer cache writes require the token transaction API")
-        if self._open_transaction_id is not None:
-            raise RuntimeError("legacy append is not allowed during an open token transaction")
-
-    def _prepare_append_inputs(self, layer_idx, request_ids, k, v):
-        layer_idx = self._validate_layer_idx(layer_idx)
-        ids = self._normalize_request_ids(request_ids)
-        if not ids:
-            raise ValueError("request_ids must be non-empty")
-        if len(set(ids)) != len(ids):
-            raise ValueError("request_ids must be unique within one append call")
-        if k.dim() == 2 and len(ids) == 1:
-            k = k.unsqueeze(0)
-        if v.dim() == 2 and len(ids) == 1:
-            v = v.unsqueeze(0)
-        if k.dim() != 3 or v.dim() != 3:
-            raise ValueError("k and v must have shape [num_requests, num_kv_heads, head_dim]")
-        if k.shape != v.shape:
-            raise ValueError("k and v must have the same shape")
-        if k.shape != (len(ids), self.num_kv_heads, self.head_dim):
-            raise ValueError("k and v shapes must match request count, num_kv_heads, and head_dim")
-        if k.device != self.device or v.device != self.device:
-            raise ValueError("k and v must be on the cache device")
-        if k.dtype != self.dtype or v.dtype != self.dtype:
-            raise ValueError("k and v must use the cache dtype")
-        if not k.is_floating_point() or not v.is_floating_point():
-            raise ValueError("k and v must be floating point tensors")
-        return layer_idx, ids, k, v
-
-    def _prepare_transaction_layer_write(self, state, layer_idx, k, v):
-        layer_idx = self._validate_layer_idx(layer_idx)
-        if layer_idx != state.next_layer_idx:
-            raise RuntimeError(f"transaction requires layer {state.next_layer_idx}, got layer {layer_idx}")
-        _, ids, k, v = self._prepare_append_inputs(layer_idx, state.request_ids, k, v)
-        if tuple(ids) != state.request_ids:
-            raise RuntimeError("transaction request order changed unexpectedly")
-        return layer_idx, k, v
-
-    def _record_transaction_layer_write(self, state, layer_idx):
-        state.written_layers.add(layer_idx)
-        state.next_layer_idx += 1
-        self._transaction_layer_write_count += 1
-        return self._transaction_view(state)
-
-    def _validate_reserved_transaction_locations(self, request_ids, states, positions, locations):
-        """Prove raw-kernel indices from host allocator state before publication."""
-        if not len(request_ids) == len(states) == len(positions) == len(locations):
-            raise RuntimeError("transaction location metadata has inconsistent rows")
-        for rid, s, pos, (blk, off) in zip(request_ids, states, positions, locations):
-            if pos < 0:
-                raise RuntimeError("transaction position must be non-negative")
-            if not 0 <= blk < self.max_blocks:
-                raise RuntimeError("transaction physical block id is out of range")
-            if not 0 <= off < self.block_size:
-                raise RuntimeError("transaction block offset is out of range")
-            if off != pos % self.block_size:
-                raise RuntimeError("transaction block offset does not match position")
-            logical = pos // self.block_size
-            if logical >= len(s.block_ids):
-                raise RuntimeError("transaction logical block is not allocated")
-            if s.block_ids[logical] != blk:
-                raise RuntimeError(f"transaction physical block does not match request {rid!r}")
-
-    def _preflight_append(self, ids):
-        needed = 0
-        for rid in ids:
-            s = self._requests.get(rid)
-            if s is not None and s.status != self.ACTIVE:
-                raise RuntimeError(f"request_id {rid!r} is {s.status} and cannot accept append")
-            if (s.seq_len if s is not None else 0) % self.block_size == 0:
-                needed += 1
-        if needed > len(self._free_blocks):
-            self._capacity_failure_count += 1
-            raise RuntimeError("PagedKVCache is out of physical blocks")
-
-    def _allocate_append_locations(self, ids):
-        locations = []
-        for rid in ids:
-            s = self._requests.get(rid)
-            if s is None:
-                s = _RequestState()
-                self._requests[rid] = s
-            off = s.seq_len % self.block_size
-            if off == 0:
-                s.block_ids.append(self._allocate_block())
-            locations.append((s.block_ids[s.seq_len // self.block_size], off))
-        return locations
-
-    def _advance_request_lengths(self, ids):
-        for rid in ids:
-            self._requests[rid].seq_len += 1
-
-    def _allocate_block(self):
-        if not self._free_blocks:
-            raise RuntimeError("PagedKVCache is out of physical blocks")
-        blk = self._free_blocks.popleft()
-        self._allocation_count += 1
-        if blk in self._ever_allocated_blocks:
-            self._reuse_count += 1
-        else:
-            self._ever_allocated_blocks.add(blk)
-            self._fresh_allocation_count += 1
-        return blk
-
-    def _close_request(self, request_id, terminal_status):
-        if self._open_transaction_id is not None:
-            raise RuntimeError("cannot close a request during an open token transaction")
-        s = self._require_active_request(request_id)
-        prefix = None
-        if s.prefix_id is not None:
-            prefix = self._prefixes.get(s.prefix_id)
-            if prefix is None or prefix.active_refcount <= 0:
-                raise RuntimeError("shared prefix reference accounting is inconsistent")
-        released = tuple(s.block_ids[s.shared_block_count :])
-        # K/V bytes are not cleared: ownership plus the next owner's seq_len mask them
-        for blk in reversed(released):
-            self._free_blocks.appendleft(blk)
-        self._free_count += len(released)
-        s.block_ids.clear()
-        if prefix is not None:
-            prefix.active_refcount -= 1
-            self._prefixes.move_to_end(s.prefix_id)
-        s.prefix_id = None
-        s.shared_block_count = 0
-        s.status = terminal_status
-        self._state_version += 1
-        return released
 
     def _validate_layer_idx(self, layer_idx):
         layer_idx = int(layer_idx)
-        if layer_idx < 0 or layer_idx >= self.num_layers:
+        if not 0 <= layer_idx < self.num_layers:
             raise ValueError("layer_idx must be in [0, num_layers)")
         return layer_idx
 
     def _normalize_request_ids(self, request_ids):
         torch = _torch()
         if isinstance(request_ids, torch.Tensor):
-            if request_ids.dim() == 0:
-                ids = [int(request_ids.detach().cpu().item())]
-            else:
-                ids = [int(x) for x in request_ids.detach().cpu().reshape(-1).tolist()]
+            ids = [int(x) for x in request_ids.detach().cpu().reshape(-1).tolist()]
         elif isinstance(request_ids, (str, bytes)):
             ids = [request_ids]
         else:
@@ -1259,93 +1334,13 @@ class PagedKVCache:
             except TypeError:
                 ids = [request_ids]
         for rid in ids:
-            self._check_request_id(rid)
+            _require_hashable(rid)
         return ids
 
     def _normalize_active_request_ids(self, request_ids):
         if request_ids is None:
-            ids = [rid for rid, s in self._requests.items() if s.status == self.ACTIVE]
-        else:
-            ids = self._normalize_request_ids(request_ids)
+            return [rid for rid, seq in self._seqs.items() if seq.status == self.ACTIVE]
+        ids = self._normalize_request_ids(request_ids)
         for rid in ids:
-            self._require_active_request(rid)
+            self._active_seq(rid)
         return ids
-
-    @staticmethod
-    def _check_request_id(request_id):
-        try:
-            hash(request_id)
-        except TypeError as exc:
-            raise ValueError("request ids must be hashable") from exc
-
-    @staticmethod
-    def _check_prefix_id(prefix_id):
-        if prefix_id is None:
-            raise ValueError("prefix_id must not be None")
-        try:
-            hash(prefix_id)
-        except TypeError as exc:
-            raise ValueError("prefix ids must be hashable") from exc
-
-    def _prepare_prefix_blocks(self, k_blocks, v_blocks):
-        torch = _torch()
-        if not isinstance(k_blocks, torch.Tensor) or not isinstance(v_blocks, torch.Tensor):
-            raise TypeError("k_blocks and v_blocks must be torch tensors")
-        if k_blocks.dim() != 5 or v_blocks.dim() != 5:
-            raise ValueError("prefix K/V must have shape [num_layers, num_prefix_blocks, num_kv_heads, block_size, head_dim]")
-        if k_blocks.shape != v_blocks.shape:
-            raise ValueError("prefix k_blocks and v_blocks must have the same shape")
-        tail = (self.num_kv_heads, self.block_size, self.head_dim)
-        if k_blocks.shape[0] != self.num_layers or tuple(k_blocks.shape[2:]) != tail:
-            raise ValueError("prefix K/V shape does not match the PagedKVCache layout")
-        if k_blocks.shape[1] <= 0:
-            raise ValueError("prefix must contain at least one full block")
-        if k_blocks.device != self.device or v_blocks.device != self.device:
-            raise ValueError("prefix K/V must be on the cache device")
-        if k_blocks.dtype != self.dtype or v_blocks.dtype != self.dtype:
-            raise ValueError("prefix K/V must use the cache dtype")
-        return k_blocks, v_blocks
-
-    def _resident_prefix_blocks(self):
-        return sum(len(p.block_ids) for p in self._prefixes.values())
-
-    def _prefix_eviction_plan(self, required_blocks):
-        if required_blocks > self.prefix_cache_capacity_blocks:
-            return None
-        need = max(0, self._resident_prefix_blocks() + required_blocks - self.prefix_cache_capacity_blocks,
-                   required_blocks - len(self._free_blocks))
-        if not need:
-            return ()
-        released = 0
-        plan = []
-        for pid, prefix in self._prefixes.items():
-            if prefix.active_refcount:
-                continue
-            plan.append(pid)
-            released += len(prefix.block_ids)
-            if released >= need:
-                return tuple(plan)
-        return None
-
-    def _evict_prefix_entry(self, prefix_id):
-        prefix = self._prefixes[prefix_id]
-        if prefix.active_refcount:
-            raise RuntimeError("cannot evict a prefix with active request references")
-        del self._prefixes[prefix_id]
-        for blk in reversed(prefix.block_ids):
-            self._free_blocks.appendleft(blk)
-        self._free_count += len(prefix.block_ids)
-        self._prefix_eviction_count += 1
-        return tuple(prefix.block_ids)
-
-    def _require_request(self, request_id):
-        s = self._requests.get(request_id)
-        if s is None:
-            raise KeyError(f"unknown request_id: {request_id!r}")
-        return s
-
-    def _require_active_request(self, request_id):
-        s = self._require_request(request_id)
-        if s.status != self.ACTIVE:
-            raise RuntimeError(f"request_id {request_id!r} is {s.status}, not active")
-        return s

@@ -158,6 +158,82 @@ class _OpenStep:
     kv_reuse: bool = False  # rows share prefix blocks (per-row path): plain, cached K/V loads
 
 
+class _Roster:
+    """The engine's request statuses, in submission order."""
+
+    __slots__ = ("status",)
+
+    def __init__(self):
+        self.status: dict = {}
+
+    def __bool__(self):
+        return bool(self.status)
+
+    def submit(self, request_id, status):
+        _require_hashable(request_id)
+        if request_id in self.status:
+            raise RuntimeError(f"request_id {request_id!r} already exists in the DecodeEngine")
+        self.status[request_id] = status
+
+    def of(self, request_id):
+        _require_hashable(request_id)
+        if request_id not in self.status:
+            raise KeyError(f"unknown request_id: {request_id!r}")
+        return self.status[request_id]
+
+    def expect(self, request_id, wanted):
+        have = self.of(request_id)
+        if have != wanted:
+            raise RuntimeError(f"request_id {request_id!r} is {have}, expected {wanted}")
+
+    def having(self, wanted):
+        return tuple(rid for rid, st in self.status.items() if st == wanted)
+
+
+class _EngineCounts:
+    """Engine event counters reported by ``DecodeEngine.metrics``."""
+
+    __slots__ = ("steps", "tokens", "backpressure", "layer_steps", "aborts")
+
+    def __init__(self):
+        self.steps = self.tokens = self.backpressure = self.layer_steps = self.aborts = 0
+
+
+def _require_hashable(request_id):
+    try:
+        hash(request_id)
+    except TypeError as exc:
+        raise ValueError("request ids must be hashable") from exc
+
+
+def _as_id_tuple(request_ids):
+    """One id (a string, bytes or any non-iterable) or an iterable of ids, as a tuple."""
+    if isinstance(request_ids, (str, bytes)):
+        return (request_ids,)
+    try:
+        return tuple(request_ids)
+    except TypeError:
+        return (request_ids,)
+
+
+def _step_input_rules(engine, ids, q, k, v):
+    """(broken?, exception, message) of one step's q/k/v, in the order they are reported."""
+    torch = _torch()
+    cache = engine.cache
+    rows = (len(ids), cache.num_kv_heads, cache.head_dim)
+    return (
+        (lambda: not all(isinstance(t, torch.Tensor) for t in (q, k, v)), TypeError,
+         "q, k, and v must be torch tensors"),
+        (lambda: q.dim() != 3, ValueError, "q must have shape [num_requests, num_q_heads, head_dim]"),
+        (lambda: q.shape[0] != len(ids) or q.shape[1] <= 0 or q.shape[2] != cache.head_dim, ValueError,
+         "q shape must match active request count and cache head_dim"),
+        (lambda: k.shape != rows or v.shape != rows, ValueError,
+         "k and v shapes must match active request count and cache dimensions"),
+        (lambda: any(t.device != cache.device for t in (q, k, v)), ValueError, "q, k, and v must be on the cache device"),
+        (lambda: any(t.dtype != cache.dtype for t in (q, k, v)), ValueError, "q, k, and v must use the cache dtype"),
+    )
+
+
 def _is_ragged(lengths):
     """A batch whose longest row is over twice its mean length."""
     if not lengths:
@@ -204,15 +280,11 @@ class DecodeEngine:
         self.num_stages = num_stages
         self.profile_ranges = profile_ranges
         self._range = _torch().profiler.record_function if profile_ranges else None
-        self._statuses: dict = {}
-        self._completed_step_count = 0
-        self._appended_token_count = 0
-        self._backpressure_count = 0
-        self._state_version = 0
-        self._observed_cache_state_version = cache.state_version
+        self._roster = _Roster()
+        self._counts = _EngineCounts()
+        self._version = 0
+        self._cache_seen = cache.state_version  # the cache version this engine last left it at
         self._open: _OpenStep | None = None
-        self._transaction_layer_step_count = 0
-        self._transaction_abort_count = 0
         # Eager steps decode rows attached to one resident prefix with the
         # shared-prefix (cascade) launch once a group's sharers x prefix tokens
         # reach this many (None: never).  On MI355X the cascade is at parity
@@ -222,94 +294,94 @@ class DecodeEngine:
         self._cascade_decode_count = 0
 
     # ------------------------------------------------------------ lifecycle
+    def _advanced(self, cache_changed=True):
+        """One engine state change; ``cache_changed``: it went through the cache,
+        whose new version is then the one this engine expects to find."""
+        if cache_changed:
+            self._cache_seen = self.cache.state_version
+        self._version += 1
+
     def register_prefix(self, prefix_id, k_blocks, v_blocks):
         """Register shared full blocks before any request enters the engine."""
         self._require_no_open_step("register a shared prefix")
-        if self._statuses:
-            raise RuntimeError("shared prefixes must be registered before request submission")
-        if self.cache.state_version != self._observed_cache_state_version:
-            raise RuntimeError("PagedKVCache mutated outside DecodeEngine")
-        m = self.cache.metrics()
-        if any(m[k] for k in ("active_requests", "finished_requests", "cancelled_requests")):
-            raise RuntimeError("shared prefix registration requires an empty PagedKVCache")
+        for broken, message in (
+                (lambda: bool(self._roster), "shared prefixes must be registered before request submission"),
+                (lambda: self.cache.state_version != self._cache_seen, "PagedKVCache mutated outside DecodeEngine"),
+                (lambda: any(self.cache.metrics()[f"{st}_requests"] for st in ("active", "finished", "cancelled")),
+                 "shared prefix registration requires an empty PagedKVCache")):
+            if broken():
+                raise RuntimeError(message)
         result = self.cache.register_prefix(prefix_id, k_blocks, v_blocks)
-        self._sync_cache_version()
+        self._cache_seen = self.cache.state_version  # no engine state changed
         return result
 
     def evict_prefix(self, prefix_id):
         """Evict one inactive prefix after every request is resolved."""
         self._require_no_open_step("evict a shared prefix")
-        if any(s in (self.WAITING, self.ACTIVE) for s in self._statuses.values()):
+        if self._roster.having(self.WAITING) or self._roster.having(self.ACTIVE):
             raise RuntimeError("shared prefixes can only be evicted after all requests are resolved")
         released = self.cache.evict_prefix(prefix_id)
-        self._sync_cache_version()
-        self._bump_state_version()
+        self._advanced()
         return released
 
     def add_request(self, request_id):
         """Submit a request in ``waiting`` state (no KV memory yet)."""
         self._require_no_open_step("submit a request")
-        self._check_request_id(request_id)
-        if request_id in self._statuses:
-            raise RuntimeError(f"request_id {request_id!r} already exists in the DecodeEngine")
-        self._statuses[request_id] = self.WAITING
-        self._bump_state_version()
+        self._roster.submit(request_id, self.WAITING)
+        self._advanced(cache_changed=False)
         return AdmissionResult(request_id=request_id, status=self.WAITING)
 
     def admit(self, request_ids=None, prefix_id=None):
         """Move waiting requests to ``active``; optionally attach a resident shared prefix."""
         self._require_no_open_step("admit requests")
-        if request_ids is None:
-            ids = tuple(r for r, s in self._statuses.items() if s == self.WAITING)
-        else:
-            ids = self._normalize_ids(request_ids)
+        ids = self._roster.having(self.WAITING) if request_ids is None else self._normalize_ids(request_ids)
         if not ids:
             raise ValueError("at least one waiting request is required for admission")
         for rid in ids:
-            self._require_status(rid, self.WAITING)
-        for rid in ids:
+            self._roster.expect(rid, self.WAITING)
+        for rid in ids:  # each row enters the cache (and its prefix) before the next
             self.cache.add_request(rid)
             if prefix_id is not None:
                 self.cache.attach_prefix(rid, prefix_id)
-            self._statuses[rid] = self.ACTIVE
-        self._sync_cache_version()
-        self._bump_state_version()
+            self._roster.status[rid] = self.ACTIVE
+        self._advanced()
         return tuple(AdmissionResult(request_id=rid, status=self.ACTIVE) for rid in ids)
 
     @property
     def state_version(self):
-        return self._state_version
+        return self._version
 
     def active_request_ids(self):
         """Active request ids in admission order."""
-        return tuple(r for r, s in self._statuses.items() if s == self.ACTIVE)
+        return self._roster.having(self.ACTIVE)
 
     def request_state(self, request_id):
-        status = self._require_known_request(request_id)
-        result = {"request_id": request_id, "status": status}
-        if status not in (self.WAITING, self.REJECTED):
-            result["cache"] = self.cache.request_state(request_id)
-        return result
+        status = self._roster.of(request_id)
+        state = {"request_id": request_id, "status": status}
+        if status in (self.ACTIVE, self.FINISHED, self.CANCELLED):  # the rows the cache knows
+            state["cache"] = self.cache.request_state(request_id)
+        return state
+
+    # terminal outcome -> (action named in the open-step error, cache method)
+    _RESOLUTIONS = {FINISHED: ("finish a request", "finish_request"),
+                    CANCELLED: ("cancel a request", "cancel_request")}
+
+    def _resolve(self, request_id, outcome):
+        action, method = self._RESOLUTIONS[outcome]
+        self._require_no_open_step(action)
+        self._roster.expect(request_id, self.ACTIVE)
+        released = getattr(self.cache, method)(request_id)
+        self._roster.status[request_id] = outcome
+        self._advanced()
+        return released
 
     def finish_request(self, request_id):
         """Finish an active request and release its blocks."""
-        self._require_no_open_step("finish a request")
-        self._require_status(request_id, self.ACTIVE)
-        released = self.cache.finish_request(request_id)
-        self._statuses[request_id] = self.FINISHED
-        self._sync_cache_version()
-        self._bump_state_version()
-        return released
+        return self._resolve(request_id, self.FINISHED)
 
     def cancel_request(self, request_id):
         """Cancel an active request and release its blocks."""
-        self._require_no_open_step("cancel a request")
-        self._require_status(request_id, self.ACTIVE)
-        released = self.cache.cancel_request(request_id)
-        self._statuses[request_id] = self.CANCELLED
-        self._sync_cache_version()
-        self._bump_state_version()
-        return released
+        return self._resolve(request_id, self.CANCELLED)
 
     # ---------------------------------------------------- token transaction
     def begin_step(self, request_ids=None):
@@ -320,21 +392,15 @@ class DecodeEngine:
         ids = self._normalize_active_ids(request_ids)
         needed = self._needed_new_blocks(ids)
         if needed > self.cache.num_free_blocks:
-            self._backpressure_count += 1
+            self._counts.backpressure += 1
             raise RuntimeError("insufficient physical blocks to begin decode step")
         tx = self.cache.begin_token(ids)
+        self._advanced()
         handle = DecodeStepTransaction(
-            transaction_id=tx.transaction_id,
-            engine_version=self._state_version + 1,
-            request_ids=ids,
-            positions=tx.positions,
-            physical_block_ids=tx.physical_block_ids,
-            block_offsets=tx.block_offsets,
-            block_tables=tx.block_tables,
-            effective_seq_lens=tx.effective_seq_lens,
-        )
-        self._sync_cache_version()
-        self._bump_state_version()
+            transaction_id=tx.transaction_id, engine_version=self._version, request_ids=ids, positions=tx.positions,
+            physical_block_ids=tx.physical_block_ids, block_offsets=tx.block_offsets, block_tables=tx.block_tables,
+            effective_seq_lens=tx.effective_seq_lens)
+        # decode planning for this batch, from host state
         lengths = self.cache._host_seq_lens(ids)
         groups = self.cache._prefix_groups(ids)
         cascade = self._step_cascade(ids, lengths, groups)
@@ -413,66 +479,62 @@ class DecodeEngine:
         try:
             layer_idx = int(layer_idx)
             if layer_idx != state.next_layer_idx:
-                raise RuntimeError(
-                    f"decode transaction requires layer {state.next_layer_idx}, got layer {layer_idx}")
-            self._validate_step_inputs(state.handle.request_ids, q, k, v)
-            if k.dim() == 2:
-                k = k.unsqueeze(0)
-            if v.dim() == 2:
-                v = v.unsqueeze(0)
-            if self._range is None:
+                raise RuntimeError(f"decode transaction requires layer {state.next_layer_idx}, got layer {layer_idx}")
+            ids = state.handle.request_ids
+            self._validate_step_inputs(ids, q, k, v)
+            k, v = (t.unsqueeze(0) if t.dim() == 2 else t for t in (k, v))
+            with self._phase(PROFILE_RANGE_APPEND):
                 q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table)
+            with self._phase(PROFILE_RANGE_DECODE):
                 output = self._decode_layer(q_rot, view, meta, layer_idx)
-            else:
-                with self._range(PROFILE_RANGE_APPEND):
-                    q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base,
-                                                          cos_sin_table)
-                with self._range(PROFILE_RANGE_DECODE):
-                    output = self._decode_layer(q_rot, view, meta, layer_idx)
         except Exception:
-            self._abort_open_step(state)
+            self._close_step(state, "aborted")
             raise
         state.next_layer_idx += 1
         state.last_output = output
-        self._transaction_layer_step_count += 1
-        return DecodeLayerResult(
-            transaction_id=state.handle.transaction_id,
-            layer_idx=layer_idx,
-            request_ids=state.handle.request_ids,
-            output=output,
-            positions=view.positions,
-            block_tables=view.block_tables,
-            effective_seq_lens=view.effective_seq_lens,
-        )
+        self._counts.layer_steps += 1
+        return DecodeLayerResult(transaction_id=state.handle.transaction_id, layer_idx=layer_idx,
+                                 request_ids=state.handle.request_ids, output=output, positions=view.positions,
+                                 block_tables=view.block_tables, effective_seq_lens=view.effective_seq_lens)
+
+    def _phase(self, name):
+        """A profiler range around one phase when ``profile_ranges`` is on."""
+        import contextlib
+
+        return self._range(name) if self._range is not None else contextlib.nullcontext()
 
     def commit_step(self, transaction):
         """Commit the open token after every layer has run."""
         state = self._require_open_step(transaction)
         if state.next_layer_idx != self.cache.num_layers:
             raise RuntimeError("cannot commit decode step before all layers are complete")
-        committed = self.cache.commit_token(state.cache_transaction)
-        state.state = "committed"
-        self._open = None
-        self._completed_step_count += 1
-        self._appended_token_count += len(state.handle.request_ids)
-        self._sync_cache_version()
-        self._bump_state_version()
-        return DecodeStepResult(
-            status=self.STEP_OK,
-            request_ids=state.handle.request_ids,
-            output=state.last_output,
-            positions=committed.positions,
-            block_tables=committed.block_tables,
-            # the committed lengths are the token's effective lengths, already on
-            # the device: no host-to-device copy per step
-            seq_lens=committed.effective_seq_lens,
-            needed_new_blocks=state.needed_new_blocks,
-            free_blocks=self.cache.num_free_blocks,
-        )
+        committed = self._close_step(state, "committed")
+        # the committed lengths are the token's effective lengths, already on the
+        # device: no host-to-device copy per step
+        return DecodeStepResult(status=self.STEP_OK, request_ids=state.handle.request_ids, output=state.last_output,
+                                positions=committed.positions, block_tables=committed.block_tables,
+                                seq_lens=committed.effective_seq_lens, needed_new_blocks=state.needed_new_blocks,
+                                free_blocks=self.cache.num_free_blocks)
 
     def abort_step(self, transaction):
         """Explicitly abort the open token transaction."""
-        return self._abort_open_step(self._require_open_step(transaction))
+        return self._close_step(self._require_open_step(transaction), "aborted")
+
+    def _close_step(self, state, outcome):
+        """Commit or abort the open step in the cache; returns the cache's final view."""
+        if self._open is not state or state.state != "open":
+            raise RuntimeError("decode step transaction is not open")
+        tx = state.cache_transaction
+        view = self.cache.commit_token(tx) if outcome == "committed" else self.cache.abort_token(tx)
+        state.state = outcome
+        self._open = None
+        if outcome == "committed":
+            self._counts.steps += 1
+            self._counts.tokens += len(state.handle.request_ids)
+        else:
+            self._counts.aborts += 1
+        self._advanced()
+        return view
 
     def capture_step_graph(self, batch_size, num_q_heads, *, rotary_dim=None, base=10_000.0, num_splits=None,
                            merge=False, kv_reuse=None, fuse_rope=None, cascade=None, cos_sin_table=None):
@@ -686,11 +748,11 @@ class DecodeEngine:
             step_graph.graph.replay()
             self.cache._record_graph_layers(state.cache_transaction)
         except Exception:
-            self._abort_open_step(state)
+            self._close_step(state, "aborted")
             raise
         state.next_layer_idx = self.cache.num_layers
         state.last_output = step_graph.out[-1]
-        self._transaction_layer_step_count += self.cache.num_layers
+        self._counts.layer_steps += self.cache.num_layers
         return step_graph.out
 
     def step(self, q, k, v, request_ids=None, layer_idx=0, rotary_dim=None, base=10_000.0):
@@ -698,22 +760,17 @@ class DecodeEngine:
         self._require_no_open_step("run the single-layer step wrapper")
         if self.cache.num_layers != 1:
             raise RuntimeError("multi-layer caches require begin_step/step_layer/commit_step")
-        if self._range is None:
+        with self._phase(PROFILE_RANGE_PREFLIGHT):
             ids = self._normalize_active_ids(request_ids)
             self._validate_step_inputs(ids, q, k, v)
             needed = self._needed_new_blocks(ids)
-        else:
-            with self._range(PROFILE_RANGE_PREFLIGHT):
-                ids = self._normalize_active_ids(request_ids)
-                self._validate_step_inputs(ids, q, k, v)
-                needed = self._needed_new_blocks(ids)
-        if needed > self.cache.num_free_blocks:
-            self._backpressure_count += 1
-            return DecodeStepResult(
-                status=self.STEP_BACKPRESSURE, request_ids=ids, output=None, positions=None, block_tables=None,
-                seq_lens=None, needed_new_blocks=needed, free_blocks=self.cache.num_free_blocks,
-                reason="insufficient_physical_blocks")
-        if self._append in ("torch", "fused_hip"):
+        free = self.cache.num_free_blocks
+        if needed > free:
+            self._counts.backpressure += 1
+            return DecodeStepResult(status=self.STEP_BACKPRESSURE, request_ids=ids, output=None, positions=None,
+                                    block_tables=None, seq_lens=None, needed_new_blocks=needed, free_blocks=free,
+                                    reason="insufficient_physical_blocks")
+        if self._append in ("torch", "fused_hip"):  # a one-layer token transaction
             if int(layer_idx) != 0:
                 raise ValueError("single-layer step requires layer_idx=0")
             tx = self.begin_step(ids)
@@ -721,40 +778,43 @@ class DecodeEngine:
             return self.commit_step(tx)
         from .rope import rope_paged_kv_append
 
-        result = rope_paged_kv_append(self.cache, layer_idx, ids, q, k, v, rotary_dim=rotary_dim, base=base,
-                                      append_backend=self._append)
-        output = self._decode(result.q, result.block_tables, result.seq_lens, layer_idx)
-        self._completed_step_count += 1
-        self._appended_token_count += len(ids)
-        self._sync_cache_version()
-        self._bump_state_version()
-        return DecodeStepResult(status=self.STEP_OK, request_ids=ids, output=output, positions=result.positions,
-                                block_tables=result.block_tables, seq_lens=result.seq_lens, needed_new_blocks=needed,
-                                free_blocks=self.cache.num_free_blocks)
+        appended = rope_paged_kv_append(self.cache, layer_idx, ids, q, k, v, rotary_dim=rotary_dim, base=base,
+                                        append_backend=self._append)
+        output = self._decode(appended.q, appended.block_tables, appended.seq_lens, layer_idx)
+        self._counts.steps += 1
+        self._counts.tokens += len(ids)
+        self._advanced()
+        return DecodeStepResult(status=self.STEP_OK, request_ids=ids, output=output, positions=appended.positions,
+                                block_tables=appended.block_tables, seq_lens=appended.seq_lens,
+                                needed_new_blocks=needed, free_blocks=self.cache.num_free_blocks)
 
     # --------------------------------------------------------------- status
     def metrics(self):
         """Engine counters together with the cache metrics."""
-        st = self._statuses.values()
+        statuses = list(self._roster.status.values())
+        by_status = {st: statuses.count(st)
+                     for st in (self.WAITING, self.ACTIVE, self.FINISHED, self.CANCELLED, self.REJECTED)}
+        c = self._counts
         return {
-            "waiting_requests": sum(s == self.WAITING for s in st),
-            "active_requests": sum(s == self.ACTIVE for s in st),
-            "finished_requests": sum(s == self.FINISHED for s in st),
-            "cancelled_requests": sum(s == self.CANCELLED for s in st),
-            "rejected_requests": sum(s == self.REJECTED for s in st),
-            "completed_step_count": self._completed_step_count,
-            "appended_token_count": self._appended_token_count,
-            "backpressure_count": self._backpressure_count,
-            "state_version": self._state_version,
+            "waiting_requests": by_status[self.WAITING],
+            "active_requests": by_status[self.ACTIVE],
+            "finished_requests": by_status[self.FINISHED],
+            "cancelled_requests": by_status[self.CANCELLED],
+            "rejected_requests": by_status[self.REJECTED],
+            "completed_step_count": c.steps,
+            "appended_token_count": c.tokens,
+            "backpressure_count": c.backpressure,
+            "state_version": self._version,
             "cache_state_version": self.cache.state_version,
+            # the reference's scheduler-managed mode (policy, outside this data path) is never on
             "scheduler_managed": False,
             "committed_blocks": 0,
             "committed_but_unallocated_blocks": 0,
             "stale_decision_count": 0,
             "applied_decision_count": 0,
             "open_step_transaction_count": int(self._open is not None),
-            "transaction_layer_step_count": self._transaction_layer_step_count,
-            "transaction_abort_count": self._transaction_abort_count,
+            "transaction_layer_step_count": c.layer_steps,
+            "transaction_abort_count": c.aborts,
             "append_backend": self.append_backend,
             "decode_backend": self.decode_backend,
             "cache": self.cache.metrics(),
@@ -762,26 +822,30 @@ class DecodeEngine:
 
     def validate_invariants(self):
         """Check engine lifecycle state against cache ownership state."""
-        self.cache.validate_invariants()
-        if self._open is None:
-            if self.cache.has_open_transaction:
-                raise RuntimeError("cache has an open transaction not owned by DecodeEngine")
-        else:
-            if not self.cache.has_open_transaction:
+        cache = self.cache
+        cache.validate_invariants()
+        open_step = self._open
+        if open_step is None and cache.has_open_transaction:
+            raise RuntimeError("cache has an open transaction not owned by DecodeEngine")
+        if open_step is not None:
+            if not cache.has_open_transaction:
                 raise RuntimeError("Engine transaction is open but cache transaction is not")
-            view = self.cache.transaction_view(self._open.cache_transaction)
-            if view.request_ids != self._open.handle.request_ids:
+            view = cache.transaction_view(open_step.cache_transaction)
+            if view.request_ids != open_step.handle.request_ids:
                 raise RuntimeError("Engine/cache transaction request rows diverged")
-            if view.next_layer_idx != self._open.next_layer_idx:
+            if view.next_layer_idx != open_step.next_layer_idx:
                 raise RuntimeError("Engine/cache transaction layer progress diverged")
-        for rid, status in self._statuses.items():
+        for rid, status in self._roster.status.items():
+            try:
+                cache_status = cache.request_state(rid)["status"]
+            except KeyError:
+                cache_status = None
             if status in (self.WAITING, self.REJECTED):
-                try:
-                    self.cache.request_state(rid)
-                except KeyError:
-                    continue
-                raise RuntimeError("waiting request unexpectedly exists in PagedKVCache")
-            if self.cache.request_state(rid)["status"] != status:
+                if cache_status is not None:
+                    raise RuntimeError("waiting request unexpectedly exists in PagedKVCache")
+            elif cache_status != status:
+                if cache_status is None:
+                    cache.request_state(rid)  # re-raises the cache's own lookup error
                 raise RuntimeError("DecodeEngine and PagedKVCache request status diverged")
         return True
 
@@ -838,23 +902,6 @@ class DecodeEngine:
                                       num_warps=self.num_warps, num_stages=self.num_stages, ragged=ragged,
                                       kv_reuse=kv_reuse)
 
-    def _abort_open_step(self, state):
-        if self._open is not state or state.state != "open":
-            raise RuntimeError("decode step transaction is not open")
-        aborted = self.cache.abort_token(state.cache_transaction)
-        state.state = "aborted"
-        self._open = None
-        self._transaction_abort_count += 1
-        self._sync_cache_version()
-        self._bump_state_version()
-        return aborted
-
-    def _bump_state_version(self):
-        self._state_version += 1
-
-    def _sync_cache_version(self):
-        self._observed_cache_state_version = self.cache.state_version
-
     def _require_no_open_step(self, action):
         if self._open is not None:
             raise RuntimeError(f"cannot {action} during an open decode step transaction")
@@ -866,73 +913,38 @@ class DecodeEngine:
         if state is None:
             raise RuntimeError("DecodeEngine has no open decode step transaction")
         h = state.handle
-        if (transaction.transaction_id != h.transaction_id or transaction.engine_version != h.engine_version
-                or transaction.request_ids != h.request_ids):
+        if (transaction.transaction_id, transaction.engine_version, transaction.request_ids) != (
+                h.transaction_id, h.engine_version, h.request_ids):
             raise RuntimeError("stale or invalid DecodeEngine transaction handle")
         if state.state != "open":
             raise RuntimeError(f"decode step transaction is already {state.state}")
         return state
 
     def _validate_step_inputs(self, ids, q, k, v):
-        torch = _torch()
-        if not isinstance(q, torch.Tensor) or not isinstance(k, torch.Tensor) or not isinstance(v, torch.Tensor):
-            raise TypeError("q, k, and v must be torch tensors")
-        if q.dim() != 3:
-            raise ValueError("q must have shape [num_requests, num_q_heads, head_dim]")
-        if k.dim() == 2 and len(ids) == 1:
-            k = k.unsqueeze(0)
-        if v.dim() == 2 and len(ids) == 1:
-            v = v.unsqueeze(0)
-        expected = (len(ids), self.cache.num_kv_heads, self.cache.head_dim)
-        if q.shape[0] != len(ids) or q.shape[1] <= 0 or q.shape[2] != self.cache.head_dim:
-            raise ValueError("q shape must match active request count and cache head_dim")
-        if k.shape != expected or v.shape != expected:
-            raise ValueError("k and v shapes must match active request count and cache dimensions")
-        if q.device != self.cache.device or k.device != self.cache.device or v.device != self.cache.device:
-            raise ValueError("q, k, and v must be on the cache device")
-        if q.dtype != self.cache.dtype or k.dtype != self.cache.dtype or v.dtype != self.cache.dtype:
-            raise ValueError("q, k, and v must use the cache dtype")
+        if len(ids) == 1:  # one request may pass its K/V row without the batch axis
+            k, v = (t.unsqueeze(0) if getattr(t, "dim", lambda: 0)() == 2 else t for t in (k, v))
+        for broken, exc, message in _step_input_rules(self, ids, q, k, v):
+            if broken():
+                raise exc(message)
 
     def _needed_new_blocks(self, ids):
+        """Requests whose next token starts a new block (one block each)."""
         bs = self.cache.block_size
-        return sum(self.cache.request_state(rid)["seq_len"] % bs == 0 for rid in ids)
+        return sum(n % bs == 0 for n in self.cache._host_seq_lens(ids))
 
     def _normalize_active_ids(self, request_ids):
         ids = self.active_request_ids() if request_ids is None else self._normalize_ids(request_ids)
         if not ids:
             raise ValueError("at least one active request is required for a decode step")
         for rid in ids:
-            self._require_status(rid, self.ACTIVE)
-        return ids
-
-    def _normalize_ids(self, request_ids):
-        if isinstance(request_ids, (str, bytes)):
-            ids = (request_ids,)
-        else:
-            try:
-                ids = tuple(request_ids)
-            except TypeError:
-                ids = (request_ids,)
-        for rid in ids:
-            self._check_request_id(rid)
-        if len(set(ids)) != len(ids):
-            raise ValueError("request_ids must be unique")
+            self._roster.expect(rid, self.ACTIVE)
         return ids
 
     @staticmethod
-    def _check_request_id(request_id):
-        try:
-            hash(request_id)
-        except TypeError as exc:
-            raise ValueError("request ids must be hashable") from exc
-
-    def _require_known_request(self, request_id):
-        self._check_request_id(request_id)
-        if request_id not in self._statuses:
-            raise KeyError(f"unknown request_id: {request_id!r}")
-        return self._statuses[request_id]
-
-    def _require_status(self, request_id, expected):
-        status = self._require_known_request(request_id)
-        if status != expected:
-            raise RuntimeError(f"request_id {request_id!r} is {status}, expected {expected}")
+    def _normalize_ids(request_ids):
+        ids = _as_id_tuple(request_ids)
+        for rid in ids:
+            _require_hashable(rid)
+        if len(set(ids)) != len(ids):
+            raise ValueError("request_ids must be unique")
+        return ids

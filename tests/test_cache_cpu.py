@@ -258,8 +258,8 @@ def test_location_proof_failure_rolls_back_reservation(monkeypatch):
 def test_location_proof_rejects_inconsistent_rows():
     cache = make_cache(num_layers=1, block_size=2, max_blocks=2)
     cache.add_request(1)
-    state = cache._requests[1]
-    state.block_ids.append(0)
+    state = cache._seqs[1]
+    state.pages.append(0)
     with pytest.raises(RuntimeError, match="offset does not match"):
         cache._validate_reserved_transaction_locations([1], [state], [0], [(0, 1)])
     with pytest.raises(RuntimeError, match="out of range"):
@@ -321,7 +321,7 @@ def test_transaction_state_machine_rejections():
 def test_terminal_history_is_bounded_and_tensor_free():
     kat = KATS["terminal_history"]
     cache = make_cache(num_layers=1, block_size=16, max_blocks=1)
-    cache._terminal_transaction_history_limit = kat["limit"]
+    cache._journal.limit = kat["limit"]
     cache.add_request("r")
     handles = []
     for i in range(kat["transactions"]):
@@ -336,8 +336,8 @@ def test_terminal_history_is_bounded_and_tensor_free():
         assert m["retained_transaction_state_count"] == 0
         assert m["terminal_transaction_history_count"] <= kat["limit"]
         assert cache.validate_invariants()
-    assert list(cache._terminal_transactions) == kat["retained_ids"]
-    assert not any(isinstance(v, torch.Tensor) for t in cache._terminal_transactions.values() for v in vars(t).values())
+    assert list(cache._journal.history) == kat["retained_ids"]
+    assert not any(isinstance(getattr(t, f), torch.Tensor) for t in cache._journal.history.values() for f in t.__slots__)
     with pytest.raises(RuntimeError, match="unknown token transaction"):
         cache.abort_token(handles[0])
     with pytest.raises(RuntimeError, match="already aborted"):
@@ -355,12 +355,12 @@ def test_terminal_view_failure_leaves_transaction_open(monkeypatch, op):
     tx = cache.begin_token(["r"])
     if op == "commit":
         write_all_layers(cache, tx)
-    original = cache._transaction_view
+    original = cache._snapshot
 
     def broken(_state):
         raise RuntimeError("planted view failure")
 
-    monkeypatch.setattr(cache, "_transaction_view", broken)
+    monkeypatch.setattr(cache, "_snapshot", broken)
     call = getattr(cache, f"{op}_token")
     with pytest.raises(RuntimeError, match="planted view failure"):
         call(tx)
@@ -369,7 +369,7 @@ def test_terminal_view_failure_leaves_transaction_open(monkeypatch, op):
     m = cache.metrics()
     assert (m["retained_transaction_state_count"], m["terminal_transaction_history_count"]) == (1, 0)
     assert cache.validate_invariants()
-    monkeypatch.setattr(cache, "_transaction_view", original)
+    monkeypatch.setattr(cache, "_snapshot", original)
     assert call(tx).state == {"commit": "committed", "abort": "aborted"}[op]
     m = cache.metrics()
     assert (m["retained_transaction_state_count"], m["terminal_transaction_history_count"]) == (0, 1)
@@ -405,11 +405,11 @@ def test_invariant_checker_detects_planted_corruption():
     cache = make_cache(block_size=2, max_blocks=4)
     cache.append(0, [1, 2], tok(2, 1), tok(2, 1))
     assert cache.validate_invariants()
-    cache._free_blocks.append(cache.request_block_ids(1)[0])
+    cache._pool.free.append(cache.request_block_ids(1)[0])
     with pytest.raises(RuntimeError):
         cache.validate_invariants()
-    cache._free_blocks.pop()
-    cache._requests[2].seq_len = 5
+    cache._pool.free.pop()
+    cache._seqs[2].length = 5
     with pytest.raises(RuntimeError, match="block count does not match"):
         cache.validate_invariants()
 
@@ -552,7 +552,7 @@ def test_seed_context_equals_token_by_token_commits():
     assert lens.tolist() == [9, 10, 9]
     for rid in ("x", "y", "z"):
         assert a.request_block_ids(rid) == b.request_block_ids(rid)
-    assert list(a._free_blocks) == list(b._free_blocks)
+    assert list(a._pool.free) == list(b._pool.free)
     assert torch.equal(a.k_cache, b.k_cache) and torch.equal(a.v_cache, b.v_cache)
     for key in ("used_blocks", "allocation_count", "fresh_allocation_count", "active_tokens"):
         assert a.metrics()[key] == b.metrics()[key]
