@@ -10,8 +10,8 @@
  * Tensors are passed as raw device pointers plus element strides, so strided
  * views (vLLM's [block, plane, token, head, dim] cache, NHD/HND permutations,
  * dim-major caches) are consumed in place without copies.  fd_paged_decode
- * runs an MFMA kernel (head_dim 64 or 128, any group size, strides
- * multiples of 8 and 16-byte aligned bases) for token-major caches with unit
+ * runs an MFMA kernel (head_dim 64 or 128, up to 256 query heads per KV head,
+ * strides multiples of 8 and 16-byte aligned bases) for token-major caches with unit
  * dim stride and for dim-major caches with unit token stride; other views run
  * a VALU kernel with the same results within rounding.
  *

@@ -244,20 +244,28 @@ def test_graph_capture_replays_match_eager():
         assert torch.equal(out, eager)
 
 
-def test_in_launch_merge_leaves_counters_zero_across_calls():
-    """Repeated auto-split calls agree bit for bit and leave the counters at zero."""
+def test_in_launch_merge_matches_the_reducer_and_leaves_counters_zero():
+    """C2 through the in-launch merge (split counters given): five calls in a row equal the
+    reducer-kernel path bit for bit, and each leaves every arrival counter at zero."""
+    from flashdec_amd import _lib
     from flashdec_amd import paged_decode as pd
 
     q, k, v, table, lens = make_paged_inputs([2048] * 8, 16, 2, 128, 32, torch.bfloat16, seed=31)
-    fd = _fd()
-    outs = [fd.decode(q, k, v, table, lens) for _ in range(5)]
-    torch.cuda.synchronize()
-    for o in outs[1:]:
-        assert torch.equal(o, outs[0])
-    key = (q.device.index, torch.cuda.current_stream().cuda_stream)
-    ws = pd._WORKSPACES[key]
-    assert torch.count_nonzero(ws.counters) == 0
-    assert_close_to_oracle(outs[0], _oracle(q, k, v, table, lens))
+    splits = _lib.paged_decode_plan(8, 16, 2, 128, 2048)
+    assert splits > 1
+    ws = (torch.empty((8, 16, splits, 128), device="cuda"), torch.empty((8, 16, splits), device="cuda"),
+          torch.empty((8, 16, splits), device="cuda"))
+    counters = torch.zeros(8 * 2 * _lib.SPLIT_COUNTER_STRIDE, device="cuda", dtype=torch.int32)
+    scale = 1.0 / math.sqrt(128)
+    reducer = torch.empty_like(q)
+    pd._decode_with_workspace(q, k, v, table, lens, reducer, scale, 32, splits, ws, k.shape[0])
+    for _ in range(5):
+        merged = torch.full_like(q, float("nan"))
+        pd._decode_with_workspace(q, k, v, table, lens, merged, scale, 32, splits, ws, k.shape[0], counters=counters)
+        torch.cuda.synchronize()
+        assert torch.equal(merged, reducer)
+        assert torch.count_nonzero(counters) == 0
+    assert_close_to_oracle(merged, _oracle(q, k, v, table, lens))
 
 
 @pytest.mark.parametrize("num_splits", [2, 16, 64, 100])

@@ -14,6 +14,8 @@ the kernel does not take run the generic kernel and must agree as well.
 Tolerance: atol 2e-2 / rtol 1e-2 against the fp32 oracle.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -273,3 +275,60 @@ def test_graph_replays_match_eager_with_new_inputs(block_size):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), step
         assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+def _fused_abi_call(q, k, v, table, lens, slots, append_k, append_v, block_size, num_splits):
+    """fd_paged_decode on a dim-major cache with the fused append, through the C ABI (the Python
+    API takes the fused append only for the reference's grouped shapes)."""
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    out = torch.empty_like(q)
+    args = _lib.PagedDecodeArgs()
+    pd._fill_common(args, q, k, v, pd._cache_strides(k, 3, 2), pd._cache_strides(v, 3, 2), table, lens, out,
+                    k.shape[1], block_size, 1.0 / math.sqrt(q.shape[2]))
+    args.num_blocks = k.shape[0]
+    args.max_seq_len = int(lens.max())
+    b, hq, d = q.shape
+    ws = None
+    if num_splits > 1:
+        ws = (torch.empty((b, hq, num_splits, d), device="cuda"), torch.empty((b, hq, num_splits), device="cuda"),
+              torch.empty((b, hq, num_splits), device="cuda"))
+    pd._fill_workspace(args, *(ws or (None, None, None)), num_splits)
+    pd._fill_append(args, append_k, append_v, torch.tensor(slots, device="cuda", dtype=torch.int64))
+    _lib.paged_decode(args, _lib.current_stream_handle(q.device))
+    return out
+
+
+@pytest.mark.parametrize("num_splits", [1, 4])
+@pytest.mark.parametrize(("hq", "head_dim", "block_size", "lens_after"), [
+    # 8-token blocks: the appended token in each quarter of a 32-token unit (pos % 32 = 4, 10, 22, 24)
+    (16, 128, 8, [101, 75, 55, 121]),
+    (16, 64, 8, [101, 75, 55, 121]),
+    # head_dim 64 on 16- and 32-token blocks
+    (16, 64, 16, [33, 1, 200, 64]),
+    (16, 64, 32, [33, 1, 200, 64]),
+    # groups of 32 and 40 query heads per KV head: head blocks past the first splice the new token
+    # from registers without storing it
+    (64, 128, 32, [33, 300, 64, 2]),
+    (80, 128, 32, [33, 300, 64, 2]),
+    (80, 128, 8, [101, 75, 55, 121]),
+])
+def test_fused_append_dim_major_beyond_the_python_shapes(hq, head_dim, block_size, lens_after, num_splits):
+    q, k, v, table, lens = make_paged_inputs(lens_after, hq, 2, head_dim, block_size, torch.bfloat16,
+                                             kv_layout="dim_major", seed=53)
+    expected = _oracle(q, k, v, table, lens)
+    slots = _slots(table, lens.cpu(), block_size)
+    append_k = torch.empty((len(lens_after), 2, head_dim), device="cuda", dtype=torch.bfloat16)
+    append_v = torch.empty_like(append_k)
+    k_expected, v_expected = k.clone(), v.clone()
+    for b, s in enumerate(slots):
+        blk, off = divmod(s, block_size)
+        append_k[b] = k[blk, :, :, off]
+        append_v[b] = v[blk, :, :, off]
+        k[blk, :, :, off] = float("nan")
+        v[blk, :, :, off] = float("nan")
+    out = _fused_abi_call(q, k, v, table, lens, slots, append_k, append_v, block_size, num_splits)
+    assert_close_to_oracle(out, expected)
+    assert torch.equal(k.view(torch.int16), k_expected.view(torch.int16))
+    assert torch.equal(v.view(torch.int16), v_expected.view(torch.int16))
