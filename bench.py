@@ -8,18 +8,27 @@ before timing starts.  Steps rotate over ``--pools`` independent KV pools
 (default 48 x 21 MB ~ 1 GB) so the 256 MB Infinity Cache cannot serve them.
 
 Timing:
-* ``ms_per_step``/``value``: K steps captured in one hipGraph, replayed once
-  between two synchronisations (the serving-loop view, launch gaps included).
+* warm-up: at least ``--warmup`` calls and at least 100 ms of calls.
+* ``ms_per_step``/``value``: p50 of the per-call time over 240 samples, each
+  one replay of a hipGraph holding one call per pool (one rotation), replayed
+  back to back with hipEvents between the replays.
+* ``single_replay_ms_per_step``: K steps captured in one hipGraph, replayed
+  once between two synchronisations (the serving-loop view, launch gaps
+  included).
 * ``roofline.achieved``: algorithmic bytes per call / mean duration of the
   dominant kernel (the attention kernel), measured live: every call of a
   separate eager loop passes HIP events through the library's
   ``timing_events`` hook, which records them around exactly that dispatch
-  (and around the split reducer, reported beside it).
+  (and around the split reducer, reported beside it).  Events cannot bracket
+  one kernel inside a captured graph; the rocprofv3 kernel trace of the
+  graph replays is the cross-check.
 * ``roofline.traffic``: HBM bytes per attention-kernel dispatch from the
   committed PMC summary ``profiles/decode_mfma_b8_ctx2048_traffic.json``
   (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null.
-* ``cpu_baseline``: the repo's numpy oracle (one thread) on a bounded sample
-  of the same workload, on this host.
+* ``cpu_baseline``: the repo's numpy oracle on this host's cores (the rows of
+  a call spread over a process pool, one BLAS thread per process), on C1 and
+  on the C2 call: p50 of >= 20 calls after 3 warm-ups, with ``os.cpu_count()``
+  and the CPU model.  It runs first, before this process touches the GPU.
 
 ``--profile-kernels N`` instead runs N eager calls and a 64 MiB device copy
 (the counter-scaling reference) and prints one line: the form profiled by
@@ -138,28 +147,116 @@ def load_traffic():
         return None, None
 
 
-def cpu_baseline(pools, budget_s, sm_scale):
-    """Median seconds per call of the numpy oracle on pool 0 (one BLAS thread)."""
+def cpu_model():
+    """The host CPU's model name (first ``model name`` of /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_inputs(name):
+    """Seeded numpy inputs of a CPU-baseline config (fp32 arrays, sm_scale, out_dtype, algorithmic bytes).
+
+    C1: B4 Hq8 Hkv2 D64 fp32, bs32, L ~ U{1..512} over a 128-block pool whose
+    table rows are consecutive slices of a permutation, seed 61.  C2: B8 Hq16 Hkv2 D128, bs32, every
+    length 2048, a 640-block pool (1.25x) with permuted tables, bf16 values (N(0,1) rounded to bf16)
+    held in fp32 as the reference upcasts them, seed 20260830 + 8 + 2048.
+    """
     import numpy as np
+
+    from oracle.rope import round_to
+
+    if name == "C1":
+        rng = np.random.default_rng(61)
+        b, hq, hkv, d, bs, pool = 4, 8, 2, 64, 32, 128
+        lens = rng.integers(1, 513, size=b).astype(np.int32)
+        dtype = "float32"
+    else:
+        rng = np.random.default_rng(20260830 + 8 + 2048)
+        b, hq, hkv, d, bs, pool = 8, 16, 2, 128, 32, 640
+        lens = np.full(b, 2048, dtype=np.int32)
+        dtype = "bfloat16"
+    nblk = [(int(n) + bs - 1) // bs for n in lens]
+    perm = rng.permutation(pool)
+    table = np.full((b, max(nblk)), -1, dtype=np.int32)
+    cursor = 0
+    for row, n in enumerate(nblk):
+        table[row, :n] = perm[cursor:cursor + n]
+        cursor += n
+    k = round_to(rng.standard_normal((pool, hkv, bs, d), dtype=np.float32), dtype)
+    v = round_to(rng.standard_normal((pool, hkv, bs, d), dtype=np.float32), dtype)
+    q = round_to(rng.standard_normal((b, hq, d), dtype=np.float32), dtype)
+    elt = 4 if dtype == "float32" else 2
+    nbytes = int(int(lens.sum()) * hkv * d * 2 * elt + 2 * q.size * elt + 4 * table.size + 4 * b)
+    return (q, k, v, table, lens), 1.0 / math.sqrt(d), dtype, nbytes
+
+
+_CPU_WORKER = {}
+
+
+def _cpu_worker_init():
+    """Process-pool initializer: one BLAS thread, and each config's inputs built locally."""
     from threadpoolctl import threadpool_limits
 
+    _CPU_WORKER["blas"] = threadpool_limits(limits=1)
+    for name in ("C1", "C2"):
+        _CPU_WORKER[name] = cpu_inputs(name)
+
+
+def _cpu_row(name, b):
+    """The oracle on row ``b`` of a config (runs in a worker)."""
     from oracle.attention import paged_decode_attention as oracle_decode
 
-    q, k, v, table, lens, _ = pools[0]
-    qn = q.float().cpu().numpy()
-    kn = k.float().cpu().numpy()
-    vn = v.float().cpu().numpy()
-    tn = table.cpu().numpy()
-    ln = lens.cpu().numpy()
+    (q, k, v, table, lens), scale, out_dtype, _ = _CPU_WORKER[name]
+    return oracle_decode(q[b:b + 1], k, v, table[b:b + 1], lens[b:b + 1], sm_scale=scale, out_dtype=out_dtype)
+
+
+def cpu_time_p50(fn, warmup=3, reps=20, budget_s=10.0):
+    """p50 seconds of fn() after ``warmup`` calls, over >= ``reps`` calls (more while under budget)."""
+    for _ in range(warmup):
+        fn()
     times = []
-    with threadpool_limits(limits=1):
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 1000):
-            t0 = time.perf_counter()
-            oracle_decode(qn, kn, vn, tn, ln, sm_scale=sm_scale, out_dtype="bfloat16")
-            times.append(time.perf_counter() - t0)
-    del np
+    t_end = time.perf_counter() + budget_s
+    while len(times) < reps or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
     return statistics.median(times), len(times)
+
+
+def cpu_baseline(budget_s):
+    """The numpy oracle (restatement of paged_reference.py:19-125) on this host's cores.
+
+    Rows of a call are independent: each call hands its rows to a process
+    pool of min(os.cpu_count(), 16, rows) workers (one BLAS thread each).
+    Timed on C1 and on the C2 call: p50 of >= 20 calls after 3 warm-ups.
+    Runs before this process touches the GPU (the workers are started as
+    fresh processes).
+    """
+    import multiprocessing as mp
+    from concurrent.futures import ProcessPoolExecutor
+
+    n_cpu = os.cpu_count() or 1
+    rows = {"C1": 4, "C2": 8}
+    workers = min(n_cpu, 16, max(rows.values()))
+    results = {}
+    with ProcessPoolExecutor(max_workers=workers, mp_context=mp.get_context("spawn"),
+                             initializer=_cpu_worker_init) as ex:
+        for name, n in rows.items():
+            nbytes = cpu_inputs(name)[3]
+
+            def one_call(name=name, n=n):
+                list(ex.map(_cpu_row, [name] * n, range(n)))
+
+            sec, reps = cpu_time_p50(one_call, budget_s=budget_s / 2)
+            results[name] = {"us_per_call": round(sec * 1e6, 1), "gb_per_s": round(nbytes / sec / 1e9, 4),
+                             "processes": min(workers, n), "calls": reps, "algorithmic_bytes": nbytes}
+    return results, n_cpu
 
 
 def back_to_back(torch, lib, prepared, n, events=None):
@@ -817,6 +914,11 @@ def main():
         )
         sys.exit(2)
 
+    # the CPU leg first: its worker processes start before this process touches the GPU
+    cpu_res = None
+    if args.workload == "decode" and not args.no_cpu and not args.profile_kernels:
+        cpu_res = cpu_baseline(args.cpu_seconds)
+
     import torch
 
     import flashdec_amd as fd
@@ -850,23 +952,34 @@ def main():
     if args.profile_kernels:
         profile_kernels(torch, dev, _lib, prepared, args.profile_kernels)
         return
-    back_to_back(torch, _lib, prepared, args.warmup)
-    log("[bench] warmup done")
+    # warm-up: at least --warmup calls and at least 100 ms of calls
+    t_warm = time.perf_counter()
+    warm_calls = 0
+    while warm_calls < args.warmup or time.perf_counter() - t_warm < 0.1:
+        n = max(len(pools), args.warmup - warm_calls)
+        back_to_back(torch, _lib, prepared, n)
+        warm_calls += n
+    warmup_ms = (time.perf_counter() - t_warm) * 1e3
+    log(f"[bench] warmup: {warm_calls} calls in {warmup_ms:.0f} ms")
 
-    # K steps in one graph, replayed once inside the timed region
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream(dev)
-    cap.wait_stream(stream)
-    with torch.cuda.stream(cap):
-        call(0)  # the capture stream's split workspace exists before capture
-        cap.synchronize()
-        with torch.cuda.graph(graph, stream=cap):
-            for i in range(args.steps):
-                call(i)
-    stream.wait_stream(cap)
-    torch.cuda.synchronize()
-    graph.replay()  # untimed replay (first-replay setup)
-    torch.cuda.synchronize()
+    def capture(n_calls):
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream(dev)
+        cap.wait_stream(stream)
+        with torch.cuda.stream(cap):
+            call(0)  # the capture stream's split workspace exists before capture
+            cap.synchronize()
+            with torch.cuda.graph(g, stream=cap):
+                for i in range(n_calls):
+                    call(i)
+        stream.wait_stream(cap)
+        torch.cuda.synchronize()
+        g.replay()  # untimed replay (first-replay setup)
+        torch.cuda.synchronize()
+        return g
+
+    # (1) exactly K steps in one graph, replayed once between synchronisations
+    graph = capture(args.steps)
     t_start = torch.cuda.Event(enable_timing=True)
     t_stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -875,8 +988,24 @@ def main():
     t_stop.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_stop)
-    ms_per_step = total_ms / args.steps
-    log(f"[bench] graph: {args.steps} calls in {total_ms:.3f} ms -> {ms_per_step * 1e3:.2f} us/call")
+    single_ms = total_ms / args.steps
+    log(f"[bench] graph: {args.steps} calls in {total_ms:.3f} ms -> {single_ms * 1e3:.2f} us/call")
+
+    # (2) p50 over samples: a graph of one call per pool (one rotation over
+    # the pools), replayed back to back with events between the replays
+    sample_graph = capture(len(pools))
+    n_samples = 240
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(n_samples + 1)]
+    torch.cuda.synchronize()
+    marks[0].record(stream)
+    for i in range(n_samples):
+        sample_graph.replay()
+        marks[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_call = sorted(marks[i].elapsed_time(marks[i + 1]) / len(pools) for i in range(n_samples))
+    ms_per_step = statistics.median(per_call)
+    log(f"[bench] p50 over {n_samples} samples of {len(pools)} calls: {ms_per_step * 1e3:.2f} us/call "
+        f"(p10 {per_call[n_samples // 10] * 1e3:.2f}, p90 {per_call[9 * n_samples // 10] * 1e3:.2f})")
 
     # live per-kernel durations: the library records events around each dispatch
     n_calls = min(4 * len(pools), 192)
@@ -898,17 +1027,23 @@ def main():
         traffic = int(round(traffic))
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     cpu = None
-    if not args.no_cpu:
-        cpu_s, reps = cpu_baseline(pools, args.cpu_seconds, sm_scale)
+    if cpu_res is not None:
+        res, n_cpu = cpu_res
+        c2 = res["C2"]
         cpu = {
-            "value": round(nbytes / cpu_s / 1e9, 4),
+            "value": c2["gb_per_s"],
             "unit": "GB/s",
-            "cores": 1,
+            "cores": c2["processes"],
             "kind": "port",
-            "sample": f"numpy oracle (oracle/attention.py), full B{batch} ctx{ctx} call on pool 0, "
-                      f"median of {reps} calls, {cpu_s * 1e6:.0f} us/call, one BLAS thread",
+            "sample": f"numpy oracle (oracle/attention.py, restating paged_reference.py:19-125) on the full "
+                      f"B8 ctx2048 call, its rows on {c2['processes']} worker processes (one BLAS thread each), "
+                      f"p50 of {c2['calls']} calls after 3 warm-ups: {c2['us_per_call']:.0f} us/call",
+            "os_cpu_count": n_cpu,
+            "cpu_model": cpu_model(),
+            "configs": res,
         }
-        log(f"[bench] cpu oracle: {cpu_s * 1e3:.1f} ms/call over {reps} calls")
+        log(f"[bench] cpu oracle: C2 {c2['us_per_call'] / 1e3:.2f} ms/call ({c2['processes']} processes), "
+            f"C1 {res['C1']['us_per_call'] / 1e3:.2f} ms/call")
 
     result = {
         "metric": METRIC,
@@ -919,6 +1054,11 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 6),
         "us_per_call": round(ms_per_step * 1e3, 3),
+        "p50_samples": n_samples,
+        "calls_per_sample": len(pools),
+        "single_replay_ms_per_step": round(single_ms, 6),
+        "warmup_ms": round(warmup_ms, 1),
+        "warmup_calls": warm_calls,
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -936,7 +1076,9 @@ def main():
             "kv_pools": len(pools),
             "kv_pool_mib": round(pool_bytes / 2**20, 1),
             "num_splits": splits,
-            "timing": "hipGraph of K calls replayed once; hipEvents",
+            "timing": "ms_per_step/value: p50 over 240 back-to-back replays of a graph of one call per pool, "
+                      "hipEvents between replays; single_replay_ms_per_step: a graph of exactly K calls replayed "
+                      "once between synchronisations",
             "merge": "reducer kernel" if splits > 1 else "none",
         },
         "roofline": {
@@ -948,6 +1090,9 @@ def main():
             "traffic": traffic,
             "kernel": "decode_mfma_kernel<bf16, bs32>",
             "kernel_us_mean": round(kernel_ms * 1e3, 3),
+            "kernel_timing": "eager back-to-back calls: the library records HIP events around exactly the "
+                             "attention dispatch (hipExtLaunchKernel), which a captured graph cannot carry per "
+                             "kernel; the rocprofv3 kernel trace of the graph replays is in profiles/",
             "reducer_us_mean": round(statistics.mean(red_ms) * 1e3, 3),
             "algorithmic_bytes_per_call": nbytes,
             "traffic_source": traffic_src,
