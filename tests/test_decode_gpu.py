@@ -278,6 +278,51 @@ def test_explicit_splits_reducer_kernel_many_splits(num_splits):
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("num_splits", [5, 40])
+def test_packed_and_strided_workspaces_merge_to_the_same_bits(num_splits, head_dim):
+    """The plain merge runs one kernel on a packed [B, Hq, S, D] workspace (addressing
+    preloaded, empty rows told by their zero denominators) and another on any other
+    workspace strides (reading each row's length and slot).  With NaN in both workspaces
+    beforehand, zero-length rows and a padding slot, the two give the same bits; 40 splits
+    take the four-wave merge."""
+    dtype = torch.bfloat16
+    hq, hkv, bs = 16, 2, 32
+    lens_after = [0, 1, 37, 300, 1100, 65]
+    q, k, v, table, lens = make_paged_inputs(lens_after, hq, hkv, head_dim, bs, dtype, seed=29)
+    expected = _oracle(q, k, v, table, lens)
+    slots = _slots(table, lens.cpu(), bs)
+    slots[4] = -1  # a graph-padding row: zero output, nothing appended
+    expected[4] = 0.0
+    append_k = torch.empty((len(lens_after), hkv, head_dim), device="cuda", dtype=dtype)
+    append_v = torch.empty_like(append_k)
+    for b, s in enumerate(slots):
+        if s >= 0:
+            blk, off = divmod(s, bs)
+            append_k[b] = k[blk, :, off]
+            append_v[b] = v[blk, :, off]
+    slot_t = torch.tensor(slots, device="cuda", dtype=torch.int64)
+    nb = len(lens_after)
+
+    from flashdec_amd.paged_decode import _decode_with_workspace
+
+    def run(shape):
+        # through the C ABI: the public API keeps the reference's refusal of a fused append at head_dim 64
+        ws = (torch.full(shape, float("nan"), device="cuda"), torch.full(shape[:3], float("nan"), device="cuda"),
+              torch.full(shape[:3], float("nan"), device="cuda"))
+        out = torch.full_like(q, float("nan"))
+        _decode_with_workspace(q, k, v, table, lens, out, 1.0 / math.sqrt(head_dim), bs, num_splits, ws, k.shape[0],
+                               append=(append_k, append_v, slot_t))
+        torch.cuda.synchronize()
+        return out
+
+    packed = run((nb, hq, num_splits, head_dim))
+    strided = run((nb + 1, hq + 3, num_splits + 2, head_dim + 8))  # as0 != hq * as1: the length-reading kernel
+    assert torch.equal(packed, strided)
+    assert torch.count_nonzero(packed[0]) == 0 and torch.count_nonzero(packed[4]) == 0
+    assert_close_to_oracle(packed, expected)
+
+
 @pytest.mark.parametrize("in_launch_merge", [False, True])
 @pytest.mark.parametrize("hint", [1, 100, 700, 5000])
 def test_max_seq_len_is_only_a_hint(hint, in_launch_merge):
