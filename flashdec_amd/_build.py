@@ -3,10 +3,11 @@
 Each ``csrc/*.hip`` file is compiled separately, then linked into
 ``flashdec_amd/libflashdec_hip.so``.  The RoPE/append file is compiled with
 FMA contraction disabled: its rotation must round every product and sum
-separately to stay bit-exact against the oracle.  The decode file is compiled
-with kernel-argument preloading: a kernel's leading scalar arguments (up to 14
-SGPRs) are written into SGPRs by the command processor at wave launch, so the
-short C2 kernels issue their first loads without a kernel-argument round trip.
+separately to stay bit-exact against the oracle.  Both kernel files are
+compiled with kernel-argument preloading: a kernel's leading scalar arguments
+(up to 14 SGPRs) are written into SGPRs by the command processor at wave
+launch, so short kernels issue their first loads without a kernel-argument
+round trip.
 """
 
 from __future__ import annotations
@@ -25,7 +26,7 @@ ARCH = "gfx950"
 SOURCES = {
     "capi.hip": [],
     "paged_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
-    "rope_append.hip": ["-ffp-contract=off"],
+    "rope_append.hip": ["-ffp-contract=off", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 COMMON_FLAGS = [

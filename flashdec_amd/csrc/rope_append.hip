@@ -200,17 +200,19 @@ struct Item {
   bool to_cache; // K/V item: stored only when the slot is valid
 };
 
-template <typename T>
+// SRC_ONLY: the source rows alone (destinations null), so that the first
+// loads need no destination argument.
+template <typename T, bool SRC_ONLY = false>
 __device__ __forceinline__ Item<T> item_at(const RopeParams& p, const ItemPlan& ip, int b, int it, int64_t slot0) {
   constexpr int N = VecOps<T>::N;
   const int D = p.head_dim, half = p.rotary_dim / 2;
   const int64_t hstride = static_cast<int64_t>(p.block_size) * D;
   const T* qb = static_cast<const T*>(p.q) + static_cast<int64_t>(b) * p.hq * D;
-  T* ob = static_cast<T*>(p.q_out) + static_cast<int64_t>(b) * p.hq * D;
+  T* ob = SRC_ONLY ? nullptr : static_cast<T*>(p.q_out) + static_cast<int64_t>(b) * p.hq * D;
   const T* kb = static_cast<const T*>(p.k) + static_cast<int64_t>(b) * p.hkv * D;
   const T* vb = static_cast<const T*>(p.v) + static_cast<int64_t>(b) * p.hkv * D;
-  T* kc = static_cast<T*>(p.k_cache) + slot0;
-  T* vc = static_cast<T*>(p.v_cache) + slot0;
+  T* kc = SRC_ONLY ? nullptr : static_cast<T*>(p.k_cache) + slot0;
+  T* vc = SRC_ONLY ? nullptr : static_cast<T*>(p.v_cache) + slot0;
   Item<T> r{nullptr, nullptr, nullptr, nullptr, 0, false};
   if (it < ip.nq) {
     const int h = it / ip.hv, j = (it % ip.hv) * N;
@@ -252,41 +254,65 @@ __device__ __forceinline__ void finish_item(const Item<T>& item, const u32x4& a,
   *reinterpret_cast<u32x4*>(item.dst1) = VecOps<T>::pack(hi);
 }
 
+// The leading scalar arguments repeat what the row loads and the work plan
+// need (source and q_out rows, sizes); the library is built with
+// amdgpu-kernarg-preload-count, so the command processor writes them into
+// SGPRs at wave launch and the row loads issue without a kernel-argument
+// round trip.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void rope_append_vec_kernel(RopeParams p) {
+__global__ __launch_bounds__(kThreads) void rope_append_vec_kernel(const void* q, const void* k, const void* v,
+                                                                   void* q_out, int32_t hq, int32_t hkv,
+                                                                   int32_t head_dim, int32_t rotary_dim,
+                                                                   int32_t idx_i64, RopeParams pa) {
+  RopeParams p = pa;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.q_out = q_out;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.head_dim = head_dim;
+  p.rotary_dim = rotary_dim;
+  p.idx_i64 = idx_i64;
+  const bool has_q_out = q_out != nullptr;
   constexpr int N = VecOps<T>::N;
   __shared__ float s_cos[kMaxHalf];
   __shared__ float s_sin[kMaxHalf];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int D = p.head_dim, R = p.rotary_dim, half = R / 2;
-  const int64_t pos = load_index(p.positions, b, p.idx_i64);
-  const int64_t blk = load_index(p.block_ids, b, p.idx_i64);
-  const int64_t off = load_index(p.block_offsets, b, p.idx_i64);
-  const bool write_kv = blk >= 0 && blk < p.num_blocks && off >= 0 && off < p.block_size;
-  // out-of-range slots are never stored; row 0 keeps the addresses in bounds
-  const int64_t slot0 = write_kv ? (blk * p.hkv * p.block_size + off) * D : 0;
   ItemPlan ip;
   ip.hv = half / N;
   ip.tv = (D - R) / N;
   ip.dv = D / N;
-  ip.nq = p.q_out != nullptr ? p.hq * ip.hv : 0;
+  ip.nq = has_q_out ? p.hq * ip.hv : 0;
   ip.nk = p.hkv * ip.hv;
-  ip.nqt = p.q_out != nullptr ? p.hq * ip.tv : 0;
+  ip.nqt = has_q_out ? p.hq * ip.tv : 0;
   ip.nkt = p.hkv * ip.tv;
   ip.nv = p.hkv * ip.dv;
   ip.total = ip.nq + ip.nk + ip.nqt + ip.nkt + ip.nv;
 
+  // The source rows first: their addresses need only the preloaded
+  // arguments (the destination slot is not known yet, and not needed).
   u32x4 ra[kPrefetch], rb[kPrefetch];
 #pragma unroll
   for (int k = 0; k < kPrefetch; ++k) {
     const int it = tid + k * kThreads;
     if (it < ip.total) {
-      const Item<T> item = item_at<T>(p, ip, b, it, slot0);
+      const Item<T> item = item_at<T, true>(p, ip, b, it, 0);
       ra[k] = *reinterpret_cast<const u32x4*>(item.src0);
       if (item.src1 != nullptr) rb[k] = *reinterpret_cast<const u32x4*>(item.src1);
     }
   }
+  // then position and slot, as one batch of scalar loads with one wait
+  const int64_t pos = load_index(p.positions, b, p.idx_i64);
+  const int64_t blk = load_index(p.block_ids, b, p.idx_i64);
+  const int64_t off = load_index(p.block_offsets, b, p.idx_i64);
+  asm volatile("" ::"s"(pos), "s"(blk), "s"(off), "s"(p.num_blocks), "s"(p.block_size), "s"(p.k_cache),
+               "s"(p.v_cache));
+  const bool write_kv = blk >= 0 && blk < p.num_blocks && off >= 0 && off < p.block_size;
+  // out-of-range slots are never stored; row 0 keeps the addresses in bounds
+  const int64_t slot0 = write_kv ? (blk * p.hkv * p.block_size + off) * D : 0;
   for (int i = tid; i < half; i += kThreads) {
     rope_angle(p, pos, i, s_cos[i], s_sin[i]);
   }
@@ -383,7 +409,7 @@ int launch_rope(const fd_rope_append_args& a, const RopeParams& p, hipStream_t s
                    (a.q_out == nullptr || aligned16(a.q_out));
   if (vec)
     hipLaunchKernelGGL((rope_append_vec_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(kThreads), 0, stream,
-                       p);
+                       p.q, p.k, p.v, p.q_out, p.hq, p.hkv, p.head_dim, p.rotary_dim, p.idx_i64, p);
   else
     hipLaunchKernelGGL((rope_append_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(256), 0, stream, p);
   const hipError_t e = hipGetLastError();
