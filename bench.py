@@ -27,8 +27,9 @@ Timing:
   (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null.
 * ``cpu_baseline``: the repo's numpy oracle on this host's cores (the rows of
   a call spread over a process pool, one BLAS thread per process), on C1 and
-  on the C2 call: p50 of >= 20 calls after 3 warm-ups, with ``os.cpu_count()``
-  and the CPU model.  It runs first, before this process touches the GPU.
+  on the C2 call at ctx1024 and ctx2048: p50 of >= 20 calls after 3 warm-ups,
+  with ``os.cpu_count()`` and the CPU model.  It runs first, before this
+  process touches the GPU.
 
 ``--profile-kernels N`` instead runs N eager calls and a 64 MiB device copy
 (the counter-scaling reference) and prints one line: the form profiled by
@@ -165,7 +166,8 @@ def cpu_inputs(name):
     C1: B4 Hq8 Hkv2 D64 fp32, bs32, L ~ U{1..512} over a 128-block pool whose
     table rows are consecutive slices of a permutation, seed 61.  C2: B8 Hq16 Hkv2 D128, bs32, every
     length 2048, a 640-block pool (1.25x) with permuted tables, bf16 values (N(0,1) rounded to bf16)
-    held in fp32 as the reference upcasts them, seed 20260830 + 8 + 2048.
+    held in fp32 as the reference upcasts them, seed 20260830 + 8 + 2048.  C2-ctx1024: the same at
+    length 1024 (a 320-block pool, seed 20260830 + 8 + 1024).
     """
     import numpy as np
 
@@ -177,9 +179,10 @@ def cpu_inputs(name):
         lens = rng.integers(1, 513, size=b).astype(np.int32)
         dtype = "float32"
     else:
-        rng = np.random.default_rng(20260830 + 8 + 2048)
-        b, hq, hkv, d, bs, pool = 8, 16, 2, 128, 32, 640
-        lens = np.full(b, 2048, dtype=np.int32)
+        ctx = 1024 if name == "C2-ctx1024" else 2048
+        rng = np.random.default_rng(20260830 + 8 + ctx)
+        b, hq, hkv, d, bs, pool = 8, 16, 2, 128, 32, 640 * ctx // 2048
+        lens = np.full(b, ctx, dtype=np.int32)
         dtype = "bfloat16"
     nblk = [(int(n) + bs - 1) // bs for n in lens]
     perm = rng.permutation(pool)
@@ -197,6 +200,8 @@ def cpu_inputs(name):
 
 
 _CPU_WORKER = {}
+# CPU-baseline configs and their rows per call
+CPU_CONFIGS = {"C1": 4, "C2-ctx1024": 8, "C2": 8}
 
 
 def _cpu_worker_init():
@@ -204,7 +209,7 @@ def _cpu_worker_init():
     from threadpoolctl import threadpool_limits
 
     _CPU_WORKER["blas"] = threadpool_limits(limits=1)
-    for name in ("C1", "C2"):
+    for name in CPU_CONFIGS:
         _CPU_WORKER[name] = cpu_inputs(name)
 
 
@@ -234,7 +239,8 @@ def cpu_baseline(budget_s):
 
     Rows of a call are independent: each call hands its rows to a process
     pool of min(os.cpu_count(), 16, rows) workers (one BLAS thread each).
-    Timed on C1 and on the C2 call: p50 of >= 20 calls after 3 warm-ups.
+    Timed on C1 and on the C2 call at ctx1024 and ctx2048: p50 of >= 20
+    calls after 3 warm-ups.
     Runs before this process touches the GPU (the workers are started as
     fresh processes).
     """
@@ -242,7 +248,7 @@ def cpu_baseline(budget_s):
     from concurrent.futures import ProcessPoolExecutor
 
     n_cpu = os.cpu_count() or 1
-    rows = {"C1": 4, "C2": 8}
+    rows = CPU_CONFIGS
     workers = min(n_cpu, 16, max(rows.values()))
     results = {}
     with ProcessPoolExecutor(max_workers=workers, mp_context=mp.get_context("spawn"),
@@ -253,7 +259,7 @@ def cpu_baseline(budget_s):
             def one_call(name=name, n=n):
                 list(ex.map(_cpu_row, [name] * n, range(n)))
 
-            sec, reps = cpu_time_p50(one_call, budget_s=budget_s / 2)
+            sec, reps = cpu_time_p50(one_call, budget_s=budget_s / len(rows))
             results[name] = {"us_per_call": round(sec * 1e6, 1), "gb_per_s": round(nbytes / sec / 1e9, 4),
                              "processes": min(workers, n), "calls": reps, "algorithmic_bytes": nbytes}
     return results, n_cpu
