@@ -418,8 +418,9 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
     stream = _lib.current_stream_handle(q.device)
     splits = _lib.paged_decode_plan(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], max(groups.max_tail_len, 1),
                                     max(groups.total_tail_len, 1))
+    chunk_rows = cascade.plan_chunk_rows(groups, q.shape[1], num_kv_heads)
     psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads,
-                                         cascade.prefix_chunks(groups, q.shape[1], num_kv_heads),
+                                         cascade.prefix_chunks(groups, q.shape[1], num_kv_heads, chunk_rows),
                                          groups.max_prefix_len, cascade._num_cus(q.device))
     acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits + psplits, stream)
     args = _lib.PagedDecodeArgs()
@@ -438,6 +439,7 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
     cas.group_prefix_len = groups.prefix_len.data_ptr()
     cas.row_prefix_len = groups.row_prefix_len.data_ptr()
     cas.max_prefix_len = groups.max_prefix_len
+    cas.chunk_rows = chunk_rows
     return args, cas, stream
 
 
@@ -546,9 +548,11 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
     prepared_c = [cascade_prepared(torch, p, g, sm_scale, bs, hkv) for p, g in zip(pools, groups)]
     attn_c, red_c = cascade_kernel_us(torch, prepared_c, min(4 * len(pools), 96))
     log(f"[bench] {name} cascade: {ms_c * 1e3:.2f} us/call (graph); prefix + tail passes {attn_c:.2f} us, reducer "
-        f"{red_c:.2f} us; tail splits {prepared_c[0][0].num_splits}, prefix splits {prepared_c[0][1].prefix_splits}")
+        f"{red_c:.2f} us; tail splits {prepared_c[0][0].num_splits}, prefix splits {prepared_c[0][1].prefix_splits}, "
+        f"chunk rows {prepared_c[0][1].chunk_rows}")
     cascade_line = {"us_per_call": round(ms_c * 1e3, 3), "value": round(unique / (ms_c * 1e-3) / 1e9, 2),
                     "num_splits": prepared_c[0][0].num_splits, "prefix_splits": prepared_c[0][1].prefix_splits,
+                    "chunk_rows": prepared_c[0][1].chunk_rows,
                     "roofline": {"bound": "hbm", "achieved": round(unique / (attn_c * 1e-6) / 1e9, 2),
                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(unique / (attn_c * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
@@ -561,7 +565,7 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
         out.update({k: cascade_line[k] for k in ("us_per_call", "value", "roofline")})
         out["ms_per_step"] = round(ms_c, 6)
         out["config"].update(path="cascade", num_splits=cascade_line["num_splits"],
-                             prefix_splits=cascade_line["prefix_splits"])
+                             prefix_splits=cascade_line["prefix_splits"], chunk_rows=cascade_line["chunk_rows"])
         out["per_row_path"] = per_row
     else:
         out["config"]["path"] = "per-row"

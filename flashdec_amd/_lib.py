@@ -22,9 +22,10 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 7
+ABI_VERSION = 8
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024  # FD_NOALLOC_SCRATCH_BYTES: per-GPU scratch of fd_paged_decode_noalloc
+CASCADE_MAX_CHUNK_ROWS = 32  # FD_CASCADE_MAX_CHUNK_ROWS: the larger chunk_rows of fd_cascade_args
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -92,6 +93,7 @@ class CascadeArgs(ctypes.Structure):
         ("group_prefix_len", _vp),
         ("row_prefix_len", _vp),
         ("max_prefix_len", _i64),
+        ("chunk_rows", _i32),
     ]
 
 

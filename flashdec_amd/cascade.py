@@ -132,7 +132,7 @@ def build_cascade_groups(block_tables, seq_lens, block_size, num_q_heads, num_kv
 
 
 def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus):
-    """Prefix partials per (group, KV head, 16-row chunk).
+    """Prefix partials per (group, KV head, chunk of ``FD_CASCADE_CHUNK_ROWS`` rows).
 
     About one prefix-role workgroup per CU, and at least 16 prefix tiles per
     split.  Best of a same-box sweep on MI355X (sharers x prefix tokens:
@@ -145,9 +145,26 @@ def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus
     return int(min(want, -(-tiles // 16), 1024))
 
 
-def prefix_chunks(groups, num_q_heads, num_kv_heads):
-    """16-row chunks per group and KV head (rows = members x query heads per KV head)."""
-    return -(-groups.max_members * (num_q_heads // num_kv_heads) // 16)
+# plan_chunk_rows: group rows (sharers x query heads per KV head) x prefix
+# tokens from which a 32-row chunk pays for its doubled per-unit work.  Same-box
+# MI355X sweep, best prefix splits each, 16- vs 32-row chunks (us/call):
+# 16 x 4096 15.1 vs 16.9; 32 x 8192 22.8 vs 23.9; 64 x 16384 54.2 vs 46.2;
+# 128 x 16384 91.5 vs 68.8 (Hq16/Hkv2: 8 rows per sharer).
+_WIDE_CHUNK_MIN_WORK = 1 << 22
+
+
+def plan_chunk_rows(groups, num_q_heads, num_kv_heads):
+    """Rows per prefix-role chunk: 16, or ``FD_CASCADE_MAX_CHUNK_ROWS`` (two MFMA column blocks per wave)
+    when the group's rows x prefix tokens are large enough that the halved prefix re-reads pay for the
+    doubled work per K/V unit."""
+    rows = groups.max_members * (num_q_heads // num_kv_heads)
+    return _lib.CASCADE_MAX_CHUNK_ROWS if rows * groups.max_prefix_len >= _WIDE_CHUNK_MIN_WORK else 16
+
+
+def prefix_chunks(groups, num_q_heads, num_kv_heads, chunk_rows=16):
+    """Prefix-role chunks per group and KV head: rows (members x query heads per KV head)
+    in chunks of ``chunk_rows``, one prefix-role workgroup each."""
+    return -(-groups.max_members * (num_q_heads // num_kv_heads) // chunk_rows)
 
 
 _NUM_CUS = {}
@@ -174,6 +191,7 @@ def paged_decode_attention_cascade_into(
     prefix_splits=None,
     kv_reuse=True,
     workspace=None,
+    chunk_rows=None,
 ):
     """Write shared-prefix decode attention into ``out``.
 
@@ -190,7 +208,9 @@ def paged_decode_attention_cascade_into(
     for 16 rows x 4096 shared tokens but 55.4 vs 52.9 us for 64 x 16384).
     ``workspace`` = ``(acc, max, sum)`` fp32 ``[>= B, >= Hq, >= S + S_p, D]`` /
     ``[..., >= S + S_p]`` (equal max/sum strides) replaces the library's own,
-    e.g. for graph capture.
+    e.g. for graph capture.  ``chunk_rows`` (16 or 32; default
+    :func:`plan_chunk_rows`) is how many of a group's rows one prefix-role
+    workgroup attends.
     """
     if block_size is None:
         if k_cache.dim() != 4:
@@ -215,10 +235,14 @@ def paged_decode_attention_cascade_into(
     if num_splits is None:
         num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim,
                                             max(groups.max_tail_len, 1), max(groups.total_tail_len, 1))
+    if chunk_rows is None:
+        chunk_rows = plan_chunk_rows(groups, num_q_heads, num_kv_heads)
+    if chunk_rows not in (16, _lib.CASCADE_MAX_CHUNK_ROWS):
+        raise ValueError(f"chunk_rows must be 16 or {_lib.CASCADE_MAX_CHUNK_ROWS}")
     if prefix_splits is None:
         prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads,
-                                           prefix_chunks(groups, num_q_heads, num_kv_heads), groups.max_prefix_len,
-                                           _num_cus(q.device))
+                                           prefix_chunks(groups, num_q_heads, num_kv_heads, chunk_rows),
+                                           groups.max_prefix_len, _num_cus(q.device))
     for name, v in (("num_splits", num_splits), ("prefix_splits", prefix_splits)):
         if isinstance(v, bool) or not isinstance(v, int) or v <= 0:
             raise ValueError(f"{name} must be a positive integer")
@@ -256,6 +280,7 @@ def paged_decode_attention_cascade_into(
     cas.group_prefix_len = groups.prefix_len.data_ptr()
     cas.row_prefix_len = groups.row_prefix_len.data_ptr()
     cas.max_prefix_len = groups.max_prefix_len
+    cas.chunk_rows = chunk_rows
     _lib.paged_decode_cascade(args, cas, stream)
     return out
 

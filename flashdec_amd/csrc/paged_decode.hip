@@ -803,6 +803,11 @@ __device__ __forceinline__ void process_unit_dm(DmRegs<D>& t, const u32x4 (&qf)[
 constexpr int kMaxWaves = 8;          // waves per workgroup of the 16-token variant
 constexpr int kWideUnitMaxTiles = 4;  // splits of at most this many tiles take 32-token units
 constexpr int kAccPitch = 132;   // floats per head row in LDS (bank spread)
+// Prefix role of the cascade: up to this many 16-row MFMA column blocks per
+// wave (a launch's chunk_rows / 16).  Each block is another 16 of the group's
+// (member, head) rows attending the same K/V registers, so the group's
+// prefix is read once per chunk instead of once per 16 rows.
+constexpr int kPrefixMaxColBlocks = FD_CASCADE_MAX_CHUNK_ROWS / 16;
 constexpr int kMergeChunk = 16;  // splits whose partials one merge pass loads at once
 constexpr int64_t kMaxSplitTiles = 64;  // split planning: tiles of the longest row per split
 // One arrival counter per 256-byte line: counters sharing a line serialise
@@ -838,7 +843,7 @@ struct CascadeParams {
   const int32_t* members;     // [groups, max_members]; entry 0 is the lead
   const int32_t* prefix_len;  // [groups], tokens
   int max_members;
-  int chunks;         // 16-row chunks per group and KV head
+  int chunks;         // chunks of NCB * 16 rows per group and KV head
   int prefix_splits;  // a group's prefix tiles are spread evenly over them
   int prefix_blocks;  // workgroups of the prefix role: groups * hkv * chunks * prefix_splits
   int hint_ptps;      // guess of the prefix tiles per split (longest prefix)
@@ -927,9 +932,10 @@ struct alignas(16) DecodeLds {
 };
 
 // DM: dim-major cache (load_unit_dm), staged through the LDS at kstage.
-// PRE: the block-table arguments arrived preloaded in SGPRs (decode_mfma_kernel)
+// PRE: the block-table arguments arrived preloaded in SGPRs (decode_mfma_kernel).
+// NCB: 16-row column blocks per wave (prefix role only)
 template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT, int D = 128,
-          int WAVES = waves_for<UNIT>(), bool DM = false, bool PRE = false>
+          int WAVES = waves_for<UNIT>(), bool DM = false, bool PRE = false, int NCB = 1>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
                                             DecodeLds<WAVES>& lds, [[maybe_unused]] uint8_t* kstage = nullptr) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
@@ -938,6 +944,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
                 "head_dim 64 runs the row role without RoPE or in-launch merge");
   static_assert(!DM || (ROLE == Role::kRow && FUSE != 2 && !MERGE && UNIT == 32),
                 "dim-major caches run the row role on 32-token units");
+  static_assert(NCB == 1 || (ROLE == Role::kPrefix && NCB <= kPrefixMaxColBlocks),
+                "several column blocks per wave are for the prefix role");
   constexpr int KS = D / 32;  // 32-dim pieces of q / K rows
   constexpr int kWaves = WAVES;
   constexpr int kUnitsPerTile = 32 / UNIT;
@@ -996,17 +1004,23 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   const int trow = lead_ok ? b : 0;  // table row read for K/V
 
   // column c's output row: the request's head kvh * G + 16 * hb + c (below
-  // G), or in the prefix role the group row 16 * chunk + c (member index,
-  // head)
-  int col_b = b, col_h = 16 * hb + c;
-  bool col_ok = col_h < G;
-  if constexpr (PREFIX) {
-    const int r = 16 * chunk + c;
-    const int mi = r / G;
-    const int32_t m = mi < cp.max_members ? mem[mi] : -1;
-    col_ok = lead_ok && m >= 0 && m < p.num_seqs;
-    col_b = col_ok ? m : 0;
-    col_h = r % G;
+  // G), or in the prefix role, for column block cb, the group row
+  // 16 * (NCB * chunk + cb) + c (member index, head)
+  int col_b[NCB], col_h[NCB];
+  bool col_ok[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    col_b[cb] = b;
+    col_h[cb] = 16 * hb + c;
+    col_ok[cb] = col_h[cb] < G;
+    if constexpr (PREFIX) {
+      const int r = 16 * (NCB * chunk + cb) + c;
+      const int mi = r / G;
+      const int32_t m = mi < cp.max_members ? mem[mi] : -1;
+      col_ok[cb] = lead_ok && m >= 0 && m < p.num_seqs;
+      col_b[cb] = col_ok[cb] ? m : 0;
+      col_h[cb] = r % G;
+    }
   }
 
   // Independent loads first.  The first unit is guessed from the host bound
@@ -1029,13 +1043,15 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
                  "s"(p.vs0), "s"(p.vs1), "s"(p.vs2), "s"(p.sl), "s"(p.sls), "s"(p.sl_i64), "s"(p.num_blocks),
                  "s"(p.block_size));
   }
-  u32x4 qf[KS];
-  {
-    const T* qrow = static_cast<const T*>(p.q) + col_b * p.qs0 + (kvh * G + (col_ok ? col_h : 0)) * p.qs1;
+  u32x4 qf[NCB][KS];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const T* qrow =
+        static_cast<const T*>(p.q) + col_b[cb] * p.qs0 + (kvh * G + (col_ok[cb] ? col_h[cb] : 0)) * p.qs1;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * g);
-      qf[s] = col_ok ? x : u32x4{0u, 0u, 0u, 0u};
+      qf[cb][s] = col_ok[cb] ? x : u32x4{0u, 0u, 0u, 0u};
     }
   }
   AppendRegs<D> ar;
@@ -1086,7 +1102,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   };
   load(unit, pages, cur);
   // the float64 cos/sin evaluation overlaps the K/V loads just issued
-  if constexpr (ROPE && D == 128) rope_operands<T>(p, seq_len, lane, g, qf, ar);
+  if constexpr (ROPE && D == 128) rope_operands<T>(p, seq_len, lane, g, qf[0], ar);
 
   // token indices fit in 32 bits: eff_len <= seq_lens[b], an int32
   const int last = static_cast<int>(eff_len) - 1;
@@ -1108,11 +1124,14 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     }
   }
 
-  WaveState<D> st;
+  WaveState<D> st[NCB];
 #pragma unroll
-  for (int n = 0; n < D / 16; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
+  for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) st[cb].acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[cb].m = -INFINITY;
+    st[cb].l = 0.f;
+  }
 
   if (unit < u_end) {
     UnitPages next_pages{0, 0};
@@ -1136,10 +1155,14 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
             store_append<T, BS, D>(p, kvh, slot, c, g, ar);
         }
       if constexpr (DM)
-        process_unit_dm<T, (FUSE != 0), D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, dar, lane,
-                                           kstage + wave * D * kDmRowBytes, st);
-      else
-        process_unit<T, (FUSE != 0), UNIT, D>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g, st);
+        process_unit_dm<T, (FUSE != 0), D>(now, qf[0], p.scale_log2, unit * UNIT, first, last, app, dar, lane,
+                                           kstage + wave * D * kDmRowBytes, st[0]);
+      else {
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+          process_unit<T, (FUSE != 0), UNIT, D>(now, qf[cb], p.scale_log2, unit * UNIT, first, last, app, ar, c, g,
+                                                st[cb]);
+      }
       unit = next;
       next_pages = after;
       return more;
@@ -1153,105 +1176,112 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       while (step(cur, alt)) cur = alt;
     }
   }
-  // denominator over the four lanes (g) that share query column c
-  const float lt = column_sum(st.l);
-
-  // Every wave publishes its state (one LDS slot each; eight slots take 68 KB,
-  // which gfx950's LDS holds in one workgroup), then threads merge across the
-  // slots.
-  if (g == 0) {
-    lds.m[wave][c] = st.m;
-    lds.l[wave][c] = lt;
-    if (PREFIX && wave == 0) {
-      lds.col_b[c] = col_ok ? col_b : -1;
-      lds.col_h[c] = col_h;
-    }
-  }
-  if constexpr (DM) {
-    // this lane's dims 16*n + 4*g + rr (load_unit_dm's V rows)
-#pragma unroll
-    for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f32x4*>(&lds.acc[wave][c][16 * n + 4 * g]) = st.acc[n];
-  } else {
-    // this lane's dims (D/4)*g + (D/16)*rr + n, n < D/16: one or two 16-byte rows
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      float* dst = &lds.acc[wave][c][(D / 4) * g + (D / 16) * rr];
-      *reinterpret_cast<f32x4*>(dst) = f32x4{st.acc[0][rr], st.acc[1][rr], st.acc[2][rr], st.acc[3][rr]};
-      if constexpr (D == 128)
-        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{st.acc[4][rr], st.acc[5][rr], st.acc[6][rr], st.acc[7][rr]};
-    }
-  }
-  __syncthreads();
-
-  // merge the slots: thread -> (column h, dims [d0, d0 + 8)), D/8 threads
-  // per column; threads past the first 2D only take part in the barrier of
-  // the in-launch merge
+  // merge threads: thread -> (column h, dims [d0, d0 + 8)), D/8 threads per
+  // column; threads past the first 2D only take part in the barriers
   constexpr int kDimThreads = D / 8;
   const int h = (threadIdx.x / kDimThreads) & 15;
   const int d0 = (threadIdx.x % kDimThreads) * 8;
   int ob = b, qh = kvh * G + 16 * hb + h;
   bool head_ok = threadIdx.x < 16 * kDimThreads && 16 * hb + h < G;
-  if constexpr (PREFIX) {
-    ob = lds.col_b[h];
-    qh = kvh * G + lds.col_h[h];
-    head_ok = threadIdx.x < 16 * kDimThreads && ob >= 0;
-  }
-  float M = -INFINITY;
+  // one round per column block: the waves' slots hold one block at a time
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds.m[w][h]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float wt = exp2f(lds.m[w][h] - Mu);
-    L += wt * lds.l[w][h];
-    const f32x4 a0 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0]);
-    const f32x4 a1 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[j] += wt * a0[j];
-      o[4 + j] += wt * a1[j];
+  for (int cb = 0; cb < NCB; ++cb) {
+    if (cb > 0) __syncthreads();  // every thread has read the previous block's slots
+    // denominator over the four lanes (g) that share query column c
+    const float lt = column_sum(st[cb].l);
+
+    // Every wave publishes its state (one LDS slot each; eight slots take 68 KB,
+    // which gfx950's LDS holds in one workgroup), then threads merge across the
+    // slots.
+    if (g == 0) {
+      lds.m[wave][c] = st[cb].m;
+      lds.l[wave][c] = lt;
+      if (PREFIX && wave == 0) {
+        lds.col_b[c] = col_ok[cb] ? col_b[cb] : -1;
+        lds.col_h[c] = col_h[cb];
+      }
     }
-  }
-  if (ROLE == Role::kRow && p.splits == 1) {
-    if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
-    return;
-  }
-  // split partial: unnormalised acc, base-2 max, denominator; the prefix
-  // role's partials follow the tail splits
-  if (head_ok) {
-    const int ws = PREFIX ? p.splits + split : split;
-    float* a = p.acc + ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3;
-    const int64_t so = ob * p.ss0 + qh * p.ss1 + ws * p.ss2;
-    if constexpr (MERGE) {
-      // device-coherent (sc1) stores, visible to every XCD once acknowledged;
-      // the host guarantees unit dim stride and 8-byte alignment here
-      uint64_t* a64 = reinterpret_cast<uint64_t*>(a);
+    if constexpr (DM) {
+      // this lane's dims 16*n + 4*g + rr (load_unit_dm's V rows)
+#pragma unroll
+      for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f32x4*>(&lds.acc[wave][c][16 * n + 4 * g]) = st[cb].acc[n];
+    } else {
+      // this lane's dims (D/4)*g + (D/16)*rr + n, n < D/16: one or two 16-byte rows
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float* dst = &lds.acc[wave][c][(D / 4) * g + (D / 16) * rr];
+        const WaveState<D>& w = st[cb];
+        *reinterpret_cast<f32x4*>(dst) = f32x4{w.acc[0][rr], w.acc[1][rr], w.acc[2][rr], w.acc[3][rr]};
+        if constexpr (D == 128)
+          *reinterpret_cast<f32x4*>(dst + 4) = f32x4{w.acc[4][rr], w.acc[5][rr], w.acc[6][rr], w.acc[7][rr]};
+      }
+    }
+    __syncthreads();
+
+    // merge the slots
+    if constexpr (PREFIX) {
+      ob = lds.col_b[h];
+      qh = kvh * G + lds.col_h[h];
+      head_ok = threadIdx.x < 16 * kDimThreads && ob >= 0;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds.m[w][h]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = exp2f(lds.m[w][h] - Mu);
+      L += wt * lds.l[w][h];
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0]);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint64_t bits = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, o[2 * j])) |
-                              (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, o[2 * j + 1])) << 32);
-        __hip_atomic_store(a64 + j, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (d0 == 0) {
-        __hip_atomic_store(p.mx + so, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.sm + so, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    } else {
-      if (p.as3 == 1) {
-        *reinterpret_cast<f32x4*>(a) = f32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<f32x4*>(a + 4) = f32x4{o[4], o[5], o[6], o[7]};
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j * p.as3] = o[j];
-      }
-      if (d0 == 0) {
-        p.mx[so] = M;
-        p.sm[so] = L;
+        o[j] += wt * a0[j];
+        o[4 + j] += wt * a1[j];
       }
     }
-  }
+    if (ROLE == Role::kRow && p.splits == 1) {
+      if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
+      return;
+    }
+    // split partial: unnormalised acc, base-2 max, denominator; the prefix
+    // role's partials follow the tail splits
+    if (head_ok) {
+      const int ws = PREFIX ? p.splits + split : split;
+      float* a = p.acc + ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3;
+      const int64_t so = ob * p.ss0 + qh * p.ss1 + ws * p.ss2;
+      if constexpr (MERGE) {
+        // device-coherent (sc1) stores, visible to every XCD once acknowledged;
+        // the host guarantees unit dim stride and 8-byte alignment here
+        uint64_t* a64 = reinterpret_cast<uint64_t*>(a);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint64_t bits = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, o[2 * j])) |
+                                (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, o[2 * j + 1])) << 32);
+          __hip_atomic_store(a64 + j, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (d0 == 0) {
+          __hip_atomic_store(p.mx + so, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(p.sm + so, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        if (p.as3 == 1) {
+          *reinterpret_cast<f32x4*>(a) = f32x4{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<f32x4*>(a + 4) = f32x4{o[4], o[5], o[6], o[7]};
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) a[j * p.as3] = o[j];
+        }
+        if (d0 == 0) {
+          p.mx[so] = M;
+          p.sm[so] = L;
+        }
+      }
+    }
+  }  // column blocks
+
   if constexpr (!MERGE) return;  // the reducer kernel merges
 
   // In-launch merge.  Partials were written with agent-scope atomic stores
@@ -1378,12 +1408,14 @@ __global__ __launch_bounds__(64 * kBalWaves, kBalPerCU) void decode_balanced_ker
 
 // Cascade launch: workgroups [0, prefix_blocks) take the prefix role, the
 // rest the tail role (both write split partials; the reducer merges them).
-template <typename T, int BS, int UNIT, bool NT>
+// NCB: the prefix role's 16-row column blocks per wave.
+template <typename T, int BS, int UNIT, bool NT, int NCB = 1>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void cascade_decode_kernel(DecodeParams p,
                                                                                     CascadeParams cp) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
   if (static_cast<int>(blockIdx.x) < cp.prefix_blocks)
-    decode_role<T, BS, false, false, UNIT, Role::kPrefix, NT>(p, cp, blockIdx.x, lds);
+    decode_role<T, BS, false, false, UNIT, Role::kPrefix, NT, 128, waves_for<UNIT>(), false, false, NCB>(
+        p, cp, blockIdx.x, lds);
   else
     decode_role<T, BS, false, false, UNIT, Role::kTail, NT>(p, cp, blockIdx.x - cp.prefix_blocks, lds);
 }
@@ -2023,9 +2055,15 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
 // Cascade: one launch of prefix- and tail-role workgroups, then the reducer
 // over tail + prefix partials.  The attention timing events bracket it.
 template <typename T, int BS, bool NT>
-void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, int64_t pairs, hipStream_t stream,
-                           void* const* ev) {
+void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, int col_blocks, int64_t pairs,
+                           hipStream_t stream, void* const* ev) {
   const dim3 grid(static_cast<unsigned>(cp.prefix_blocks + pairs * p.splits));
+  if (col_blocks == 2) {
+    // long prefixes shared by many rows: 16-token units, two column blocks
+    dispatch(cascade_decode_kernel<T, BS, 16, NT, 2>, grid, dim3(64 * waves_for<16>()), stream, ev[0], ev[1], p,
+             cp);
+    return;
+  }
   if constexpr (BS >= 16) {
     if (p.hint_tps <= kWideUnitMaxTiles && cp.hint_ptps <= kWideUnitMaxTiles) {
       dispatch(cascade_decode_kernel<T, BS, 32, NT>, grid, dim3(64 * waves_for<32>()), stream, ev[0], ev[1], p,
@@ -2038,22 +2076,24 @@ void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, int64
 
 // NT applies to the tail role; the prefix role always uses plain loads
 template <typename T, int BS>
-void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, bool nt, int64_t pairs,
+void launch_cascade_kernel(const DecodeParams& p, const CascadeParams& cp, int col_blocks, bool nt, int64_t pairs,
                            hipStream_t stream, void* const* ev) {
   if (nt)
-    launch_cascade_kernel<T, BS, true>(p, cp, pairs, stream, ev);
+    launch_cascade_kernel<T, BS, true>(p, cp, col_blocks, pairs, stream, ev);
   else
-    launch_cascade_kernel<T, BS, false>(p, cp, pairs, stream, ev);
+    launch_cascade_kernel<T, BS, false>(p, cp, col_blocks, pairs, stream, ev);
 }
 
 template <typename T>
-int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const CascadeParams& cp,
+int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const CascadeParams& cp, int col_blocks,
                    hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
+  const bool nt = a.kv_reuse == 0;
+  void* const* ev = a.timing_events;
   switch (a.block_size) {
-    case 8: launch_cascade_kernel<T, 8>(p, cp, a.kv_reuse == 0, pairs, stream, a.timing_events); break;
-    case 16: launch_cascade_kernel<T, 16>(p, cp, a.kv_reuse == 0, pairs, stream, a.timing_events); break;
-    default: launch_cascade_kernel<T, 32>(p, cp, a.kv_reuse == 0, pairs, stream, a.timing_events); break;
+    case 8: launch_cascade_kernel<T, 8>(p, cp, col_blocks, nt, pairs, stream, ev); break;
+    case 16: launch_cascade_kernel<T, 16>(p, cp, col_blocks, nt, pairs, stream, ev); break;
+    default: launch_cascade_kernel<T, 32>(p, cp, col_blocks, nt, pairs, stream, ev); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "cascade decode launch failed: %s", hipGetErrorString(e));
@@ -2402,7 +2442,10 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
   if (!c.row_prefix_len || (c.num_groups > 0 && (!c.group_members || !c.group_prefix_len)))
     return set_error(FD_E_INVALID, "%s: NULL group pointer", fn);
   if (c.max_prefix_len < 0) return set_error(FD_E_INVALID, "%s: max_prefix_len must be >= 0", fn);
-  const int64_t chunks = (static_cast<int64_t>(c.max_members) * p.group + 15) / 16;
+  if (c.chunk_rows != 0 && c.chunk_rows != 16 && c.chunk_rows != FD_CASCADE_MAX_CHUNK_ROWS)
+    return set_error(FD_E_INVALID, "%s: chunk_rows must be 0, 16 or %d", fn, FD_CASCADE_MAX_CHUNK_ROWS);
+  const int chunk_rows = c.chunk_rows == 0 ? 16 : c.chunk_rows;
+  const int64_t chunks = (static_cast<int64_t>(c.max_members) * p.group + chunk_rows - 1) / chunk_rows;
   const int64_t prefix_blocks = static_cast<int64_t>(c.num_groups) * a.num_kv_heads * chunks * c.prefix_splits;
   if (prefix_blocks + a.num_seqs * a.num_kv_heads * a.num_splits > 0x7fffffffLL)
     return set_error(FD_E_INVALID, "%s: launch grid too large", fn);
@@ -2427,6 +2470,6 @@ extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const f
   cp.prefix_blocks = static_cast<int>(prefix_blocks);
   cp.hint_ptps = static_cast<int>(((pre + 31) / 32 + c.prefix_splits - 1) / c.prefix_splits);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (a.dtype == FD_DTYPE_BF16) return launch_cascade<__bf16>(a, p, cp, stream);
-  return launch_cascade<_Float16>(a, p, cp, stream);
+  if (a.dtype == FD_DTYPE_BF16) return launch_cascade<__bf16>(a, p, cp, chunk_rows / 16, stream);
+  return launch_cascade<_Float16>(a, p, cp, chunk_rows / 16, stream);
 }

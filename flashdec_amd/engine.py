@@ -611,10 +611,11 @@ class DecodeEngine:
         balance = 0
         gc = None
         prefix_splits = 0
+        chunk_rows = 16
         if cascade:
             from ._lib import paged_decode_plan
             from .cache import _StagingRing
-            from .cascade import CascadeGroups, _num_cus, plan_prefix_splits, prefix_chunks
+            from .cascade import CascadeGroups, _num_cus, plan_chunk_rows, plan_prefix_splits, prefix_chunks
 
             ng = len(groups_now)
             mm = max(len(rows) for rows, _ in groups_now)
@@ -634,8 +635,9 @@ class DecodeEngine:
             if num_splits is None:
                 num_splits = paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
                                                groups.max_tail_len, groups.total_tail_len)
-            prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads, prefix_chunks(groups, num_q_heads,
-                                                                                     cache.num_kv_heads),
+            chunk_rows = plan_chunk_rows(groups, num_q_heads, cache.num_kv_heads)
+            prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads,
+                                               prefix_chunks(groups, num_q_heads, cache.num_kv_heads, chunk_rows),
                                                groups.max_prefix_len, _num_cus(dev))
         if cascade:
             splits = int(num_splits)
@@ -699,7 +701,8 @@ class DecodeEngine:
                                                             meta.block_tables, meta.eff_lens, out[layer],
                                                             gc.groups, sm_scale=self.sm_scale,
                                                             block_size=cache.block_size, num_splits=splits,
-                                                            prefix_splits=prefix_splits, workspace=workspace)
+                                                            prefix_splits=prefix_splits, workspace=workspace,
+                                                            chunk_rows=chunk_rows)
                         continue
                     if fuse_rope:
                         _decode_with_workspace(q[layer], cache.k_cache[layer], cache.v_cache[layer],

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 7
+#define FD_ABI_VERSION 8
 
 /* status codes */
 #define FD_OK 0
@@ -239,7 +239,8 @@ int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream
  * block ids are read from its table row.  row_prefix_len[b] is that length
  * for each member row and 0 for rows in no group; a row belongs to at most
  * one group.  One launch holds prefix-role workgroups -- one per (group, KV
- * head, 16 of the group's member x query-head rows, prefix split), writing
+ * head, chunk of chunk_rows of the group's member x query-head rows, prefix
+ * split), writing
  * prefix_splits partials per (row, head) at workspace splits
  * [num_splits, num_splits + prefix_splits) -- and tail-role workgroups
  * attending tokens [row_prefix_len[b], seq_lens[b]) of each row at splits
@@ -252,6 +253,14 @@ int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream
  * is a hint (the longest group prefix) for where each split starts.  The
  * timing events [0]/[1] bracket the attention launch, [2]/[3] the reducer.
  */
+/* chunk_rows: member x query-head rows of a group that one prefix-role
+ * workgroup attends (16 per MFMA column block of its waves), 16 or
+ * FD_CASCADE_MAX_CHUNK_ROWS; 0 means 16.  The prefix is read once per
+ * chunk; a chunk of 32 rows doubles each wave's work per K/V unit, which pays
+ * for long prefixes shared by many rows.  There are ceil(max_members * G /
+ * chunk_rows) chunks per (group, KV head). */
+#define FD_CASCADE_MAX_CHUNK_ROWS 32
+
 typedef struct fd_cascade_args {
   uint32_t struct_size; /* sizeof(fd_cascade_args): ABI guard */
   int32_t num_groups;
@@ -261,6 +270,7 @@ typedef struct fd_cascade_args {
   const int32_t* group_prefix_len; /* [num_groups], tokens */
   const int32_t* row_prefix_len;   /* [num_seqs], tokens */
   int64_t max_prefix_len;
+  int32_t chunk_rows;              /* 0, 16 or FD_CASCADE_MAX_CHUNK_ROWS (see above) */
 } fd_cascade_args;
 
 int fd_paged_decode_cascade(const fd_paged_decode_args* args, const fd_cascade_args* cascade,

@@ -66,8 +66,25 @@ def test_group_size_bound():
     g = cascade.build_cascade_groups(bt, sl, 16, num_q_heads=16, num_kv_heads=2, max_members=16)
     assert g.num_groups == 3 and g.max_members == 14  # 40 rows: 14 + 13 + 13
     assert sorted(len([x for x in m if x >= 0]) for m in g.members.tolist()) == [13, 13, 14]
-    # 16-row chunks: 40 members x 8 query heads per KV head = 320 rows
-    assert cascade.prefix_chunks(cascade.build_cascade_groups(bt, sl, 16, 16, 2), 16, 2) == 20
+    # 40 members x 8 query heads per KV head = 320 rows: 20 chunks of 16 rows, 10 of 32
+    g = cascade.build_cascade_groups(bt, sl, 16, 16, 2)
+    assert cascade.prefix_chunks(g, 16, 2) == 20
+    assert cascade.prefix_chunks(g, 16, 2, chunk_rows=32) == 10
+
+
+def test_chunk_rows_plan():
+    # 32-row chunks once group rows x prefix tokens reach 2^22 (64 sharers x 8 heads x 16384 tokens)
+    def groups(members, prefix):
+        return cascade.CascadeGroups(members=torch.zeros((1, members), dtype=torch.int32),
+                                     prefix_len=torch.zeros(1, dtype=torch.int32),
+                                     row_prefix_len=torch.zeros(members, dtype=torch.int32), max_prefix_len=prefix,
+                                     max_tail_len=1, total_tail_len=1)
+
+    assert cascade.plan_chunk_rows(groups(16, 4096), 16, 2) == 16
+    assert cascade.plan_chunk_rows(groups(32, 8192), 16, 2) == 16
+    assert cascade.plan_chunk_rows(groups(64, 16384), 16, 2) == 32
+    assert cascade.plan_chunk_rows(groups(128, 16384), 16, 2) == 32
+    assert cascade.plan_chunk_rows(groups(64, 8192), 16, 2) == 32  # exactly 2^22
 
 
 def test_prefix_split_plan():
