@@ -286,7 +286,8 @@ def paged_decode_attention_cascade_into(
 
 
 def paged_decode_attention_cascade(q, k_cache, v_cache, block_tables, seq_lens, groups=None, sm_scale=None,
-                                   block_size=None, num_splits=None, prefix_splits=None, kv_reuse=True):
+                                   block_size=None, num_splits=None, prefix_splits=None, kv_reuse=True,
+                                   chunk_rows=None):
     """Allocating form of :func:`paged_decode_attention_cascade_into`; builds
     the groups from the tables when ``groups`` is None."""
     if block_size is None:
@@ -299,4 +300,5 @@ def paged_decode_attention_cascade(q, k_cache, v_cache, block_tables, seq_lens, 
     out = torch.empty_like(q)
     return paged_decode_attention_cascade_into(q, k_cache, v_cache, block_tables, seq_lens, out, groups,
                                                sm_scale=sm_scale, block_size=block_size, num_splits=num_splits,
-                                               prefix_splits=prefix_splits, kv_reuse=kv_reuse)
+                                               prefix_splits=prefix_splits, kv_reuse=kv_reuse,
+                                               chunk_rows=chunk_rows)

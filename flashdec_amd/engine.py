@@ -143,6 +143,7 @@ class _GraphCascade:
     num_groups: int
     max_members: int
     staging: Any
+    chunk_rows: int = 16  # group rows per prefix-role workgroup, fixed at capture
 
 
 @dataclass
@@ -635,7 +636,7 @@ class DecodeEngine:
             if num_splits is None:
                 num_splits = paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
                                                groups.max_tail_len, groups.total_tail_len)
-            chunk_rows = plan_chunk_rows(groups, num_q_heads, cache.num_kv_heads)
+            chunk_rows = gc.chunk_rows = plan_chunk_rows(groups, num_q_heads, cache.num_kv_heads)
             prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads,
                                                prefix_chunks(groups, num_q_heads, cache.num_kv_heads, chunk_rows),
                                                groups.max_prefix_len, _num_cus(dev))

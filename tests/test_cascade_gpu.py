@@ -8,8 +8,9 @@ group sizes 1/8/16, fp16 and bf16, prefixes that end inside a 32-token tile,
 rows whose tail is empty, zero-length rows, rows in no group, groups of 32
 and 40 members (16 and 20 sixteen-row chunks per KV head), more prefix
 splits than prefix tiles, explicit tail split counts, groups whose prefix is
-shorter than what the tables share, and padded member lists.  Tolerance:
-atol 2e-2 / rtol 1e-2.
+shorter than what the tables share, and padded member lists -- with 16-row
+and 32-row prefix chunks (one or two MFMA column blocks per wave).
+Tolerance: atol 2e-2 / rtol 1e-2.
 """
 
 import numpy as np
@@ -85,10 +86,11 @@ def _groups_as_sets(groups):
     return sorted((tuple(int(x) for x in m if x >= 0), int(p)) for m, p in zip(members, plen))
 
 
+@pytest.mark.parametrize("chunk_rows", [16, 32])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("block_size", [8, 16, 32])
 @pytest.mark.parametrize(("hq", "hkv"), [(16, 2), (8, 8), (32, 2)])
-def test_shared_prefix_matches_oracle(hq, hkv, block_size, dtype):
+def test_shared_prefix_matches_oracle(hq, hkv, block_size, dtype, chunk_rows):
     # prefixes of 13 and 3 blocks (ends inside a 32-token tile for bs 8/16),
     # tails including empty ones, rows in no group, one zero-length row
     groups = [(13, [5, 0, 77, 1, 40]), (3, [9, block_size])]
@@ -96,7 +98,8 @@ def test_shared_prefix_matches_oracle(hq, hkv, block_size, dtype):
     cas = _cascade()
     g = cas.build_cascade_groups(table, lens, block_size, hq, hkv)
     assert _groups_as_sets(g) == sorted((tuple(r), p * block_size) for r, p in expected)
-    out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g, block_size=block_size)
+    out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g, block_size=block_size,
+                                             chunk_rows=chunk_rows)
     expected_out = _oracle(q, k, v, table, lens)
     assert_close_to_oracle(out, expected_out)
     assert torch.count_nonzero(out[7]) == 0  # the zero-length row
@@ -114,27 +117,29 @@ def test_group_of_32_members(dtype):
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
 
 
-def test_large_group_spans_many_chunks():
-    # 40 members x 8 query heads per KV head = 320 rows: 20 chunks of 16
+@pytest.mark.parametrize("chunk_rows", [16, 32])
+def test_large_group_spans_many_chunks(chunk_rows):
+    # 40 members x 8 query heads per KV head = 320 rows: 20 chunks of 16, or 10 of 32
     rng = np.random.default_rng(8)
     tails = [int(x) for x in rng.integers(0, 70, size=40)]
     q, k, v, table, lens, _ = make_prefix_inputs([(9, tails)], [33], 16, 2, 16, torch.bfloat16, seed=13)
     cas = _cascade()
     g = cas.build_cascade_groups(table, lens, 16, 16, 2)
     assert g.num_groups == 1 and g.max_members == 40
-    out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g)
+    out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g, chunk_rows=chunk_rows)
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
 
 
+@pytest.mark.parametrize("chunk_rows", [16, 32])
 @pytest.mark.parametrize(("num_splits", "prefix_splits"), [(1, 1), (3, 2), (2, 40), (8, 7)])
-def test_explicit_split_counts(num_splits, prefix_splits):
+def test_explicit_split_counts(num_splits, prefix_splits, chunk_rows):
     # prefix of 20 blocks of 16 = 10 tiles: 40 prefix splits leave 30 empty
     q, k, v, table, lens, _ = make_prefix_inputs([(20, [33, 200, 7, 64])], [90, 1], 16, 2, 16, torch.bfloat16,
                                                  seed=11)
     cas = _cascade()
     g = cas.build_cascade_groups(table, lens, 16, 16, 2)
     out = cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g, num_splits=num_splits,
-                                             prefix_splits=prefix_splits)
+                                             prefix_splits=prefix_splits, chunk_rows=chunk_rows)
     assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
 
 
@@ -161,9 +166,11 @@ def test_hand_built_groups_shorter_prefix_and_padding():
         max_tail_len=int(lens.max()),
         total_tail_len=int(lens.sum()),
     )
-    out = torch.empty_like(q)
-    cas.paged_decode_attention_cascade_into(q, k, v, table, lens, out, groups, prefix_splits=3)
-    assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+    for chunk_rows in (16, 32):
+        out = torch.empty_like(q)
+        cas.paged_decode_attention_cascade_into(q, k, v, table, lens, out, groups, prefix_splits=3,
+                                                chunk_rows=chunk_rows)
+        assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
 
 
 def test_two_calls_reuse_the_workspace():

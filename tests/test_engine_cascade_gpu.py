@@ -77,15 +77,22 @@ def test_prefix_group_decodes_with_the_cascade():
     assert cascaded.validate_invariants() and per_row.validate_invariants()
 
 
-def test_cascade_step_graph_matches_per_row_graph():
+@pytest.mark.parametrize("wide_chunks", [False, True])
+def test_cascade_step_graph_matches_per_row_graph(wide_chunks, monkeypatch):
     """Step graphs with the shared-prefix launch: every replay reads the step's groups, also after the
-    group's membership changes; outputs match a per-row graph and the oracle, cache bytes are equal."""
+    group's membership changes; outputs match a per-row graph and the oracle, cache bytes are equal.
+    wide_chunks: the plan's threshold for 32-row prefix chunks lowered to 0, so the graph captures them."""
+    from flashdec_amd import cascade
+
+    if wide_chunks:
+        monkeypatch.setattr(cascade, "_WIDE_CHUNK_MIN_WORK", 0)
     cascaded, per_row = make_engine(1), make_engine(None)
     for e in (cascaded, per_row):
         e.cache.enable_graph_metadata(5, 16)
     sg_c = cascaded.capture_step_graph(5, HQ, base=1e6)
     sg_p = per_row.capture_step_graph(5, HQ, base=1e6)
     assert sg_c.cascade is not None and sg_c.cascade.num_groups == 1 and sg_c.cascade.max_members == 4
+    assert sg_c.cascade.chunk_rows == (32 if wide_chunks else 16)
     assert sg_p.cascade is None and sg_p.kv_reuse
     g = torch.Generator(device="cuda").manual_seed(8)
     for step in range(6):
