@@ -683,8 +683,9 @@ __device__ __forceinline__ void load_append_dm(const DecodeParams& p, int b, int
   const uint16_t* av = static_cast<const uint16_t*>(p.av) + b * p.avs0 + kvh * p.avs1;
 #pragma unroll
   for (int j = 0; j < D / 32; ++j) {
-    ar.k[j] = ak[(32 * j + (lane >> 2)) * p.aks2] | (static_cast<uint32_t>(ak[(32 * j + 16 + (lane >> 2)) * p.aks2]) << 16);
-    ar.v[j] = av[(32 * j + (lane & 15)) * p.avs2] | (static_cast<uint32_t>(av[(32 * j + 16 + (lane & 15)) * p.avs2]) << 16);
+    const int kd = 32 * j + (lane >> 2), vd = 32 * j + (lane & 15);
+    ar.k[j] = ak[kd * p.aks2] | (static_cast<uint32_t>(ak[(kd + 16) * p.aks2]) << 16);
+    ar.v[j] = av[vd * p.avs2] | (static_cast<uint32_t>(av[(vd + 16) * p.avs2]) << 16);
   }
 }
 
@@ -1836,8 +1837,11 @@ void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, 
 }
 
 // decode_mfma_kernel's arguments: the preloaded block-table fields, then the parameter block
-#define FD_MFMA_ARGS(p) \
-  (p).bt, (p).bts0, (p).bts1, (p).max_blocks_per_seq, (p).splits, (p).hkv, (p).group, (p).hint_tps, (p).bt_i64, (p)
+template <typename K>
+void dispatch_mfma(K kernel, dim3 grid, dim3 block, hipStream_t stream, void* const* ev, const DecodeParams& p) {
+  dispatch(kernel, grid, block, stream, ev[0], ev[1], p.bt, p.bts0, p.bts1, p.max_blocks_per_seq, p.splits, p.hkv,
+           p.group, p.hint_tps, p.bt_i64, p);
+}
 
 template <typename T, int BS, int UNIT, bool NT>
 void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
@@ -1846,24 +1850,24 @@ void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void
   if (p.head_dim == 64) {
     // head_dim 64: the host gives it no RoPE and no in-launch merge
     if (p.fuse)
-      dispatch(decode_mfma_kernel<T, BS, 1, false, UNIT, NT, 64>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, UNIT, NT, 64>, grid, block, stream, ev, p);
     else
-      dispatch(decode_mfma_kernel<T, BS, 0, false, UNIT, NT, 64>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, UNIT, NT, 64>, grid, block, stream, ev, p);
     return;
   }
   if (p.fuse && p.rope_dim > 0) {
     // the host refuses RoPE with the in-launch merge
-    dispatch(decode_mfma_kernel<T, BS, 2, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+    dispatch_mfma(decode_mfma_kernel<T, BS, 2, false, UNIT, NT>, grid, block, stream, ev, p);
   } else if (p.fuse) {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, 1, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, true, UNIT, NT>, grid, block, stream, ev, p);
     else
-      dispatch(decode_mfma_kernel<T, BS, 1, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, UNIT, NT>, grid, block, stream, ev, p);
   } else {
     if (merge)
-      dispatch(decode_mfma_kernel<T, BS, 0, true, UNIT, NT>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, true, UNIT, NT>, grid, block, stream, ev, p);
     else
-      dispatch(decode_mfma_kernel<T, BS, 0, false, UNIT, NT>, grid, block, stream, ev[0], ev[1], FD_MFMA_ARGS(p));
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, UNIT, NT>, grid, block, stream, ev, p);
   }
 }
 
@@ -1948,18 +1952,20 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
   void* e0 = a.timing_events[2];
   void* e1 = a.timing_events[3];
   if (MODE == kReducePlain && reduce_layout_packed(r)) {
-#define FD_REDUCE_PRE_ARGS r.acc, r.mx, r.sm, r.as1, r.as2, r.ss1, r.splits, r.hq, r
+    // the partials' addressing leads the argument list (preloaded into SGPRs)
+    auto pre = [&](auto kernel, dim3 block) {
+      dispatch(kernel, grid, block, stream, e0, e1, r.acc, r.mx, r.sm, r.as1, r.as2, r.ss1, r.splits, r.hq, r);
+    };
     if (r.splits > 32) {
       if (a.head_dim == 64)
-        dispatch(split_reduce_pre_kernel<T, 64, 4>, grid, dim3(256), stream, e0, e1, FD_REDUCE_PRE_ARGS);
+        pre(split_reduce_pre_kernel<T, 64, 4>, dim3(256));
       else
-        dispatch(split_reduce_pre_kernel<T, 128, 4>, grid, dim3(256), stream, e0, e1, FD_REDUCE_PRE_ARGS);
+        pre(split_reduce_pre_kernel<T, 128, 4>, dim3(256));
     } else if (a.head_dim == 64) {
-      dispatch(split_reduce_pre_kernel<T, 64>, grid, dim3(64), stream, e0, e1, FD_REDUCE_PRE_ARGS);
+      pre(split_reduce_pre_kernel<T, 64>, dim3(64));
     } else {
-      dispatch(split_reduce_pre_kernel<T, 128>, grid, dim3(64), stream, e0, e1, FD_REDUCE_PRE_ARGS);
+      pre(split_reduce_pre_kernel<T, 128>, dim3(64));
     }
-#undef FD_REDUCE_PRE_ARGS
   } else if (r.splits > 32) {
     // more than 32 splits: four waves per row share them
     if (a.head_dim == 64)
