@@ -128,12 +128,22 @@ def _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rota
     """One ``fd_fused_rope_kv_append`` launch; the three index tensors share a dtype."""
     if q_out is None:
         q_out = torch.empty_like(q)
-    idx_dtype = block_ids.dtype
-    if block_offsets.dtype != idx_dtype or positions.dtype != idx_dtype:
+    if block_offsets.dtype != block_ids.dtype or positions.dtype != block_ids.dtype:
+        # held here until the launch is enqueued
         block_ids = block_ids.to(torch.int64)
         block_offsets = block_offsets.to(torch.int64)
         positions = positions.to(torch.int64)
-        idx_dtype = torch.int64
+    args = _launch_args(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base, q_out,
+                        cos_sin_table)
+    _lib.rope_append(args, _lib.current_stream_handle(q.device), rotate=True)
+    return q_out
+
+
+def _launch_args(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim, base, q_out,
+                 cos_sin_table):
+    """The filled ``RopeAppendArgs`` of :func:`_launch` (checked inputs; the three index tensors
+    share a dtype)."""
+    idx_dtype = block_ids.dtype
     args = _lib.RopeAppendArgs()
     args.dtype = _lib.dtype_code(q.dtype)
     args.batch = q.shape[0]
@@ -157,8 +167,7 @@ def _launch(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rota
     if cos_sin_table is not None:
         args.cos_sin_table = cos_sin_table.data_ptr()
         args.table_rows = cos_sin_table.shape[1]
-    _lib.rope_append(args, _lib.current_stream_handle(q.device), rotate=True)
-    return q_out
+    return args
 
 
 def fused_rope_kv_append(q, k, v, k_cache, v_cache, block_ids, block_offsets, positions, rotary_dim=None,

@@ -46,7 +46,12 @@ import numpy as np
 
 @dataclass(frozen=True)
 class KVTokenTransactionView:
-    """Detached public snapshot of one multi-layer token transaction."""
+    """Detached public snapshot of one multi-layer token transaction.
+
+    Its tensors are a device copy of the transaction's metadata, apart from
+    the allocator's own; the views of one transaction share that copy (the
+    metadata does not change while the transaction is open).
+    """
 
     transaction_id: int
     cache_version: int
@@ -308,7 +313,8 @@ class _PrefixBook:
 class _Txn:
     """The open token transaction."""
 
-    __slots__ = ("tid", "version", "rids", "positions", "slots", "grown", "meta", "layers", "phase")
+    __slots__ = ("tid", "version", "rids", "positions", "slots", "grown", "meta", "layers", "phase", "view_meta",
+                 "launch")
     tid: int
     version: int  # the state version its opening published
     rids: tuple
@@ -318,6 +324,8 @@ class _Txn:
     meta: object  # _DeviceMeta
     layers: int  # layers written so far (always 0 .. layers-1, in order)
     phase: str
+    view_meta: object  # the callers' copy of meta, made by the first view (meta never changes); None before
+    launch: object  # prepared fused RoPE + append arguments: ((rotary_dim, base, table), RopeAppendArgs) or None
 
 
 @dataclass(frozen=True)
@@ -823,7 +831,7 @@ class PagedKVCache:
             self._tally.failures += 1
             raise
         self._publish()
-        txn = _Txn(tid, self._version, ids, positions, slots, tuple(grown), meta, 0, "open")
+        txn = _Txn(tid, self._version, ids, positions, slots, tuple(grown), meta, 0, "open", None, None)
         self._journal.open = txn
         self._journal.next_id += 1
         self._tally.begins += 1
@@ -867,13 +875,15 @@ class PagedKVCache:
                 raise RuntimeError(problem)
 
     def _layer_rows(self, txn, layer_idx, k, v):
-        """One transaction layer write's contract: returns (layer, k, v)."""
+        """One transaction layer write's contract: returns (layer, k, v).  The
+        transaction's request ids were checked when it opened."""
         layer_idx = self._validate_layer_idx(layer_idx)
         if layer_idx != txn.layers:
             raise RuntimeError(f"transaction requires layer {txn.layers}, got layer {layer_idx}")
-        _, ids, k, v = self._kv_rows(layer_idx, txn.rids, k, v, "request_ids must be unique within one append call")
-        if tuple(ids) != txn.rids:
-            raise RuntimeError("transaction request order changed unexpectedly")
+        if len(txn.rids) == 1:
+            k = k.unsqueeze(0) if k.dim() == 2 else k
+            v = v.unsqueeze(0) if v.dim() == 2 else v
+        _check_kv_rows(self, len(txn.rids), k, v)
         return layer_idx, k, v
 
     def _layer_written(self, txn):
@@ -928,6 +938,52 @@ class PagedKVCache:
         return q_rot, self._layer_written(txn)
 
     write_token_layer_fused_hip = write_token_layer_fused_cuda
+
+    def _write_layer_fused_prepared(self, transaction, layer_idx, q, k, v, rotary_dim, base, cos_sin_table):
+        """``write_token_layer_fused_cuda`` for ``DecodeEngine.step_layer``, whose step-input rules
+        have checked q, k and v (types, [batch, heads, head_dim] shapes, device, dtype).
+
+        The transaction's first layer (or a change of RoPE setting) goes the
+        checked way and leaves the filled launch arguments in the
+        transaction; its later layers check the layer order and contiguity
+        and change only the q, out, k, v and per-layer cache pointers.
+        """
+        torch = _torch()
+        from . import _lib
+
+        txn = self._journal.find_open(transaction)
+        key = (rotary_dim, base, 0 if cos_sin_table is None else cos_sin_table.data_ptr())
+        if (txn.launch is None or txn.launch[0] != key or not q.is_contiguous() or not k.is_contiguous()
+                or not v.is_contiguous()):
+            extra = {} if cos_sin_table is None else {"cos_sin_table": cos_sin_table}
+            q_rot, view = self.write_token_layer_fused_cuda(transaction, layer_idx, q, k, v, rotary_dim=rotary_dim,
+                                                            base=base, **extra)
+            if q_rot.is_contiguous() and q.is_contiguous() and k.is_contiguous() and v.is_contiguous():
+                from ._fused_rope_kv_append import _launch_args
+
+                layer = txn.layers - 1
+                rdim = q.shape[-1] if rotary_dim is None else rotary_dim
+                txn.launch = (key, _launch_args(q, k, v, self.k_cache[layer], self.v_cache[layer], txn.meta.block_ids,
+                                                txn.meta.offsets, txn.meta.positions, rdim, float(base), q_rot,
+                                                cos_sin_table))
+            return q_rot, view
+        try:
+            layer_idx = self._validate_layer_idx(layer_idx)
+            if layer_idx != txn.layers:
+                raise RuntimeError(f"transaction requires layer {txn.layers}, got layer {layer_idx}")
+            q_out = torch.empty_like(q)
+            args = txn.launch[1]
+            args.q_out = q_out.data_ptr()
+            args.q = q.data_ptr()
+            args.k = k.data_ptr()
+            args.v = v.data_ptr()
+            args.k_cache = self.k_cache.data_ptr() + layer_idx * self.k_cache.stride(0) * self.k_cache.element_size()
+            args.v_cache = self.v_cache.data_ptr() + layer_idx * self.v_cache.stride(0) * self.v_cache.element_size()
+            _lib.rope_append(args, _lib.current_stream_handle(q.device), rotate=True)
+        except Exception:
+            self._tally.failures += 1
+            raise
+        return q_out, self._layer_written(txn)
 
     def _record_graph_layers(self, transaction):
         """Record every layer as written by a replayed step graph (see DecodeEngine.step_graph)."""
@@ -986,7 +1042,12 @@ class PagedKVCache:
         return self._journal.find_open(transaction).meta
 
     def _snapshot(self, txn):
-        meta = txn.meta.clone()
+        # one device copy per transaction serves every view of it: the
+        # metadata is fixed when the transaction opens, and the copy keeps
+        # callers away from the allocator's own
+        if txn.view_meta is None:
+            txn.view_meta = txn.meta.clone()
+        meta = txn.view_meta
         return KVTokenTransactionView(
             transaction_id=txn.tid, cache_version=txn.version, request_ids=txn.rids, positions=meta.positions,
             physical_block_ids=meta.block_ids, block_offsets=meta.offsets, block_tables=meta.block_tables,

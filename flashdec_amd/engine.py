@@ -26,6 +26,7 @@ performs no host synchronisation.
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 from typing import Any, Hashable
 
@@ -157,6 +158,7 @@ class _OpenStep:
     ragged: bool = False  # the batch's lengths vary widely: per-row split counts
     cascade: Any = None  # CascadeGroups: rows sharing a resident prefix decode it once per group
     kv_reuse: bool = False  # rows share prefix blocks (per-row path): plain, cached K/V loads
+    decode_launch: Any = None  # eager HIP decode: ((stream, q shape, q strides), PagedDecodeArgs) of this step
 
 
 class _Roster:
@@ -233,6 +235,14 @@ def _step_input_rules(engine, ids, q, k, v):
         (lambda: any(t.device != cache.device for t in (q, k, v)), ValueError, "q, k, and v must be on the cache device"),
         (lambda: any(t.dtype != cache.dtype for t in (q, k, v)), ValueError, "q, k, and v must use the cache dtype"),
     )
+
+
+_NO_RANGE = contextlib.nullcontext()  # reusable: a phase without a profiler range
+
+
+def _own_method(obj, name):
+    """``obj.name`` is its class's own method, not one replaced on the instance."""
+    return getattr(getattr(obj, name, None), "__func__", None) is getattr(type(obj), name, None)
 
 
 def _is_ragged(lengths):
@@ -500,9 +510,7 @@ class DecodeEngine:
 
     def _phase(self, name):
         """A profiler range around one phase when ``profile_ranges`` is on."""
-        import contextlib
-
-        return self._range(name) if self._range is not None else contextlib.nullcontext()
+        return self._range(name) if self._range is not None else _NO_RANGE
 
     def commit_step(self, transaction):
         """Commit the open token after every layer has run."""
@@ -859,6 +867,12 @@ class DecodeEngine:
         tx = state.cache_transaction
         if self._append == "fused_hip":
             meta = self.cache.transaction_device_metadata(tx)
+            prepared = getattr(self.cache, "_write_layer_fused_prepared", None)
+            if prepared is not None and self.cache.device.type == "cuda" and _own_method(
+                    self.cache, "write_token_layer_fused_cuda"):
+                # this package's cache, its fused write not replaced: the step's launch arguments are reused
+                q_rot, view = prepared(tx, layer_idx, q, k, v, rotary_dim, base, cos_sin_table)
+                return q_rot, view, meta
             # the table keyword goes only where it is used: the call keeps the
             # reference's signature otherwise
             extra = {} if cos_sin_table is None else {"cos_sin_table": cos_sin_table}
@@ -877,11 +891,48 @@ class DecodeEngine:
         ragged = self._open is not None and self._open.ragged
         cascade = self._open.cascade if self._open is not None else None
         kv_reuse = self._open is not None and self._open.kv_reuse
+        if meta is not None and cascade is None and self._decode_kind == "hip":
+            return self._decode_prepared(self._open, q_rot, meta, layer_idx, ragged, kv_reuse)
         if meta is not None:  # the allocator's own copy, not the caller-visible clone
             return self._decode(q_rot, meta.block_tables, meta.eff_lens, layer_idx, ragged=ragged, cascade=cascade,
                                 kv_reuse=kv_reuse)
         return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx, ragged=ragged,
                             cascade=cascade, kv_reuse=kv_reuse)
+
+    def _decode_prepared(self, state, q, meta, layer_idx, ragged, kv_reuse):
+        """Eager HIP decode of one layer of the open step (the allocator's metadata).
+
+        The step's first layer goes through ``paged_decode_attention``'s
+        validation, split plan and workspace; the later layers of the step
+        share them and change only the q, out and per-layer cache pointers
+        (every layer's tables, lengths and shapes are the step's), which takes
+        the host cost of a layer's decode from ~36 to a few us on MI355X.
+        """
+        from . import _lib
+        from .paged_decode import _decode_args
+
+        layer_idx = int(layer_idx)
+        if layer_idx < 0 or layer_idx >= self.cache.num_layers:
+            raise ValueError("layer_idx must be in [0, num_layers)")
+        torch = _torch()
+        cache = self.cache
+        out = torch.empty_like(q)
+        stream = _lib.current_stream_handle(q.device)
+        key = (stream, tuple(q.shape), q.stride())
+        if state.decode_launch is None or state.decode_launch[0] != key:
+            args, _ = _decode_args(q, cache.k_cache[layer_idx], cache.v_cache[layer_idx], meta.block_tables,
+                                   meta.eff_lens, out, self.sm_scale, cache.block_size, self.num_warps,
+                                   "token_major", self.num_stages, None, 1, None, None, None, ragged, kv_reuse)
+            state.decode_launch = (key, args)
+        else:
+            args = state.decode_launch[1]
+            args.q = q.data_ptr()
+            args.out = out.data_ptr()
+            layer_bytes = cache.k_cache.stride(0) * cache.k_cache.element_size()
+            args.k_cache = cache.k_cache.data_ptr() + layer_idx * layer_bytes
+            args.v_cache = cache.v_cache.data_ptr() + layer_idx * layer_bytes
+        _lib.paged_decode(args, stream)
+        return out
 
     def _decode(self, q, block_tables, seq_lens, layer_idx=0, ragged=False, cascade=None, kv_reuse=False):
         layer_idx = int(layer_idx)

@@ -298,6 +298,17 @@ def paged_decode_attention_into(
     assumed to be read once per call and is streamed with non-temporal loads.
     The result is the same either way.
     """
+    args, stream = _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_warps,
+                                kv_layout, num_stages, split_kv_workspace, num_splits, append_k, append_v,
+                                slot_mapping, ragged, kv_reuse)
+    _lib.paged_decode(args, stream)
+    return out
+
+
+def _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_warps, kv_layout,
+                 num_stages, split_kv_workspace, num_splits, append_k, append_v, slot_mapping, ragged, kv_reuse):
+    """Validation, split plan and workspace of :func:`paged_decode_attention_into`: returns the
+    filled ``PagedDecodeArgs`` and the stream handle, without launching."""
     token_axis, dim_axis = _layout_axes(kv_layout)
     if block_size is None:
         if k_cache.dim() != 4:
@@ -411,8 +422,7 @@ def paged_decode_attention_into(
     _fill_workspace(args, split_acc, split_max, split_sum, num_splits, counters)
     if fuse_kv_append:
         _fill_append(args, append_k, append_v, slot_mapping)
-    _lib.paged_decode(args, stream)
-    return out
+    return args, stream
 
 
 def _decode_with_workspace(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_splits,
