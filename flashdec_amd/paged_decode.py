@@ -422,6 +422,9 @@ def _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, blo
     _fill_workspace(args, split_acc, split_max, split_sum, num_splits, counters)
     if fuse_kv_append:
         _fill_append(args, append_k, append_v, slot_mapping)
+    # the workspace stays alive as long as the arguments that point into it
+    # (a later, larger call may replace the stream's own workspace)
+    args.workspace = (split_acc, split_max, split_sum)
     return args, stream
 
 
