@@ -77,6 +77,17 @@ __device__ __forceinline__ int32_t load_index(const void* base, int64_t elem, in
   return *reinterpret_cast<const int32_t*>(ptr);
 }
 
+// The same read for a wave-uniform index, through the scalar data cache
+// (s_load, waited on with lgkmcnt): a vector load here would be followed by
+// a vmcnt wait before its readfirstlane, and vmcnt retires in order, so that
+// wait would also cover every K/V load issued before it.  Only for data no
+// kernel of this launch writes (block tables).
+__device__ __forceinline__ int32_t load_index_uniform(const void* base, int64_t elem, int is64) {
+  using ConstI32 = const __attribute__((address_space(4))) int32_t;
+  const char* ptr = static_cast<const char*>(base) + (elem << (is64 ? 3 : 2));
+  return *(ConstI32*)(ptr);
+}
+
 // ----------------------------------------------------------- wave utils --
 __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
   return __shfl_xor(v, mask, 64);

@@ -213,15 +213,16 @@ __device__ __forceinline__ V kv_load(const void* a) {
     return *reinterpret_cast<const V*>(a);
 }
 
-// Physical block ids a unit needs (wave-uniform, so scalar loads); pages are
-// clamped to the table row so the read is in bounds whatever the row's
-// length.  A unit spans one block, or UNIT / BS consecutive ones (at most
-// four: the dim-major kernel's 32-token units on 8-token blocks).
+// Physical block ids a unit needs (wave-uniform; SCALAR: read through the
+// scalar cache); pages are clamped to the table row so the read is in bounds
+// whatever the row's length.  A unit spans one block, or UNIT / BS
+// consecutive ones (at most four: the dim-major kernel's 32-token units on
+// 8-token blocks).
 struct UnitPages {
   int32_t a, b, c, d;
 };
 
-template <int BS, int UNIT>
+template <int BS, int UNIT, bool SCALAR = false>
 __device__ __forceinline__ UnitPages fetch_pages(const DecodeParams& p, int b, int unit) {
   static_assert(BS >= UNIT / 4, "a unit spans at most four blocks");
   constexpr int kPages = BS < UNIT ? UNIT / BS : 1;
@@ -231,7 +232,8 @@ __device__ __forceinline__ UnitPages fetch_pages(const DecodeParams& p, int b, i
   const int64_t first = (static_cast<int64_t>(unit) * UNIT) / BS;
   auto entry = [&](int i) -> int32_t {
     const int64_t pg = first + i < width ? first + i : width - 1;
-    return load_index(p.bt, row + pg * p.bts1, p.bt_i64);
+    const int64_t at = row + pg * p.bts1;
+    return SCALAR ? load_index_uniform(p.bt, at, p.bt_i64) : load_index(p.bt, at, p.bt_i64);
   };
   up.a = entry(0);
   if constexpr (kPages >= 2) up.b = entry(1);
@@ -555,19 +557,58 @@ __device__ __forceinline__ float column_sum(float x) { return pair_rows32_sum(pa
 // only drops probabilities that small relative to the running maximum.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// One unit: mask (row length, invalid blocks), splice in the appended token,
-// QK^T, online softmax, PV.  `last` is the last attended token, `first` the
-// first (0: from the row's start), `app` the token taken from the append
-// registers (-1: none).  The probabilities enter the PV product rounded to
-// the cache dtype, as the reference's grouped kernels do
-// (flashdec/kernels/paged_decode.py:308-310); the denominator sums them in
-// fp32.  Masking is skipped for units whose tokens are all live and the
-// rescale of the accumulator when no lane's maximum moved (wave-uniform
-// tests).
-template <typename T, bool FUSE, int UNIT, int D>
-__device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (&qf)[D / 32], float scale_log2,
-                                             int tok0, int first, int last, int app, const AppendRegs<D>& ar, int c,
-                                             int g, WaveState<D>& st) {
+// Online-softmax step over one unit's scores of a lane (base-2 domain): the
+// probabilities pr, and st updated for them.  The reference's kernels move
+// the running maximum to every new block maximum and rescale acc and l each
+// time (flashdec/kernels/paged_decode.py:293-312).  Here the maximum st.m
+// moves only when a column's maximum exceeds it by more than kRescaleSlack:
+// the probabilities, taken against st.m, stay below 2^kRescaleSlack (no
+// overflow in fp32, the same relative rounding in the cache dtype), and the
+// accumulator's multiply runs only on such moves instead of on most units.
+// acc and l are always taken against the same st.m, so the partial they
+// stand for is the same up to rounding.
+constexpr float kRescaleSlack = 8.f;
+
+template <int VR, int D>
+__device__ __forceinline__ void softmax_step(const float (&sc)[VR], float (&pr)[VR], WaveState<D>& st) {
+  float mx = sc[0];
+#pragma unroll
+  for (int i = 1; i < VR; ++i) mx = fmaxf(mx, sc[i]);
+  mx = column_max(mx);
+  // st.m == -inf: -inf + slack is -inf, so the first live unit moves it
+  const bool move = mx > st.m + kRescaleSlack;
+  const float m_ref = move ? mx : st.m;
+  const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < VR; ++i) {
+    pr[i] = exp2_fast(sc[i] - m_use);
+    psum += pr[i];
+  }
+  // while st.m is -inf, acc and l are zero: nothing to rescale
+  if (__ballot(move && st.m != -INFINITY)) {
+    const float alpha = exp2_fast(st.m - m_use);  // 1 where st.m stays
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) st.acc[n] *= alpha;
+    st.l *= alpha;
+  }
+  st.l += psum;
+  st.m = m_ref;
+}
+
+// One unit for NCB 16-column blocks of query rows: mask (row length, invalid
+// blocks), splice in the appended token, QK^T, online softmax, PV.  The
+// blocks share the unit's K/V registers, its mask and its V^T operands.
+// `last` is the last attended token, `first` the first (0: from the row's
+// start), `app` the token taken from the append registers (-1: none).  The
+// probabilities enter the PV product rounded to the cache dtype, as the
+// reference's grouped kernels do (flashdec/kernels/paged_decode.py:308-310);
+// the denominator sums them in fp32.  Masking is skipped for units whose
+// tokens are all live (wave-uniform test).
+template <typename T, bool FUSE, int UNIT, int D, int NCB>
+__device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (&qf)[NCB][D / 32],
+                                             float scale_log2, int tok0, int first, int last, int app,
+                                             const AppendRegs<D>& ar, int c, int g, WaveState<D> (&st)[NCB]) {
   constexpr int MT = UnitRegs<UNIT, D>::MT;
   constexpr int VR = UnitRegs<UNIT, D>::VR;
   constexpr int KS = UnitRegs<UNIT, D>::KS;
@@ -596,71 +637,65 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (
     }
   }
   // S^T[token][head] = K . Q^T  (MT 16-token row blocks)
-  float sc[VR];
+  float sc[NCB][VR];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    f32x4 sb = {0.f, 0.f, 0.f, 0.f};
+  for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-    for (int s = 0; s < KS; ++s) sb = mfma16x16x32<T>(t.kf[mt][s], qf[s], sb);
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[4 * mt + r] = sb[r] * scale_log2;
-  }
+      for (int s = 0; s < KS; ++s) sb = mfma16x16x32<T>(t.kf[mt][s], qf[cb][s], sb);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[cb][4 * mt + r] = sb[r] * scale_log2;
+    }
   // masked tokens: -inf scores and zero V rows (their memory may hold
   // NaN/Inf, and 0 * NaN is NaN)
   if (__ballot(vmask != kAll)) {
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
       const bool keep = (vmask >> i) & 1u;
-      sc[i] = keep ? sc[i] : -INFINITY;
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) sc[cb][i] = keep ? sc[cb][i] : -INFINITY;
 #pragma unroll
       for (int k = 0; k < NW; ++k) t.vf[i][k] = keep ? t.vf[i][k] : 0u;
     }
   }
-  float mx = sc[0];
+  // P^T operands (k = VR*g + i: this lane's tokens)
+  uint32_t ph[NCB][VR / 2];
 #pragma unroll
-  for (int i = 1; i < VR; ++i) mx = fmaxf(mx, sc[i]);
-  mx = column_max(mx);
-  const float m_new = fmaxf(st.m, mx);
-  const float m_use = m_new == -INFINITY ? 0.f : m_new;
-  const float alpha = exp2_fast(st.m - m_use);
-  float pr[VR];
-  float psum = 0.f;
+  for (int cb = 0; cb < NCB; ++cb) {
+    float pr[VR];
+    softmax_step<VR, D>(sc[cb], pr, st[cb]);
 #pragma unroll
-  for (int i = 0; i < VR; ++i) {
-    pr[i] = exp2_fast(sc[i] - m_use);
-    psum += pr[i];
+    for (int j = 0; j < VR / 2; ++j) ph[cb][j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
   }
-  st.l = st.l * alpha + psum;
-  st.m = m_new;
-  if (__ballot(alpha != 1.f)) {
-#pragma unroll
-    for (int n = 0; n < NTILE; ++n) st.acc[n] *= alpha;
-  }
-  // P^T operand (k = VR*g + i: this lane's tokens)
-  uint32_t ph[VR / 2];
-#pragma unroll
-  for (int j = 0; j < VR / 2; ++j) ph[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
   // V^T operands: vt_n holds dim (D/16)*c + n of the lane's tokens
 #pragma unroll
   for (int n = 0; n < NTILE; ++n) {
     const int w = n >> 1;
     const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
     if constexpr (UNIT == 32) {
-      u32x4 vt, pp;
+      u32x4 vt;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vt[j] = __builtin_amdgcn_perm(t.vf[2 * j + 1][w], t.vf[2 * j][w], sel);
-        pp[j] = ph[j];
+      for (int j = 0; j < 4; ++j) vt[j] = __builtin_amdgcn_perm(t.vf[2 * j + 1][w], t.vf[2 * j][w], sel);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        u32x4 pp;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pp[j] = ph[cb][j];
+        st[cb].acc[n] = mfma16x16x32<T>(vt, pp, st[cb].acc[n]);
       }
-      st.acc[n] = mfma16x16x32<T>(vt, pp, st.acc[n]);
     } else {
-      u32x2 vt, pp;
+      u32x2 vt;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        vt[j] = __builtin_amdgcn_perm(t.vf[2 * j + 1][w], t.vf[2 * j][w], sel);
-        pp[j] = ph[j];
+      for (int j = 0; j < 2; ++j) vt[j] = __builtin_amdgcn_perm(t.vf[2 * j + 1][w], t.vf[2 * j][w], sel);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        u32x2 pp;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) pp[j] = ph[cb][j];
+        st[cb].acc[n] = mfma16x16x16<T>(vt, pp, st[cb].acc[n]);
       }
-      st.acc[n] = mfma16x16x16<T>(vt, pp, st.acc[n]);
     }
   }
 }
@@ -774,26 +809,8 @@ __device__ __forceinline__ void process_unit_dm(DmRegs<D>& t, const u32x4 (&qf)[
 #pragma unroll
       for (int w = 0; w < 4; ++w) t.vf[n][w] &= keep[w];
   }
-  float mx = sc[0];
-#pragma unroll
-  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[i]);
-  mx = column_max(mx);
-  const float m_new = fmaxf(st.m, mx);
-  const float m_use = m_new == -INFINITY ? 0.f : m_new;
-  const float alpha = exp2_fast(st.m - m_use);
   float pr[8];
-  float psum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    pr[i] = exp2_fast(sc[i] - m_use);
-    psum += pr[i];
-  }
-  st.l = st.l * alpha + psum;
-  st.m = m_new;
-  if (__ballot(alpha != 1.f)) {
-#pragma unroll
-    for (int n = 0; n < NTILE; ++n) st.acc[n] *= alpha;
-  }
+  softmax_step<8, D>(sc, pr, st);
   u32x4 pp;
 #pragma unroll
   for (int j = 0; j < 4; ++j) pp[j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
@@ -954,6 +971,17 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   constexpr bool TAIL = ROLE == Role::kTail;
   constexpr bool BAL = ROLE == Role::kBalanced;
   constexpr bool ROPE = FUSE == 2;  // fused append with RoPE of q and the appended K
+  // Block ids come through the scalar cache (s_load, lgkmcnt) except in the
+  // kernels that stream K/V with non-temporal loads.  A vector read of the
+  // id needs a vmcnt wait before its readfirstlane, and vmcnt retires in
+  // order, so that wait also covers the next unit's K/V loads issued just
+  // before it: each unit then waits out the next one's loads.  Kernels whose
+  // K/V reads hit the caches gain from keeping them in flight (64 rows on a
+  // 16384-token shared prefix: 41.9 -> 39.5 us per call; dim-major D128
+  // 28.0 -> 27.0 us); the streaming kernels, already at the HBM rate,
+  // measured slower with more loads in flight (36-layer B64 ctx8192 step
+  // 3.14 -> 3.21 ms) and keep the vector read.
+  constexpr bool kScalarPages = !(NT && ROLE != Role::kPrefix) || DM;
   if constexpr (ROLE == Role::kRow && UNIT == 32 && !PRE) {
     // Short splits (about one unit per wave) spend most of their time before
     // the first K/V loads.  Every argument those loads need goes into SGPRs
@@ -1035,7 +1063,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     split_tiles(nsplit, split, bal_eff, 0, guess_begin, t1);
   }
   int unit = kUnitsPerTile * guess_begin + wave;
-  UnitPages pages = fetch_pages<BS, UNIT>(p, trow, unit);  // clamped, always in bounds
+  UnitPages pages = fetch_pages<BS, UNIT, kScalarPages>(p, trow, unit);  // clamped, always in bounds
   if constexpr (ROLE == Role::kRow && UNIT == 32 && PRE) {
     // The table load above needed only preloaded arguments.  The K/V and q
     // addressing arguments come in one batch of kernel-argument loads, in
@@ -1120,7 +1148,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   if (t_begin != guess_begin) {
     unit = kUnitsPerTile * t_begin + wave;
     if (unit < u_end) {
-      pages = fetch_pages<BS, UNIT>(p, trow, unit);
+      pages = fetch_pages<BS, UNIT, kScalarPages>(p, trow, unit);
       load(unit, pages, cur);
     }
   }
@@ -1136,7 +1164,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 
   if (unit < u_end) {
     UnitPages next_pages{0, 0};
-    if (unit + kWaves < u_end) next_pages = fetch_pages<BS, UNIT>(p, trow, unit + kWaves);
+    if (unit + kWaves < u_end) next_pages = fetch_pages<BS, UNIT, kScalarPages>(p, trow, unit + kWaves);
     // One unit: issue the next unit's loads into `ahead` (and the block ids
     // after it), then consume `now`; false when `now` was the last.  The two
     // buffers take turns, so no registers are copied between units.
@@ -1146,7 +1174,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       UnitPages after{0, 0};
       if (more) {
         load(next, next_pages, ahead);
-        if (next + kWaves < u_end) after = fetch_pages<BS, UNIT>(p, trow, next + kWaves);
+        if (next + kWaves < u_end) after = fetch_pages<BS, UNIT, kScalarPages>(p, trow, next + kWaves);
       }
       if constexpr (FUSE)
         if (app >= 0 && app / UNIT == unit && hb == 0) {
@@ -1159,10 +1187,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         process_unit_dm<T, (FUSE != 0), D>(now, qf[0], p.scale_log2, unit * UNIT, first, last, app, dar, lane,
                                            kstage + wave * D * kDmRowBytes, st[0]);
       else {
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
-          process_unit<T, (FUSE != 0), UNIT, D>(now, qf[cb], p.scale_log2, unit * UNIT, first, last, app, ar, c, g,
-                                                st[cb]);
+        process_unit<T, (FUSE != 0), UNIT, D, NCB>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g,
+                                                   st);
       }
       unit = next;
       next_pages = after;
