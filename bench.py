@@ -74,12 +74,13 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "engine",
-                                          "engine-prefix", "formats", "vllm"),
+    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "prefix-sweep",
+                                          "engine", "engine-prefix", "formats", "vllm"),
                    default="decode",
                    help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
                         "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
-                        "sharing a 16384-token prefix; engine: C5 36-layer step; engine-prefix: 36-layer steps "
+                        "sharing a 16384-token prefix; prefix-sweep: cascade chunk rows x prefix splits at four "
+                        "shared-prefix sizes; engine: C5 36-layer step; engine-prefix: 36-layer steps "
                         "of 64 rows sharing a 16384-token prefix; formats: head_dim 64, large groups, MHA, "
                         "dim-major caches and 8-token blocks; vllm: the vLLM hook's launch at B8 ctx1024/2048, "
                         "block size 16, fused append")
@@ -597,6 +598,41 @@ def run_prefix_large(torch, dev, args):
     return run_decode_variant(torch, dev, args, "shared-prefix-64x16384+U512", lens, 3, 7, prefix_blocks=512)
 
 
+def run_prefix_sweep(torch, dev, args):
+    """Shared-prefix cascade over chunk rows x prefix splits at four sizes (sharers x prefix tokens, tails
+    ~ U{1..512}, seed 1701): the sweep behind the library's chunk-rows and prefix-split plans."""
+    import numpy as np
+
+    from flashdec_amd import cascade
+
+    hq, hkv, d, bs = 16, 2, 128, 32
+    sm = 1.0 / math.sqrt(d)
+    shapes = [(16, 4096, 40, (4, 8, 16, 32)), (32, 8192, 10, (4, 8, 16, 32)), (64, 16384, 3, (2, 4, 8, 16)),
+              (128, 16384, 2, (1, 2, 4, 8))]
+    results = []
+    for n, prefix, npools, sweep in shapes:
+        tails = np.random.default_rng(1701).integers(1, 513, size=n)
+        lens = [prefix + int(t) for t in tails]
+        pools = decode_pools(torch, dev, lens, hq, hkv, d, bs, npools, 1701, prefix // bs)
+        groups = [cascade.build_cascade_groups(p[3], p[4], bs, hq, hkv) for p in pools]
+        plan_rows = cascade.plan_chunk_rows(groups[0], hq, hkv)
+        for rows in (16, 32):
+            times = {}
+            for sp in sweep:
+                def fn(i, sp=sp, rows=rows):
+                    q, k, v, t, sl, o = pools[i % len(pools)]
+                    cascade.paged_decode_attention_cascade_into(q, k, v, t, sl, o, groups[i % len(pools)],
+                                                                sm_scale=sm, prefix_splits=sp, chunk_rows=rows)
+                times[sp] = round(graph_ms_per_call(torch, dev, fn, 200 if n <= 32 else 40) * 1e3, 2)
+            log(f"[bench] prefix-sweep {n}x{prefix} rows {rows}: "
+                + ", ".join(f"{sp}: {t:.2f}" for sp, t in times.items()) + f" us/call (plan: rows {plan_rows})")
+            results.append({"sharers": n, "prefix": prefix, "chunk_rows": rows, "us_per_call": times,
+                            "planned_chunk_rows": plan_rows})
+        del pools, groups
+        torch.cuda.empty_cache()
+    return {"workload": "prefix-sweep", "unit": "us/call by prefix splits", "results": results}
+
+
 def run_formats(torch, dev, args):
     """General-path formats (beyond the C2 shape): head_dim 64, more than 16 query heads per KV
     head, MHA, dim-major caches and 8-token blocks, each B16 x 8192 tokens, bf16, block size 32
@@ -939,7 +975,7 @@ def main():
     _lib.load_library()
     if args.workload != "decode":
         run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
-               "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
+               "prefix-sweep": run_prefix_sweep, "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
                "vllm": run_vllm}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
         return

@@ -826,6 +826,10 @@ constexpr int kAccPitch = 132;   // floats per head row in LDS (bank spread)
 // (member, head) rows attending the same K/V registers, so the group's
 // prefix is read once per chunk instead of once per 16 rows.
 constexpr int kPrefixMaxColBlocks = FD_CASCADE_MAX_CHUNK_ROWS / 16;
+// Row role: groups of more than 16 query heads per KV head run this many
+// 16-column blocks per wave (32 heads per workgroup on one read of the K/V,
+// instead of one workgroup per 16 heads each reading it).
+constexpr int kRowWideColBlocks = 2;
 constexpr int kMergeChunk = 16;  // splits whose partials one merge pass loads at once
 constexpr int64_t kMaxSplitTiles = 64;  // split planning: tiles of the longest row per split
 // One arrival counter per 256-byte line: counters sharing a line serialise
@@ -962,8 +966,9 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
                 "head_dim 64 runs the row role without RoPE or in-launch merge");
   static_assert(!DM || (ROLE == Role::kRow && FUSE != 2 && !MERGE && UNIT == 32),
                 "dim-major caches run the row role on 32-token units");
-  static_assert(NCB == 1 || (ROLE == Role::kPrefix && NCB <= kPrefixMaxColBlocks),
-                "several column blocks per wave are for the prefix role");
+  static_assert(NCB == 1 || (ROLE == Role::kPrefix && NCB <= kPrefixMaxColBlocks) ||
+                    (ROLE == Role::kRow && NCB == kRowWideColBlocks && FUSE != 2 && !MERGE && !DM),
+                "several column blocks per wave: the prefix role, and the row role's wide groups");
   constexpr int KS = D / 32;  // 32-dim pieces of q / K rows
   constexpr int kWaves = WAVES;
   constexpr int kUnitsPerTile = 32 / UNIT;
@@ -1002,9 +1007,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   // (request, KV head[, head block]), or (group, KV head, chunk)
   const int pair = block / nsplit;
   const int G = p.group;
-  // Row role: more than 16 query heads per KV head take ceil(G / 16) head
-  // blocks of 16 MFMA columns, one per workgroup (each reads the K/V again).
-  const int hblocks = ROLE == Role::kRow ? (G + 15) >> 4 : 1;
+  // Row role: more than 16 query heads per KV head take ceil(G / (16 NCB))
+  // head blocks of NCB 16-column blocks, one per workgroup (each reads the
+  // K/V again).
+  const int hblocks = ROLE == Role::kRow ? (G + 16 * NCB - 1) / (16 * NCB) : 1;
   int b, kvh, chunk = 0, hb = 0;
   const int32_t* mem = nullptr;
   int64_t bal_eff = 0;
@@ -1032,15 +1038,15 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   const bool lead_ok = !PREFIX || (b >= 0 && b < p.num_seqs);
   const int trow = lead_ok ? b : 0;  // table row read for K/V
 
-  // column c's output row: the request's head kvh * G + 16 * hb + c (below
-  // G), or in the prefix role, for column block cb, the group row
-  // 16 * (NCB * chunk + cb) + c (member index, head)
+  // column c of column block cb: the request's head kvh * G + 16 * (NCB * hb
+  // + cb) + c (below G), or in the prefix role the group row 16 * (NCB *
+  // chunk + cb) + c (member index, head)
   int col_b[NCB], col_h[NCB];
   bool col_ok[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     col_b[cb] = b;
-    col_h[cb] = 16 * hb + c;
+    col_h[cb] = 16 * (NCB * hb + cb) + c;
     col_ok[cb] = col_h[cb] < G;
     if constexpr (PREFIX) {
       const int r = 16 * (NCB * chunk + cb) + c;
@@ -1250,6 +1256,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       ob = lds.col_b[h];
       qh = kvh * G + lds.col_h[h];
       head_ok = threadIdx.x < 16 * kDimThreads && ob >= 0;
+    } else if constexpr (NCB > 1) {
+      const int hh = 16 * (NCB * hb + cb) + h;
+      qh = kvh * G + hh;
+      head_ok = threadIdx.x < 16 * kDimThreads && hh < G;
     }
     float M = -INFINITY;
 #pragma unroll
@@ -1271,7 +1281,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     }
     if (ROLE == Role::kRow && p.splits == 1) {
       if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
-      return;
+      continue;
     }
     // split partial: unnormalised acc, base-2 max, denominator; the prefix
     // role's partials follow the tail splits
@@ -1310,6 +1320,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   }  // column blocks
 
   if constexpr (!MERGE) return;  // the reducer kernel merges
+  if (p.splits == 1) return;     // rows went straight to the output
 
   // In-launch merge.  Partials were written with agent-scope atomic stores
   // (sc1, coherent across the XCD L2s); waiting for their acknowledgement
@@ -1374,7 +1385,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 }
 
 // FUSE: 0 none, 1 fused append, 2 fused append with RoPE of q and the new K;
-// D: head_dim 128 or 64.
+// D: head_dim 128 or 64.  NCB: 16-column blocks of query heads per wave (2
+// for groups of more than 16 heads per KV head).
 //
 // The leading scalar arguments repeat what the first block-table load needs.
 // The library is built with amdgpu-kernarg-preload-count, so the command
@@ -1384,7 +1396,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 // kernel 5.53 -> 5.33 us on MI355X).  Firmware without argument preloading
 // runs the compiler's fallback prologue, which loads them from the argument
 // buffer instead.
-template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 128>
+template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 128, int NCB = 1>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
     const void* bt, int64_t bts0, int64_t bts1, int64_t max_blocks_per_seq, int32_t splits, int32_t hkv,
     int32_t group, int32_t hint_tps, int32_t bt_i64, DecodeParams p) {
@@ -1399,8 +1411,8 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   q.group = group;
   q.hint_tps = hint_tps;
   q.bt_i64 = bt_i64;
-  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT, D, waves_for<UNIT>(), false, true>(q, CascadeParams{},
-                                                                                         blockIdx.x, lds);
+  decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT, D, waves_for<UNIT>(), false, true, NCB>(
+      q, CascadeParams{}, blockIdx.x, lds);
 }
 
 // Dim-major caches: 32-token units on kDmWaves waves, K staged through LDS.
@@ -1901,8 +1913,32 @@ void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void
 // (C2: 4 tiles per split, 6.4 vs 6.7 us), 16-token units on eight waves for
 // longer splits (ragged B32: 70 -> 60 us; C5 layer: 97 -> 93 us).  8-token
 // blocks always take 16-token units (a unit spans at most two blocks).
+// Groups of more than 16 query heads per KV head: two 16-column blocks per
+// wave on 16-token units (the head dims and fused append as above; the host
+// gives them no RoPE and no in-launch merge).
+template <typename T, int BS, bool NT>
+void launch_mfma_wide(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
+  constexpr int W = kRowWideColBlocks;
+  const dim3 block(64 * waves_for<16>());
+  if (p.head_dim == 64) {
+    if (p.fuse)
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, 16, NT, 64, W>, grid, block, stream, ev, p);
+    else
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, 16, NT, 64, W>, grid, block, stream, ev, p);
+  } else {
+    if (p.fuse)
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, 16, NT, 128, W>, grid, block, stream, ev, p);
+    else
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, 16, NT, 128, W>, grid, block, stream, ev, p);
+  }
+}
+
 template <typename T, int BS, bool NT>
 void launch_mfma(const DecodeParams& p, dim3 grid, hipStream_t stream, void* const* ev) {
+  if (p.group > 16) {
+    launch_mfma_wide<T, BS, NT>(p, grid, stream, ev);
+    return;
+  }
   if constexpr (BS >= 16) {
     if (p.hint_tps <= kWideUnitMaxTiles) {
       launch_mfma_unit<T, BS, 32, NT>(p, grid, stream, ev);
@@ -2009,6 +2045,12 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
 }
 
 
+// Workgroups per (request, KV head, split) of the MFMA row kernel: one for
+// up to 16 query heads per KV head, else one per 32 (two column blocks).
+int64_t row_head_blocks(int64_t group) {
+  return group > 16 ? (group + 16 * kRowWideColBlocks - 1) / (16 * kRowWideColBlocks) : 1;
+}
+
 template <typename T>
 int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
@@ -2045,7 +2087,7 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
         break;
     }
   } else if (fast) {
-    const int64_t hblocks = (p.group + 15) / 16;
+    const int64_t hblocks = row_head_blocks(p.group);
     const dim3 grid(static_cast<unsigned>(pairs * hblocks * p.splits));
     switch (a.block_size) {
       case 8: launch_mfma<T, 8>(p, nt, grid, stream, a.timing_events); break;
@@ -2162,9 +2204,9 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
     return set_error(FD_E_INVALID, "fd_paged_decode_plan: non-positive shape");
   const int64_t tiles = (max_seq_len + 31) / 32;
   // groups of more than 16 query heads per KV head: one workgroup per head
-  // block of 16, each reading the row's K/V
+  // block of 32, each reading the row's K/V
   const int64_t group = num_q_heads / num_kv_heads;
-  const int64_t hblocks = (head_dim == 128 || head_dim == 64) ? (group + 15) / 16 : 1;
+  const int64_t hblocks = (head_dim == 128 || head_dim == 64) ? row_head_blocks(group) : 1;
   const int64_t pairs = num_seqs * num_kv_heads * hblocks;
   const int64_t cus = device_cus();
   // one workgroup per CU for a batch of equal rows: fewer, longer splits
@@ -2305,7 +2347,7 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
       return set_error(FD_E_INVALID, "%s: rotary_dim needs the fused append (append_k, append_v, slot_mapping)", fn);
     if (!(a.rope_base > 0.0) || a.rope_base > 3.4e38)
       return set_error(FD_E_INVALID, "%s: rope_base must be a positive finite number", fn);
-    if (a.head_dim != 128 || !fast_path_ok(a, p.group))
+    if (a.head_dim != 128 || p.group > 16 || !fast_path_ok(a, p.group))
       return set_error(FD_E_UNSUPPORTED,
                        "%s: fused RoPE needs head_dim 128, <= 16 query heads per KV head, unit dim stride and "
                        "16-byte rows",

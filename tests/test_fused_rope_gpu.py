@@ -112,6 +112,10 @@ def test_fused_rope_refusals():
     with pytest.raises(RuntimeError, match="fused RoPE needs head_dim 128"):
         _decode_with_workspace(q64, k64, v64, t64, sl64, torch.empty_like(q64), 0.1, 32, 1, None, k64.shape[0],
                                append=(ak64, ak64, slot), rope=(64, 1e4))
+    q32, k32, v32, t32, sl32 = make_paged_inputs([40, 50], 64, 2, 128, 32, torch.bfloat16, seed=5)
+    with pytest.raises(RuntimeError, match="<= 16 query heads per KV head"):
+        _decode_with_workspace(q32, k32, v32, t32, sl32, torch.empty_like(q32), 0.1, 32, 1, None, k32.shape[0],
+                               append=(ak, ak, slot), rope=(128, 1e4))
     # nothing above launched: the caches are untouched
     q2, k2, v2, _, _ = make_paged_inputs([40, 50], 16, 2, 128, 32, torch.bfloat16, seed=3)
     assert torch.equal(k, k2) and torch.equal(v, v2)
