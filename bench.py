@@ -643,8 +643,8 @@ def run_formats(torch, dev, args):
         ("d128-g8-token-major", 16, 2, 128, "token_major", 32, "mfma"),
         ("d64-g8-token-major", 16, 2, 64, "token_major", 32, "mfma"),
         ("d64-g7-token-major (Qwen2.5-0.5B heads)", 14, 2, 64, "token_major", 32, "mfma"),
-        ("d128-g32-token-major", 64, 2, 128, "token_major", 32, "mfma, 2 head blocks"),
-        ("d64-g71-token-major (MQA)", 71, 1, 64, "token_major", 32, "mfma, 5 head blocks"),
+        ("d128-g32-token-major", 64, 2, 128, "token_major", 32, "mfma, two 16-column blocks per wave"),
+        ("d64-g71-token-major (MQA)", 71, 1, 64, "token_major", 32, "mfma, 3 head blocks of two column blocks"),
         ("d128-mha-token-major (B4)", 16, 16, 128, "token_major", 32, "mfma"),
         ("d128-g8-dim-major", 16, 2, 128, "dim_major", 32, "mfma dim-major, K staged through LDS"),
         ("d64-g8-dim-major", 16, 2, 64, "dim_major", 32, "mfma dim-major, K staged through LDS"),
