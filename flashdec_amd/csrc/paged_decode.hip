@@ -2228,11 +2228,31 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
   // Whole waves of workgroups: a grid of 2.5 workgroups per CU ends with a
   // half-empty wave (one C5 layer, 128 pairs: 4 or 6 splits 109 us, 5 splits
   // 116 us), so round up to the next count that fills every CU (at most 2x).
-  for (int64_t t = s; t <= 2 * s; ++t)
+  bool whole = false;
+  for (int64_t t = s; t <= 2 * s && !whole; ++t)
     if ((pairs * t) % cus == 0) {
       s = t;
-      break;
+      whole = true;
     }
+  if (!whole) {
+    // No count up to 2x fills whole waves (the pair count shares too few
+    // factors with the CU count: 48 pairs took 6 splits, 288 workgroups, a
+    // second wave of 32).  Take the count from the balance bound up whose
+    // last wave is fullest; on a tie, fewer workgroups (48 pairs: 5 splits,
+    // one wave of 240).
+    int64_t best = s;
+    int64_t best_num = 0, best_den = 1;  // fullness best_num / best_den
+    for (int64_t t = balance > 1 ? balance : 1; t <= 2 * s; ++t) {
+      const int64_t wgs = pairs * t;
+      const int64_t den = (wgs + cus - 1) / cus * cus;
+      if (wgs * best_den > best_num * den) {
+        best = t;
+        best_num = wgs;
+        best_den = den;
+      }
+    }
+    s = best;
+  }
   const int64_t cap = (2 * tiles + kMaxWaves - 1) / kMaxWaves;  // >= one unit per wave
   if (s > cap) s = cap;
   if (s > 256) s = 256;

@@ -1,0 +1,52 @@
+"""CPU checks of the library's split plan (``fd_paged_decode_plan``).
+
+Without a GPU the library plans for 256 CUs (MI355X's count).  Each case is
+worked by hand from the plan's rules: one workgroup per CU at least
+(ceil(256 / pairs)), the balance bound from the batch's total length, whole
+waves of 256 workgroups where a count up to twice the start gives them, else
+the count from the balance bound up whose last wave is fullest (ties: fewer
+workgroups), then the cap of one 16-token unit per wave.  No counterpart in
+the reference, whose split count is per launch (flashdec/kernels/
+paged_decode.py:408-411).
+"""
+
+import pytest
+
+CASES = [
+    # (num_seqs, Hq, Hkv, D, max_len, total_len) -> splits
+    # C2: 16 pairs, 16 splits = 256 workgroups
+    ((8, 16, 2, 128, 2048, 0), 16),
+    # ctx1024: 16 pairs want 16, the cap (2 * 32 tiles / 8 waves) gives 8
+    ((8, 16, 2, 128, 1024, 0), 8),
+    # C5 layer: 128 pairs, 2 splits
+    ((64, 16, 2, 128, 8192, 64 * 8192), 2),
+    # B16 x 8192, G8: 32 pairs, 8 splits
+    ((16, 16, 2, 128, 8192, 16 * 8192), 8),
+    # B16 x 8192, G32: one head block of 32 heads, so 32 pairs, 8 splits
+    ((16, 64, 2, 128, 8192, 16 * 8192), 8),
+    # MQA G71 D64: 3 head blocks, 48 pairs.  Start 6 (288 workgroups); no
+    # count in [6, 12] fills whole waves; from the balance bound 5 up, 5
+    # (240 of 256) and 10 (480 of 512) are fullest: 5
+    ((16, 71, 1, 64, 8192, 16 * 8192), 5),
+    # 6 pairs of 32768 tokens: start 43 (258 workgroups, a second wave of 2);
+    # 85 splits fill 510 of 512
+    ((3, 16, 2, 128, 32768, 3 * 32768), 85),
+    # C1's shape: 8 pairs want 32, the cap (2 * 16 tiles / 8 waves) gives 4
+    ((4, 8, 2, 64, 512, 4 * 512), 4),
+]
+
+
+@pytest.mark.parametrize(("shape", "splits"), CASES)
+def test_plan_cases(shape, splits):
+    from flashdec_amd import _lib
+
+    assert _lib.paged_decode_plan(*shape) == splits
+
+
+def test_plan_fills_whole_waves_when_it_can():
+    # every pair count that divides 256 gets a grid of whole waves
+    from flashdec_amd import _lib
+
+    for pairs_b in (1, 2, 4, 8, 16, 32, 64, 128):
+        s = _lib.paged_decode_plan(pairs_b, 16, 2, 128, 65536, pairs_b * 65536)
+        assert (pairs_b * 2 * s) % 256 == 0, (pairs_b, s)
