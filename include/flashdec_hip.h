@@ -178,8 +178,9 @@ typedef struct fd_paged_decode_args {
    * No counterpart in the reference. */
   int32_t kv_reuse;
 
-  /* Fused RoPE: 0 = off; 64 or 128 = rotary width (head_dim 128, split-half
-   * rotation as flashdec/rope.py:26-85, frequencies rope_base^(-2i/R)).  Needs
+  /* Fused RoPE: 0 = off; 64 or 128 = rotary width (head_dim 128, at most 16
+   * query heads per KV head, split-half rotation as flashdec/rope.py:26-85,
+   * frequencies rope_base^(-2i/R)).  Needs
    * the fused append: q and append_k are then unrotated, both are rotated at
    * position seq_len - 1 (the appended token's index) and the cache receives
    * the rotated K.  Bit-identical to fd_fused_rope_kv_append at those
