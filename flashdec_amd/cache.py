@@ -985,6 +985,25 @@ class PagedKVCache:
             raise
         return q_out, self._layer_written(txn)
 
+    def _layer_in_fused_decode(self, transaction, layer_idx, rotary_dim, base, cos_sin_table):
+        """Bookkeeping of one layer whose RoPE + K/V write runs inside the decode launch
+        (``DecodeEngine.step_layer``).  Only after an earlier layer of the transaction went
+        the checked way (``_write_layer_fused_prepared``) with the same RoPE setting: then
+        the layer order is all there is left to check.  Returns the view, or None (nothing
+        recorded) without such a layer."""
+        txn = self._journal.find_open(transaction)
+        key = (rotary_dim, base, 0 if cos_sin_table is None else cos_sin_table.data_ptr())
+        if txn.launch is None or txn.launch[0] != key:
+            return None
+        try:
+            layer_idx = self._validate_layer_idx(layer_idx)
+            if layer_idx != txn.layers:
+                raise RuntimeError(f"transaction requires layer {txn.layers}, got layer {layer_idx}")
+        except Exception:
+            self._tally.failures += 1
+            raise
+        return self._layer_written(txn)
+
     def _record_graph_layers(self, transaction):
         """Record every layer as written by a replayed step graph (see DecodeEngine.step_graph)."""
         txn = self._journal.find_open(transaction)

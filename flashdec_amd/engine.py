@@ -159,6 +159,7 @@ class _OpenStep:
     cascade: Any = None  # CascadeGroups: rows sharing a resident prefix decode it once per group
     kv_reuse: bool = False  # rows share prefix blocks (per-row path): plain, cached K/V loads
     decode_launch: Any = None  # eager HIP decode: ((stream, q shape, q strides), PagedDecodeArgs) of this step
+    fused_launch: Any = None  # eager decode with RoPE + append inside the launch: PagedDecodeArgs of this step
 
 
 class _Roster:
@@ -290,6 +291,10 @@ class DecodeEngine:
         self.num_warps = num_warps
         self.num_stages = num_stages
         self.profile_ranges = profile_ranges
+        # eager steps: layers after the first run RoPE + K/V write inside the
+        # decode launch where it applies (no counterpart in the reference; the
+        # bits are those of the two launches, and False keeps two)
+        self.eager_fuse_rope = True
         self._range = _torch().profiler.record_function if profile_ranges else None
         self._roster = _Roster()
         self._counts = _EngineCounts()
@@ -495,9 +500,18 @@ class DecodeEngine:
             self._validate_step_inputs(ids, q, k, v)
             k, v = (t.unsqueeze(0) if t.dim() == 2 else t for t in (k, v))
             with self._phase(PROFILE_RANGE_APPEND):
-                q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table)
+                fused = self._fused_layer(state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table)
+                if fused is None:
+                    q_rot, view, meta = self._write_layer(state, layer_idx, q, k, v, rotary_dim, base,
+                                                          cos_sin_table)
+                else:
+                    view, meta = fused
             with self._phase(PROFILE_RANGE_DECODE):
-                output = self._decode_layer(q_rot, view, meta, layer_idx)
+                if fused is None:
+                    output = self._decode_layer(q_rot, view, meta, layer_idx)
+                else:
+                    output = self._decode_fused_layer(state, q, k, v, meta, layer_idx, rotary_dim, base,
+                                                      cos_sin_table)
         except Exception:
             self._close_step(state, "aborted")
             raise
@@ -898,6 +912,75 @@ class DecodeEngine:
                                 kv_reuse=kv_reuse)
         return self._decode(q_rot, view.block_tables, view.effective_seq_lens, layer_idx, ragged=ragged,
                             cascade=cascade, kv_reuse=kv_reuse)
+
+    def _fused_layer(self, state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table):
+        """Whether this eager layer runs RoPE + K/V write inside its decode launch.
+
+        After the step's first layer went the checked way (the RoPE + append
+        kernel, then the prepared decode), later layers with the same RoPE
+        setting and shapes take one launch: the decode kernel rotates q and
+        the new K at the token's position, stores K/V at the reserved slot
+        and attends to it from registers -- the same bits as the two kernels
+        (the engine's step graphs do the same), minus a launch per layer.
+        Returns ``(view, device metadata)`` once the cache recorded the
+        layer, else None.
+        """
+        if not self.eager_fuse_rope or state.decode_launch is None or state.cascade is not None or state.ragged:
+            return None
+        cache = self.cache
+        if self._append != "fused_hip" or self._decode_kind != "hip" or cache.device.type != "cuda":
+            return None
+        record = getattr(cache, "_layer_in_fused_decode", None)
+        if record is None or not _own_method(cache, "write_token_layer_fused_cuda"):
+            return None
+        torch = _torch()
+        head_dim = q.shape[-1]
+        rdim = head_dim if rotary_dim is None else rotary_dim
+        if (head_dim != 128 or rdim not in (64, 128) or q.shape[1] // cache.num_kv_heads > 16
+                or q.dtype not in (torch.bfloat16, torch.float16)):
+            return None
+        if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+            return None
+        from . import _lib
+
+        if state.decode_launch[0] != (_lib.current_stream_handle(q.device), tuple(q.shape), q.stride()):
+            return None
+        view = record(state.cache_transaction, layer_idx, rotary_dim, base, cos_sin_table)
+        if view is None:
+            return None
+        return view, cache.transaction_device_metadata(state.cache_transaction)
+
+    def _decode_fused_layer(self, state, q, k, v, meta, layer_idx, rotary_dim, base, cos_sin_table):
+        """Eager decode of one layer with RoPE + K/V write inside the launch (see ``_fused_layer``):
+        the step's decode arguments plus the append rows, the reserved slots and the RoPE setting."""
+        from . import _lib
+        from .paged_decode import _fill_append
+
+        torch = _torch()
+        cache = self.cache
+        out = torch.empty_like(q)
+        args = state.fused_launch
+        if args is None:
+            base_args = state.decode_launch[1]
+            args = type(base_args).from_buffer_copy(base_args)
+            args.workspace = base_args.workspace
+            _fill_append(args, k, v, meta.slots)
+            args.rotary_dim = q.shape[-1] if rotary_dim is None else int(rotary_dim)
+            args.rope_base = float(base)
+            if cos_sin_table is not None:
+                args.rope_cos_sin_table = cos_sin_table.data_ptr()
+                args.rope_table_rows = cos_sin_table.shape[1]
+            state.fused_launch = args
+        else:
+            args.append_k = k.data_ptr()
+            args.append_v = v.data_ptr()
+        args.q = q.data_ptr()
+        args.out = out.data_ptr()
+        layer_bytes = cache.k_cache.stride(0) * cache.k_cache.element_size()
+        args.k_cache = cache.k_cache.data_ptr() + layer_idx * layer_bytes
+        args.v_cache = cache.v_cache.data_ptr() + layer_idx * layer_bytes
+        _lib.paged_decode(args, _lib.current_stream_handle(q.device))
+        return out
 
     def _decode_prepared(self, state, q, meta, layer_idx, ragged, kv_reuse):
         """Eager HIP decode of one layer of the open step (the allocator's metadata).

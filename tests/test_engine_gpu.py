@@ -138,3 +138,44 @@ def test_engine_abort_mid_token_then_continue():
     assert engine.cache.seq_lens_tensor([1, 2]).tolist() == [committed, committed]
     assert engine.metrics()["transaction_abort_count"] == 2
     assert engine.validate_invariants()
+
+
+@pytest.mark.parametrize("table", [False, True])
+@pytest.mark.parametrize("rotary_dim", [None, 64])
+@pytest.mark.parametrize("hq,bs", [(16, 16), (8, 32), (2, 8)])
+def test_eager_layers_with_rope_in_the_decode_launch_match_two_launches(hq, bs, rotary_dim, table):
+    """Eager steps: layers after the first run RoPE + K/V write inside the decode launch; outputs and cache
+    bytes equal the two-launch path's bit for bit, over steps that cross block boundaries."""
+    from flashdec_amd.rope import rope_cos_sin_table
+
+    print(f"eager fused hq={hq} bs={bs} rotary_dim={rotary_dim} table={table}", flush=True)
+    num_layers, hkv, d = 4, 2, 128
+    engines = []
+    for fuse in (False, True):
+        e = DecodeEngine(cache_of(num_layers, hkv, d, bs, max_blocks=96))
+        e.eager_fuse_rope = fuse
+        for rid in ("a", "b", "c"):
+            e.add_request(rid)
+        e.admit()
+        engines.append(e)
+    tab = rope_cos_sin_table(256, rotary_dim or d, base=1e6) if table else None
+    g = torch.Generator().manual_seed(hq + bs)
+    fused_layers = 0
+    for step in range(bs + 3):
+        txs = [e.begin_step(["a", "b", "c"]) for e in engines]
+        for layer in range(num_layers):
+            q, k, v = rand_inputs(g, 3, hq, hkv, d, torch.bfloat16)
+            outs = [e.step_layer(tx, layer, q, k, v, rotary_dim=rotary_dim, base=1e6, cos_sin_table=tab).output
+                    for e, tx in zip(engines, txs)]
+            fused_layers += engines[1]._open.fused_launch is not None and layer > 0
+            assert engines[0]._open.fused_launch is None
+            assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (step, layer)
+        for e, tx in zip(engines, txs):
+            e.commit_step(tx)
+    assert fused_layers == (bs + 3) * (num_layers - 1)
+    torch.cuda.synchronize()
+    for a, b in ((engines[0].cache.k_cache, engines[1].cache.k_cache),
+                 (engines[0].cache.v_cache, engines[1].cache.v_cache)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert engines[1].validate_invariants()
+    assert engines[0].metrics() == engines[1].metrics()
