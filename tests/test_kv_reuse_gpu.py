@@ -2,8 +2,10 @@
 
 Streaming (non-temporal) and plain loads must give bit-identical outputs on
 every kernel that takes the switch: the row kernel (one and several units per
-wave, fused append), per-row (balanced) splits, the cascade launch and the
-vLLM launcher.  Both are also checked against the fp32 oracle.  A value other
+wave, one and two column blocks per wave, fused append), the dim-major
+kernel, per-row (balanced) splits, the cascade launch and the vLLM
+launcher.  (The plain-load kernels also read block ids through the scalar
+cache, the streaming ones through vector loads.)  Both are also checked against the fp32 oracle.  A value other
 than 0 or 1 is rejected before any launch.
 """
 
@@ -25,14 +27,31 @@ def _oracle(q, k, v, table, lens):
 
 @pytest.mark.parametrize("lens", [[2048] * 8, [40, 5, 3000, 777], [16384, 9000]])
 @pytest.mark.parametrize("block_size", [16, 32])
-def test_row_kernel_same_bits_either_policy(lens, block_size):
+@pytest.mark.parametrize(("hq", "head_dim"), [(16, 128), (64, 128), (40, 64)])
+def test_row_kernel_same_bits_either_policy(lens, block_size, hq, head_dim):
+    # G 8 (one column block), G 32 and G 20 (two column blocks per wave)
     import flashdec_amd as fd
 
-    q, k, v, table, sl = make_paged_inputs(lens, 16, 2, 128, block_size, torch.bfloat16, seed=5 + len(lens))
+    q, k, v, table, sl = make_paged_inputs(lens, hq, 2, head_dim, block_size, torch.bfloat16, seed=5 + len(lens))
     streamed = fd.decode(q, k, v, table, sl)
     cached = fd.decode(q, k, v, table, sl, kv_reuse=True)
     assert torch.equal(streamed.view(torch.int16), cached.view(torch.int16))
     assert_close_to_oracle(streamed, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("block_size", [8, 32])
+def test_dim_major_same_bits_either_policy(block_size, head_dim):
+    import flashdec_amd as fd
+
+    lens = [4096, 1000, 33]
+    q, k, v, table, sl = make_paged_inputs(lens, 16, 2, head_dim, block_size, torch.bfloat16, seed=9,
+                                           kv_layout="dim_major")
+    streamed = fd.decode(q, k, v, table, sl, kv_layout="dim_major")
+    cached = fd.decode(q, k, v, table, sl, kv_layout="dim_major", kv_reuse=True)
+    assert torch.equal(streamed.view(torch.int16), cached.view(torch.int16))
+    expected = oracle_decode(np32(q), np32(k), np32(v), table.cpu().numpy(), sl.cpu().numpy(), kv_layout="dim_major")
+    assert_close_to_oracle(streamed, expected)
 
 
 def test_balanced_splits_same_bits_either_policy():
@@ -92,7 +111,8 @@ def test_cascade_same_bits_either_policy():
     q = torch.randn((rows, 16, 128), generator=gen).to(torch.bfloat16).cuda()
     table, sl = table.cuda(), sl.cuda()
     groups = build_cascade_groups(table, sl, bs, 16, 2, device=q.device)
-    streamed = paged_decode_attention_cascade(q, k, v, table, sl, groups=groups)
+    # the cascade's own default is kv_reuse=True: the streamed run asks for it
+    streamed = paged_decode_attention_cascade(q, k, v, table, sl, groups=groups, kv_reuse=False)
     cached = paged_decode_attention_cascade(q, k, v, table, sl, groups=groups, kv_reuse=True)
     assert torch.equal(streamed.view(torch.int16), cached.view(torch.int16))
     assert_close_to_oracle(streamed, _oracle(q, k, v, table, sl))
