@@ -452,34 +452,36 @@ def test_head_dim_64_fused_append_through_the_abi(num_splits, block_size):
     assert np.array_equal(bits16(v), bits16(v_expected))
 
 
+@pytest.mark.parametrize("block_size", [8, 16, 32])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(32, 2, 128), (48, 2, 128), (24, 1, 64), (71, 1, 64),
                                                      (64, 1, 128), (34, 2, 128), (66, 2, 128), (40, 1, 64),
                                                      (17, 1, 64)])
-def test_groups_above_16_heads_take_head_blocks(hq, hkv, head_dim, dtype):
+def test_groups_above_16_heads_take_head_blocks(hq, hkv, head_dim, dtype, block_size):
     """More than 16 query heads per KV head: ceil(G / 32) head blocks of two 16-column blocks on the MFMA
-    kernel (G 17 and 33: a last column block with a single head)."""
+    kernel (G 17 and 33: a last column block with a single head), every block size."""
     lens = [1, 100, 2048, 3000]
-    q, k, v, table, sl = make_paged_inputs(lens, hq, hkv, head_dim, 32, dtype, seed=hq + head_dim)
-    out = _fd().decode(q, k, v, table, sl)
+    q, k, v, table, sl = make_paged_inputs(lens, hq, hkv, head_dim, block_size, dtype, seed=hq + head_dim)
+    out = _fd().decode(q, k, v, table, sl, block_size=block_size)
     assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
 
 
+@pytest.mark.parametrize("block_size", [8, 32])
 @pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(40, 2, 128), (34, 1, 64), (80, 2, 128)])
 @pytest.mark.parametrize("num_splits", [1, 5])
-def test_groups_above_16_fused_append_written_once(num_splits, hq, hkv, head_dim):
+def test_groups_above_16_fused_append_written_once(num_splits, hq, hkv, head_dim, block_size):
     """Every head block attends to the appended token; the cache holds it exactly."""
     from flashdec_amd.paged_decode import _decode_with_workspace
 
     lens_after = [18, 257, 64]
-    q, k, v, table, lens = make_paged_inputs(lens_after, hq, hkv, head_dim, 32, torch.bfloat16, seed=41)
+    q, k, v, table, lens = make_paged_inputs(lens_after, hq, hkv, head_dim, block_size, torch.bfloat16, seed=41)
     expected = _oracle(q, k, v, table, lens)
-    slots = _slots(table, lens.cpu(), 32)
+    slots = _slots(table, lens.cpu(), block_size)
     ak = torch.empty((3, hkv, head_dim), device="cuda", dtype=torch.bfloat16)
     av = torch.empty_like(ak)
     k_expected, v_expected = k.clone(), v.clone()
     for b, s in enumerate(slots):
-        blk, off = divmod(s, 32)
+        blk, off = divmod(s, block_size)
         ak[b] = k[blk, :, off]
         av[b] = v[blk, :, off]
         k[blk, :, off] = float("nan")
@@ -489,8 +491,8 @@ def test_groups_above_16_fused_append_written_once(num_splits, hq, hkv, head_dim
         ws = (torch.empty((3, hq, num_splits, head_dim), device="cuda"),
               torch.empty((3, hq, num_splits), device="cuda"), torch.empty((3, hq, num_splits), device="cuda"))
     out = torch.empty_like(q)
-    _decode_with_workspace(q, k, v, table, lens, out, 1.0 / math.sqrt(head_dim), 32, num_splits, ws, k.shape[0],
-                           append=(ak, av, torch.tensor(slots, device="cuda", dtype=torch.int64)))
+    _decode_with_workspace(q, k, v, table, lens, out, 1.0 / math.sqrt(head_dim), block_size, num_splits, ws,
+                           k.shape[0], append=(ak, av, torch.tensor(slots, device="cuda", dtype=torch.int64)))
     assert_close_to_oracle(out, expected)
     assert np.array_equal(bits16(k), bits16(k_expected))
     assert np.array_equal(bits16(v), bits16(v_expected))
