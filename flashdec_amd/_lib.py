@@ -22,7 +22,7 @@ FD_DTYPE_BF16 = 1
 FD_DTYPE_F32 = 2
 FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
-ABI_VERSION = 8
+ABI_VERSION = 9
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024  # FD_NOALLOC_SCRATCH_BYTES: per-GPU scratch of fd_paged_decode_noalloc
 CASCADE_MAX_CHUNK_ROWS = 32  # FD_CASCADE_MAX_CHUNK_ROWS: the larger chunk_rows of fd_cascade_args
@@ -134,6 +134,8 @@ EXPORTED_SYMBOLS = (
     "fd_kv_append",
     "fd_last_error",
     "fd_abi_version",
+    "fd_record_launches",
+    "fd_last_launch",
 )
 
 _lock = threading.Lock()
@@ -181,11 +183,27 @@ def load_library():
         lib.fd_last_error.restype = ctypes.c_char_p
         lib.fd_abi_version.argtypes = []
         lib.fd_abi_version.restype = ctypes.c_int
+        lib.fd_record_launches.argtypes = [ctypes.c_int]
+        lib.fd_record_launches.restype = None
+        lib.fd_last_launch.argtypes = []
+        lib.fd_last_launch.restype = ctypes.c_char_p
         version = lib.fd_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
         _lib = lib
         return lib
+
+
+def record_launches(on: bool = True) -> None:
+    """Turn the library's launch record on or off (process-wide; see ``last_launch``)."""
+    load_library().fd_record_launches(1 if on else 0)
+
+
+def last_launch() -> list:
+    """Kernels the last library call on this thread launched (demangled names), while the
+    launch record is on; no counterpart in the reference."""
+    text = load_library().fd_last_launch().decode("utf-8", "replace")
+    return text.split(";") if text else []
 
 
 def check(rc: int, what: str) -> None:

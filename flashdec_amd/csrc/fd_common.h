@@ -22,6 +22,14 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 std::string& last_error_slot();
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// -------------------------------------------------------- launch record --
+// Off unless fd_record_launches(1): then every launch appends its kernel's
+// name to a thread-local record that each public entry point clears first,
+// and fd_last_launch() returns it.  Off, a launch pays one relaxed load.
+bool launch_record_on();
+void clear_launch_record();
+void record_launch(const void* kernel, hipStream_t stream);
+
 // ------------------------------------------------------------ conversions --
 template <typename T>
 __device__ __forceinline__ float to_f32(T x) {

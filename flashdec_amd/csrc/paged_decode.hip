@@ -1867,6 +1867,7 @@ bool dm_path_ok(const fd_paged_decode_args& a, int64_t group) {
 // One dispatch; events given are recorded at its start / end (profiling hook).
 template <typename F, typename... Args>
 void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, void* stop, Args... args) {
+  if (launch_record_on()) record_launch(reinterpret_cast<const void*>(kernel), stream);
   if (start || stop)
     hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, static_cast<hipEvent_t>(start),
                           static_cast<hipEvent_t>(stop), 0, args...);
@@ -2398,6 +2399,7 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
 }
 
 extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream_) {
+  clear_launch_record();
   DecodeParams p;
   const int rc = fill_decode_params(args, "fd_paged_decode", p);
   if (rc != FD_OK) return rc;
@@ -2453,6 +2455,7 @@ int scratch_address(hipStream_t stream, const char* fn, float** out) {
 }  // namespace
 
 extern "C" int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream_) {
+  clear_launch_record();
   static const char* fn = "fd_paged_decode_noalloc";
   if (args == nullptr) return set_error(FD_E_INVALID, "%s: args is NULL", fn);
   if (args->struct_size != sizeof(fd_paged_decode_args))
@@ -2513,6 +2516,7 @@ extern "C" int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stre
 
 extern "C" int fd_paged_decode_cascade(const fd_paged_decode_args* args, const fd_cascade_args* cascade,
                                        fd_stream_t stream_) {
+  clear_launch_record();
   static const char* fn = "fd_paged_decode_cascade";
   DecodeParams p;
   const int rc = fill_decode_params(args, fn, p);

@@ -407,11 +407,14 @@ int launch_rope(const fd_rope_append_args& a, const RopeParams& p, hipStream_t s
   const bool vec = a.head_dim % N == 0 && (a.rotary_dim / 2) % N == 0 && aligned16(a.q) && aligned16(a.k) &&
                    aligned16(a.v) && aligned16(a.k_cache) && aligned16(a.v_cache) &&
                    (a.q_out == nullptr || aligned16(a.q_out));
-  if (vec)
+  if (vec) {
+    if (launch_record_on()) record_launch(reinterpret_cast<const void*>(rope_append_vec_kernel<T>), stream);
     hipLaunchKernelGGL((rope_append_vec_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(kThreads), 0, stream,
                        p.q, p.k, p.v, p.q_out, p.hq, p.hkv, p.head_dim, p.rotary_dim, p.idx_i64, p);
-  else
+  } else {
+    if (launch_record_on()) record_launch(reinterpret_cast<const void*>(rope_append_kernel<T>), stream);
     hipLaunchKernelGGL((rope_append_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(256), 0, stream, p);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "rope append launch failed: %s", hipGetErrorString(e));
   return FD_OK;
@@ -419,6 +422,7 @@ int launch_rope(const fd_rope_append_args& a, const RopeParams& p, hipStream_t s
 
 template <typename T>
 int launch_kv(const fd_rope_append_args& a, const RopeParams& p, hipStream_t stream) {
+  if (launch_record_on()) record_launch(reinterpret_cast<const void*>(kv_append_kernel<T>), stream);
   hipLaunchKernelGGL((kv_append_kernel<T>), dim3(static_cast<unsigned>(a.batch)), dim3(256), 0, stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_E_LAUNCH, "kv append launch failed: %s", hipGetErrorString(e));
@@ -431,6 +435,7 @@ int launch_kv(const fd_rope_append_args& a, const RopeParams& p, hipStream_t str
 using namespace fd;
 
 extern "C" int fd_fused_rope_kv_append(const fd_rope_append_args* args, fd_stream_t stream_) {
+  clear_launch_record();
   RopeParams p{};
   int rc = fill_params(args, p, true, "fd_fused_rope_kv_append");
   if (rc != FD_OK) return rc;
@@ -444,6 +449,7 @@ extern "C" int fd_fused_rope_kv_append(const fd_rope_append_args* args, fd_strea
 }
 
 extern "C" int fd_kv_append(const fd_rope_append_args* args, fd_stream_t stream_) {
+  clear_launch_record();
   RopeParams p{};
   int rc = fill_params(args, p, false, "fd_kv_append");
   if (rc != FD_OK) return rc;

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FD_ABI_VERSION 8
+#define FD_ABI_VERSION 9
 
 /* status codes */
 #define FD_OK 0
@@ -365,6 +365,18 @@ const char* fd_last_error(void);
 
 /* FD_ABI_VERSION of the loaded library */
 int fd_abi_version(void);
+
+/*
+ * Launch record (no counterpart in the reference; for tests and debugging).
+ * fd_record_launches(1) turns it on for the process: each fd_paged_decode*,
+ * fd_fused_rope_kv_append and fd_kv_append call then clears this thread's
+ * record and appends the demangled name of every kernel it launches
+ * ("fd::decode_mfma_kernel<__bf16, 32, 0, false, 32, true, 128, 1>;
+ * fd::split_reduce_pre_kernel<__bf16, 128, 1>"), which fd_last_launch()
+ * returns.  Off by default; off, a launch pays one relaxed load.
+ */
+void fd_record_launches(int on);
+const char* fd_last_launch(void);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "flashdec_hip.h"
 def declared_functions():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:int|const\s+char\s*\*)\s*(fd_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|void|const\s+char\s*\*)\s*(fd_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_exactly_the_bound_symbols():
