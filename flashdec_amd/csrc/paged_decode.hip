@@ -1010,7 +1010,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   // Row role: more than 16 query heads per KV head take ceil(G / (16 NCB))
   // head blocks of NCB 16-column blocks, one per workgroup (each reads the
   // K/V again).
-  const int hblocks = ROLE == Role::kRow ? (G + 16 * NCB - 1) / (16 * NCB) : 1;
+  const int hblocks =
+      ROLE == Role::kRow ? static_cast<int>(static_cast<unsigned>(G + 16 * NCB - 1) / (16u * NCB)) : 1;
   int b, kvh, chunk = 0, hb = 0;
   const int32_t* mem = nullptr;
   int64_t bal_eff = 0;
