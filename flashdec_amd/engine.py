@@ -159,7 +159,7 @@ class _OpenStep:
     cascade: Any = None  # CascadeGroups: rows sharing a resident prefix decode it once per group
     kv_reuse: bool = False  # rows share prefix blocks (per-row path): plain, cached K/V loads
     decode_launch: Any = None  # eager HIP decode: ((stream, q shape, q strides), PagedDecodeArgs) of this step
-    fused_launch: Any = None  # eager decode with RoPE + append inside the launch: PagedDecodeArgs of this step
+    fused_launch: Any = None  # eager decode with RoPE + append inside the launch: (RoPE key, PagedDecodeArgs)
 
 
 class _Roster:
@@ -959,8 +959,9 @@ class DecodeEngine:
         torch = _torch()
         cache = self.cache
         out = torch.empty_like(q)
-        args = state.fused_launch
-        if args is None:
+        # the RoPE setting may change between layers: the arguments follow it
+        key = (rotary_dim, base, 0 if cos_sin_table is None else cos_sin_table.data_ptr())
+        if state.fused_launch is None or state.fused_launch[0] != key:
             base_args = state.decode_launch[1]
             args = type(base_args).from_buffer_copy(base_args)
             args.workspace = base_args.workspace
@@ -970,8 +971,9 @@ class DecodeEngine:
             if cos_sin_table is not None:
                 args.rope_cos_sin_table = cos_sin_table.data_ptr()
                 args.rope_table_rows = cos_sin_table.shape[1]
-            state.fused_launch = args
+            state.fused_launch = (key, args)
         else:
+            args = state.fused_launch[1]
             args.append_k = k.data_ptr()
             args.append_v = v.data_ptr()
         args.q = q.data_ptr()

@@ -179,3 +179,28 @@ def test_eager_layers_with_rope_in_the_decode_launch_match_two_launches(hq, bs, 
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert engines[1].validate_invariants()
     assert engines[0].metrics() == engines[1].metrics()
+
+
+def test_eager_fused_layers_follow_a_rope_setting_that_changes_within_the_step():
+    """Layers 0-1 rotate all 128 dims, layers 2-3 the first 64, layer 4 a different base: the layers that
+    run RoPE inside the decode launch use each layer's own setting (bits equal to the two-launch path)."""
+    settings = [(None, 1e6), (None, 1e6), (64, 1e6), (64, 1e6), (64, 1e4)]
+    engines = []
+    for fuse in (False, True):
+        e = DecodeEngine(cache_of(len(settings), 2, 128, 16, max_blocks=32))
+        e.eager_fuse_rope = fuse
+        e.add_request("a")
+        e.add_request("b")
+        e.admit()
+        engines.append(e)
+    g = torch.Generator().manual_seed(5)
+    for step in range(3):
+        txs = [e.begin_step(["a", "b"]) for e in engines]
+        for layer, (rdim, base) in enumerate(settings):
+            q, k, v = rand_inputs(g, 2, 16, 2, 128, torch.bfloat16)
+            outs = [e.step_layer(tx, layer, q, k, v, rotary_dim=rdim, base=base).output for e, tx in zip(engines, txs)]
+            assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (step, layer)
+        for e, tx in zip(engines, txs):
+            e.commit_step(tx)
+    torch.cuda.synchronize()
+    assert torch.equal(engines[0].cache.k_cache.view(torch.int16), engines[1].cache.k_cache.view(torch.int16))
