@@ -69,6 +69,13 @@ def _meta_nbytes(capacity, width):
     return 32 * capacity + 4 * capacity * (1 + width)
 
 
+def _rope_key(rotary_dim, base, cos_sin_table):
+    """What a layer's prepared RoPE launch arguments depend on: the rotary width, the base and
+    the cos/sin table (its address and rows)."""
+    table = (0, 0) if cos_sin_table is None else (cos_sin_table.data_ptr(), tuple(cos_sin_table.shape))
+    return rotary_dim, base, table
+
+
 class _DeviceMeta:
     """Transaction metadata resident on the cache device (one packed buffer).
 
@@ -952,7 +959,7 @@ class PagedKVCache:
         from . import _lib
 
         txn = self._journal.find_open(transaction)
-        key = (rotary_dim, base, 0 if cos_sin_table is None else cos_sin_table.data_ptr())
+        key = _rope_key(rotary_dim, base, cos_sin_table)
         if (txn.launch is None or txn.launch[0] != key or not q.is_contiguous() or not k.is_contiguous()
                 or not v.is_contiguous()):
             extra = {} if cos_sin_table is None else {"cos_sin_table": cos_sin_table}
@@ -992,7 +999,7 @@ class PagedKVCache:
         the layer order is all there is left to check.  Returns the view, or None (nothing
         recorded) without such a layer."""
         txn = self._journal.find_open(transaction)
-        key = (rotary_dim, base, 0 if cos_sin_table is None else cos_sin_table.data_ptr())
+        key = _rope_key(rotary_dim, base, cos_sin_table)
         if txn.launch is None or txn.launch[0] != key:
             return None
         try:

@@ -959,8 +959,10 @@ class DecodeEngine:
         torch = _torch()
         cache = self.cache
         out = torch.empty_like(q)
+        from .cache import _rope_key
+
         # the RoPE setting may change between layers: the arguments follow it
-        key = (rotary_dim, base, 0 if cos_sin_table is None else cos_sin_table.data_ptr())
+        key = _rope_key(rotary_dim, base, cos_sin_table)
         if state.fused_launch is None or state.fused_launch[0] != key:
             base_args = state.decode_launch[1]
             args = type(base_args).from_buffer_copy(base_args)
