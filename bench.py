@@ -802,8 +802,9 @@ def run_engine(torch, dev, args):
 
     layers, batch, hq, hkv, d, bs, ctx = 36, 64, 16, 2, 128, 32, 8192
     steps = args.engine_steps
-    # room for the warm-ups, the timed steps and the separate-RoPE comparison steps
-    width = (ctx + 2 * 20 + 2 * steps + 2 + bs - 1) // bs
+    # room for the warm-ups, the timed steps, the separate-RoPE comparison steps and the eager steps
+    n_eager, warm_eager = 20, 5
+    width = (ctx + 2 * 20 + 2 * steps + 2 + n_eager + warm_eager + bs - 1) // bs
     cache = PagedKVCache(layers, hkv, d, bs, max_blocks=batch * width, dtype=torch.bfloat16, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(109)
@@ -900,6 +901,30 @@ def run_engine(torch, dev, args):
         separate = start.elapsed_time(stop) / n_sep
     else:
         committed_sep = 0
+    # the same steps without a graph: step_layer per layer, as the reference's
+    # engine runs (after layer 0, RoPE + append inside the decode launch)
+
+    def eager_step():
+        tx_ = engine.begin_step(ids)
+        for layer in range(layers):
+            engine.step_layer(tx_, layer, sg.q[layer], sg.k[layer], sg.v[layer], base=1e6)
+        engine.commit_step(tx_)
+
+    ctx_eager = ctx + warm + committed + committed_sep  # the rows' length when the eager steps start
+    for _ in range(warm_eager):
+        eager_step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    start.record()
+    for _ in range(n_eager):
+        eager_step()
+    stop.record()
+    torch.cuda.synchronize()
+    eager_ms = start.elapsed_time(stop) / n_eager
+    eager_wall_ms = (time.perf_counter() - t1) * 1e3 / n_eager
+    committed_eager = warm_eager + n_eager
+    log(f"[bench] engine: eager steps (step_layer per layer): {eager_ms:.3f} ms/step, wall {eager_wall_ms:.3f} "
+        f"(context {ctx_eager + warm_eager}, after the graph steps)")
     # per-layer attention kernel, measured on the same shapes through the timing hook
     from flashdec_amd import paged_decode as pd
 
@@ -925,7 +950,8 @@ def run_engine(torch, dev, args):
         prepared.append((args_, pd._lib.current_stream_handle(dev)))
     attn_us, red_us = attention_kernel_us(torch, prepared, 16)
     engine.abort_step(tx)
-    kv_layer = (ctx + warm + committed + committed_sep) * batch * hkv * d * 2 * 2  # K+V bytes one layer's decode reads at the end
+    # K+V bytes one layer's decode reads at the end
+    kv_layer = (ctx + warm + committed + committed_sep + committed_eager) * batch * hkv * d * 2 * 2
     log(f"[bench] engine: {ms_per_step:.3f} ms/step over {steps} steps ({committed} committed, {aborts} aborted, "
         f"{rollbacks_ok} clean rollbacks); wall {wall_s * 1e3 / steps:.3f} ms/step; attention kernel {attn_us:.1f} us"
         f" per layer, reducer {red_us:.2f} us")
@@ -939,6 +965,10 @@ def run_engine(torch, dev, args):
     out["steps"] = steps
     out["tokens_per_s"] = round(committed * batch / (device_ms * 1e-3), 1)
     out["wall_ms_per_step"] = round(wall_s * 1e3 / steps, 4)
+    out["eager_path"] = {"ms_per_step": round(eager_ms, 4), "wall_ms_per_step": round(eager_wall_ms, 4),
+                         "steps": n_eager, "context_at_start": ctx_eager + warm_eager,
+                         "note": "begin_step, 36 x step_layer, commit_step; no graph; measured after the graph "
+                                 "steps, so at a longer context than the graph line"}
     if separate is not None:
         out["separate_rope_kernel_path"] = {"ms_per_step": round(separate, 4), "kernels_per_layer": 3,
                                             "steps": steps}
