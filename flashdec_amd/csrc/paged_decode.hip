@@ -2255,7 +2255,13 @@ extern "C" int fd_paged_decode_plan(int64_t num_seqs, int64_t num_q_heads, int64
     }
     s = best;
   }
-  const int64_t cap = (2 * tiles + kMaxWaves - 1) / kMaxWaves;  // >= one unit per wave
+  int64_t cap = (2 * tiles + kMaxWaves - 1) / kMaxWaves;  // >= one unit per wave
+  // Rows of at most 8 tiles: two splits of one unit per wave lose to one
+  // split of two (16-token) units per wave, which needs no reducer launch
+  // (same-box graphs, us/call, S = 1 vs 2: B2/B32/B64 ctx256 D128 5.95/7.69/
+  // 8.17 vs 6.85/8.06/9.07; B4 ctx256 D64 5.06 vs 6.19).  Longer rows keep
+  // their splits (B8 ctx512 D64: 4 splits 6.54, 1 split 7.22 us).
+  if (cap == 2) cap = 1;
   if (s > cap) s = cap;
   if (s > 256) s = 256;
   if (s < 1) s = 1;

@@ -5,9 +5,9 @@ worked by hand from the plan's rules: one workgroup per CU at least
 (ceil(256 / pairs)), the balance bound from the batch's total length, whole
 waves of 256 workgroups where a count up to twice the start gives them, else
 the count from the balance bound up whose last wave is fullest (ties: fewer
-workgroups), then the cap of one 16-token unit per wave.  No counterpart in
-the reference, whose split count is per launch (flashdec/kernels/
-paged_decode.py:408-411).
+workgroups), then the cap of one 16-token unit per wave (one split where that
+cap is two).  No counterpart in the reference, whose split count is per
+launch (flashdec/kernels/paged_decode.py:408-411).
 """
 
 import pytest
@@ -33,6 +33,11 @@ CASES = [
     ((3, 16, 2, 128, 32768, 3 * 32768), 85),
     # C1's shape: 8 pairs want 32, the cap (2 * 16 tiles / 8 waves) gives 4
     ((4, 8, 2, 64, 512, 4 * 512), 4),
+    # rows of 8 tiles: the cap would be 2 (one unit per wave); one split, no reducer
+    ((8, 16, 2, 128, 256, 8 * 256), 1),
+    ((64, 16, 2, 128, 256, 64 * 256), 1),
+    # 12 tiles: cap 3 (one 32-token unit per wave of 4)
+    ((8, 16, 2, 128, 384, 8 * 384), 3),
 ]
 
 
