@@ -17,6 +17,7 @@ fill 256 CUs); a caller that passes a workspace gets exactly ``num_splits``.
 from __future__ import annotations
 
 import math
+import threading
 
 import torch
 
@@ -298,11 +299,66 @@ def paged_decode_attention_into(
     assumed to be read once per call and is streamed with non-temporal loads.
     The result is the same either way.
     """
-    args, stream = _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_warps,
-                                kv_layout, num_stages, split_kv_workspace, num_splits, append_k, append_v,
-                                slot_mapping, ragged, kv_reuse)
+    key = None
+    last = getattr(_LAST_LAUNCH, "entry", None)
+    if last is not None and isinstance(q, torch.Tensor) and q.is_cuda:
+        stream = _lib.current_stream_handle(q.device)
+        key = _launch_key(q, k_cache, v_cache, block_tables, seq_lens, out, split_kv_workspace, append_k, append_v,
+                          slot_mapping, (sm_scale, block_size, num_warps, kv_layout, num_stages, num_splits, ragged,
+                                         kv_reuse, stream))
+    if key is not None and last[0] == key:
+        # the previous call's shapes, strides, dtypes, devices and settings:
+        # its validation and plan stand; only the data pointers change
+        args = last[1]
+        _set_pointers(args, q, k_cache, v_cache, block_tables, seq_lens, out, split_kv_workspace, append_k,
+                      append_v, slot_mapping)
+    else:
+        args, stream = _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size,
+                                    num_warps, kv_layout, num_stages, split_kv_workspace, num_splits, append_k,
+                                    append_v, slot_mapping, ragged, kv_reuse)
+        if key is None:
+            key = _launch_key(q, k_cache, v_cache, block_tables, seq_lens, out, split_kv_workspace, append_k,
+                              append_v, slot_mapping, (sm_scale, block_size, num_warps, kv_layout, num_stages,
+                                                       num_splits, ragged, kv_reuse, stream))
+        _LAST_LAUNCH.entry = (key, args)
     _lib.paged_decode(args, stream)
     return out
+
+
+# The last launch of each thread: (metadata key, PagedDecodeArgs).
+_LAST_LAUNCH = threading.local()
+
+
+def _launch_key(q, k_cache, v_cache, block_tables, seq_lens, out, workspace, append_k, append_v, slot_mapping,
+                settings):
+    """Everything the validation, the plan and the launch arguments depend on except data pointers:
+    each tensor's shape, strides, dtype and device, and the call's settings (with the stream, whose
+    workspace the library plans into)."""
+    def meta(t):
+        return None if t is None else (t.shape, t.stride(), t.dtype, t.device)
+
+    ws = None if workspace is None else tuple(meta(t) for t in workspace)
+    return (meta(q), meta(k_cache), meta(v_cache), meta(block_tables), meta(seq_lens), meta(out), ws,
+            meta(append_k), meta(append_v), meta(slot_mapping), settings)
+
+
+def _set_pointers(args, q, k_cache, v_cache, block_tables, seq_lens, out, workspace, append_k, append_v,
+                  slot_mapping):
+    args.q = q.data_ptr()
+    args.k_cache = k_cache.data_ptr()
+    args.v_cache = v_cache.data_ptr()
+    args.block_tables = block_tables.data_ptr()
+    args.seq_lens = seq_lens.data_ptr()
+    args.out = out.data_ptr()
+    if args.caller_workspace:
+        args.split_acc = workspace[0].data_ptr()
+        args.split_max = workspace[1].data_ptr()
+        args.split_sum = workspace[2].data_ptr()
+        args.workspace = tuple(workspace)
+    if append_k is not None:
+        args.append_k = append_k.data_ptr()
+        args.append_v = append_v.data_ptr()
+        args.slot_mapping = slot_mapping.data_ptr()
 
 
 def _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, block_size, num_warps, kv_layout,
@@ -425,6 +481,7 @@ def _decode_args(q, k_cache, v_cache, block_tables, seq_lens, out, sm_scale, blo
     # the workspace stays alive as long as the arguments that point into it
     # (a later, larger call may replace the stream's own workspace)
     args.workspace = (split_acc, split_max, split_sum)
+    args.caller_workspace = use_split_kv
     return args, stream
 
 

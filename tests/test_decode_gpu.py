@@ -496,3 +496,42 @@ def test_groups_above_16_fused_append_written_once(num_splits, hq, hkv, head_dim
     assert_close_to_oracle(out, expected)
     assert np.array_equal(bits16(k), bits16(k_expected))
     assert np.array_equal(bits16(v), bits16(v_expected))
+
+
+def test_repeated_calls_reuse_arguments_but_follow_every_pointer():
+    """paged_decode_attention_into keeps the last call's validated arguments when only data pointers change:
+    alternating inputs, caller workspaces and fused-append rows of one shape, then another shape, must each
+    give their own result."""
+    from flashdec_amd.paged_decode import paged_decode_attention_into
+
+    sets = [make_paged_inputs([300, 2048, 1], 16, 2, 128, 32, torch.bfloat16, seed=s) for s in (71, 72)]
+    other = make_paged_inputs([100, 40], 8, 2, 64, 16, torch.bfloat16, seed=73)
+    wss = [(torch.empty((3, 16, 4, 128), device="cuda"), torch.empty((3, 16, 4), device="cuda"),
+            torch.empty((3, 16, 4), device="cuda")) for _ in range(2)]
+    for rnd in range(3):
+        for i, (q, k, v, table, sl) in enumerate(sets):
+            out = torch.empty_like(q)
+            paged_decode_attention_into(q, k, v, table, sl, out)
+            assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+            out2 = torch.empty_like(q)
+            paged_decode_attention_into(q, k, v, table, sl, out2, split_kv_workspace=wss[(i + rnd) % 2], num_splits=4)
+            assert_close_to_oracle(out2, _oracle(q, k, v, table, sl))
+        q, k, v, table, sl = other
+        out = torch.empty_like(q)
+        paged_decode_attention_into(q, k, v, table, sl, out)
+        assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+    # fused append: each call's rows land at each call's slots
+    for s in (74, 75):
+        q, k, v, table, sl = make_paged_inputs([64, 257], 16, 2, 128, 32, torch.bfloat16, seed=s)
+        expected = _oracle(q, k, v, table, sl)
+        slots = torch.tensor(_slots(table, sl.cpu(), 32), device="cuda", dtype=torch.int64)
+        blk, off = slots // 32, slots % 32
+        ak, av = k[blk, :, off].clone(), v[blk, :, off].clone()
+        k_expected, v_expected = k.clone(), v.clone()
+        k[blk, :, off] = float("nan")
+        v[blk, :, off] = float("nan")
+        out = torch.empty_like(q)
+        paged_decode_attention_into(q, k, v, table, sl, out, append_k=ak, append_v=av, slot_mapping=slots)
+        assert_close_to_oracle(out, expected)
+        assert np.array_equal(bits16(k), bits16(k_expected))
+        assert np.array_equal(bits16(v), bits16(v_expected))
