@@ -23,13 +23,15 @@ when tables change.
 from __future__ import annotations
 
 import math
+import threading
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
 from . import _lib
-from .paged_decode import _auto_workspace, _cache_strides, _fill_common, _fill_workspace, _validate_inputs
+from .paged_decode import (_auto_workspace, _cache_strides, _fill_common, _fill_workspace, _launch_key,
+                           _validate_inputs)
 
 @dataclass(frozen=True)
 class CascadeGroups:
@@ -212,6 +214,31 @@ def paged_decode_attention_cascade_into(
     :func:`plan_chunk_rows`) is how many of a group's rows one prefix-role
     workgroup attends.
     """
+    key = None
+    last = getattr(_LAST_CASCADE, "entry", None)
+    if last is not None and isinstance(q, torch.Tensor) and q.is_cuda and isinstance(groups, CascadeGroups):
+        stream = _lib.current_stream_handle(q.device)
+        key = _cascade_key(q, k_cache, v_cache, block_tables, seq_lens, out, groups, workspace,
+                           (sm_scale, block_size, num_splits, prefix_splits, kv_reuse, chunk_rows, stream))
+        if last[0] == key:
+            # the previous call's metadata and settings: only data pointers change
+            args, cas = last[1]
+            args.q = q.data_ptr()
+            args.k_cache = k_cache.data_ptr()
+            args.v_cache = v_cache.data_ptr()
+            args.block_tables = block_tables.data_ptr()
+            args.seq_lens = seq_lens.data_ptr()
+            args.out = out.data_ptr()
+            if workspace is not None:
+                args.split_acc, args.split_max, args.split_sum = (t.data_ptr() for t in workspace)
+                args.workspace = tuple(workspace)
+            cas.group_members = groups.members.data_ptr()
+            cas.group_prefix_len = groups.prefix_len.data_ptr()
+            cas.row_prefix_len = groups.row_prefix_len.data_ptr()
+            _lib.paged_decode_cascade(args, cas, stream)
+            return out
+    sm_scale_in, block_size_in, num_splits_in, prefix_splits_in, chunk_rows_in = (sm_scale, block_size, num_splits,
+                                                                                   prefix_splits, chunk_rows)
     if block_size is None:
         if k_cache.dim() != 4:
             raise ValueError("k_cache must be a 4D tensor")
@@ -281,8 +308,30 @@ def paged_decode_attention_cascade_into(
     cas.row_prefix_len = groups.row_prefix_len.data_ptr()
     cas.max_prefix_len = groups.max_prefix_len
     cas.chunk_rows = chunk_rows
+    args.workspace = (acc, mx, sm)  # alive as long as the arguments that point into it
     _lib.paged_decode_cascade(args, cas, stream)
+    if key is None:
+        key = _cascade_key(q, k_cache, v_cache, block_tables, seq_lens, out, groups, workspace,
+                           (sm_scale_in, block_size_in, num_splits_in, prefix_splits_in, kv_reuse, chunk_rows_in,
+                            stream))
+    _LAST_CASCADE.entry = (key, (args, cas))
     return out
+
+
+# The last cascade launch of each thread: (metadata key, (PagedDecodeArgs, CascadeArgs)).
+_LAST_CASCADE = threading.local()
+
+
+def _cascade_key(q, k_cache, v_cache, block_tables, seq_lens, out, groups, workspace, settings):
+    """What a cascade launch's validation, plans and arguments depend on except data pointers: the
+    tensors' metadata, the groups' host figures and index-tensor metadata, and the settings."""
+    def meta(t):
+        return (t.shape, t.stride(), t.dtype, t.device)
+
+    figures = (groups.num_groups, groups.max_members, groups.max_prefix_len, groups.max_tail_len,
+               groups.total_tail_len, meta(groups.members), meta(groups.prefix_len), meta(groups.row_prefix_len))
+    return (_launch_key(q, k_cache, v_cache, block_tables, seq_lens, out, workspace, None, None, None, settings),
+            figures)
 
 
 def paged_decode_attention_cascade(q, k_cache, v_cache, block_tables, seq_lens, groups=None, sm_scale=None,

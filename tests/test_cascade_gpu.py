@@ -193,3 +193,27 @@ def test_unsupported_shapes_raise():
     g = cas.build_cascade_groups(table, lens, 16, 8, 2)
     with pytest.raises(RuntimeError, match="head_dim 128"):
         cas.paged_decode_attention_cascade(q, k, v, table, lens, groups=g)
+
+
+def test_repeated_cascade_calls_reuse_arguments_but_follow_every_pointer():
+    """The cascade entry keeps the last call's arguments when only data pointers change: two input sets
+    with their own groups objects, alternated, and a caller workspace swapped between calls, each give
+    their own result."""
+    cas = _cascade()
+    groups_def = [(13, [5, 0, 77, 1, 40]), (3, [9, 32])]
+    sets = []
+    for seed in (31, 32):
+        q, k, v, table, lens, _ = make_prefix_inputs(groups_def, [0, 50, 130], 16, 2, 32, torch.bfloat16, seed=seed)
+        sets.append((q, k, v, table, lens, cas.build_cascade_groups(table, lens, 32, 16, 2)))
+    wss = [(torch.empty((10, 16, 24, 128), device="cuda"), torch.empty((10, 16, 24), device="cuda"),
+            torch.empty((10, 16, 24), device="cuda")) for _ in range(2)]
+    for rnd in range(3):
+        for i, (q, k, v, table, lens, g) in enumerate(sets):
+            expected = _oracle(q, k, v, table, lens)
+            out = torch.empty_like(q)
+            cas.paged_decode_attention_cascade_into(q, k, v, table, lens, out, g)
+            assert_close_to_oracle(out, expected)
+            out2 = torch.empty_like(q)
+            cas.paged_decode_attention_cascade_into(q, k, v, table, lens, out2, g, num_splits=4, prefix_splits=8,
+                                                    workspace=wss[(i + rnd) % 2])
+            assert_close_to_oracle(out2, expected)
