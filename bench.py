@@ -417,12 +417,12 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
 
     q, k, v, table, lens, out = pool
     stream = _lib.current_stream_handle(q.device)
-    splits = _lib.paged_decode_plan(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], max(groups.max_tail_len, 1),
-                                    max(groups.total_tail_len, 1))
     chunk_rows = cascade.plan_chunk_rows(groups, q.shape[1], num_kv_heads)
-    psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads,
-                                         cascade.prefix_chunks(groups, q.shape[1], num_kv_heads, chunk_rows),
-                                         groups.max_prefix_len, cascade._num_cus(q.device))
+    chunks = cascade.prefix_chunks(groups, q.shape[1], num_kv_heads, chunk_rows)
+    psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads, chunks, groups.max_prefix_len,
+                                         cascade._num_cus(q.device))
+    splits = cascade.plan_tail_splits(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], groups,
+                                      groups.num_groups * num_kv_heads * chunks * psplits, cascade._num_cus(q.device))
     acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits + psplits, stream)
     args = _lib.PagedDecodeArgs()
     pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,

@@ -147,6 +147,26 @@ def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus
     return int(min(want, -(-tiles // 16), 1024))
 
 
+def plan_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, prefix_blocks, num_cus):
+    """Tail splits of a cascade launch: the fewest from half the library's plan for the tails alone
+    up to that plan that make the launch (``prefix_blocks`` prefix-role workgroups plus the
+    tail-role ones) whole waves of workgroups; the plan where none does.  The lower bound keeps a
+    tail-role workgroup at no more than about twice the tokens the plan gives it.
+
+    The tail-role workgroups run after the prefix role's, so the tails' own plan (sized as if they
+    had the GPU to themselves) can add a wave: same-box MI355X sweep, us/call by tail splits,
+    64 x 16384 (256 prefix-role workgroups, 128 rows x KV heads): 1: 40.2, 2: 39.4, 4: 42.5 (the
+    tails' plan), 8: 48.1; 32 x 8192 (256 + 64 per split): 2: 22.9, 4: 22.0, 8: 24.4.
+    """
+    base = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max(groups.max_tail_len, 1),
+                                  max(groups.total_tail_len, 1))
+    pairs = num_seqs * num_kv_heads
+    for splits in range(max(1, (base + 1) // 2), base + 1):
+        if (prefix_blocks + pairs * splits) % num_cus == 0:
+            return splits
+    return base
+
+
 # plan_chunk_rows: group rows (sharers x query heads per KV head) x prefix
 # tokens from which a 32-row chunk pays for its doubled per-unit work.  Same-box
 # MI355X sweep, best prefix splits each, 16- vs 32-row chunks (us/call):
@@ -259,17 +279,21 @@ def paged_decode_attention_cascade_into(
         raise ValueError("groups.prefix_len must have one entry per group")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(head_dim)
-    if num_splits is None:
-        num_splits = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim,
-                                            max(groups.max_tail_len, 1), max(groups.total_tail_len, 1))
     if chunk_rows is None:
         chunk_rows = plan_chunk_rows(groups, num_q_heads, num_kv_heads)
     if chunk_rows not in (16, _lib.CASCADE_MAX_CHUNK_ROWS):
         raise ValueError(f"chunk_rows must be 16 or {_lib.CASCADE_MAX_CHUNK_ROWS}")
+    chunks = prefix_chunks(groups, num_q_heads, num_kv_heads, chunk_rows)
     if prefix_splits is None:
-        prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads,
-                                           prefix_chunks(groups, num_q_heads, num_kv_heads, chunk_rows),
-                                           groups.max_prefix_len, _num_cus(q.device))
+        prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads, chunks, groups.max_prefix_len,
+                                           _num_cus(q.device))
+    if num_splits is None:
+        if isinstance(prefix_splits, int) and not isinstance(prefix_splits, bool) and prefix_splits > 0:
+            num_splits = plan_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups,
+                                          groups.num_groups * num_kv_heads * chunks * prefix_splits,
+                                          _num_cus(q.device))
+        else:
+            num_splits = 1  # the check below reports prefix_splits
     for name, v in (("num_splits", num_splits), ("prefix_splits", prefix_splits)):
         if isinstance(v, bool) or not isinstance(v, int) or v <= 0:
             raise ValueError(f"{name} must be a positive integer")

@@ -638,7 +638,8 @@ class DecodeEngine:
         if cascade:
             from ._lib import paged_decode_plan
             from .cache import _StagingRing
-            from .cascade import CascadeGroups, _num_cus, plan_chunk_rows, plan_prefix_splits, prefix_chunks
+            from .cascade import (CascadeGroups, _num_cus, plan_chunk_rows, plan_prefix_splits, plan_tail_splits,
+                                  prefix_chunks)
 
             ng = len(groups_now)
             mm = max(len(rows) for rows, _ in groups_now)
@@ -655,13 +656,12 @@ class DecodeEngine:
                                    max_tail_len=max(tails), total_tail_len=sum(tails))
             gc = _GraphCascade(groups=groups, buf=buf, num_groups=ng, max_members=mm,
                                staging=_StagingRing(buf.numel() * 4))
-            if num_splits is None:
-                num_splits = paged_decode_plan(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim,
-                                               groups.max_tail_len, groups.total_tail_len)
             chunk_rows = gc.chunk_rows = plan_chunk_rows(groups, num_q_heads, cache.num_kv_heads)
-            prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads,
-                                               prefix_chunks(groups, num_q_heads, cache.num_kv_heads, chunk_rows),
-                                               groups.max_prefix_len, _num_cus(dev))
+            chunks = prefix_chunks(groups, num_q_heads, cache.num_kv_heads, chunk_rows)
+            prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads, chunks, groups.max_prefix_len, _num_cus(dev))
+            if num_splits is None:
+                num_splits = plan_tail_splits(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim, groups,
+                                              ng * cache.num_kv_heads * chunks * prefix_splits, _num_cus(dev))
         if cascade:
             splits = int(num_splits)
             if splits <= 0:

@@ -55,3 +55,34 @@ def test_plan_fills_whole_waves_when_it_can():
     for pairs_b in (1, 2, 4, 8, 16, 32, 64, 128):
         s = _lib.paged_decode_plan(pairs_b, 16, 2, 128, 65536, pairs_b * 65536)
         assert (pairs_b * 2 * s) % 256 == 0, (pairs_b, s)
+
+
+# Cascade tail splits (flashdec_amd.cascade.plan_tail_splits): the fewest in
+# [ceil(plan / 2), plan] that make prefix-role plus tail-role workgroups whole
+# waves of 256, else the tails' own plan.  Tails ~ U{1..512} on the bench's
+# shared-prefix sizes: (rows, prefix-role workgroups, max tail, total tail).
+TAIL_CASES = [
+    # 64 rows on 16384 tokens: 256 prefix-role workgroups, 128 pairs; plan 4, 2 gives 512
+    ((64, 256, 512, 64 * 256), 4, 2),
+    # 128 rows: 256 + 256 per split; plan 2, 1 gives 512
+    ((128, 256, 512, 128 * 256), 2, 1),
+    # 32 rows: 256 + 64 per split; plan 4, and only 4 in [2, 4] gives whole waves
+    ((32, 256, 512, 32 * 256), 4, 4),
+    # 16 rows: 128 + 32 per split; 4 gives 256
+    ((16, 128, 512, 16 * 256), 4, 4),
+    # 8 rows of 8192-token tails beside 240 prefix-role workgroups: 1 split would fill the
+    # wave but holds 8192 tokens a workgroup; none in [8, 16] does, so the plan (16)
+    ((8, 240, 8192, 8 * 8192), 16, 16),
+]
+
+
+@pytest.mark.parametrize(("shape", "plan", "splits"), TAIL_CASES)
+def test_cascade_tail_split_cases(shape, plan, splits):
+    from types import SimpleNamespace
+
+    from flashdec_amd import _lib, cascade
+
+    rows, prefix_blocks, max_tail, total_tail = shape
+    groups = SimpleNamespace(max_tail_len=max_tail, total_tail_len=total_tail)
+    assert _lib.paged_decode_plan(rows, 16, 2, 128, max_tail, total_tail) == plan
+    assert cascade.plan_tail_splits(rows, 16, 2, 128, groups, prefix_blocks, 256) == splits
