@@ -953,6 +953,15 @@ struct alignas(16) DecodeLds {
   int last;
 };
 
+// The hardware dispatches consecutive workgroup ids round-robin over the
+// XCDs (8 on MI355X, each with its own L2).  With per_xcd = grid / 8 (a grid
+// of a multiple of 8 workgroups), the i-th workgroup on XCD x takes logical
+// index x * per_xcd + i, so each run of per_xcd consecutive logical
+// workgroups shares one XCD; per_xcd 0 keeps the hardware order.
+__device__ __forceinline__ int xcd_logical_block(int block, int per_xcd) {
+  return per_xcd > 0 ? (block & 7) * per_xcd + (block >> 3) : block;
+}
+
 // DM: dim-major cache (load_unit_dm), staged through the LDS at kstage.
 // PRE: the block-table arguments arrived preloaded in SGPRs (decode_mfma_kernel).
 // NCB: 16-row column blocks per wave (prefix role only)
@@ -1389,7 +1398,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 // D: head_dim 128 or 64.  NCB: 16-column blocks of query heads per wave (2
 // for groups of more than 16 heads per KV head).
 //
-// The leading scalar arguments repeat what the first block-table load needs.
+// The leading scalar arguments repeat what the first block-table load needs,
+// with the grid's XCD layout (xcd_blocks, for xcd_logical_block).
 // The library is built with amdgpu-kernarg-preload-count, so the command
 // processor writes them into SGPRs at wave launch: the table load issues
 // without waiting for a kernel-argument fetch from a cold scalar cache, and
@@ -1400,7 +1410,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 128, int NCB = 1>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
     const void* bt, int64_t bts0, int64_t bts1, int64_t max_blocks_per_seq, int32_t splits, int32_t hkv,
-    int32_t group, int32_t hint_tps, int32_t bt_i64, DecodeParams p) {
+    int32_t group, int32_t hint_tps, int32_t bt_i64, int32_t xcd_blocks, DecodeParams p) {
   __shared__ DecodeLds<waves_for<UNIT>()> lds;
   DecodeParams q = p;
   q.bt = bt;
@@ -1413,7 +1423,7 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   q.hint_tps = hint_tps;
   q.bt_i64 = bt_i64;
   decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT, D, waves_for<UNIT>(), false, true, NCB>(
-      q, CascadeParams{}, blockIdx.x, lds);
+      q, CascadeParams{}, xcd_logical_block(blockIdx.x, xcd_blocks), lds);
 }
 
 // Dim-major caches: 32-token units on kDmWaves waves, K staged through LDS.
@@ -1425,11 +1435,12 @@ constexpr int kDmPerCU = 2;
 // FUSE: fused current-token append.  Its variant runs one workgroup per CU:
 // within two per CU (256 registers a wave) the 128-dim variant spilled.
 template <typename T, int BS, bool NT, int D, int FUSE>
-__global__ __launch_bounds__(64 * kDmWaves, FUSE ? 1 : kDmPerCU) void decode_dm_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kDmWaves, FUSE ? 1 : kDmPerCU) void decode_dm_kernel(DecodeParams p,
+                                                                                       int32_t xcd_blocks) {
   __shared__ DecodeLds<kDmWaves> lds;
   __shared__ __attribute__((aligned(16))) uint8_t stage[kDmWaves * D * kDmRowBytes];
-  decode_role<T, BS, FUSE, false, 32, Role::kRow, NT, D, kDmWaves, true>(p, CascadeParams{}, blockIdx.x, lds,
-                                                                         stage);
+  decode_role<T, BS, FUSE, false, 32, Role::kRow, NT, D, kDmWaves, true>(
+      p, CascadeParams{}, xcd_logical_block(blockIdx.x, xcd_blocks), lds, stage);
 }
 
 // Balanced splits (ragged batches): the row and split of each workgroup come
@@ -1652,7 +1663,7 @@ __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
 // (zero length, or a padding slot) has denominator 0 in every split, which
 // selects the zero row below just as the length test does.
 template <typename T, int D, int MODE, int W, bool PRE>
-__device__ __forceinline__ void reduce_row(const ReduceParams& p) {
+__device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row = blockIdx.x) {
   static_assert(!PRE || MODE == kReducePlain, "preloaded reducer arguments are for the plain merge");
   if constexpr (!PRE) {
     // every argument in SGPRs before any use: one batch of argument loads,
@@ -1663,8 +1674,8 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p) {
                  "s"(p.os2), "s"(p.sls), "s"(p.slots), "s"(p.hq), "s"(p.splits), "s"(p.fuse), "s"(p.sl_i64),
                  "s"(p.slot_i64));
   }
-  const int b = blockIdx.x / p.hq;
-  const int qh = blockIdx.x % p.hq;
+  const int b = row / p.hq;
+  const int qh = row % p.hq;
   const int lane = threadIdx.x & 63;
   const int wave = W > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
   constexpr int E = D / 64;  // dims per lane
@@ -1692,8 +1703,8 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p) {
     const int tiles = static_cast<int>((eff_of(__builtin_amdgcn_readfirstlane(seq_len)) + 31) / 32);
     splits = min(max(1, (tiles + tps - 1) / tps), p.splits);
   }
-  const int64_t sb = PRE ? blockIdx.x * p.ss1 : b * p.ss0 + qh * p.ss1;
-  const float* ab = p.acc + (PRE ? blockIdx.x * p.as1 : b * p.as0 + qh * p.as1);
+  const int64_t sb = PRE ? row * p.ss1 : b * p.ss0 + qh * p.ss1;
+  const float* ab = p.acc + (PRE ? row * p.as1 : b * p.as0 + qh * p.as1);
   const int64_t as3 = PRE ? 1 : p.as3;
   const int64_t ss2 = PRE ? 1 : p.ss2;
   float M = -INFINITY;
@@ -1791,7 +1802,8 @@ __global__ __launch_bounds__(64 * W) void split_reduce_kernel(ReduceParams p) {
 template <typename T, int D, int W = 1>
 __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* acc, const float* mx, const float* sm,
                                                                   int64_t as1, int64_t as2, int64_t ss1,
-                                                                  int32_t splits, int32_t hq, ReduceParams p) {
+                                                                  int32_t splits, int32_t hq, int32_t xcd_rows,
+                                                                  ReduceParams p) {
   ReduceParams q = p;
   q.acc = acc;
   q.mx = mx;
@@ -1801,7 +1813,7 @@ __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* a
   q.ss1 = ss1;
   q.splits = splits;
   q.hq = hq;
-  reduce_row<T, D, kReducePlain, W, true>(q);
+  reduce_row<T, D, kReducePlain, W, true>(q, xcd_logical_block(blockIdx.x, xcd_rows));
 }
 
 // ========================================================== host glue ====
@@ -1876,11 +1888,39 @@ void dispatch(F kernel, dim3 grid, dim3 block, hipStream_t stream, void* start, 
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
 }
 
+// Workgroups per (request, KV head, split) of the MFMA row kernel: one for
+// up to 16 query heads per KV head, else one per 32 (two column blocks).
+int64_t row_head_blocks(int64_t group) {
+  return group > 16 ? (group + 16 * kRowWideColBlocks - 1) / (16 * kRowWideColBlocks) : 1;
+}
+
+// A streaming row kernel's grid is laid out XCD by XCD (xcd_logical_block)
+// when it is a multiple of 8 workgroups and each (request, KV head) has at
+// least kXcdMinPairBlocks of them (splits x head blocks): they then share the
+// q rows, the block-table row and, across head blocks, the K/V through one
+// XCD's L2 instead of fetching them into several.  Same-box MI355X A/B,
+// us/call: C2 (B8 ctx2048, 16 splits) 8.74 -> 8.41, attention kernel 5.39 ->
+// 5.18; B16 x 8192 G71 D64 (3 head blocks, 5 splits) 27.4 -> 22.8; G32 32.2
+// -> 31.6; dim-major D128 27.0 -> 26.5.  With 2 splits (B64 ctx8192) the
+// kernel measured 1 % slower (91.7 -> 92.7 us), hence the threshold.  Cached
+// loads (kv_reuse) keep the hardware order: rows sharing a prefix then read
+// its tiles on the same XCDs (consecutive workgroups are splits of one row,
+// and a split's tile range recurs on the same XCD every 4 rows at 10
+// splits), which the XCD-by-XCD layout breaks: 64 rows on a 16384-token
+// prefix, 94.8 -> 114.0 us.
+constexpr int64_t kXcdMinPairBlocks = 4;
+
+// Workgroups per XCD for xcd_logical_block (0: hardware order)
+int32_t row_xcd_blocks(unsigned grid, int64_t pair_blocks, bool nt) {
+  return nt && grid % 8 == 0 && pair_blocks >= kXcdMinPairBlocks ? static_cast<int32_t>(grid / 8) : 0;
+}
+
 // decode_mfma_kernel's arguments: the preloaded block-table fields, then the parameter block
 template <typename K>
-void dispatch_mfma(K kernel, dim3 grid, dim3 block, hipStream_t stream, void* const* ev, const DecodeParams& p) {
+void dispatch_mfma(K kernel, dim3 grid, dim3 block, hipStream_t stream, void* const* ev, const DecodeParams& p,
+                   bool nt) {
   dispatch(kernel, grid, block, stream, ev[0], ev[1], p.bt, p.bts0, p.bts1, p.max_blocks_per_seq, p.splits, p.hkv,
-           p.group, p.hint_tps, p.bt_i64, p);
+           p.group, p.hint_tps, p.bt_i64, row_xcd_blocks(grid.x, p.splits * row_head_blocks(p.group), nt), p);
 }
 
 template <typename T, int BS, int UNIT, bool NT>
@@ -1890,24 +1930,24 @@ void launch_mfma_unit(const DecodeParams& p, dim3 grid, hipStream_t stream, void
   if (p.head_dim == 64) {
     // head_dim 64: the host gives it no RoPE and no in-launch merge
     if (p.fuse)
-      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, UNIT, NT, 64>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, UNIT, NT, 64>, grid, block, stream, ev, p, NT);
     else
-      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, UNIT, NT, 64>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, UNIT, NT, 64>, grid, block, stream, ev, p, NT);
     return;
   }
   if (p.fuse && p.rope_dim > 0) {
     // the host refuses RoPE with the in-launch merge
-    dispatch_mfma(decode_mfma_kernel<T, BS, 2, false, UNIT, NT>, grid, block, stream, ev, p);
+    dispatch_mfma(decode_mfma_kernel<T, BS, 2, false, UNIT, NT>, grid, block, stream, ev, p, NT);
   } else if (p.fuse) {
     if (merge)
-      dispatch_mfma(decode_mfma_kernel<T, BS, 1, true, UNIT, NT>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, true, UNIT, NT>, grid, block, stream, ev, p, NT);
     else
-      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, UNIT, NT>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, UNIT, NT>, grid, block, stream, ev, p, NT);
   } else {
     if (merge)
-      dispatch_mfma(decode_mfma_kernel<T, BS, 0, true, UNIT, NT>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, true, UNIT, NT>, grid, block, stream, ev, p, NT);
     else
-      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, UNIT, NT>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, UNIT, NT>, grid, block, stream, ev, p, NT);
   }
 }
 
@@ -1924,14 +1964,14 @@ void launch_mfma_wide(const DecodeParams& p, dim3 grid, hipStream_t stream, void
   const dim3 block(64 * waves_for<16>());
   if (p.head_dim == 64) {
     if (p.fuse)
-      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, 16, NT, 64, W>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, 16, NT, 64, W>, grid, block, stream, ev, p, NT);
     else
-      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, 16, NT, 64, W>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, 16, NT, 64, W>, grid, block, stream, ev, p, NT);
   } else {
     if (p.fuse)
-      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, 16, NT, 128, W>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 1, false, 16, NT, 128, W>, grid, block, stream, ev, p, NT);
     else
-      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, 16, NT, 128, W>, grid, block, stream, ev, p);
+      dispatch_mfma(decode_mfma_kernel<T, BS, 0, false, 16, NT, 128, W>, grid, block, stream, ev, p, NT);
   }
 }
 
@@ -1960,16 +2000,16 @@ void launch_mfma(const DecodeParams& p, bool nt, dim3 grid, hipStream_t stream, 
 
 template <typename T, int D, int FUSE>
 void launch_dm(const DecodeParams& p, int64_t block_size, bool nt, dim3 grid, dim3 block, hipStream_t stream,
-               void* const* ev) {
+               void* const* ev, int32_t xcd) {
   if (block_size == 8)
-    nt ? dispatch(decode_dm_kernel<T, 8, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p)
-       : dispatch(decode_dm_kernel<T, 8, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p);
+    nt ? dispatch(decode_dm_kernel<T, 8, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p, xcd)
+       : dispatch(decode_dm_kernel<T, 8, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p, xcd);
   else if (block_size == 16)
-    nt ? dispatch(decode_dm_kernel<T, 16, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p)
-       : dispatch(decode_dm_kernel<T, 16, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p);
+    nt ? dispatch(decode_dm_kernel<T, 16, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p, xcd)
+       : dispatch(decode_dm_kernel<T, 16, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p, xcd);
   else
-    nt ? dispatch(decode_dm_kernel<T, 32, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p)
-       : dispatch(decode_dm_kernel<T, 32, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p);
+    nt ? dispatch(decode_dm_kernel<T, 32, true, D, FUSE>, grid, block, stream, ev[0], ev[1], p, xcd)
+       : dispatch(decode_dm_kernel<T, 32, false, D, FUSE>, grid, block, stream, ev[0], ev[1], p, xcd);
 }
 
 ReduceParams reduce_params(const DecodeParams& p) {
@@ -2010,15 +2050,19 @@ bool reduce_layout_packed(const ReduceParams& r) {
   return r.as3 == 1 && r.ss2 == 1 && r.as0 == r.hq * r.as1 && r.ss0 == r.hq * r.ss1;
 }
 
+// xcd_rows: the plain merge of a row kernel laid out XCD by XCD takes the same
+// layout (grid / 8 rows per XCD), so that each row's merge runs on the XCD
+// whose workgroups wrote its partials; false keeps the hardware order.
 template <typename T, int MODE>
-int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStream_t stream) {
+int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStream_t stream, bool xcd_rows = false) {
   const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
   void* e0 = a.timing_events[2];
   void* e1 = a.timing_events[3];
   if (MODE == kReducePlain && reduce_layout_packed(r)) {
     // the partials' addressing leads the argument list (preloaded into SGPRs)
     auto pre = [&](auto kernel, dim3 block) {
-      dispatch(kernel, grid, block, stream, e0, e1, r.acc, r.mx, r.sm, r.as1, r.as2, r.ss1, r.splits, r.hq, r);
+      dispatch(kernel, grid, block, stream, e0, e1, r.acc, r.mx, r.sm, r.as1, r.as2, r.ss1, r.splits, r.hq,
+               xcd_rows && grid.x % 8 == 0 ? static_cast<int32_t>(grid.x / 8) : 0, r);
     };
     if (r.splits > 32) {
       if (a.head_dim == 64)
@@ -2047,12 +2091,6 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
 }
 
 
-// Workgroups per (request, KV head, split) of the MFMA row kernel: one for
-// up to 16 query heads per KV head, else one per 32 (two column blocks).
-int64_t row_head_blocks(int64_t group) {
-  return group > 16 ? (group + 16 * kRowWideColBlocks - 1) / (16 * kRowWideColBlocks) : 1;
-}
-
 template <typename T>
 int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t stream) {
   const int64_t pairs = a.num_seqs * a.num_kv_heads;
@@ -2068,6 +2106,7 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   // heads, no fused append and a workspace
   const bool balanced = p.bal_target > 0 && fast && narrow && !p.fuse && p.splits > 1;
   if (!balanced) p.bal_target = 0;
+  bool xcd = false;  // the row kernel's grid laid out XCD by XCD
   if (balanced) {
     p.counters = nullptr;
     // sum over rows of ceil(tiles_b / T) <= bal_target + num_seqs
@@ -2091,6 +2130,7 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   } else if (fast) {
     const int64_t hblocks = row_head_blocks(p.group);
     const dim3 grid(static_cast<unsigned>(pairs * hblocks * p.splits));
+    xcd = row_xcd_blocks(grid.x, p.splits * hblocks, nt) > 0;
     switch (a.block_size) {
       case 8: launch_mfma<T, 8>(p, nt, grid, stream, a.timing_events); break;
       case 16: launch_mfma<T, 16>(p, nt, grid, stream, a.timing_events); break;
@@ -2101,12 +2141,14 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
     const dim3 grid(static_cast<unsigned>(pairs * hblocks * p.splits));
     const dim3 block(64 * kDmWaves);
     void* const* ev = a.timing_events;
+    const int32_t per_xcd = row_xcd_blocks(grid.x, p.splits * hblocks, nt);
+    xcd = per_xcd > 0;
     if (a.head_dim == 64)
-      p.fuse ? launch_dm<T, 64, 1>(p, a.block_size, nt, grid, block, stream, ev)
-             : launch_dm<T, 64, 0>(p, a.block_size, nt, grid, block, stream, ev);
+      p.fuse ? launch_dm<T, 64, 1>(p, a.block_size, nt, grid, block, stream, ev, per_xcd)
+             : launch_dm<T, 64, 0>(p, a.block_size, nt, grid, block, stream, ev, per_xcd);
     else
-      p.fuse ? launch_dm<T, 128, 1>(p, a.block_size, nt, grid, block, stream, ev)
-             : launch_dm<T, 128, 0>(p, a.block_size, nt, grid, block, stream, ev);
+      p.fuse ? launch_dm<T, 128, 1>(p, a.block_size, nt, grid, block, stream, ev, per_xcd)
+             : launch_dm<T, 128, 0>(p, a.block_size, nt, grid, block, stream, ev, per_xcd);
   } else {
     const int hg = static_cast<int>((p.group + kGenHeads - 1) / kGenHeads);
     const dim3 grid(static_cast<unsigned>(pairs * hg), static_cast<unsigned>(p.splits));
@@ -2121,7 +2163,7 @@ int launch_decode(const fd_paged_decode_args& a, DecodeParams& p, hipStream_t st
   if (p.splits > 1 && p.counters == nullptr) {
     const ReduceParams r = reduce_params(p);
     const int rc =
-        balanced ? launch_reduce<T, kReduceBalanced>(a, r, stream) : launch_reduce<T, kReducePlain>(a, r, stream);
+        balanced ? launch_reduce<T, kReduceBalanced>(a, r, stream) : launch_reduce<T, kReducePlain>(a, r, stream, xcd);
     if (rc != FD_OK) return rc;
   }
   return FD_OK;
