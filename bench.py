@@ -25,8 +25,9 @@ Timing:
 * ``roofline.traffic``: HBM bytes per attention-kernel dispatch from the
   committed PMC summary ``profiles/decode_mfma_b8_ctx2048_traffic.json``
   (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null.
-* ``cpu_baseline``: the repo's numpy oracle on this host's cores (the rows of
-  a call spread over a process pool, one BLAS thread per process), on C1 and
+* ``cpu_baseline``: the repo's numpy oracle on this host's cores (the (row,
+  KV head) pairs of a call spread over a process pool, one BLAS thread per
+  process), on C1 and
   on the C2 call at ctx1024 and ctx2048: p50 of >= 20 calls after 3 warm-ups,
   with ``os.cpu_count()`` and the CPU model.  It runs first, before this
   process touches the GPU.
@@ -201,8 +202,8 @@ def cpu_inputs(name):
 
 
 _CPU_WORKER = {}
-# CPU-baseline configs and their rows per call
-CPU_CONFIGS = {"C1": 4, "C2-ctx1024": 8, "C2": 8}
+# CPU-baseline configs: (rows, KV heads) per call; a work item is one (row, KV head)
+CPU_CONFIGS = {"C1": (4, 2), "C2-ctx1024": (8, 2), "C2": (8, 2)}
 
 
 def _cpu_worker_init():
@@ -214,34 +215,44 @@ def _cpu_worker_init():
         _CPU_WORKER[name] = cpu_inputs(name)
 
 
-def _cpu_row(name, b):
-    """The oracle on row ``b`` of a config (runs in a worker)."""
+def _cpu_item(name, item):
+    """The oracle on one (row, KV head) of a config: the row's query heads of that KV head (runs in a worker)."""
     from oracle.attention import paged_decode_attention as oracle_decode
 
     (q, k, v, table, lens), scale, out_dtype, _ = _CPU_WORKER[name]
-    return oracle_decode(q[b:b + 1], k, v, table[b:b + 1], lens[b:b + 1], sm_scale=scale, out_dtype=out_dtype)
+    hkv = k.shape[1]
+    b, h = divmod(item, hkv)
+    group = q.shape[1] // hkv
+    return oracle_decode(q[b:b + 1, h * group:(h + 1) * group], k[:, h:h + 1], v[:, h:h + 1], table[b:b + 1],
+                         lens[b:b + 1], sm_scale=scale, out_dtype=out_dtype)
 
 
-def cpu_time_p50(fn, warmup=3, reps=20, budget_s=10.0):
-    """p50 seconds of fn() after ``warmup`` calls, over >= ``reps`` calls (more while under budget)."""
+def _cpu_worker_share(name, items, warmup, reps):
+    """Per-call seconds of this worker's share (``items``) of a call, over ``reps`` calls after
+    ``warmup`` (runs in a worker; the call's other shares run at the same time on other workers)."""
     for _ in range(warmup):
-        fn()
+        for item in items:
+            _cpu_item(name, item)
     times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < reps or (time.perf_counter() < t_end and len(times) < 200):
+    for _ in range(reps):
         t0 = time.perf_counter()
-        fn()
+        for item in items:
+            _cpu_item(name, item)
         times.append(time.perf_counter() - t0)
-    return statistics.median(times), len(times)
+    return times
 
 
 def cpu_baseline(budget_s):
     """The numpy oracle (restatement of paged_reference.py:19-125) on this host's cores.
 
-    Rows of a call are independent: each call hands its rows to a process
-    pool of min(os.cpu_count(), 16, rows) workers (one BLAS thread each).
+    The (row, KV head) pairs of a call are independent, so each of
+    min(os.cpu_count(), 16, pairs) worker processes (one BLAS thread each)
+    takes a fixed share of them and runs that share call after call; a call's
+    time is the slowest share's time for it.  The workers run their calls
+    concurrently and report per-call times, so the figure is the port's
+    compute on that many cores, without a process-pool round trip per call.
     Timed on C1 and on the C2 call at ctx1024 and ctx2048: p50 of >= 20
-    calls after 3 warm-ups.
+    calls after 3 warm-ups (more calls while within the budget, at most 200).
     Runs before this process touches the GPU (the workers are started as
     fresh processes).
     """
@@ -249,20 +260,22 @@ def cpu_baseline(budget_s):
     from concurrent.futures import ProcessPoolExecutor
 
     n_cpu = os.cpu_count() or 1
-    rows = CPU_CONFIGS
-    workers = min(n_cpu, 16, max(rows.values()))
+    items = {name: rows * hkv for name, (rows, hkv) in CPU_CONFIGS.items()}
+    workers = min(n_cpu, 16, max(items.values()))
     results = {}
     with ProcessPoolExecutor(max_workers=workers, mp_context=mp.get_context("spawn"),
                              initializer=_cpu_worker_init) as ex:
-        for name, n in rows.items():
+        for name, n in items.items():
             nbytes = cpu_inputs(name)[3]
-
-            def one_call(name=name, n=n):
-                list(ex.map(_cpu_row, [name] * n, range(n)))
-
-            sec, reps = cpu_time_p50(one_call, budget_s=budget_s / len(rows))
+            w = min(workers, n)
+            shares = [list(range(i, n, w)) for i in range(w)]
+            # one call's slowest share, measured once, sizes the sample to the budget
+            probe = max(ex.map(_cpu_worker_share, [name] * w, shares, [1] * w, [1] * w), key=lambda t: t[0])[0]
+            reps = int(min(200, max(20, budget_s / len(items) / max(probe, 1e-6))))
+            per_share = list(ex.map(_cpu_worker_share, [name] * w, shares, [3] * w, [reps] * w))
+            sec = statistics.median(max(t[r] for t in per_share) for r in range(reps))
             results[name] = {"us_per_call": round(sec * 1e6, 1), "gb_per_s": round(nbytes / sec / 1e9, 4),
-                             "processes": min(workers, n), "calls": reps, "algorithmic_bytes": nbytes}
+                             "processes": w, "calls": reps, "algorithmic_bytes": nbytes}
     return results, n_cpu
 
 
@@ -1112,7 +1125,8 @@ def main():
             "cores": c2["processes"],
             "kind": "port",
             "sample": f"numpy oracle (oracle/attention.py, restating paged_reference.py:19-125) on the full "
-                      f"B8 ctx2048 call, its rows on {c2['processes']} worker processes (one BLAS thread each), "
+                      f"B8 ctx2048 call, its 16 (row, KV head) pairs shared by {c2['processes']} worker processes (one "
+                      f"BLAS thread each, each running its share call after call; a call = its slowest share), "
                       f"p50 of {c2['calls']} calls after 3 warm-ups: {c2['us_per_call']:.0f} us/call",
             "os_cpu_count": n_cpu,
             "cpu_model": cpu_model(),
