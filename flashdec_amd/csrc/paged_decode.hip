@@ -836,6 +836,12 @@ constexpr int64_t kMaxSplitTiles = 64;  // split planning: tiles of the longest 
 // every workgroup's atomic on that line (measured ~3x slower arrival).
 constexpr int kCounterStride = FD_SPLIT_COUNTER_STRIDE;
 
+// An output row's eight elements.  ``out`` may be any strided view (the
+// reference indexes it through its strides), so with unit dim stride the
+// 16-byte store can be unaligned: gfx9+ global memory runs in the
+// unaligned-access mode, which splits such a store in hardware (checked on
+// views one element past an aligned base in tests/test_unaligned_views_gpu.py;
+// the split partials' 16-byte stores below take caller workspaces the same way).
 template <typename T>
 __device__ __forceinline__ void store_row(const DecodeParams& p, int b, int qh, int d0, const float (&o)[8],
                                           float inv) {
