@@ -432,10 +432,8 @@ def cascade_prepared(torch, pool, groups, sm_scale, block_size, num_kv_heads):
     stream = _lib.current_stream_handle(q.device)
     chunk_rows = cascade.plan_chunk_rows(groups, q.shape[1], num_kv_heads)
     chunks = cascade.prefix_chunks(groups, q.shape[1], num_kv_heads, chunk_rows)
-    psplits = cascade.plan_prefix_splits(groups.num_groups, num_kv_heads, chunks, groups.max_prefix_len,
-                                         cascade._num_cus(q.device))
-    splits = cascade.plan_tail_splits(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], groups,
-                                      groups.num_groups * num_kv_heads * chunks * psplits, cascade._num_cus(q.device))
+    psplits, splits = cascade.plan_cascade_splits(q.shape[0], q.shape[1], num_kv_heads, q.shape[2], groups, chunks,
+                                                  cascade._num_cus(q.device))
     acc, mx, sm, _ = pd._auto_workspace(q, num_kv_heads, splits + psplits, stream)
     args = _lib.PagedDecodeArgs()
     pd._fill_common(args, q, k, v, pd._cache_strides(k, 2, 3), pd._cache_strides(v, 2, 3), table, lens, out,

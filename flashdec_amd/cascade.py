@@ -133,18 +133,37 @@ def build_cascade_groups(block_tables, seq_lens, block_size, num_q_heads, num_kv
     )
 
 
-def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus):
+def plan_prefix_splits(num_groups, num_kv_heads, chunks, max_prefix_len, num_cus, share=1.0, min_tiles=16):
     """Prefix partials per (group, KV head, chunk of ``FD_CASCADE_CHUNK_ROWS`` rows).
 
-    About one prefix-role workgroup per CU, and at least 16 prefix tiles per
-    split.  Best of a same-box sweep on MI355X (sharers x prefix tokens:
-    prefix splits chosen -> cascade vs per-row us/call): 16 x 4096: 8 ->
-    14.2 vs 14.5; 32 x 8192: 8 -> 23.4 vs 32.8; 64 x 16384: 4 -> 50.5 vs
-    96.0; 128 x 16384: 2 -> 88.7 vs 183.0.
+    About ``share`` of the CUs take one prefix-role workgroup each, and a
+    split holds at least ``min_tiles`` prefix tiles.  With the defaults, the
+    best of a same-box sweep on MI355X (sharers x prefix tokens: prefix splits
+    chosen -> cascade vs per-row us/call): 16 x 4096: 8 -> 14.2 vs 14.5;
+    32 x 8192: 8 -> 23.4 vs 32.8; 64 x 16384: 4 -> 50.5 vs 96.0; 128 x 16384:
+    2 -> 88.7 vs 183.0 (each split's tail count planned on its own).
+    :func:`plan_cascade_splits` plans both counts together.
     """
     tiles = max(1, -(-max_prefix_len // 32))
-    want = max(1, num_cus // max(1, num_groups * num_kv_heads * chunks))
-    return int(min(want, -(-tiles // 16), 1024))
+    want = max(1, int(num_cus * share) // max(1, num_groups * num_kv_heads * chunks))
+    return int(min(want, -(-tiles // min_tiles), 1024))
+
+
+def _whole_wave_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, prefix_blocks, num_cus,
+                            prefix_tiles=None):
+    """(the tails' own plan, the fewest tail splits that make the launch whole waves or None)."""
+    base = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max(groups.max_tail_len, 1),
+                                  max(groups.total_tail_len, 1))
+    pairs = num_seqs * num_kv_heads
+    low = max(1, (base + 1) // 2)
+    if prefix_tiles is not None:
+        # a tail-role workgroup may also be as long as a prefix-role one
+        tail_tiles = max(1, -(-groups.max_tail_len // 32))
+        low = min(low, max(1, -(-tail_tiles // max(1, prefix_tiles))))
+    for splits in range(low, base + 1):
+        if (prefix_blocks + pairs * splits) % num_cus == 0:
+            return base, splits
+    return base, None
 
 
 def plan_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, prefix_blocks, num_cus):
@@ -158,21 +177,46 @@ def plan_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, pref
     64 x 16384 (256 prefix-role workgroups, 128 rows x KV heads): 1: 40.2, 2: 39.4, 4: 42.5 (the
     tails' plan), 8: 48.1; 32 x 8192 (256 + 64 per split): 2: 22.9, 4: 22.0, 8: 24.4.
     """
-    base = _lib.paged_decode_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, max(groups.max_tail_len, 1),
-                                  max(groups.total_tail_len, 1))
-    pairs = num_seqs * num_kv_heads
-    for splits in range(max(1, (base + 1) // 2), base + 1):
-        if (prefix_blocks + pairs * splits) % num_cus == 0:
-            return splits
-    return base
+    base, splits = _whole_wave_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, prefix_blocks,
+                                           num_cus)
+    return base if splits is None else splits
+
+
+def plan_cascade_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, chunks, num_cus):
+    """(prefix splits, tail splits) of a cascade launch over ``chunks`` prefix chunks per (group, KV head).
+
+    The launch's time is its longest workgroup's, and a prefix-role workgroup
+    streams its tiles through one CU's vector memory path (the prefix is read
+    from L2 by every chunk), so the plan first gives the prefix role about
+    three quarters of the CUs, at least 8 tiles a split, and the tail role
+    the rest of one wave (a tail-role workgroup no longer than a prefix-role
+    one); where no tail split count fills whole waves it falls back to one
+    prefix-role workgroup per CU (:func:`plan_prefix_splits`,
+    :func:`plan_tail_splits`).  Same-box MI355X sweep, us/call (chunk rows /
+    prefix splits / tail splits): 16 x 4096: 16/12/2 13.48 (16/8/4, the
+    earlier plan, 14.68; 16/14/1 14.04; 16/10/2 13.96); 32 x 8192: 32/12/1
+    18.59, 32/12/2 18.36 (16/8/4, the earlier plan, 22.03); 64 x 16384: 32/8/2
+    36.98 (32/6/2 37.48).
+    """
+    units = max(1, groups.num_groups * num_kv_heads * chunks)
+    prefix_tiles = max(1, -(-groups.max_prefix_len // 32))
+    for share, min_tiles in ((0.75, 8), (1.0, 16)):
+        sp = plan_prefix_splits(groups.num_groups, num_kv_heads, chunks, groups.max_prefix_len, num_cus, share,
+                                min_tiles)
+        base, st = _whole_wave_tail_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups, units * sp,
+                                           num_cus, prefix_tiles=-(-prefix_tiles // sp))
+        if st is not None:
+            return sp, st
+    return sp, base
 
 
 # plan_chunk_rows: group rows (sharers x query heads per KV head) x prefix
 # tokens from which a 32-row chunk pays for its doubled per-unit work.  Same-box
-# MI355X sweep, best prefix splits each, 16- vs 32-row chunks (us/call):
-# 16 x 4096 15.1 vs 16.9; 32 x 8192 22.8 vs 23.9; 64 x 16384 54.2 vs 46.2;
-# 128 x 16384 91.5 vs 68.8 (Hq16/Hkv2: 8 rows per sharer).
-_WIDE_CHUNK_MIN_WORK = 1 << 22
+# MI355X sweep, best prefix / tail splits each, 16- vs 32-row chunks (us/call):
+# 16 x 4096 13.48 vs 16.09; 32 x 8192 21.30 vs 18.36; 64 x 16384 (earlier
+# build, best prefix splits) 54.2 vs 46.2; 128 x 16384 91.5 vs 68.8 (Hq16/Hkv2:
+# 8 rows per sharer).
+_WIDE_CHUNK_MIN_WORK = 1 << 21
 
 
 def plan_chunk_rows(groups, num_q_heads, num_kv_heads):
@@ -284,6 +328,9 @@ def paged_decode_attention_cascade_into(
     if chunk_rows not in (16, _lib.CASCADE_MAX_CHUNK_ROWS):
         raise ValueError(f"chunk_rows must be 16 or {_lib.CASCADE_MAX_CHUNK_ROWS}")
     chunks = prefix_chunks(groups, num_q_heads, num_kv_heads, chunk_rows)
+    if prefix_splits is None and num_splits is None:
+        prefix_splits, num_splits = plan_cascade_splits(num_seqs, num_q_heads, num_kv_heads, head_dim, groups,
+                                                        chunks, _num_cus(q.device))
     if prefix_splits is None:
         prefix_splits = plan_prefix_splits(groups.num_groups, num_kv_heads, chunks, groups.max_prefix_len,
                                            _num_cus(q.device))

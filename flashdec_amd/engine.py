@@ -638,7 +638,7 @@ class DecodeEngine:
         if cascade:
             from ._lib import paged_decode_plan
             from .cache import _StagingRing
-            from .cascade import (CascadeGroups, _num_cus, plan_chunk_rows, plan_prefix_splits, plan_tail_splits,
+            from .cascade import (CascadeGroups, _num_cus, plan_cascade_splits, plan_chunk_rows, plan_prefix_splits,
                                   prefix_chunks)
 
             ng = len(groups_now)
@@ -658,10 +658,12 @@ class DecodeEngine:
                                staging=_StagingRing(buf.numel() * 4))
             chunk_rows = gc.chunk_rows = plan_chunk_rows(groups, num_q_heads, cache.num_kv_heads)
             chunks = prefix_chunks(groups, num_q_heads, cache.num_kv_heads, chunk_rows)
-            prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads, chunks, groups.max_prefix_len, _num_cus(dev))
             if num_splits is None:
-                num_splits = plan_tail_splits(batch_size, num_q_heads, cache.num_kv_heads, cache.head_dim, groups,
-                                              ng * cache.num_kv_heads * chunks * prefix_splits, _num_cus(dev))
+                prefix_splits, num_splits = plan_cascade_splits(batch_size, num_q_heads, cache.num_kv_heads,
+                                                                cache.head_dim, groups, chunks, _num_cus(dev))
+            else:
+                prefix_splits = plan_prefix_splits(ng, cache.num_kv_heads, chunks, groups.max_prefix_len,
+                                                   _num_cus(dev))
         if cascade:
             splits = int(num_splits)
             if splits <= 0:

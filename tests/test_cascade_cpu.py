@@ -73,7 +73,7 @@ def test_group_size_bound():
 
 
 def test_chunk_rows_plan():
-    # 32-row chunks once group rows x prefix tokens reach 2^22 (64 sharers x 8 heads x 16384 tokens)
+    # 32-row chunks once group rows x prefix tokens reach 2^21 (32 sharers x 8 heads x 8192 tokens)
     def groups(members, prefix):
         return cascade.CascadeGroups(members=torch.zeros((1, members), dtype=torch.int32),
                                      prefix_len=torch.zeros(1, dtype=torch.int32),
@@ -81,10 +81,11 @@ def test_chunk_rows_plan():
                                      max_tail_len=1, total_tail_len=1)
 
     assert cascade.plan_chunk_rows(groups(16, 4096), 16, 2) == 16
-    assert cascade.plan_chunk_rows(groups(32, 8192), 16, 2) == 16
+    assert cascade.plan_chunk_rows(groups(32, 8192), 16, 2) == 32  # exactly 2^21
+    assert cascade.plan_chunk_rows(groups(31, 8192), 16, 2) == 16
     assert cascade.plan_chunk_rows(groups(64, 16384), 16, 2) == 32
     assert cascade.plan_chunk_rows(groups(128, 16384), 16, 2) == 32
-    assert cascade.plan_chunk_rows(groups(64, 8192), 16, 2) == 32  # exactly 2^22
+    assert cascade.plan_chunk_rows(groups(64, 8192), 16, 2) == 32
 
 
 def test_prefix_split_plan():

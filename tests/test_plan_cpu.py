@@ -86,3 +86,35 @@ def test_cascade_tail_split_cases(shape, plan, splits):
     groups = SimpleNamespace(max_tail_len=max_tail, total_tail_len=total_tail)
     assert _lib.paged_decode_plan(rows, 16, 2, 128, max_tail, total_tail) == plan
     assert cascade.plan_tail_splits(rows, 16, 2, 128, groups, prefix_blocks, 256) == splits
+
+
+# Cascade prefix and tail splits together (flashdec_amd.cascade.plan_cascade_splits), worked by
+# hand for 256 CUs, Hq16/Hkv2/D128, tails ~ U{1..512} (max 512 tokens, mean 256), one group:
+# (sharers, prefix tokens, chunk rows) -> (prefix splits, tail splits)
+CASCADE_CASES = [
+    # 8 chunks x 2 KV heads = 16 prefix units; 3/4 of the CUs: 192 // 16 = 12 splits of ceil(128 / 12)
+    # = 11 tiles; the tails' plan is 4, and 32 pairs x 2 fill the wave: 192 + 64 = 256
+    ((16, 4096, 16), (12, 2)),
+    # 32-row chunks: 8 chunks x 2 = 16 units -> 12 splits of 22 tiles; one tail split (16 tiles, no
+    # longer than a prefix-role workgroup) fills the wave: 192 + 64 = 256
+    ((32, 8192, 32), (12, 1)),
+    # 16 chunks x 2 = 32 units: 192 // 32 = 6 splits leave 64 CUs that 128 pairs cannot fill in whole
+    # waves; one workgroup per CU instead: 8 splits, 2 tail splits -> 256 + 256
+    ((64, 16384, 32), (8, 2)),
+    # 64 units: 3 splits leave no whole wave; 4 splits + 1 tail split -> 256 + 256
+    ((128, 16384, 32), (4, 1)),
+]
+
+
+@pytest.mark.parametrize(("shape", "splits"), CASCADE_CASES)
+def test_cascade_split_plan_cases(shape, splits):
+    from types import SimpleNamespace
+
+    from flashdec_amd import cascade
+
+    sharers, prefix, rows = shape
+    groups = SimpleNamespace(num_groups=1, max_members=sharers, max_prefix_len=prefix, max_tail_len=512,
+                             total_tail_len=sharers * 256)
+    assert cascade.plan_chunk_rows(groups, 16, 2) == rows
+    chunks = cascade.prefix_chunks(groups, 16, 2, rows)
+    assert cascade.plan_cascade_splits(sharers, 16, 2, 128, groups, chunks, 256) == splits
