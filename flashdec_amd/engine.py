@@ -303,9 +303,9 @@ class DecodeEngine:
         self._open: _OpenStep | None = None
         # Eager steps decode rows attached to one resident prefix with the
         # shared-prefix (cascade) launch once a group's sharers x prefix tokens
-        # reach this many (None: never).  On MI355X the cascade is at parity
-        # with per-row decode at 16 x 4096 and 1.4x faster at 32 x 8192.
-        self.cascade_min_shared_tokens = 128 * 1024
+        # reach this many (None: never).  On MI355X the cascade takes 13.2 us
+        # against 14.4 per row at 16 x 4096 and 18.6 against 32.8 at 32 x 8192.
+        self.cascade_min_shared_tokens = 64 * 1024
         self._cascade_cache = None
         self._cascade_decode_count = 0
 
