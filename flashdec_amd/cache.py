@@ -332,7 +332,7 @@ class _Txn:
     layers: int  # layers written so far (always 0 .. layers-1, in order)
     phase: str
     view_meta: object  # the callers' copy of meta, made by the first view (meta never changes); None before
-    launch: object  # prepared fused RoPE + append arguments: ((rotary_dim, base, table), RopeAppendArgs) or None
+    launch: object  # prepared fused RoPE + append arguments: ((RoPE key, q/k/v shapes), RopeAppendArgs) or None
 
 
 @dataclass(frozen=True)
@@ -529,6 +529,13 @@ class PagedKVCache:
         self._version = 0
         self._meta_arena = None  # (device buffer, capacity rows, table width) once enabled
         self._meta_staging = None  # pinned staging ring of the arena copies
+        # The HIP RoPE + append launches read cos/sin from the cache's own
+        # tables (rope_table), evaluated with apply_rope's torch expression,
+        # so the appended K and the rotated q equal the torch backend's bit
+        # for bit.  False: the kernels evaluate cos/sin themselves (float64,
+        # rounded once), which may differ from torch by one fp32 ulp.
+        self.rope_tables = True
+        self._rope_tables: dict = {}  # (rotary_dim, base) -> fp32 [2, rows, rotary_dim // 2]
 
     # ---------------------------------------------------------- state guards
     def _no_transaction(self, message):
@@ -770,11 +777,50 @@ class PagedKVCache:
 
     append_hip = append_cuda
 
+    def rope_table(self, rotary_dim=None, base=10_000.0, rows=1):
+        """The cache's cos/sin table for ``(rotary_dim, base)`` with at least ``rows`` rows.
+
+        fp32 ``[2, R, rotary_dim // 2]`` on the cache device, built by
+        :func:`flashdec_amd.rope.rope_cos_sin_table` (``apply_rope``'s own
+        torch expression, flashdec/rope.py:66-70).  Row counts grow in powers
+        of two (at least 4096) and never shrink; a grown table is a new
+        tensor, so launches prepared or captured with the old one keep it
+        alive through their own reference.  No counterpart in the reference.
+        """
+        from .rope import rope_cos_sin_table
+
+        rotary_dim, base = _rotary_dim_and_base(self.head_dim, rotary_dim, base)
+        rows = int(rows)
+        table = self._rope_tables.get((rotary_dim, base))
+        if table is None or table.shape[1] < rows:
+            n = max(rows, 4096 if table is None else 2 * table.shape[1])
+            table = rope_cos_sin_table(1 << (n - 1).bit_length(), rotary_dim, base, device=self.device)
+            self._rope_tables[(rotary_dim, base)] = table
+        return table
+
+    def _launch_table(self, cos_sin_table, rotary_dim, base, max_position):
+        """The cos/sin table a fused RoPE launch reads: the caller's (checked to cover
+        ``max_position``), the cache's own by default, or None (cos/sin evaluated in the
+        kernels) with ``rope_tables`` off."""
+        if cos_sin_table is None:
+            if not self.rope_tables or self.device.type != "cuda":
+                return None
+            return self.rope_table(rotary_dim, base, max_position + 1)
+        if max_position >= cos_sin_table.shape[1]:
+            raise ValueError("positions must be below the cos_sin_table's rows")
+        return cos_sin_table
+
+    def _txn_max_position(self, transaction):
+        """Largest position the open transaction writes (host-side, no device sync)."""
+        return max(self._journal.find_open(transaction).positions)
+
     def append_fused_cuda(self, layer_idx, request_ids, q, k, v, positions, rotary_dim=None, base=10_000.0,
                           cos_sin_table=None):
         """Fused RoPE + K/V append via ``fd_fused_rope_kv_append``; returns ``(q_rot, tables)``.
 
-        ``cos_sin_table``: see :func:`flashdec_amd.rope.rope_cos_sin_table`.
+        ``cos_sin_table``: see :func:`flashdec_amd.rope.rope_cos_sin_table`;
+        by default the cache's own table (:meth:`rope_table`), so q and K are
+        rotated exactly as ``apply_rope`` rotates them on this device.
         """
         torch = _torch()
         layer_idx, ids, k, v = self._single_layer_rows(layer_idx, request_ids, k, v)
@@ -795,6 +841,8 @@ class PagedKVCache:
             _check_cos_sin_table(cos_sin_table, rotary_dim, self.device)
             if bool(torch.any(positions >= cos_sin_table.shape[1]).item()):
                 raise ValueError("positions must be below the cos_sin_table's rows")
+        elif self.rope_tables:
+            cos_sin_table = self.rope_table(rotary_dim, base, int(positions.max().item()) + 1)
         load_fused_rope_kv_append_extension()
         blk, off = self._slot_tensors(self._reserve_single_layer(ids))
         q_rot = _launch(q, k, v, self.k_cache[layer_idx], self.v_cache[layer_idx], blk, off,
@@ -919,7 +967,8 @@ class PagedKVCache:
         locations (resolved from the transaction id, never from the caller's
         view).  Returns ``(q_rotated, view)``.  ``cos_sin_table``: see
         :func:`flashdec_amd.rope.rope_cos_sin_table` (rows must cover the
-        transaction's positions).
+        transaction's positions); by default the cache's own
+        (:meth:`rope_table`).
         """
         txn = self._journal.find_open(transaction)
         try:
@@ -934,6 +983,8 @@ class PagedKVCache:
                 raise ValueError("write_token_layer_fused_cuda requires contiguous q, k, and v tensors")
             from ._fused_rope_kv_append import _fused_rope_kv_append_trusted
 
+            rdim, rbase = _rotary_dim_and_base(self.head_dim, rotary_dim, base)
+            cos_sin_table = self._launch_table(cos_sin_table, rdim, rbase, max(txn.positions))
             meta = txn.meta
             q_rot = _fused_rope_kv_append_trusted(q, k, v, self.k_cache[layer_idx], self.v_cache[layer_idx],
                                                   meta.block_ids, meta.offsets, meta.positions,
@@ -959,7 +1010,15 @@ class PagedKVCache:
         from . import _lib
 
         txn = self._journal.find_open(transaction)
-        key = _rope_key(rotary_dim, base, cos_sin_table)
+        try:
+            rdim, rbase = _rotary_dim_and_base(self.head_dim, rotary_dim, base)
+            cos_sin_table = self._launch_table(cos_sin_table, rdim, rbase, max(txn.positions))
+        except Exception:
+            self._tally.failures += 1
+            raise
+        # the prepared arguments fix the batch and head counts of q, k and v as
+        # well: a layer of other shapes goes the checked way
+        key = (_rope_key(rotary_dim, base, cos_sin_table), tuple(q.shape), tuple(k.shape), tuple(v.shape))
         if (txn.launch is None or txn.launch[0] != key or not q.is_contiguous() or not k.is_contiguous()
                 or not v.is_contiguous()):
             extra = {} if cos_sin_table is None else {"cos_sin_table": cos_sin_table}
@@ -999,8 +1058,7 @@ class PagedKVCache:
         the layer order is all there is left to check.  Returns the view, or None (nothing
         recorded) without such a layer."""
         txn = self._journal.find_open(transaction)
-        key = _rope_key(rotary_dim, base, cos_sin_table)
-        if txn.launch is None or txn.launch[0] != key:
+        if txn.launch is None or txn.launch[0][0] != _rope_key(rotary_dim, base, cos_sin_table):
             return None
         try:
             layer_idx = self._validate_layer_idx(layer_idx)

@@ -968,6 +968,13 @@ __device__ __forceinline__ int xcd_logical_block(int block, int per_xcd) {
   return per_xcd > 0 ? (block & 7) * per_xcd + (block >> 3) : block;
 }
 
+// The XCD this wave runs on (hardware register XCC_ID, bits 3:0).
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x & 0xfu;
+}
+
 // DM: dim-major cache (load_unit_dm), staged through the LDS at kstage.
 // PRE: the block-table arguments arrived preloaded in SGPRs (decode_mfma_kernel).
 // NCB: 16-row column blocks per wave (prefix role only)
@@ -1339,24 +1346,101 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   if (p.splits == 1) return;     // rows went straight to the output
 
   // In-launch merge.  Partials were written with agent-scope atomic stores
-  // (sc1, coherent across the XCD L2s); waiting for their acknowledgement
+  // (sc1: written through to memory, and through the writer's own XCD L2,
+  // which stays coherent with them); waiting for their acknowledgement
   // (vmcnt 0) before the arrival increment is the release for them, without
   // the L2-wide write-back an agent-scope fence would do in every
-  // workgroup.  The last workgroup of this (request, KV head) to arrive reads
-  // them back with agent-scope atomic loads -- all loads of a chunk of
-  // splits issued before any is used -- merges, and returns the counter to
-  // zero for the next launch.
+  // workgroup.  The last workgroup of this (request, KV head) to arrive
+  // merges and returns the arrival word to zero for the next launch.  When
+  // every arrival came from its own XCD -- the hardware hands workgroup i to
+  // XCD i mod 8, and the XCD-by-XCD grid layout keeps a pair's workgroups on
+  // one XCD -- it reads the partials from that XCD's L2 (after invalidating
+  // its own L1), otherwise with agent-scope loads from memory.  C2 on
+  // MI355X: 10.65 us per call with agent-scope reads, 9.24 us with the L2
+  // reads (the reducer kernel path: 8.43 us).
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(p.counters + pair * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    lds.last = prev == static_cast<uint32_t>(p.splits - 1);
+    // One 64-bit arrival word per (request, KV head): the count in bits
+    // 0-15, the sum of the arrivals' XCD ids in bits 16-31 and the sum of
+    // their squares in bits 32-63.  The last arrival reads all three: the
+    // ids are all equal exactly when S * sum(x^2) == sum(x)^2, and then the
+    // pair's partials all passed through its own XCD's L2.
+    const uint32_t xcc = xcc_id();
+    const uint64_t mine = 1ull | (static_cast<uint64_t>(xcc) << 16) | (static_cast<uint64_t>(xcc * xcc) << 32);
+    uint64_t* word = reinterpret_cast<uint64_t*>(p.counters + pair * kCounterStride);
+    const uint64_t now = __hip_atomic_fetch_add(word, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    const uint64_t n = now & 0xffffu, sx = (now >> 16) & 0xffffu, sxx = now >> 32;
+    int last = 0;
+    if (n == static_cast<uint64_t>(p.splits)) {
+      last = 1;
+      if (n * sxx == sx * sx && sx == n * xcc) last = 2;
+      __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    lds.last = last;
   }
   __syncthreads();
-  if (!lds.last) return;
-  if (threadIdx.x == 0)
-    __hip_atomic_store(p.counters + pair * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int last_kind = lds.last;
+  if (last_kind == 0) return;
+  if (last_kind == 2 && p.splits <= kMergeChunk && p.as3 == 1 && ((p.as0 | p.as1 | p.as2) & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(p.acc) & 15u) == 0) {
+    // Every partial sits in this XCD's L2: all four waves read them with
+    // 16-byte loads after invalidating this CU's L1.  Thread -> (head hh,
+    // dims [dd, dd + DPT)): 4 dims per thread for up to 8 heads, else 8.
+    const int dpt = G <= 8 ? 4 : 8;
+    const int tph = D / dpt;
+    const int hh = threadIdx.x / tph;
+    const int dd = (threadIdx.x % tph) * dpt;
+    if (hh >= G) return;
+    const int qq = kvh * G + hh;
+    asm volatile("buffer_inv sc0" ::: "memory");
+    const float* pa = p.acc + b * p.as0 + qq * p.as1 + dd;
+    const int64_t sbase = b * p.ss0 + qq * p.ss1;
+    f32x4 part[kMergeChunk][2];
+    float pm[kMergeChunk], pl[kMergeChunk];
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int ss = min(j, p.splits - 1);
+      part[j][0] = *reinterpret_cast<const f32x4*>(pa + ss * p.as2);
+      part[j][1] = dpt == 8 ? *reinterpret_cast<const f32x4*>(pa + ss * p.as2 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      pm[j] = p.mx[sbase + ss * p.ss2];
+      pl[j] = p.sm[sbase + ss * p.ss2];
+    }
+    float cm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) cm = j < p.splits ? fmaxf(cm, pm[j]) : cm;
+    const float nmu = cm == -INFINITY ? 0.f : cm;
+    float GLx = 0.f;
+    float gx[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const float w = j < p.splits ? exp2f(pm[j] - nmu) : 0.f;
+      GLx += w * pl[j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        gx[k] += w * part[j][0][k];
+        gx[4 + k] += w * part[j][1][k];
+      }
+    }
+    const float inv = GLx > 0.f ? 1.f / GLx : 0.f;
+    T* dst = static_cast<T*>(p.out) + b * p.os0 + qq * p.os1 + dd * p.os2;
+    if (p.os2 == 1 && dpt == 8) {
+      u32x4 w4;
+      w4[0] = pack2<T>(gx[0] * inv, gx[1] * inv);
+      w4[1] = pack2<T>(gx[2] * inv, gx[3] * inv);
+      w4[2] = pack2<T>(gx[4] * inv, gx[5] * inv);
+      w4[3] = pack2<T>(gx[6] * inv, gx[7] * inv);
+      *reinterpret_cast<u32x4*>(dst) = w4;
+    } else if (p.os2 == 1) {
+      u32x2 w2;
+      w2[0] = pack2<T>(gx[0] * inv, gx[1] * inv);
+      w2[1] = pack2<T>(gx[2] * inv, gx[3] * inv);
+      *reinterpret_cast<u32x2*>(dst) = w2;
+    } else {
+      for (int j = 0; j < dpt; ++j) dst[j * p.os2] = from_f32<T>(gx[j] * inv);
+    }
+    return;
+  }
   if (!head_ok) return;
 
   const int64_t sb = b * p.ss0 + qh * p.ss1;
@@ -1364,6 +1448,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   float GM = -INFINITY;
   float GL = 0.f;
   float go[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // Every split ran on this XCD: its write-through stores left the L2 of
+  // this XCD coherent with memory, so the partials are read from there
+  // (workgroup-scope loads miss only the CU's own L1), not from memory.
+  const bool local = last_kind == 2;
   for (int s0 = 0; s0 < p.splits; s0 += kMergeChunk) {
     uint64_t raw[kMergeChunk][4];
     float pm[kMergeChunk], pl[kMergeChunk];
@@ -1371,10 +1459,19 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     for (int j = 0; j < kMergeChunk; ++j) {
       const int ss = min(s0 + j, p.splits - 1);  // past the end: re-read, masked below
       const uint64_t* a64 = reinterpret_cast<const uint64_t*>(ab + ss * p.as2);
+      if (local) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) raw[j][k] = __hip_atomic_load(a64 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pm[j] = __hip_atomic_load(p.mx + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pl[j] = __hip_atomic_load(p.sm + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < 4; ++k)
+          raw[j][k] = __hip_atomic_load(a64 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        pm[j] = __hip_atomic_load(p.mx + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        pl[j] = __hip_atomic_load(p.sm + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          raw[j][k] = __hip_atomic_load(a64 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pm[j] = __hip_atomic_load(p.mx + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pl[j] = __hip_atomic_load(p.sm + sb + ss * p.ss2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     float cm = -INFINITY;
 #pragma unroll
@@ -2386,6 +2483,8 @@ static int fill_decode_params(const fd_paged_decode_args* args, const char* fn, 
   p.ss1 = a.split_stats_stride[1];
   p.ss2 = a.split_stats_stride[2];
   p.counters = a.num_splits > 1 ? a.split_counters : nullptr;
+  if (p.counters != nullptr && (reinterpret_cast<uintptr_t>(p.counters) & 7u) != 0)
+    return set_error(FD_E_INVALID, "%s: split_counters must be 8-byte aligned", fn);
   p.fuse = fuse ? 1 : 0;
   if (fuse) {
     p.ak = a.append_k;

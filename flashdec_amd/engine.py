@@ -488,8 +488,11 @@ class DecodeEngine:
 
         ``cos_sin_table`` (HIP append backend; no counterpart in the reference):
         a :func:`flashdec_amd.rope.rope_cos_sin_table` covering the step's
-        positions, so q and the appended K are rotated exactly as
-        :func:`flashdec_amd.rope.apply_rope` does on this device.
+        positions (checked on the host; a short table raises ``ValueError``
+        and aborts the step).  By default the cache's own table
+        (``PagedKVCache.rope_table``): either way q and the appended K are
+        rotated exactly as :func:`flashdec_amd.rope.apply_rope` rotates them
+        on this device.
         """
         state = self._require_open_step(transaction)
         try:
@@ -499,6 +502,7 @@ class DecodeEngine:
             ids = state.handle.request_ids
             self._validate_step_inputs(ids, q, k, v)
             k, v = (t.unsqueeze(0) if t.dim() == 2 else t for t in (k, v))
+            cos_sin_table = self._step_rope_table(state, rotary_dim, base, cos_sin_table)
             with self._phase(PROFILE_RANGE_APPEND):
                 fused = self._fused_layer(state, layer_idx, q, k, v, rotary_dim, base, cos_sin_table)
                 if fused is None:
@@ -521,6 +525,21 @@ class DecodeEngine:
         return DecodeLayerResult(transaction_id=state.handle.transaction_id, layer_idx=layer_idx,
                                  request_ids=state.handle.request_ids, output=output, positions=view.positions,
                                  block_tables=view.block_tables, effective_seq_lens=view.effective_seq_lens)
+
+    def _step_rope_table(self, state, rotary_dim, base, cos_sin_table):
+        """The cos/sin table this layer's HIP RoPE launches read: the caller's, checked to
+        cover the step's positions, else the cache's own (None where the kernels evaluate
+        cos/sin themselves: ``rope_tables`` off, other append backends, caches without
+        tables)."""
+        cache = self.cache
+        launch_table = getattr(cache, "_launch_table", None)
+        if (self._append != "fused_hip" or launch_table is None or not _own_method(cache, "_launch_table")
+                or not _own_method(cache, "write_token_layer_fused_cuda")):
+            return cos_sin_table  # a replaced fused write keeps the reference's signature
+        from .cache import _rotary_dim_and_base
+
+        rdim, rbase = _rotary_dim_and_base(cache.head_dim, rotary_dim, base)
+        return launch_table(cos_sin_table, rdim, rbase, cache._txn_max_position(state.cache_transaction))
 
     def _phase(self, name):
         """A profiler range around one phase when ``profile_ranges`` is on."""
@@ -585,6 +604,8 @@ class DecodeEngine:
         ``cos_sin_table``: a :func:`flashdec_amd.rope.rope_cos_sin_table` with a
         row for every position the arena's table width allows; every launch
         then rotates with it (bit-identical to ``apply_rope`` on this device).
+        By default the cache's own table (``PagedKVCache.rope_table``, unless
+        its ``rope_tables`` is off).
         """
         torch = _torch()
         from . import _lib
@@ -603,6 +624,10 @@ class DecodeEngine:
         meta = cache.graph_metadata(batch_size)
         if rotary_dim is None:
             rotary_dim = cache.head_dim
+        if cos_sin_table is None and getattr(cache, "rope_tables", False):
+            # the cache's own table, with a row for every position the arena's
+            # table width allows (the graph keeps a reference to it)
+            cos_sin_table = cache.rope_table(int(rotary_dim), base, meta.block_tables.shape[1] * cache.block_size)
         if cos_sin_table is not None:
             from ._fused_rope_kv_append import _check_cos_sin_table
 
@@ -963,8 +988,9 @@ class DecodeEngine:
         out = torch.empty_like(q)
         from .cache import _rope_key
 
-        # the RoPE setting may change between layers: the arguments follow it
-        key = _rope_key(rotary_dim, base, cos_sin_table)
+        # the RoPE setting and the step's decode arguments (q's shape among
+        # them) may change between layers: the arguments follow both
+        key = (_rope_key(rotary_dim, base, cos_sin_table), state.decode_launch[0])
         if state.fused_launch is None or state.fused_launch[0] != key:
             base_args = state.decode_launch[1]
             args = type(base_args).from_buffer_copy(base_args)

@@ -81,7 +81,8 @@ typedef struct ihipStream_t* fd_stream_t; /* == hipStream_t */
  *
  * split_counters (optional, S > 1): >= num_seqs * num_kv_heads *
  * FD_SPLIT_COUNTER_STRIDE uint32 words (one 256-byte line per (request,
- * KV head)), all zero before the first launch.  With it the merge happens inside the
+ * KV head), whose first two words form one 64-bit arrival word), 8-byte
+ * aligned, all zero before the first launch.  With it the merge happens inside the
  * same launch (the last workgroup of each (request, KV head) to finish
  * merges, then returns its counter to zero, so the buffer is zero again
  * after every launch and replays of a captured graph stay valid).  Launches

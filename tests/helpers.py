@@ -87,3 +87,14 @@ def rope_pair_bound(x, pos, rotary_dim, base):
     pair = np.abs(x[..., :half]) + np.abs(x[..., half:rotary_dim])
     per = pair * (2.0 * (np.asarray(pos, dtype=np.float64)[:, None, None] + 1) * inv * 2.0**-23 + 2.0**-21)
     return np.concatenate([per, per], axis=-1)
+
+
+def device_rope(x, positions, rotary_dim=None, base=10_000.0):
+    """float32 numpy of the reference's torch RoPE (flashdec/rope.py:26-85, restated as
+    ``flashdec_amd.rope.apply_rope``) evaluated on x's device, in x's dtype: the HIP RoPE
+    launches that read the cache's cos/sin tables (the engine's and the cache's default)
+    reproduce it bit for bit."""
+    from flashdec_amd.rope import apply_rope
+
+    pos = torch.as_tensor(np.asarray(positions), dtype=torch.int64).to(x.device)
+    return apply_rope(x, pos, rotary_dim=rotary_dim, base=base).float().cpu().numpy()

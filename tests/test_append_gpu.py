@@ -210,8 +210,13 @@ def test_append_cuda_failures_keep_allocator_atomic():
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_rope_paged_kv_append_backends_agree(dtype):
+@pytest.mark.parametrize("rope_tables", [True, False])
+def test_rope_paged_kv_append_backends_agree(dtype, rope_tables):
+    """With the cache's own cos/sin tables (the default) the fused backend rotates q and K
+    exactly as the torch backend (the reference's rope.py:66-82 expression) does, bit for
+    bit; with them off the kernel's own evaluation equals the float64 oracle bit for bit."""
     caches = {name: gpu_cache(dtype, bs=8) for name in ("torch", "cuda", "fused_cuda")}
+    caches["fused_cuda"].rope_tables = rope_tables
     g = torch.Generator().manual_seed(11)
     for step in range(12):
         ids = [5, 6, 7]
@@ -223,11 +228,16 @@ def test_rope_paged_kv_append_backends_agree(dtype):
         assert all(torch.equal(r.positions, pos) for r in results.values())
         assert all(torch.equal(r.block_tables, results["torch"].block_tables) for r in results.values())
         exp_q = orope.apply_rope(q.float().cpu().numpy(), pos.cpu().numpy(), base=1e6, out_dtype=NAME[dtype])
-        assert np.array_equal(bits(results["fused_cuda"].q), oracle_bits(exp_q, dtype))
+        if rope_tables:
+            assert torch.equal(results["torch"].q.view(torch.int16), results["fused_cuda"].q.view(torch.int16))
+        else:
+            assert np.array_equal(bits(results["fused_cuda"].q), oracle_bits(exp_q, dtype))
         # torch's fp32 pow/cos/sin may differ from the correctly rounded values by an ulp
         torch.testing.assert_close(results["torch"].q, results["fused_cuda"].q, atol=2e-2, rtol=1e-2)
     torch.cuda.synchronize()
     assert torch.equal(caches["torch"].v_cache, caches["fused_cuda"].v_cache)
+    if rope_tables:
+        assert torch.equal(caches["torch"].k_cache.view(torch.int16), caches["fused_cuda"].k_cache.view(torch.int16))
     torch.testing.assert_close(caches["torch"].k_cache, caches["fused_cuda"].k_cache, atol=2e-2, rtol=1e-2)
     assert caches["torch"].metrics() == caches["fused_cuda"].metrics()
 

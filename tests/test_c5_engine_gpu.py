@@ -11,8 +11,10 @@ rollback); one more graph step follows.
 Checked against the oracle on several steps, for three layers x four rows:
 - attention output within atol 2e-2 / rtol 1e-2 (fp32 oracle over the rows'
   blocks, q rotated at the pre-append position);
-- the appended K bytes equal the oracle's RoPE of k and the V bytes equal v,
-  bit for bit, at the slots the transaction reserved.
+- the appended K bytes equal the reference's torch RoPE of k on the device
+  (apply_rope, rope.py:66-82; the graph reads the cache's cos/sin table) and
+  the V bytes equal v, bit for bit, at the slots the transaction reserved;
+  the rotated K stays within tolerance of the oracle's correctly rounded RoPE.
 The rollback must leave block tables, lengths and free/used counts as they
 were before the aborted step; the cache's state version advances by two
 (begin and abort each publish one, flashdec/cache.py:438-648).
@@ -24,7 +26,7 @@ import torch
 
 from oracle import attention as oa
 from oracle import rope as orope
-from tests.helpers import assert_close_to_oracle, np32
+from tests.helpers import assert_close_to_oracle, device_rope, np32
 
 pytestmark = pytest.mark.gpu
 
@@ -52,13 +54,16 @@ def check_step(cache, sg, tx, step):
     compact = np.arange(len(rows) * width, dtype=np.int32).reshape(len(rows), width)
     for layer in CHECK_LAYERS:
         k_in, v_in = sg.k[layer][rows], sg.v[layer][rows]
-        k_rot = orope.apply_rope(np32(k_in), pos, base=1e6, out_dtype="bfloat16")
+        # the step graph rotates with the cache's cos/sin table: apply_rope's bits on this device
+        k_rot = device_rope(k_in, pos, base=1e6)
+        assert np.allclose(k_rot, orope.apply_rope(np32(k_in), pos, base=1e6, out_dtype="bfloat16"),
+                           atol=2e-2, rtol=1e-2)
         for i in range(len(rows)):
             got_k = cache.k_cache[layer][int(blk[i]), :, int(off[i])]
             got_v = cache.v_cache[layer][int(blk[i]), :, int(off[i])]
             assert np.array_equal(bits(got_k), bits(torch.from_numpy(k_rot[i]).to(torch.bfloat16))), (step, layer, i)
             assert np.array_equal(bits(got_v), bits(v_in[i])), (step, layer, i)
-        q_rot = orope.apply_rope(np32(sg.q[layer][rows]), pos, base=1e6, out_dtype="bfloat16")
+        q_rot = device_rope(sg.q[layer][rows], pos, base=1e6)
         kp = np32(cache.k_cache[layer][flat])
         vp = np32(cache.v_cache[layer][flat])
         expected = oa.paged_decode_attention(q_rot, kp, vp, compact, lens)

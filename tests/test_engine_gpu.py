@@ -17,7 +17,7 @@ from flashdec_amd.cache import PagedKVCache
 from flashdec_amd.engine import DecodeEngine
 from oracle import attention as oa
 from oracle import rope as orope
-from tests.helpers import assert_close_to_oracle
+from tests.helpers import assert_close_to_oracle, device_rope
 
 pytestmark = pytest.mark.gpu
 
@@ -62,8 +62,12 @@ def test_engine_hip_layers_match_oracle(dtype, hq, hkv, d, bs):
             torch.cuda.synchronize()
             kc = engine.cache.k_cache[layer].float().cpu().numpy()
             vc = engine.cache.v_cache[layer].float().cpu().numpy()
-            q_rot = orope.apply_rope(q.float().cpu().numpy(), pos, base=1e6, out_dtype=name)
-            k_rot = orope.apply_rope(k.float().cpu().numpy(), pos, base=1e6, out_dtype=name)
+            # the cache's cos/sin tables: apply_rope's bits on this device
+            q_rot = device_rope(q, pos, base=1e6)
+            k_rot = device_rope(k, pos, base=1e6)
+            # and within the per-frequency bound of the correctly rounded RoPE
+            assert np.allclose(k_rot, orope.apply_rope(k.float().cpu().numpy(), pos, base=1e6, out_dtype=name),
+                               atol=2e-2, rtol=1e-2)
             blk, off = tx.physical_block_ids.tolist(), tx.block_offsets.tolist()
             for row in range(3):
                 assert np.array_equal(as_bits(kc[blk[row], :, off[row]], dtype), as_bits(k_rot[row], dtype))
@@ -73,6 +77,40 @@ def test_engine_hip_layers_match_oracle(dtype, hq, hkv, d, bs):
             assert_close_to_oracle(res.output, expected)
         engine.commit_step(tx)
     assert engine.cache.seq_lens_tensor(ids).tolist() == [2 * bs + 3] * 3
+    assert engine.validate_invariants()
+
+
+def test_layers_with_different_head_counts_take_their_own_launch():
+    """A later layer whose q has another head count than the step's earlier layers must not
+    reuse their prepared RoPE + append or fused-decode arguments (which fix the head count):
+    every layer is checked against the oracle, and the appended K / V bytes bit for bit."""
+    num_layers, hkv, d, bs = 5, 2, 128, 16
+    engine = DecodeEngine(cache_of(num_layers, hkv, d, bs, max_blocks=64))
+    ids = ["a", "b", "c"]
+    for rid in ids:
+        engine.add_request(rid)
+    engine.admit()
+    g = torch.Generator().manual_seed(777)
+    for step in range(3):
+        tx = engine.begin_step(ids)
+        pos = tx.positions.cpu().numpy()
+        for layer, hq in enumerate((16, 8, 4, 16, 2)):
+            print(f"head counts: step {step} layer {layer} hq {hq}", flush=True)
+            q, k, v = rand_inputs(g, 3, hq, hkv, d, torch.bfloat16)
+            res = engine.step_layer(tx, layer, q, k, v, base=1e6)
+            torch.cuda.synchronize()
+            assert res.output.shape == q.shape
+            kc = engine.cache.k_cache[layer].float().cpu().numpy()
+            vc = engine.cache.v_cache[layer].float().cpu().numpy()
+            k_rot = device_rope(k, pos, base=1e6)
+            blk, off = tx.physical_block_ids.tolist(), tx.block_offsets.tolist()
+            for row in range(3):
+                assert np.array_equal(as_bits(kc[blk[row], :, off[row]]), as_bits(k_rot[row]))
+                assert np.array_equal(as_bits(vc[blk[row], :, off[row]]), as_bits(v[row]))
+            expected = oa.paged_decode_attention(device_rope(q, pos, base=1e6), kc, vc,
+                                                 tx.block_tables.cpu().numpy(), tx.effective_seq_lens.cpu().numpy())
+            assert_close_to_oracle(res.output, expected)
+        engine.commit_step(tx)
     assert engine.validate_invariants()
 
 

@@ -30,7 +30,6 @@ import torch
 from flashdec_amd.cache import PagedKVCache
 from flashdec_amd.engine import DecodeEngine
 from oracle import attention as oa
-from oracle import rope as orope
 from tests.helpers import assert_close_to_oracle
 
 L, HQ, HKV, D, BS = 3, 16, 2, 128, 8
@@ -143,14 +142,13 @@ def _step_inputs(g, batch, device):
 
 
 def _rotated(x, pos):
-    """The appended K / rotated q the engine must produce: on the GPU the HIP kernels match the oracle's
-    RoPE bit for bit; the CPU (torch) backend rotates with torch's fp32 functions, the reference's own
-    formula (flashdec/rope.py:66-82), which may sit an ulp off the correctly rounded values."""
-    if x.device.type == "cpu":
-        from flashdec_amd.rope import apply_rope
+    """The appended K / rotated q the engine must produce: the reference's own formula
+    (flashdec/rope.py:66-82, torch's fp32 functions) on x's device -- the CPU (torch) backend
+    evaluates it directly, the HIP kernels read the cache's cos/sin tables built with it --
+    which may sit an ulp off the correctly rounded values of the oracle's RoPE."""
+    from flashdec_amd.rope import apply_rope
 
-        return apply_rope(x, torch.as_tensor(pos), base=BASE).float().numpy()
-    return orope.apply_rope(x.float().cpu().numpy(), pos, base=BASE, out_dtype="bfloat16")
+    return apply_rope(x, torch.as_tensor(pos).to(x.device), base=BASE).float().cpu().numpy()
 
 
 def run_eager_lifecycle(device, seed, iters, max_blocks=56):

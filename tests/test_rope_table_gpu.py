@@ -106,9 +106,13 @@ def test_table_mode_rejects_positions_past_the_table():
         fd.fused_rope_kv_append(q, k, v, kc, vc, blk, off, pos, rotary_dim=64, base=1e6, cos_sin_table=tab)
 
 
+@pytest.mark.parametrize("table", ["default", "explicit"])
 @pytest.mark.parametrize("graph", [False, True])
-def test_engine_step_in_table_mode_equals_torch_rope(graph):
-    """Eager steps (RoPE + append kernel) and a step graph (RoPE fused into the decode launch) in table mode."""
+def test_engine_step_in_table_mode_equals_torch_rope(graph, table):
+    """Eager steps (RoPE + append kernel, then RoPE fused into the decode launch) and a step
+    graph (RoPE fused into the decode launch) rotate with a cos/sin table: the caller's, or
+    by default (no table passed) the cache's own.  Appended K equals apply_rope on the
+    device bit for bit (the reference's rope.py:66-82 expression)."""
     from flashdec_amd.cache import PagedKVCache
     from flashdec_amd.engine import DecodeEngine
     from flashdec_amd.rope import apply_rope, rope_cos_sin_table
@@ -127,10 +131,11 @@ def test_engine_step_in_table_mode_equals_torch_rope(graph):
         engine.add_request(rid)
     engine.admit()
     cache.seed_context(ids, ctx)
-    tab = rope_cos_sin_table(width * bs, d, 1e6, device="cuda")
+    tab = rope_cos_sin_table(width * bs, d, 1e6, device="cuda") if table == "explicit" else None
     sg = engine.capture_step_graph(b, hq, base=1e6, cos_sin_table=tab) if graph else None
     if graph:
-        assert sg.fused_rope and sg.cos_sin_table is tab
+        assert sg.fused_rope and sg.cos_sin_table is (tab if table == "explicit" else cache.rope_table(d, 1e6))
+        assert sg.cos_sin_table.shape[1] >= width * bs
     for step in range(3):
         q = torch.randn((layers, b, hq, d), device="cuda", generator=g).to(torch.bfloat16)
         k = torch.randn((layers, b, hkv, d), device="cuda", generator=g).to(torch.bfloat16)
@@ -143,7 +148,8 @@ def test_engine_step_in_table_mode_equals_torch_rope(graph):
             engine.step_graph(tx, sg)
             outs = [sg.out[layer] for layer in range(layers)]
         else:
-            outs = [engine.step_layer(tx, layer, q[layer], k[layer], v[layer], base=1e6, cos_sin_table=tab).output
+            extra = {} if tab is None else {"cos_sin_table": tab}
+            outs = [engine.step_layer(tx, layer, q[layer], k[layer], v[layer], base=1e6, **extra).output
                     for layer in range(layers)]
         torch.cuda.synchronize()
         blk, off = tx.physical_block_ids, tx.block_offsets
@@ -158,3 +164,88 @@ def test_engine_step_in_table_mode_equals_torch_rope(graph):
             assert_close_to_oracle(outs[layer], expected)
         engine.commit_step(tx)
     assert np.all(cache.seq_lens_tensor(ids).cpu().numpy() == ctx + 3)
+
+
+def test_default_engine_steps_equal_the_torch_append_backend_bit_for_bit():
+    """No table passed anywhere: the default HIP engine (RoPE + append kernel on layer 0, RoPE
+    fused into the decode launch on later layers) and an engine whose append is the torch
+    backend (apply_rope, then a torch scatter; the reference's rope_paged_kv_append_ref path)
+    give the same attention outputs and the same cache bytes, bit for bit: q is rotated
+    exactly as apply_rope rotates it, since the output is a deterministic function of the
+    rotated q's bits.  The cache's fused write returns q_rot itself, checked against apply_rope."""
+    from flashdec_amd.cache import PagedKVCache
+    from flashdec_amd.engine import DecodeEngine
+    from flashdec_amd.rope import apply_rope
+
+    layers, b, hq, hkv, d, bs, ctx = 3, 6, 16, 2, 128, 32, 3000
+    width = (ctx + 8 + bs - 1) // bs
+    engines = []
+    for backend in ("fused_cuda", "torch"):
+        cache = PagedKVCache(layers, hkv, d, bs, max_blocks=b * width, dtype=torch.bfloat16, device="cuda")
+        g = torch.Generator(device="cuda").manual_seed(5)
+        cache.k_cache.normal_(generator=g)
+        cache.v_cache.normal_(generator=g)
+        engine = DecodeEngine(cache, append_backend=backend)
+        for rid in range(b):
+            engine.add_request(rid)
+        engine.admit()
+        cache.seed_context(list(range(b)), ctx)
+        engines.append(engine)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    ids = list(range(b))
+    for step in range(4):
+        q = torch.randn((layers, b, hq, d), device="cuda", generator=g).to(torch.bfloat16)
+        k = torch.randn((layers, b, hkv, d), device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn((layers, b, hkv, d), device="cuda", generator=g).to(torch.bfloat16)
+        outs = []
+        for engine in engines:
+            tx = engine.begin_step(ids)
+            outs.append([engine.step_layer(tx, layer, q[layer], k[layer], v[layer], base=1e6).output
+                         for layer in range(layers)])
+            engine.commit_step(tx)
+        torch.cuda.synchronize()
+        for layer in range(layers):
+            assert torch.equal(outs[0][layer].view(torch.int16), outs[1][layer].view(torch.int16)), (step, layer)
+    fused, ref = (e.cache for e in engines)
+    assert torch.equal(fused.k_cache.view(torch.int16), ref.k_cache.view(torch.int16))
+    assert torch.equal(fused.v_cache.view(torch.int16), ref.v_cache.view(torch.int16))
+    # the cache's fused write hands back q_rot: apply_rope's bits
+    tx = fused.begin_token(ids)
+    pos = torch.as_tensor(fused.transaction_view(tx).positions, device="cuda")
+    q_rot, _ = fused.write_token_layer_fused_cuda(tx, 0, q[0], k[0], v[0], base=1e6)
+    assert torch.equal(q_rot.view(torch.int16), apply_rope(q[0], pos, base=1e6).view(torch.int16))
+    fused.abort_token(tx)
+
+
+def test_short_table_raises_in_eager_steps_and_aborts_the_step():
+    """A caller's table without a row for every position of the step raises before any launch
+    (the kernels would clamp to the last row) and aborts the token."""
+    from flashdec_amd.cache import PagedKVCache
+    from flashdec_amd.engine import DecodeEngine
+    from flashdec_amd.rope import rope_cos_sin_table
+
+    cache = PagedKVCache(2, 2, 128, 32, max_blocks=64, dtype=torch.bfloat16, device="cuda")
+    engine = DecodeEngine(cache)
+    ids = [0, 1]
+    for rid in ids:
+        engine.add_request(rid)
+    engine.admit()
+    cache.seed_context(ids, 100)  # positions 100
+    short = rope_cos_sin_table(100, 128, 1e6, device="cuda")  # rows 0..99
+    q = torch.randn((2, 16, 128), device="cuda").to(torch.bfloat16)
+    k = torch.randn((2, 2, 128), device="cuda").to(torch.bfloat16)
+    for layer_with_short in (0, 1):
+        before = (cache.seq_lens_tensor(ids).cpu(), cache.num_free_blocks, cache.state_version)
+        tx = engine.begin_step(ids)
+        with pytest.raises(ValueError, match="cos_sin_table"):
+            for layer in range(2):
+                extra = {"cos_sin_table": short} if layer == layer_with_short else {}
+                engine.step_layer(tx, layer, q, k, k, base=1e6, **extra)
+        assert torch.equal(cache.seq_lens_tensor(ids).cpu(), before[0]) and cache.num_free_blocks == before[1]
+        assert cache.state_version == before[2] + 2
+    long = rope_cos_sin_table(101, 128, 1e6, device="cuda")
+    tx = engine.begin_step(ids)
+    for layer in range(2):
+        engine.step_layer(tx, layer, q, k, k, base=1e6, cos_sin_table=long)
+    engine.commit_step(tx)
+    assert engine.validate_invariants()
