@@ -25,12 +25,16 @@ Timing:
 * ``roofline.traffic``: HBM bytes per attention-kernel dispatch from the
   committed PMC summary ``profiles/decode_mfma_b8_ctx2048_traffic.json``
   (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null.
-* ``cpu_baseline``: the repo's numpy oracle on this host's cores (the (row,
-  KV head) pairs of a call spread over a process pool, one BLAS thread per
-  process), on C1 and
-  on the C2 call at ctx1024 and ctx2048: p50 of >= 20 calls after 3 warm-ups,
-  with ``os.cpu_count()`` and the CPU model.  It runs first, before this
-  process touches the GPU.
+* ``ctx1024``: the same call at ctx1024 (BASELINE's C2 names both
+  contexts), timed the same way on 48 pools of its own.
+* ``cpu_baseline``: the reference's CPU path as fp32 torch-CPU ops in its
+  per-(sequence, query-head) loop (oracle/torch_loop.py) under
+  ``torch.set_num_threads`` (os.cpu_count(), capped at the box's 16-thread
+  share; ``torch.get_num_threads()`` recorded), one synchronous call at a
+  time; beside it the numpy oracle over worker processes, each call one
+  synchronised unit between two barriers.  C1 and the C2 call at ctx1024
+  and ctx2048: p50 of >= 20 calls after 3 warm-ups, with the CPU model.  It
+  runs first, before this process touches the GPU.
 
 ``--profile-kernels N`` instead runs N eager calls and a 64 MiB device copy
 (the counter-scaling reference) and prints one line: the form profiled by
@@ -75,10 +79,11 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "rope", "ragged", "prefix", "prefix-large", "prefix-sweep",
-                                          "engine", "engine-prefix", "formats", "vllm"),
+    p.add_argument("--workload", choices=("decode", "c2-floor", "rope", "ragged", "prefix", "prefix-large",
+                                          "prefix-sweep", "engine", "engine-prefix", "formats", "vllm"),
                    default="decode",
-                   help="decode: the headline C2 call (default); rope: C3 fused RoPE + KV append; ragged / "
+                   help="decode: the headline C2 call (default); c2-floor: the C2 call beside a bare read of "
+                        "its bytes and a dependent empty launch (the floor of a call of that size); rope: C3 fused RoPE + KV append; ragged / "
                         "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
                         "sharing a 16384-token prefix; prefix-sweep: cascade chunk rows x prefix splits at four "
                         "shared-prefix sizes; engine: C5 36-layer step; engine-prefix: 36-layer steps "
@@ -204,10 +209,56 @@ def cpu_inputs(name):
 _CPU_WORKER = {}
 # CPU-baseline configs: (rows, KV heads) per call; a work item is one (row, KV head)
 CPU_CONFIGS = {"C1": (4, 2), "C2-ctx1024": (8, 2), "C2": (8, 2)}
+# host threads of the GPU box's share (its OMP_NUM_THREADS), whatever os.cpu_count() shows
+CPU_THREAD_CAP = 16
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: os.cpu_count(), capped at the box's CPU share."""
+    return max(1, min(os.cpu_count() or 1, CPU_THREAD_CAP))
+
+
+def cpu_baseline_torch(budget_s):
+    """The reference's CPU path as fp32 torch-CPU ops (oracle/torch_loop.py, restating
+    paged_reference.py:92-125: the per-(sequence, query-head) loop) under
+    ``torch.set_num_threads(cpu_threads())``.  Each config's inputs are the seeded
+    ``cpu_inputs`` arrays as torch tensors (bf16 for C2, as the reference's callers hold
+    them); a call is one synchronous ``paged_decode_attention_loop``.  p50 of >= 20 calls
+    after 3 warm-ups (more while within the budget, at most 200)."""
+    import torch
+
+    from oracle.torch_loop import paged_decode_attention_loop
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    results = {}
+    for name in CPU_CONFIGS:
+        (q, k, v, table, lens), scale, dtype, nbytes = cpu_inputs(name)
+        tdt = torch.float32 if dtype == "float32" else torch.bfloat16
+        args = [torch.from_numpy(x).to(tdt) for x in (q, k, v)] + [torch.from_numpy(table), torch.from_numpy(lens)]
+
+        def call():
+            paged_decode_attention_loop(*args, scale)
+
+        for _ in range(3):
+            call()
+        t0 = time.perf_counter()
+        call()
+        probe = time.perf_counter() - t0
+        reps = int(min(200, max(20, budget_s / len(CPU_CONFIGS) / max(probe, 1e-6))))
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            call()
+            times.append(time.perf_counter() - t0)
+        sec = statistics.median(times)
+        results[name] = {"us_per_call": round(sec * 1e6, 1), "gb_per_s": round(nbytes / sec / 1e9, 4),
+                         "threads": torch.get_num_threads(), "calls": reps, "algorithmic_bytes": nbytes}
+    return results, threads
 
 
 def _cpu_worker_init():
-    """Process-pool initializer: one BLAS thread, and each config's inputs built locally."""
+    """Worker initializer: one BLAS thread, and each config's inputs built locally."""
     from threadpoolctl import threadpool_limits
 
     _CPU_WORKER["blas"] = threadpool_limits(limits=1)
@@ -227,56 +278,85 @@ def _cpu_item(name, item):
                          lens[b:b + 1], sm_scale=scale, out_dtype=out_dtype)
 
 
-def _cpu_worker_share(name, items, warmup, reps):
-    """Per-call seconds of this worker's share (``items``) of a call, over ``reps`` calls after
-    ``warmup`` (runs in a worker; the call's other shares run at the same time on other workers)."""
-    for _ in range(warmup):
-        for item in items:
-            _cpu_item(name, item)
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        for item in items:
-            _cpu_item(name, item)
-        times.append(time.perf_counter() - t0)
-    return times
+def _cpu_worker_loop(rank, workers, start, done, jobs):
+    """A baseline worker: for every job (config, calls), run its share of each call between two
+    barriers that every worker and the parent pass together (runs in a worker process)."""
+    _cpu_worker_init()
+    while True:
+        job = jobs.get()
+        if job is None:
+            return
+        name, calls = job
+        n = CPU_CONFIGS[name][0] * CPU_CONFIGS[name][1]
+        share = list(range(rank, n, workers))
+        for _ in range(calls):
+            start.wait()
+            for item in share:
+                _cpu_item(name, item)
+            done.wait()
+
+
+def cpu_baseline_numpy(budget_s):
+    """The numpy oracle (oracle/attention.py) on this host's cores, one call at a time.
+
+    A call's (row, KV head) pairs are independent: each of
+    min(cpu_threads(), pairs) worker processes (one BLAS thread each) takes a
+    fixed share.  Every call is one synchronised unit: the parent and all
+    workers pass a start barrier, the workers run their shares, and all pass
+    an end barrier; a call's time is the parent's time between the two
+    barriers (barrier overhead included).  p50 of >= 20 calls after 3
+    warm-ups per config.  Started before this process touches the GPU.
+    """
+    import multiprocessing as mp
+
+    ctx = mp.get_context("spawn")
+    workers = min(cpu_threads(), max(r * h for r, h in CPU_CONFIGS.values()))
+    start, done = ctx.Barrier(workers + 1), ctx.Barrier(workers + 1)
+    queues = [ctx.Queue() for _ in range(workers)]
+    procs = [ctx.Process(target=_cpu_worker_loop, args=(r, workers, start, done, queues[r]), daemon=True)
+             for r in range(workers)]
+    for p in procs:
+        p.start()
+    results = {}
+    try:
+        for name in CPU_CONFIGS:
+            nbytes = cpu_inputs(name)[3]
+            # 3 warm-ups and one probe call size the sample to the budget
+            for qu in queues:
+                qu.put((name, 4))
+            for i in range(4):
+                start.wait()
+                t0 = time.perf_counter()
+                done.wait()
+                probe = time.perf_counter() - t0
+            reps = int(min(200, max(20, budget_s / len(CPU_CONFIGS) / max(probe, 1e-6))))
+            for qu in queues:
+                qu.put((name, reps))
+            times = []
+            for _ in range(reps):
+                start.wait()
+                t0 = time.perf_counter()
+                done.wait()
+                times.append(time.perf_counter() - t0)
+            sec = statistics.median(times)
+            used = min(workers, CPU_CONFIGS[name][0] * CPU_CONFIGS[name][1])
+            results[name] = {"us_per_call": round(sec * 1e6, 1), "gb_per_s": round(nbytes / sec / 1e9, 4),
+                             "processes": workers, "busy_processes": used, "calls": reps,
+                             "algorithmic_bytes": nbytes}
+    finally:
+        for qu in queues:
+            qu.put(None)
+        for p in procs:
+            p.join(timeout=10)
+    return results
 
 
 def cpu_baseline(budget_s):
-    """The numpy oracle (restatement of paged_reference.py:19-125) on this host's cores.
-
-    The (row, KV head) pairs of a call are independent, so each of
-    min(os.cpu_count(), 16, pairs) worker processes (one BLAS thread each)
-    takes a fixed share of them and runs that share call after call; a call's
-    time is the slowest share's time for it.  The workers run their calls
-    concurrently and report per-call times, so the figure is the port's
-    compute on that many cores, without a process-pool round trip per call.
-    Timed on C1 and on the C2 call at ctx1024 and ctx2048: p50 of >= 20
-    calls after 3 warm-ups (more calls while within the budget, at most 200).
-    Runs before this process touches the GPU (the workers are started as
-    fresh processes).
-    """
-    import multiprocessing as mp
-    from concurrent.futures import ProcessPoolExecutor
-
-    n_cpu = os.cpu_count() or 1
-    items = {name: rows * hkv for name, (rows, hkv) in CPU_CONFIGS.items()}
-    workers = min(n_cpu, 16, max(items.values()))
-    results = {}
-    with ProcessPoolExecutor(max_workers=workers, mp_context=mp.get_context("spawn"),
-                             initializer=_cpu_worker_init) as ex:
-        for name, n in items.items():
-            nbytes = cpu_inputs(name)[3]
-            w = min(workers, n)
-            shares = [list(range(i, n, w)) for i in range(w)]
-            # one call's slowest share, measured once, sizes the sample to the budget
-            probe = max(ex.map(_cpu_worker_share, [name] * w, shares, [1] * w, [1] * w), key=lambda t: t[0])[0]
-            reps = int(min(200, max(20, budget_s / len(items) / max(probe, 1e-6))))
-            per_share = list(ex.map(_cpu_worker_share, [name] * w, shares, [3] * w, [reps] * w))
-            sec = statistics.median(max(t[r] for t in per_share) for r in range(reps))
-            results[name] = {"us_per_call": round(sec * 1e6, 1), "gb_per_s": round(nbytes / sec / 1e9, 4),
-                             "processes": w, "calls": reps, "algorithmic_bytes": nbytes}
-    return results, n_cpu
+    """Both CPU baselines (reported, not targets): the torch-CPU loop form of the reference's
+    path (the primary figure) and the numpy oracle spread over worker processes."""
+    numpy_res = cpu_baseline_numpy(budget_s / 2)
+    torch_res, threads = cpu_baseline_torch(budget_s / 2)
+    return torch_res, numpy_res, threads
 
 
 def back_to_back(torch, lib, prepared, n, events=None):
@@ -332,6 +412,34 @@ def graph_ms_per_call(torch, dev, fn, n_calls, warmup=8):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / n_calls
+
+
+def graph_p50_us(torch, dev, fn, n_calls, samples=240, warmup=96):
+    """p50 us per call of ``fn(i)``: one hipGraph holding ``n_calls`` calls (one per pool),
+    replayed ``samples`` times back to back with hipEvents between the replays."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn(0)  # per-stream workspaces exist before capture
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(n_calls):
+                fn(i)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(samples + 1)]
+    marks[0].record()
+    for i in range(samples):
+        graph.replay()
+        marks[i + 1].record()
+    torch.cuda.synchronize()
+    per = sorted(marks[i].elapsed_time(marks[i + 1]) / n_calls * 1e3 for i in range(samples))
+    return statistics.median(per)
 
 
 def attention_kernel_us(torch, prepared, n_calls):
@@ -582,6 +690,128 @@ def run_decode_variant(torch, dev, args, name, lens, n_pools, seed, prefix_block
     else:
         out["config"]["path"] = "per-row"
         out["cascade_path"] = cascade_line
+    return out
+
+
+def load_probes():
+    """``libflashdec_probe.so`` (csrc/floor_probe.hip): the floor workload's probe kernels."""
+    import ctypes
+
+    from flashdec_amd import _build
+
+    path = _build.PROBE_LIB_PATH
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    vp, u64 = ctypes.c_void_p, ctypes.c_uint64
+    lib.fdp_stream_read.argtypes = [vp, u64, vp, vp, vp, vp]
+    lib.fdp_empty.argtypes = [ctypes.c_uint, ctypes.c_uint, vp]
+    lib.fdp_xcc_map.argtypes = [vp, ctypes.c_uint, vp]
+    for f in (lib.fdp_stream_read, lib.fdp_empty, lib.fdp_xcc_map):
+        f.restype = ctypes.c_int
+    return lib
+
+
+def run_c2_floor(torch, dev, args):
+    """What a C2 call costs against what a call of its bytes costs with no attention work.
+
+    For ctx 2048 and 1024 (B8 Hq16 Hkv2 D128 bs32 bf16, the headline pools),
+    every term is a p50 over 240 replays of a hipGraph of one call per pool
+    (48 pools or 48 buffers of the call's algorithmic bytes, so the Infinity
+    Cache serves none of them):
+      read        -- one non-temporal read of the call's bytes (fdp_stream_read);
+      read+empty  -- that read, then a dependent empty kernel of the reducer's
+                     grid (B*Hq workgroups of 64 threads): two dependent
+                     launches with no work beyond the read;
+      shipped     -- paged_decode_attention_into: attention + reducer kernel;
+      merge       -- the opt-in single-dispatch path (split_counters: the last
+                     workgroup of each (request, KV head) merges);
+    plus eager kernel durations (HIP events around each dispatch) of the bare
+    read, the attention kernel and the reducer, and the workgroup -> XCD map
+    of a 256-workgroup grid (the in-launch merge reads same-XCD partials from L2).
+    """
+    import flashdec_amd as fd
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    probes = load_probes()
+    batch, hq, hkv, d, bs = 8, 16, 2, 128, 32
+    sm_scale = 1.0 / math.sqrt(d)
+    res = {}
+    xmap = torch.zeros(256, dtype=torch.int32, device=dev)
+    stream0 = torch.cuda.current_stream(dev).cuda_stream
+    assert probes.fdp_xcc_map(xmap.data_ptr(), 256, stream0) == 0
+    torch.cuda.synchronize()
+    xcc = xmap.cpu().tolist()
+    for ctx in (2048, 1024):
+        pools = build_pools(torch, args.pools, batch, ctx, hq, hkv, d, bs, dev)
+        nbytes = algorithmic_bytes(batch, ctx, hq, hkv, d, bs)
+        n16 = (nbytes + 15) // 16 * 16
+        bufs = [torch.randint(0, 255, (n16,), dtype=torch.uint8, device=dev) for _ in range(args.pools)]
+        sink = torch.zeros(256, dtype=torch.int32, device=dev)
+
+        def rd(i, events=(None, None)):
+            st = torch.cuda.current_stream(dev).cuda_stream
+            assert probes.fdp_stream_read(bufs[i % len(bufs)].data_ptr(), n16, sink.data_ptr(), st, *events) == 0
+
+        def rd_empty(i):
+            rd(i)
+            assert probes.fdp_empty(batch * hq, 64, torch.cuda.current_stream(dev).cuda_stream) == 0
+
+        def shipped(i):
+            q, k, v, table, lens, out = pools[i % len(pools)]
+            fd.paged_decode_attention_into(q, k, v, table, lens, out, sm_scale=sm_scale)
+
+        splits = _lib.paged_decode_plan(batch, hq, hkv, d, pools[0][3].shape[1] * bs)
+        ws = (torch.empty((batch, hq, splits, d), device=dev), torch.empty((batch, hq, splits), device=dev),
+              torch.empty((batch, hq, splits), device=dev))
+        counters = torch.zeros(batch * hkv * _lib.SPLIT_COUNTER_STRIDE, device=dev, dtype=torch.int32)
+
+        def merge(i):
+            q, k, v, table, lens, out = pools[i % len(pools)]
+            pd._decode_with_workspace(q, k, v, table, lens, out, sm_scale, bs, splits, ws, k.shape[0],
+                                      counters=counters)
+
+        n = len(pools)
+        terms = {name: round(graph_p50_us(torch, dev, fn, n), 3)
+                 for name, fn in (("read", rd), ("read+empty", rd_empty), ("shipped", shipped), ("merge", merge))}
+        # eager durations: HIP events recorded around exactly each bare-read
+        # dispatch (hipExtLaunchKernel), the reads back to back behind a sleep
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2 * n)]
+        for a, b in evs:  # create the HIP events before their handles are passed down
+            a.record()
+            b.record()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(100_000_000)
+        for i, (a, b) in enumerate(evs):
+            rd(i, (a.cuda_event, b.cuda_event))
+        torch.cuda.synchronize()
+        read_kernel = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
+        shipped(0)
+        prepared = [prepared_args(pool, sm_scale, bs, hkv) for pool in pools]
+        attn_us, red_us = attention_kernel_us(torch, prepared, min(4 * n, 192))
+        floor = {
+            "us_per_call": terms,
+            "eager_kernel_us": {"read": round(read_kernel, 3), "attention": round(attn_us, 3),
+                                "reducer": round(red_us, 3)},
+            "dependent_launch_us": round(terms["read+empty"] - terms["read"], 3),
+            "shipped_over_two_launch_floor_us": round(terms["shipped"] - terms["read+empty"], 3),
+            "hbm_frac": {k: round(nbytes / (v * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) for k, v in terms.items()},
+            "algorithmic_bytes": nbytes,
+            "num_splits": splits,
+        }
+        log(f"[bench] c2-floor ctx{ctx}: " + ", ".join(f"{k} {v:.2f}" for k, v in terms.items())
+            + f" us/call; eager read {read_kernel:.2f}, attention {attn_us:.2f}, reducer {red_us:.2f} us")
+        res[f"ctx{ctx}"] = floor
+        del pools, bufs
+        torch.cuda.empty_cache()
+    c2 = res["ctx2048"]
+    out = common_fields(args, "C2 call vs the floor of a call of its bytes (us/call)", c2["us_per_call"]["shipped"],
+                        "us/call", c2["us_per_call"]["shipped"] * 1e-3, False,
+                        {"workload": "c2-floor-b8-hq16-hkv2-d128-bs32", "kv_pools": args.pools})
+    out.update(res)
+    out["xcd_of_workgroup"] = {"grid": 256, "round_robin": all(x == i % 8 for i, x in enumerate(xcc)),
+                               "first16": xcc[:16]}
     return out
 
 
@@ -1015,7 +1245,7 @@ def main():
     torch.cuda.set_device(dev)
     _lib.load_library()
     if args.workload != "decode":
-        run = {"rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
+        run = {"c2-floor": run_c2_floor, "rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
                "prefix-sweep": run_prefix_sweep, "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
                "vllm": run_vllm}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
@@ -1107,6 +1337,33 @@ def main():
     log(f"[bench] attention kernel: mean {kernel_ms * 1e3:.2f} us, median {statistics.median(attn_ms) * 1e3:.2f} us"
         f"; reducer: mean {statistics.mean(red_ms) * 1e3:.2f} us ({n_calls} calls)")
 
+    # BASELINE's C2 names ctx1024 too: the same call on 48 pools at ctx1024,
+    # timed the same way, rides along in the line
+    companion = None
+    if (batch, ctx) == (8, 2048):
+        pools_1k = build_pools(torch, args.pools, batch, 1024, hq, hkv, d, bs, dev)
+
+        def call_1k(i):
+            q, k, v, table, lens, out = pools_1k[i % len(pools_1k)]
+            fd.paged_decode_attention_into(q, k, v, table, lens, out, sm_scale=sm_scale)
+
+        us_1k = graph_p50_us(torch, dev, call_1k, len(pools_1k))
+        prepared_1k = [prepared_args(pool, sm_scale, bs, hkv) for pool in pools_1k]
+        attn_1k, red_1k = attention_kernel_us(torch, prepared_1k, min(4 * len(pools_1k), 192))
+        nb_1k = algorithmic_bytes(batch, 1024, hq, hkv, d, bs)
+        companion = {
+            "us_per_call": round(us_1k, 3),
+            "value": round(nb_1k / (us_1k * 1e-6) / 1e9, 2),
+            "unit": "GB/s",
+            "hbm_frac": round(nb_1k / (us_1k * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "num_splits": prepared_1k[0][0].num_splits,
+            "kernel_us_mean": round(attn_1k, 3),
+            "reducer_us_mean": round(red_1k, 3),
+            "roofline_frac": round(nb_1k / (attn_1k * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_call": nb_1k,
+        }
+        log(f"[bench] ctx1024: {us_1k:.2f} us/call, attention kernel {attn_1k:.2f} us, reducer {red_1k:.2f} us")
+
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     traffic, traffic_meta = load_traffic()
     traffic_src = None if traffic_meta is None else os.path.relpath(TRAFFIC_SUMMARY, ROOT)
@@ -1115,23 +1372,33 @@ def main():
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     cpu = None
     if cpu_res is not None:
-        res, n_cpu = cpu_res
-        c2 = res["C2"]
+        torch_res, numpy_res, threads = cpu_res
+        c2 = torch_res["C2"]
         cpu = {
             "value": c2["gb_per_s"],
             "unit": "GB/s",
-            "cores": c2["processes"],
+            "cores": c2["threads"],
             "kind": "port",
-            "sample": f"numpy oracle (oracle/attention.py, restating paged_reference.py:19-125) on the full "
-                      f"B8 ctx2048 call, its 16 (row, KV head) pairs shared by {c2['processes']} worker processes (one "
-                      f"BLAS thread each, each running its share call after call; a call = its slowest share), "
-                      f"p50 of {c2['calls']} calls after 3 warm-ups: {c2['us_per_call']:.0f} us/call",
-            "os_cpu_count": n_cpu,
+            "sample": f"fp32 torch-CPU restatement of paged_reference.py:92-125 in its per-(sequence, query-head) "
+                      f"loop (oracle/torch_loop.py) on the full B8 ctx2048 call (bf16 inputs upcast per head, as "
+                      f"the reference does), torch.set_num_threads({threads}) (os.cpu_count() "
+                      f"{os.cpu_count()}, capped at the box's {CPU_THREAD_CAP}-thread share), one synchronous call "
+                      f"at a time, p50 of {c2['calls']} calls after 3 warm-ups: {c2['us_per_call']:.0f} us/call",
+            "torch_get_num_threads": c2["threads"],
+            "os_cpu_count": os.cpu_count(),
             "cpu_model": cpu_model(),
-            "configs": res,
+            "configs": torch_res,
+            "numpy_oracle": {
+                "kind": "port",
+                "sample": "numpy oracle (oracle/attention.py) with a call's (row, KV head) pairs shared by worker "
+                          "processes (one BLAS thread each); each call one synchronised unit between two barriers "
+                          "that the parent and every worker pass, p50 after 3 warm-ups",
+                "configs": numpy_res,
+            },
         }
-        log(f"[bench] cpu oracle: C2 {c2['us_per_call'] / 1e3:.2f} ms/call ({c2['processes']} processes), "
-            f"C1 {res['C1']['us_per_call'] / 1e3:.2f} ms/call")
+        log(f"[bench] cpu torch loop: C2 {c2['us_per_call'] / 1e3:.2f} ms/call ({c2['threads']} threads), "
+            f"C1 {torch_res['C1']['us_per_call'] / 1e3:.2f} ms/call; numpy oracle C2 "
+            f"{numpy_res['C2']['us_per_call'] / 1e3:.2f} ms/call ({numpy_res['C2']['processes']} processes)")
 
     result = {
         "metric": METRIC,
@@ -1187,6 +1454,8 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if companion is not None:
+        result["ctx1024"] = companion
     print(json.dumps(result), flush=True)
 
 

@@ -1,4 +1,5 @@
-"""Build ``libflashdec_hip.so`` (the C-ABI library) in-tree with hipcc for gfx950.
+"""Build ``libflashdec_hip.so`` (the C-ABI library) in-tree with hipcc for gfx950,
+and ``libflashdec_probe.so`` (bench.py's floor probes, ``csrc/floor_probe.hip``).
 
 Each ``csrc/*.hip`` file is compiled separately, then linked into
 ``flashdec_amd/libflashdec_hip.so``.  The RoPE/append file is compiled with
@@ -21,6 +22,9 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC = PACKAGE_DIR / "csrc"
 BUILD_DIR = PACKAGE_DIR / "_build"
 LIB_PATH = PACKAGE_DIR / "libflashdec_hip.so"
+# measurement probes for bench.py's floor workload (not the decode library)
+PROBE_SOURCE = "floor_probe.hip"
+PROBE_LIB_PATH = PACKAGE_DIR / "libflashdec_probe.so"
 ARCH = "gfx950"
 
 SOURCES = {
@@ -68,7 +72,16 @@ def build_library(verbose: bool = False) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
+    build_probe_library(verbose)
     return LIB_PATH
+
+
+def build_probe_library(verbose: bool = False) -> Path:
+    """Compile ``libflashdec_probe.so`` (bench.py's floor probes); returns its path."""
+    tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
+    _run([_hipcc(), *COMMON_FLAGS, "-shared", str(CSRC / PROBE_SOURCE), "-o", str(tmp)], verbose)
+    os.replace(tmp, PROBE_LIB_PATH)
+    return PROBE_LIB_PATH
 
 
 def _run(cmd, verbose):

@@ -409,13 +409,24 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // group addresses dim row base + c'/4 at tokens 8*(c'%4) + 4*mt + [0, 4).
 // A wave's LDS operations run in order, so the stage needs no barrier
 // between the writes and the reads, nor before the next unit's writes.
+//
+// Rows 8r .. 8r+7 with r odd hold each 16-byte piece with its two 8-byte
+// halves swapped.  The read of a 16-lane group covers the same 8-byte half of
+// every piece in four rows; groups g and g + 1 read rows 8 apart, which without
+// the swap sit on the same banks (rows 64 bytes apart, 512 bytes per 8 rows).
+// Row 16i + lane/4 is odd-eighth exactly for lanes 32..63; read row
+// 8g + c/4 (+4, +32s) for odd g.
 template <int D>
 __device__ __forceinline__ void stage_k_dm(DmRegs<D>& t, uint8_t* stage, int lane) {
   constexpr int KS = DmRegs<D>::KS;
   lds_u8* st = (lds_u8*)stage;
+  const bool swap = lane >= 32;
 #pragma unroll
-  for (int i = 0; i < D / 16; ++i)
-    *(lds_u32x4*)(st + (16 * i + (lane >> 2)) * kDmRowBytes + 16 * (lane & 3)) = t.kf[i / KS][i % KS];
+  for (int i = 0; i < D / 16; ++i) {
+    const u32x4 k = t.kf[i / KS][i % KS];
+    *(lds_u32x4*)(st + (16 * i + (lane >> 2)) * kDmRowBytes + 16 * (lane & 3)) =
+        swap ? u32x4{k[2], k[3], k[0], k[1]} : k;
+  }
   const int c = lane & 15;
   const int g = lane >> 4;
   lds_u8* rd = st + (8 * g + (c >> 2)) * kDmRowBytes + 16 * (c & 3);
@@ -423,7 +434,7 @@ __device__ __forceinline__ void stage_k_dm(DmRegs<D>& t, uint8_t* stage, int lan
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      lds_u8* a = rd + 32 * s * kDmRowBytes + 8 * mt;
+      lds_u8* a = rd + 32 * s * kDmRowBytes + 8 * (mt ^ (g & 1));
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a);
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a + 4 * kDmRowBytes));
       const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
@@ -820,7 +831,24 @@ __device__ __forceinline__ void process_unit_dm(DmRegs<D>& t, const u32x4 (&qf)[
 
 constexpr int kMaxWaves = 8;          // waves per workgroup of the 16-token variant
 constexpr int kWideUnitMaxTiles = 4;  // splits of at most this many tiles take 32-token units
-constexpr int kAccPitch = 132;   // floats per head row in LDS (bank spread)
+// Floats per head row of the LDS merge slots (16-byte pieces, written and
+// merged with 128-bit LDS accesses), and where a head's dims sit in its row:
+// the 16-byte piece of dims [d, d + 4) starts at float acc_spread<D>() * d.
+// Measured on MI355X (SQ_LDS_BANK_CONFLICT of a one-wave probe): a
+// ds_write_b128 is conflict-free when each 8 consecutive lanes cover the 32
+// banks once; a ds_read_b128 where each 16 lanes read 16 bytes at a 32-byte
+// stride from rows 528 bytes apart is conflict-free, while 16 lanes reading
+// 256 contiguous bytes from such rows is not.  So the rows are 132 floats
+// apart, and head_dim-64 rows keep their pieces 32 bytes apart as head_dim
+// 128's are (the merge then reads them with the same pattern).
+template <int D>
+constexpr int acc_pitch() {
+  return 132;
+}
+template <int D>
+constexpr int acc_spread() {
+  return D == 64 ? 2 : 1;
+}
 // Prefix role of the cascade: up to this many 16-row MFMA column blocks per
 // wave (a launch's chunk_rows / 16).  Each block is another 16 of the group's
 // (member, head) rows attending the same K/V registers, so the group's
@@ -842,20 +870,29 @@ constexpr int kCounterStride = FD_SPLIT_COUNTER_STRIDE;
 // unaligned-access mode, which splits such a store in hardware (checked on
 // views one element past an aligned base in tests/test_unaligned_views_gpu.py;
 // the split partials' 16-byte stores below take caller workspaces the same way).
-template <typename T>
+// N: the first 4 or all 8 elements of o.
+template <typename T, int N = 8>
 __device__ __forceinline__ void store_row(const DecodeParams& p, int b, int qh, int d0, const float (&o)[8],
                                           float inv) {
+  static_assert(N == 4 || N == 8, "4 or 8 elements");
   T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1 + d0 * p.os2;
   if (p.os2 == 1) {
-    u32x4 w;
-    w[0] = pack2<T>(o[0] * inv, o[1] * inv);
-    w[1] = pack2<T>(o[2] * inv, o[3] * inv);
-    w[2] = pack2<T>(o[4] * inv, o[5] * inv);
-    w[3] = pack2<T>(o[6] * inv, o[7] * inv);
-    *reinterpret_cast<u32x4*>(dst) = w;
+    if constexpr (N == 8) {
+      u32x4 w;
+      w[0] = pack2<T>(o[0] * inv, o[1] * inv);
+      w[1] = pack2<T>(o[2] * inv, o[3] * inv);
+      w[2] = pack2<T>(o[4] * inv, o[5] * inv);
+      w[3] = pack2<T>(o[6] * inv, o[7] * inv);
+      *reinterpret_cast<u32x4*>(dst) = w;
+    } else {
+      u32x2 w;
+      w[0] = pack2<T>(o[0] * inv, o[1] * inv);
+      w[1] = pack2<T>(o[2] * inv, o[3] * inv);
+      *reinterpret_cast<u32x2*>(dst) = w;
+    }
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dst[j * p.os2] = from_f32<T>(o[j] * inv);
+    for (int j = 0; j < N; ++j) dst[j * p.os2] = from_f32<T>(o[j] * inv);
   }
 }
 
@@ -948,9 +985,9 @@ __device__ __forceinline__ void balanced_locate(const DecodeParams& p, int v, in
 
 // LDS of one decode workgroup: each wave's state for the merge, and the
 // output row of every MFMA column.
-template <int W>
+template <int W, int P = acc_pitch<128>()>
 struct alignas(16) DecodeLds {
-  float acc[W][16][kAccPitch];  // 16-byte rows: merged with 128-bit LDS reads
+  float acc[W][16][P];  // 16-byte rows: merged with 128-bit LDS reads
   float m[W][16];
   float l[W][16];
   int col_b[16];
@@ -981,7 +1018,8 @@ __device__ __forceinline__ uint32_t xcc_id() {
 template <typename T, int BS, int FUSE, bool MERGE, int UNIT, Role ROLE, bool NT, int D = 128,
           int WAVES = waves_for<UNIT>(), bool DM = false, bool PRE = false, int NCB = 1>
 __device__ __forceinline__ void decode_role(const DecodeParams& p, const CascadeParams& cp, int block,
-                                            DecodeLds<WAVES>& lds, [[maybe_unused]] uint8_t* kstage = nullptr) {
+                                            DecodeLds<WAVES, acc_pitch<D>()>& lds,
+                                            [[maybe_unused]] uint8_t* kstage = nullptr) {
   static_assert(ROLE == Role::kRow || !(FUSE || MERGE),
                 "cascade and balanced roles have no fused append or in-launch merge");
   static_assert(D == 128 || (ROLE == Role::kRow && FUSE != 2 && !MERGE),
@@ -1232,11 +1270,14 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       while (step(cur, alt)) cur = alt;
     }
   }
-  // merge threads: thread -> (column h, dims [d0, d0 + 8)), D/8 threads per
-  // column; threads past the first 2D only take part in the barriers
-  constexpr int kDimThreads = D / 8;
+  // merge threads: thread -> (column h, dims [d0, d0 + kDpt)), 16 threads
+  // per column (8 dims each at head_dim 128, 4 at 64), so that every merge
+  // read has the conflict-free pattern of acc_pitch; threads past the first
+  // 256 only take part in the barriers
+  constexpr int kDpt = D == 128 ? 8 : 4;
+  constexpr int kDimThreads = D / kDpt;
   const int h = (threadIdx.x / kDimThreads) & 15;
-  const int d0 = (threadIdx.x % kDimThreads) * 8;
+  const int d0 = (threadIdx.x % kDimThreads) * kDpt;
   int ob = b, qh = kvh * G + 16 * hb + h;
   bool head_ok = threadIdx.x < 16 * kDimThreads && 16 * hb + h < G;
   // one round per column block: the waves' slots hold one block at a time
@@ -1257,15 +1298,17 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         lds.col_h[c] = col_h[cb];
       }
     }
+    constexpr int kSpread = acc_spread<D>();
     if constexpr (DM) {
       // this lane's dims 16*n + 4*g + rr (load_unit_dm's V rows)
 #pragma unroll
-      for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f32x4*>(&lds.acc[wave][c][16 * n + 4 * g]) = st[cb].acc[n];
+      for (int n = 0; n < D / 16; ++n)
+        *reinterpret_cast<f32x4*>(&lds.acc[wave][c][kSpread * (16 * n + 4 * g)]) = st[cb].acc[n];
     } else {
       // this lane's dims (D/4)*g + (D/16)*rr + n, n < D/16: one or two 16-byte rows
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        float* dst = &lds.acc[wave][c][(D / 4) * g + (D / 16) * rr];
+        float* dst = &lds.acc[wave][c][kSpread * ((D / 4) * g + (D / 16) * rr)];
         const WaveState<D>& w = st[cb];
         *reinterpret_cast<f32x4*>(dst) = f32x4{w.acc[0][rr], w.acc[1][rr], w.acc[2][rr], w.acc[3][rr]};
         if constexpr (D == 128)
@@ -1294,16 +1337,17 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     for (int w = 0; w < kWaves; ++w) {
       const float wt = exp2f(lds.m[w][h] - Mu);
       L += wt * lds.l[w][h];
-      const f32x4 a0 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0]);
-      const f32x4 a1 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][kSpread * d0]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        o[j] += wt * a0[j];
-        o[4 + j] += wt * a1[j];
+      for (int j = 0; j < 4; ++j) o[j] += wt * a0[j];
+      if constexpr (kDpt == 8) {
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[4 + j] += wt * a1[j];
       }
     }
     if (ROLE == Role::kRow && p.splits == 1) {
-      if (head_ok) store_row<T>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
+      if (head_ok) store_row<T, kDpt>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
       continue;
     }
     // split partial: unnormalised acc, base-2 max, denominator; the prefix
@@ -1329,10 +1373,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       } else {
         if (p.as3 == 1) {
           *reinterpret_cast<f32x4*>(a) = f32x4{o[0], o[1], o[2], o[3]};
-          *reinterpret_cast<f32x4*>(a + 4) = f32x4{o[4], o[5], o[6], o[7]};
+          if constexpr (kDpt == 8) *reinterpret_cast<f32x4*>(a + 4) = f32x4{o[4], o[5], o[6], o[7]};
         } else {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) a[j * p.as3] = o[j];
+          for (int j = 0; j < kDpt; ++j) a[j * p.as3] = o[j];
         }
         if (d0 == 0) {
           p.mx[so] = M;
@@ -1514,7 +1558,7 @@ template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 1
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
     const void* bt, int64_t bts0, int64_t bts1, int64_t max_blocks_per_seq, int32_t splits, int32_t hkv,
     int32_t group, int32_t hint_tps, int32_t bt_i64, int32_t xcd_blocks, DecodeParams p) {
-  __shared__ DecodeLds<waves_for<UNIT>()> lds;
+  __shared__ DecodeLds<waves_for<UNIT>(), acc_pitch<D>()> lds;
   DecodeParams q = p;
   q.bt = bt;
   q.bts0 = bts0;
@@ -1540,7 +1584,7 @@ constexpr int kDmPerCU = 2;
 template <typename T, int BS, bool NT, int D, int FUSE>
 __global__ __launch_bounds__(64 * kDmWaves, FUSE ? 1 : kDmPerCU) void decode_dm_kernel(DecodeParams p,
                                                                                        int32_t xcd_blocks) {
-  __shared__ DecodeLds<kDmWaves> lds;
+  __shared__ DecodeLds<kDmWaves, acc_pitch<D>()> lds;
   __shared__ __attribute__((aligned(16))) uint8_t stage[kDmWaves * D * kDmRowBytes];
   decode_role<T, BS, FUSE, false, 32, Role::kRow, NT, D, kDmWaves, true>(
       p, CascadeParams{}, xcd_logical_block(blockIdx.x, xcd_blocks), lds, stage);

@@ -189,15 +189,32 @@ def test_rope_hand_calculation_kat():
     np.testing.assert_allclose(out[1, 0], expected, atol=kat["tolerance"], rtol=0)
 
 
-def test_rope_cos_sin_are_correctly_rounded():
-    pos = np.array([0, 1, 7, 1000, 131071])
-    cos, sin = orope.rope_cos_sin(pos, 128, base=1e6)
-    for b, p in enumerate(pos):
-        for i in range(64):
-            e = np.float32(-np.float32(2 * i) / np.float32(128))
-            inv = np.float32(math.pow(1e6, float(e)))
-            ang = float(np.float32(np.float32(p) * inv))
-            assert cos[b, i] == np.float32(math.cos(ang)) and sin[b, i] == np.float32(math.sin(ang))
+def test_rope_cos_sin_match_the_float64_closed_form():
+    """cos/sin of frequency i at position p against the float64 closed form cos(p * base^(-2i/R)):
+    the fp32 algorithm rounds the frequency and the angle once each (relative 2^-24 apiece) and
+    the result once more, so it may be off by at most angle * 2^-22 + 2^-23.  A frequency index
+    off by one, or another base, moves the angle by a fraction of itself and fails the same
+    bound at the positions tested."""
+    pos = np.array([1, 7, 1000, 8191, 131071])
+    rotary_dim, base = 128, 1e6
+    half = rotary_dim // 2
+
+    def exact(p, shift=0, b=base):
+        theta = np.exp(-2.0 * (np.arange(half) + shift) / rotary_dim * math.log(b))
+        ang = p[:, None].astype(np.float64) * theta[None, :]
+        return np.cos(ang), np.sin(ang), ang
+
+    cos, sin = orope.rope_cos_sin(pos, rotary_dim, base=base)
+    ec, es, ang = exact(pos)
+    tol = ang * 2.0**-22 + 2.0**-23
+    assert (np.abs(cos - ec) <= tol).all() and (np.abs(sin - es) <= tol).all()
+    # position 0 is the identity rotation, exactly
+    c0, s0 = orope.rope_cos_sin(np.array([0]), rotary_dim, base=base)
+    assert (c0 == 1.0).all() and (s0 == 0.0).all()
+    # planted mistakes: the oracle's values must miss each wrong closed form somewhere
+    for shift, b in ((1, base), (-1, base), (0, 1e4)):
+        wc, ws, _ = exact(pos, shift, b)
+        assert (np.abs(cos - wc) > tol).any() or (np.abs(sin - ws) > tol).any()
 
 
 def test_rope_invariants():
@@ -331,3 +348,22 @@ def test_split_policy_kats():
     for value in kat["invalid_requests"]:
         with pytest.raises(ValueError, match=r"0, 1, 2, 4, 8, or 16 \(0 selects auto\)"):
             osp.parse_requested_splits(value)
+
+
+def test_torch_loop_restatement_matches_the_numpy_oracle():
+    """The torch-CPU loop form (bench.py's CPU baseline) against the independently pinned numpy
+    oracle: fp32 C1-shaped inputs with an empty row and ragged lengths, and bf16 inputs."""
+    from oracle.torch_loop import paged_decode_attention_loop
+
+    q, k, v, table, lens = random_paged([37, 0, 512, 1, 300], 8, 2, 64, 32, seed=61)
+    got = paged_decode_attention_loop(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                      torch.from_numpy(table), torch.from_numpy(lens), 0.125).numpy()
+    want = oa.paged_decode_attention(q, k, v, table, lens, sm_scale=0.125)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    assert (got[1] == 0).all()
+    bf = [torch.from_numpy(x).to(torch.bfloat16) for x in (q, k, v)]
+    got = paged_decode_attention_loop(*bf, torch.from_numpy(table), torch.from_numpy(lens), 0.125)
+    assert got.dtype == torch.bfloat16
+    want = oa.paged_decode_attention(*(x.float().numpy() for x in bf), table, lens, sm_scale=0.125,
+                                     out_dtype="bfloat16")
+    np.testing.assert_allclose(got.float().numpy(), want, rtol=1e-2, atol=1e-2)
