@@ -489,13 +489,27 @@ def run_rope(torch, dev, args):
         _fused_rope_kv_append_trusted(q, k, v, kc, vc, blk, off, pos, base=1e6, q_out=qo)
 
     ms = graph_ms_per_call(torch, dev, fn, args.steps)
+    # the same launch reading cos/sin from a table (what the cache and the
+    # engine pass by default: apply_rope's bits), 8192 rows
+    from flashdec_amd.rope import rope_cos_sin_table
+
+    tab = rope_cos_sin_table(8192, d, 1e6, device=dev)
+
+    def fn_table(i):
+        q, k, v, qo = calls[i % len(calls)]
+        _fused_rope_kv_append_trusted(q, k, v, kc, vc, blk, off, pos, base=1e6, q_out=qo, cos_sin_table=tab)
+
+    ms_t = graph_ms_per_call(torch, dev, fn_table, args.steps)
     nbytes = batch * (2 * hq + 3 * hkv) * d * 2 + 24 * batch
-    log(f"[bench] rope+append: {ms * 1e3:.2f} us/call, {nbytes} B/call")
+    log(f"[bench] rope+append: {ms * 1e3:.2f} us/call (cos/sin evaluated), {ms_t * 1e3:.2f} us/call (cos/sin table), "
+        f"{nbytes} B/call")
     out = common_fields(args, "fused RoPE + KV append us/call, B64 Hq16 Hkv2 D128 bf16 (C3)", round(ms * 1e3, 3),
                         "us", ms, False, {"workload": "rope-kv-append-b64-hq16-hkv2-d128-bs32", "batch": batch,
                                           "rope_theta": 1e6, "positions": "U{1..8191} seed 251"})
     out["roofline"] = {"bound": "launch", "algorithmic_bytes_per_call": nbytes,
                        "achieved": round(nbytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "peak": HBM_PEAK_GBS}
+    out["cos_sin_table"] = {"us_per_call": round(ms_t * 1e3, 3), "rows": 8192,
+                            "note": "the default of PagedKVCache / DecodeEngine launches (bit-exact to apply_rope)"}
     return out
 
 
@@ -1045,7 +1059,7 @@ def run_engine(torch, dev, args):
     steps = args.engine_steps
     # room for the warm-ups, the timed steps, the separate-RoPE comparison steps and the eager steps
     n_eager, warm_eager = 20, 5
-    width = (ctx + 2 * 20 + 2 * steps + 2 + n_eager + warm_eager + bs - 1) // bs
+    width = (ctx + 3 * 20 + 3 * steps + 2 + n_eager + warm_eager + bs - 1) // bs
     cache = PagedKVCache(layers, hkv, d, bs, max_blocks=batch * width, dtype=torch.bfloat16, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(109)
@@ -1142,6 +1156,32 @@ def run_engine(torch, dev, args):
         separate = start.elapsed_time(stop) / n_sep
     else:
         committed_sep = 0
+    # the same graph steps with cos/sin evaluated inside the kernels (the
+    # cache's rope_tables off) instead of read from the cache's table
+    cache.rope_tables = False
+    sg_eval = engine.capture_step_graph(batch, hq, base=1e6)
+    cache.rope_tables = True
+    assert sg_eval.cos_sin_table is None and sg.cos_sin_table is not None
+    sg_eval.q.copy_(sg.q)
+    sg_eval.k.copy_(sg.k)
+    sg_eval.v.copy_(sg.v)
+
+    def graph_step_eval():
+        tx_ = engine.begin_step(ids)
+        engine.step_graph(tx_, sg_eval)
+        engine.commit_step(tx_)
+
+    for _ in range(warm):
+        graph_step_eval()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        graph_step_eval()
+    stop.record()
+    torch.cuda.synchronize()
+    eval_ms = start.elapsed_time(stop) / steps
+    committed_sep += warm + steps
+    log(f"[bench] engine: graph steps with cos/sin evaluated in the kernels (no table): {eval_ms:.3f} ms/step")
     # the same steps without a graph: step_layer per layer, as the reference's
     # engine runs (after layer 0, RoPE + append inside the decode launch)
 
@@ -1188,6 +1228,9 @@ def run_engine(torch, dev, args):
             pd._fill_append(args_, sg.k[layer], sg.v[layer], meta.slots)
             args_.rotary_dim = sg.rotary_dim
             args_.rope_base = sg.base
+            if sg.cos_sin_table is not None:
+                args_.rope_cos_sin_table = sg.cos_sin_table.data_ptr()
+                args_.rope_table_rows = sg.cos_sin_table.shape[1]
         prepared.append((args_, pd._lib.current_stream_handle(dev)))
     attn_us, red_us = attention_kernel_us(torch, prepared, 16)
     engine.abort_step(tx)
@@ -1210,6 +1253,10 @@ def run_engine(torch, dev, args):
                          "steps": n_eager, "context_at_start": ctx_eager + warm_eager,
                          "note": "begin_step, 36 x step_layer, commit_step; no graph; measured after the graph "
                                  "steps, so at a longer context than the graph line"}
+    out["rope_cos_sin"] = {"table": "the cache's own (PagedKVCache.rope_table), the default: bit-exact to apply_rope",
+                           "no_table_ms_per_step": round(eval_ms, 4),
+                           "no_table_note": "rope_tables off: cos/sin evaluated in the kernels (float64, rounded "
+                                            "once), same graph steps without aborts"}
     if separate is not None:
         out["separate_rope_kernel_path"] = {"ms_per_step": round(separate, 4), "kernels_per_layer": 3,
                                             "steps": steps}
