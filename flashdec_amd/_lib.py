@@ -127,6 +127,7 @@ class RopeAppendArgs(ctypes.Structure):
 EXPORTED_SYMBOLS = (
     "fd_paged_decode",
     "fd_paged_decode_noalloc",
+    "fd_paged_decode_noalloc_prepare",
     "fd_paged_decode_cascade",
     "fd_paged_decode_plan",
     "fd_paged_decode_balance_target",
@@ -169,6 +170,8 @@ def load_library():
         lib.fd_paged_decode.restype = ctypes.c_int
         lib.fd_paged_decode_noalloc.argtypes = [ctypes.POINTER(PagedDecodeArgs), _vp]
         lib.fd_paged_decode_noalloc.restype = ctypes.c_int
+        lib.fd_paged_decode_noalloc_prepare.argtypes = [_vp]
+        lib.fd_paged_decode_noalloc_prepare.restype = ctypes.c_int
         lib.fd_paged_decode_cascade.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(CascadeArgs), _vp]
         lib.fd_paged_decode_cascade.restype = ctypes.c_int
         lib.fd_paged_decode_balance_target.argtypes = [_i64, _i64]
@@ -245,6 +248,13 @@ def paged_decode(args: PagedDecodeArgs, stream: int) -> None:
     lib = load_library()
     args.struct_size = ctypes.sizeof(PagedDecodeArgs)
     check(lib.fd_paged_decode(ctypes.byref(args), stream), "fd_paged_decode")
+
+
+def paged_decode_noalloc_prepare(stream: int) -> None:
+    """``fd_paged_decode_noalloc_prepare``: resolve the scratch address on the stream's device
+    (before capturing ``paged_decode_noalloc`` into a graph)."""
+    lib = load_library()
+    check(lib.fd_paged_decode_noalloc_prepare(stream), "fd_paged_decode_noalloc_prepare")
 
 
 def paged_decode_noalloc(args: PagedDecodeArgs, stream: int) -> None:

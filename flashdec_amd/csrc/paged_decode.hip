@@ -2652,6 +2652,12 @@ int scratch_address(hipStream_t stream, const char* fn, float** out) {
 }
 }  // namespace
 
+extern "C" int fd_paged_decode_noalloc_prepare(fd_stream_t stream_) {
+  clear_launch_record();
+  float* base = nullptr;
+  return scratch_address(reinterpret_cast<hipStream_t>(stream_), "fd_paged_decode_noalloc_prepare", &base);
+}
+
 extern "C" int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream_) {
   clear_launch_record();
   static const char* fn = "fd_paged_decode_noalloc";

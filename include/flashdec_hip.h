@@ -220,10 +220,22 @@ int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
  * merged by the reducer kernel (no in-launch merge).  Nothing in the array
  * needs to start at zero.  Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (two streams, two threads) race and must be
- * serialised by the caller.  The first call on a device looks the array's
- * address up once (hipGetSymbolAddress); no call allocates or frees memory.
+ * serialised by the caller.  The array's address on a device is looked up
+ * once (hipGetSymbolAddress) by fd_paged_decode_noalloc_prepare or, failing
+ * that, by the first call on the device; no call allocates or frees memory.
  */
 int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream);
+
+/*
+ * Set-up of fd_paged_decode_noalloc on the stream's device (the current
+ * device for a NULL stream): looks the scratch array's device address up,
+ * once per device, with that device current, and launches nothing.  Call it
+ * (or make one eager fd_paged_decode_noalloc call) on every device before
+ * capturing fd_paged_decode_noalloc into a hipGraph, so that no lookup runs
+ * inside the capture.  Allocates nothing; idempotent.  No counterpart in the
+ * reference.
+ */
+int fd_paged_decode_noalloc_prepare(fd_stream_t stream);
 
 /*
  * Shared-prefix (cascade) decode: the result of fd_paged_decode, with the

@@ -127,3 +127,56 @@ def test_fused_append_writes_the_same_cache_bytes():
     for b, s in enumerate(slots):
         assert torch.equal(k2[s // bs, :, s % bs], ak[b]) and torch.equal(v2[s // bs, :, s % bs], av[b])
     assert_close_to_oracle(out, _oracle(q, k2, v2, table, lens))
+
+
+def test_captured_noalloc_launch_replays_like_the_workspace_entry_point():
+    """fd_paged_decode_noalloc captured into a hipGraph (after fd_paged_decode_noalloc_prepare
+    resolved the scratch address outside the capture): every replay, with new inputs copied
+    into the captured buffers and eager work of the program's own between the replays, equals
+    fd_paged_decode on the same inputs bit for bit, and the oracle within tolerance."""
+    from flashdec_amd import _lib
+
+    b, hq, hkv, d, bs = 8, 16, 2, 128, 32
+    splits = _lib.paged_decode_plan(b, hq, hkv, d, 1024)
+    assert splits > 1
+    q, k, v, table, lens = make_paged_inputs([1024, 999, 1, 512, 1024, 77, 640, 1000], hq, hkv, d, bs, seed=41)
+    out = torch.full_like(q, float("nan"))
+    args = _args(q, k, v, table, lens, out, bs, hkv, splits)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        stream = _lib.current_stream_handle(q.device)
+        _lib.paged_decode_noalloc_prepare(stream)
+        with torch.cuda.graph(graph, stream=side):
+            _lib.paged_decode_noalloc(args, _lib.current_stream_handle(q.device))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    ws = _workspace(b, hq, splits, d)
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        q2, k2, v2, _, lens2 = make_paged_inputs([1024, 999, 1, 512, 1024, 77, 640, 1000], hq, hkv, d, bs,
+                                                  seed=100 + rep)
+        q.copy_(q2)
+        k.copy_(k2)
+        v.copy_(v2)
+        lens.copy_(torch.clamp(lens2 - rep * 100, min=0))
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = torch.empty_like(q)
+        _lib.paged_decode(_args(q, k, v, table, lens, ref, bs, hkv, splits, ws), _lib.current_stream_handle(q.device))
+        # the program's own eager work between the replays: a different noalloc launch
+        _both(*make_paged_inputs([300, 5], 8, 2, 64, 16, seed=7 + rep), 16, 2, 4)
+        torch.cuda.synchronize()
+        assert torch.equal(ref, out), rep
+        assert_close_to_oracle(out, _oracle(q, k, v, table, lens))
+
+
+def test_prepare_needs_no_launch_and_is_idempotent():
+    from flashdec_amd import _lib
+
+    stream = _lib.current_stream_handle(torch.device("cuda"))
+    for _ in range(3):
+        _lib.paged_decode_noalloc_prepare(stream)
+    _lib.paged_decode_noalloc_prepare(0)  # the null stream: the current device
