@@ -1811,7 +1811,8 @@ __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
 // selects the zero row below just as the length test does.
 template <typename T, int D, int MODE, int W, bool PRE>
 __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row = blockIdx.x) {
-  static_assert(!PRE || MODE == kReducePlain, "preloaded reducer arguments are for the plain merge");
+  static_assert(!PRE || MODE == kReducePlain || MODE == kReduceCascade,
+                "preloaded reducer arguments are for the plain and cascade merges");
   if constexpr (!PRE) {
     // every argument in SGPRs before any use: one batch of argument loads,
     // one wait (left alone the compiler fetched the strides lazily, a second
@@ -1835,8 +1836,19 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
     slot = load_index(p.slot, b * p.slots + vzero, p.slot_i64);  // seq_lens when not fused
   }
   int splits = p.splits;
-  if constexpr (MODE == kReduceCascade)
-    splits = __builtin_amdgcn_readfirstlane(p.tb[b + vzero]) > 0 ? p.splits : p.tail_splits;
+  // splits of this row that hold partials: all of them, or in the cascade
+  // the tail splits only for rows without a prefix.  With preloaded
+  // arguments the loads below cover every split and issue without waiting
+  // for the row's prefix length; the splits past `valid` are masked.
+  int valid = p.splits;
+  if constexpr (MODE == kReduceCascade) {
+    if constexpr (PRE) {
+      valid = p.tb[b + vzero] > 0 ? p.splits : p.tail_splits;
+    } else {
+      splits = __builtin_amdgcn_readfirstlane(p.tb[b + vzero]) > 0 ? p.splits : p.tail_splits;
+      valid = splits;
+    }
+  }
   if constexpr (MODE == kReduceBalanced) {
     // the same counts as the attention kernel: T from the batch's total tiles
     auto eff_of = [&](int64_t len) -> int64_t { return len > 0 ? (len < p.cap ? len : p.cap) : 0; };
@@ -1884,7 +1896,7 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
         const int src = min(c0 + j, n - 1);
         m[j] = lane_bcast(lm, src);
         l[j] = lane_bcast(ll, src);
-        cm = c0 + j < n ? fmaxf(cm, m[j]) : cm;
+        cm = c0 + j < n && s64 + c0 + j < valid ? fmaxf(cm, m[j]) : cm;
       }
       const float nm = fmaxf(M, cm);
       const float nmu = nm == -INFINITY ? 0.f : nm;
@@ -1894,10 +1906,12 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
       for (int e = 0; e < E; ++e) o[e] *= sc;
 #pragma unroll
       for (int j = 0; j < kReduceChunk; ++j) {
-        const float w = c0 + j < n ? exp2f(m[j] - nmu) : 0.f;
-        L += w * l[j];
+        // masked splits may hold stale or NaN partials: selected away, not weighted by 0
+        const bool use = c0 + j < n && s64 + c0 + j < valid;
+        const float w = use ? exp2f(m[j] - nmu) : 0.f;
+        L += use ? w * l[j] : 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
+        for (int e = 0; e < E; ++e) o[e] += use ? w * a[j][e] : 0.f;
       }
       M = nm;
     }
@@ -1961,6 +1975,28 @@ __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* a
   q.splits = splits;
   q.hq = hq;
   reduce_row<T, D, kReducePlain, W, true>(q, xcd_logical_block(blockIdx.x, xcd_rows));
+}
+
+// The cascade merge over a packed workspace (as split_reduce_pre_kernel),
+// with the row prefix lengths preloaded too: every split's partial loads
+// issue at wave start, and rows without a prefix mask the prefix splits once
+// their length arrives (before, the length was a round trip ahead of them).
+template <typename T, int D>
+__global__ __launch_bounds__(64) void split_reduce_cascade_pre_kernel(const float* acc, const float* mx,
+                                                                      const float* sm, int64_t as1, int64_t as2,
+                                                                      int64_t ss1, int32_t splits, int32_t hq,
+                                                                      const int32_t* tb, ReduceParams p) {
+  ReduceParams q = p;
+  q.acc = acc;
+  q.mx = mx;
+  q.sm = sm;
+  q.as1 = as1;
+  q.as2 = as2;
+  q.ss1 = ss1;
+  q.splits = splits;
+  q.hq = hq;
+  q.tb = tb;
+  reduce_row<T, D, kReduceCascade, 1, true>(q);
 }
 
 // ========================================================== host glue ====
@@ -2221,6 +2257,9 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
     } else {
       pre(split_reduce_pre_kernel<T, 128>, dim3(64));
     }
+  } else if (MODE == kReduceCascade && reduce_layout_packed(r) && r.splits <= 32 && a.head_dim == 128) {
+    dispatch(split_reduce_cascade_pre_kernel<T, 128>, grid, dim3(64), stream, e0, e1, r.acc, r.mx, r.sm, r.as1,
+             r.as2, r.ss1, r.splits, r.hq, r.tb, r);
   } else if (r.splits > 32) {
     // more than 32 splits: four waves per row share them
     if (a.head_dim == 64)

@@ -29,6 +29,15 @@ def _cascade():
     return cascade
 
 
+@pytest.fixture
+def record():
+    from flashdec_amd import _lib
+
+    _lib.record_launches(True)
+    yield _lib
+    _lib.record_launches(False)
+
+
 def make_prefix_inputs(groups, singles, hq, hkv, block_size, dtype, seed=3, head_dim=128):
     """groups: list of (prefix_blocks, [tail tokens per member]); singles:
     lengths of rows that share nothing.  Returns q, k, v, table, lens (cuda)
@@ -217,3 +226,38 @@ def test_repeated_cascade_calls_reuse_arguments_but_follow_every_pointer():
             cas.paged_decode_attention_cascade_into(q, k, v, table, lens, out2, g, num_splits=4, prefix_splits=8,
                                                     workspace=wss[(i + rnd) % 2])
             assert_close_to_oracle(out2, expected)
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_rows_without_a_prefix_ignore_poisoned_prefix_slots(packed, record):
+    """Rows in no group (and zero-length rows) have no prefix partials: the merge must not read
+    them.  With a packed workspace the preloaded cascade merge loads every split before the row's
+    prefix length arrives and masks the prefix splits by selection, so NaN left in those slots
+    must not reach the output; a strided workspace takes the other merge.  Both must equal the
+    oracle on a workspace poisoned with NaN before every call."""
+    cas = _cascade()
+    groups_def = [(20, [7, 0, 300]), (5, [64, 1])]
+    q, k, v, table, lens, _ = make_prefix_inputs(groups_def, [0, 90, 513, 1], 16, 2, 32, torch.bfloat16, seed=71)
+    g = cas.build_cascade_groups(table, lens, 32, 16, 2)
+    b, hq = q.shape[:2]
+    tail, pre = 3, 4
+    if packed:
+        ws = (torch.full((b, hq, tail + pre, 128), float("nan"), device="cuda"),
+              torch.full((b, hq, tail + pre), float("nan"), device="cuda"),
+              torch.full((b, hq, tail + pre), float("nan"), device="cuda"))
+    else:
+        # statistics with a split stride of 2: not the packed layout
+        big = torch.full((b, hq, tail + pre + 2, 136), float("nan"), device="cuda")
+        st = torch.full((b, hq, 2 * (tail + pre)), float("nan"), device="cuda")
+        ws = (big[:, :, 1:tail + pre + 1, :128], st[:, :, ::2], st.clone()[:, :, ::2])
+    expected = _oracle(q, k, v, table, lens)
+    for rep in range(2):
+        for t in ws:
+            t.fill_(float("nan"))
+        out = torch.empty_like(q)
+        cas.paged_decode_attention_cascade_into(q, k, v, table, lens, out, g, num_splits=tail, prefix_splits=pre,
+                                                workspace=ws)
+        torch.cuda.synchronize()
+        reducer = record.last_launch()[-1]
+        assert ("split_reduce_cascade_pre_kernel" in reducer) == packed, reducer
+        assert_close_to_oracle(out, expected)

@@ -109,8 +109,9 @@ def test_cascade_launch_and_reducer(kv_reuse, nt, record):
     out = cascade.paged_decode_attention_cascade(q, k, v, table, sl, groups=g, kv_reuse=kv_reuse)
     names = record.last_launch()
     # 64 rows on a 16384-token prefix: 32-row chunks (two column blocks per wave)
+    # the library's packed workspace: the cascade merge with preloaded arguments
     assert names == [f"fd::cascade_decode_kernel<__bf16, 32, 16, {nt}, 2>",
-                     "fd::split_reduce_kernel<__bf16, 128, 1, 1>"], names
+                     "fd::split_reduce_cascade_pre_kernel<__bf16, 128>"], names
     assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
 
 
