@@ -721,7 +721,10 @@ def load_probes():
     lib.fdp_stream_read.argtypes = [vp, u64, vp, vp, vp, vp]
     lib.fdp_empty.argtypes = [ctypes.c_uint, ctypes.c_uint, vp]
     lib.fdp_xcc_map.argtypes = [vp, ctypes.c_uint, vp]
-    for f in (lib.fdp_stream_read, lib.fdp_empty, lib.fdp_xcc_map):
+    i32, i64 = ctypes.c_int, ctypes.c_int64
+    lib.fdp_paged_read.argtypes = [vp, i32, i32, i32, i32, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp]
+    lib.fdp_reduce_read.argtypes = [vp, vp, vp, i32, i32, vp, vp]
+    for f in (lib.fdp_stream_read, lib.fdp_empty, lib.fdp_xcc_map, lib.fdp_paged_read, lib.fdp_reduce_read):
         f.restype = ctypes.c_int
     return lib
 
@@ -737,12 +740,22 @@ def run_c2_floor(torch, dev, args):
       read+empty  -- that read, then a dependent empty kernel of the reducer's
                      grid (B*Hq workgroups of 64 threads): two dependent
                      launches with no work beyond the read;
+      paged_read  -- the attention kernel's memory pattern without its
+                     arithmetic (fdp_paged_read): its grid, each wave's
+                     block-table entry then its K/V unit, the waves combined
+                     through LDS, one partial per (query head, split) stored;
+      paged_read+reduce_read
+                  -- then the reducer's memory pattern (fdp_reduce_read):
+                     every split's partials and statistics loaded up front, a
+                     weighted sum, the output row stored.  The floor of a
+                     two-launch split-KV paged call of this shape;
       shipped     -- paged_decode_attention_into: attention + reducer kernel;
       merge       -- the opt-in single-dispatch path (split_counters: the last
                      workgroup of each (request, KV head) merges);
     plus eager kernel durations (HIP events around each dispatch) of the bare
-    read, the attention kernel and the reducer, and the workgroup -> XCD map
-    of a 256-workgroup grid (the in-launch merge reads same-XCD partials from L2).
+    read, the paged read, the attention kernel and the reducer, and the
+    workgroup -> XCD map of a 256-workgroup grid (the in-launch merge reads
+    same-XCD partials from L2).
     """
     import flashdec_amd as fd
     from flashdec_amd import _lib
@@ -777,6 +790,21 @@ def run_c2_floor(torch, dev, args):
             fd.paged_decode_attention_into(q, k, v, table, lens, out, sm_scale=sm_scale)
 
         splits = _lib.paged_decode_plan(batch, hq, hkv, d, pools[0][3].shape[1] * bs)
+        probe_ws = (torch.empty((batch * hq, splits, d), device=dev), torch.empty((batch * hq, splits), device=dev),
+                    torch.empty((batch * hq, splits), device=dev))
+
+        def paged_read(i, events=(None, None)):
+            q, k, v, table, lens, out = pools[i % len(pools)]
+            st = torch.cuda.current_stream(dev).cuda_stream
+            assert probes.fdp_paged_read(table.data_ptr(), table.shape[1], batch, hkv, splits, k.data_ptr(),
+                                         v.data_ptr(), k.stride(0) * 2, k.stride(1) * 2,
+                                         *(t.data_ptr() for t in probe_ws), st, *events) == 0
+
+        def paged_reduce(i):
+            paged_read(i)
+            out = pools[i % len(pools)][5]
+            assert probes.fdp_reduce_read(*(t.data_ptr() for t in probe_ws), batch * hq, splits, out.data_ptr(),
+                                          torch.cuda.current_stream(dev).cuda_stream) == 0
         ws = (torch.empty((batch, hq, splits, d), device=dev), torch.empty((batch, hq, splits), device=dev),
               torch.empty((batch, hq, splits), device=dev))
         counters = torch.zeros(batch * hkv * _lib.SPLIT_COUNTER_STRIDE, device=dev, dtype=torch.int32)
@@ -788,7 +816,8 @@ def run_c2_floor(torch, dev, args):
 
         n = len(pools)
         terms = {name: round(graph_p50_us(torch, dev, fn, n), 3)
-                 for name, fn in (("read", rd), ("read+empty", rd_empty), ("shipped", shipped), ("merge", merge))}
+                 for name, fn in (("read", rd), ("read+empty", rd_empty), ("paged_read", paged_read),
+                                  ("paged_read+reduce_read", paged_reduce), ("shipped", shipped), ("merge", merge))}
         # eager durations: HIP events recorded around exactly each bare-read
         # dispatch (hipExtLaunchKernel), the reads back to back behind a sleep
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2 * n)]
@@ -801,21 +830,28 @@ def run_c2_floor(torch, dev, args):
             rd(i, (a.cuda_event, b.cuda_event))
         torch.cuda.synchronize()
         read_kernel = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
+        torch.cuda._sleep(100_000_000)
+        for i, (a, b) in enumerate(evs):
+            paged_read(i, (a.cuda_event, b.cuda_event))
+        torch.cuda.synchronize()
+        paged_kernel = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
         shipped(0)
         prepared = [prepared_args(pool, sm_scale, bs, hkv) for pool in pools]
         attn_us, red_us = attention_kernel_us(torch, prepared, min(4 * n, 192))
         floor = {
             "us_per_call": terms,
-            "eager_kernel_us": {"read": round(read_kernel, 3), "attention": round(attn_us, 3),
-                                "reducer": round(red_us, 3)},
+            "eager_kernel_us": {"read": round(read_kernel, 3), "paged_read": round(paged_kernel, 3),
+                                "attention": round(attn_us, 3), "reducer": round(red_us, 3)},
             "dependent_launch_us": round(terms["read+empty"] - terms["read"], 3),
             "shipped_over_two_launch_floor_us": round(terms["shipped"] - terms["read+empty"], 3),
+            "shipped_over_paged_floor_us": round(terms["shipped"] - terms["paged_read+reduce_read"], 3),
             "hbm_frac": {k: round(nbytes / (v * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) for k, v in terms.items()},
             "algorithmic_bytes": nbytes,
             "num_splits": splits,
         }
         log(f"[bench] c2-floor ctx{ctx}: " + ", ".join(f"{k} {v:.2f}" for k, v in terms.items())
-            + f" us/call; eager read {read_kernel:.2f}, attention {attn_us:.2f}, reducer {red_us:.2f} us")
+            + f" us/call; eager read {read_kernel:.2f}, paged read {paged_kernel:.2f}, attention {attn_us:.2f},"
+            + f" reducer {red_us:.2f} us")
         res[f"ctx{ctx}"] = floor
         del pools, bufs
         torch.cuda.empty_cache()

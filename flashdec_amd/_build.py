@@ -33,6 +33,10 @@ SOURCES = {
     "rope_append.hip": ["-ffp-contract=off", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
+# the probes get the decode kernels' kernel-argument preloading, so that they
+# are timed on the same footing
+PROBE_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -79,7 +83,7 @@ def build_library(verbose: bool = False) -> Path:
 def build_probe_library(verbose: bool = False) -> Path:
     """Compile ``libflashdec_probe.so`` (bench.py's floor probes); returns its path."""
     tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
-    _run([_hipcc(), *COMMON_FLAGS, "-shared", str(CSRC / PROBE_SOURCE), "-o", str(tmp)], verbose)
+    _run([_hipcc(), *COMMON_FLAGS, *PROBE_FLAGS, "-shared", str(CSRC / PROBE_SOURCE), "-o", str(tmp)], verbose)
     os.replace(tmp, PROBE_LIB_PATH)
     return PROBE_LIB_PATH
 

@@ -10,7 +10,24 @@
 //   * fdp_empty -- an empty kernel: launched after fdp_stream_read on the same
 //     stream it prices a dependent second launch (the reducer's launch);
 //   * fdp_xcc_map -- each workgroup's XCD (hardware register XCC_ID), to check
-//     the round-robin workgroup -> XCD dispatch the decode grid layout uses.
+//     the round-robin workgroup -> XCD dispatch the decode grid layout uses;
+//   * fdp_paged_read -- the split attention kernel's memory pattern with no
+//     attention arithmetic: the same grid (one workgroup of four waves per
+//     (request, KV head, split), XCD by XCD), each wave's block-table entry,
+//     then its 32-token K and V unit (non-temporal 16-byte loads, all issued
+//     before any is used), the four waves' results combined through LDS, and
+//     one split partial per (query head, split) stored as the attention kernel
+//     stores its partials;
+//   * fdp_reduce_read -- the split reducer's memory pattern with the
+//     arithmetic cut to a weighted sum: one wave per (request, query head),
+//     every split's partial row and statistics loaded up front, one output
+//     row stored.
+// fdp_paged_read then fdp_reduce_read is the floor of a two-launch split-KV
+// paged call of that shape: two dependent launches, the block-table round
+// trip ahead of the K/V loads, and the round trip to the partials.
+//
+// Built with the decode library's kernel-argument preloading, so the probes'
+// first loads issue without a kernel-argument fetch, as the decode kernels' do.
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
@@ -40,6 +57,97 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const u32x4* src,
 }
 
 __global__ void empty_kernel() {}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kUnit16 = 512;  // one 32-token block of one KV head: 32 * 128 bf16 = 8 KB = 512 x 16 B
+constexpr int kGroup = 8;     // query heads per KV head (the probe's shape: D 128, so 8 x 32 threads)
+
+// grid: batch * hkv * splits workgroups of 256 threads; per_xcd > 0: the
+// i-th workgroup on XCD x is logical workgroup x * per_xcd + i
+__global__ __launch_bounds__(kThreads, 1) void paged_read_kernel(const int32_t* bt, int32_t nblk, int32_t splits,
+                                                                 int32_t hkv, int32_t per_xcd, int32_t pad,
+                                                                 const u32x4* k, const u32x4* v, int64_t kblk16,
+                                                                 int64_t khd16, float* part, float* mx, float* sm) {
+  const int wg = per_xcd > 0 ? (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3) : blockIdx.x;
+  const int split = wg % splits;
+  const int pair = wg / splits;
+  const int b = pair / hkv;
+  const int h = pair % hkv;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int per_split = (nblk + splits - 1) / splits;
+  int vzero = 0;  // keeps the uniform table load on the vector path, as the decode kernel does
+  asm volatile("" : "+v"(vzero));
+  uint32_t acc = 0;
+  for (int u = wave; u < per_split; u += kThreads / 64) {
+    const int bi = split * per_split + u;
+    if (bi >= nblk) break;
+    const int64_t blk = bt[static_cast<int64_t>(b) * nblk + bi + vzero];
+    const u32x4* kb = k + blk * kblk16 + h * khd16 + lane;
+    const u32x4* vb = v + blk * kblk16 + h * khd16 + lane;
+    u32x4 kk[kUnit16 / 64], vv[kUnit16 / 64];
+#pragma unroll
+    for (int i = 0; i < kUnit16 / 64; ++i) kk[i] = __builtin_nontemporal_load(kb + 64 * i);
+#pragma unroll
+    for (int i = 0; i < kUnit16 / 64; ++i) vv[i] = __builtin_nontemporal_load(vb + 64 * i);
+    __builtin_amdgcn_sched_barrier(0);  // all sixteen loads issue before the first use
+#pragma unroll
+    for (int i = 0; i < kUnit16 / 64; ++i) acc ^= kk[i].x ^ kk[i].y ^ kk[i].z ^ kk[i].w ^ vv[i].x ^ vv[i].y ^ vv[i].z ^ vv[i].w;
+  }
+  __shared__ uint32_t s_acc[kThreads / 64][64];
+  s_acc[wave][lane] = acc;
+  __syncthreads();
+  const uint32_t x = s_acc[0][lane] ^ s_acc[1][lane] ^ s_acc[2][lane] ^ s_acc[3][lane];
+  // thread t: query head t / 32 of this KV head, dims 4 (t % 32) .. + 3
+  const int hh = threadIdx.x >> 5;
+  const int64_t row = static_cast<int64_t>(b) * hkv * kGroup + h * kGroup + hh;
+  const int64_t so = row * splits + split;
+  const float f = static_cast<float>(x & 0xffffu);
+  *reinterpret_cast<f32x4*>(part + so * 128 + 4 * (threadIdx.x & 31)) = f32x4{f, f + 1.f, f + 2.f, f + 3.f};
+  if ((threadIdx.x & 31) == 0) {
+    mx[so] = f;
+    sm[so] = 1.f;
+  }
+}
+
+constexpr int kMaxSplits = 16;
+
+// grid: rows (= batch * hq) workgroups of one wave, XCD by XCD as above;
+// splits <= 16; partials [rows, splits, 128], statistics [rows, splits]
+__global__ __launch_bounds__(64) void reduce_read_kernel(const float* part, const float* mx, const float* sm,
+                                                         int32_t splits, int32_t per_xcd, __bf16* out) {
+  const int row = per_xcd > 0 ? (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3) : blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* pr = part + static_cast<int64_t>(row) * splits * 128;
+  const int sj = min(lane, splits - 1);
+  const float lm = mx[static_cast<int64_t>(row) * splits + sj];
+  const float ll = sm[static_cast<int64_t>(row) * splits + sj];
+  float a[kMaxSplits][2];
+#pragma unroll
+  for (int j = 0; j < kMaxSplits; ++j) {
+    const int s = min(j, splits - 1);
+    a[j][0] = pr[s * 128 + lane];
+    a[j][1] = pr[s * 128 + lane + 64];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float o0 = 0.f, o1 = 0.f, L = 0.f, M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kMaxSplits; ++j) {
+    const int src = min(j, splits - 1);
+    const float lj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ll), src));
+    const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lm), src));
+    const float w = j < splits ? lj : 0.f;
+    M = j < splits ? fmaxf(M, m) : M;
+    L += w;
+    o0 += w * a[j][0];
+    o1 += w * a[j][1];
+  }
+  const float inv = L > 0.f && M < INFINITY ? 1.f / L : 0.f;
+  __bf16* dst = out + static_cast<int64_t>(row) * 128;
+  dst[lane] = static_cast<__bf16>(o0 * inv);
+  dst[lane + 64] = static_cast<__bf16>(o1 * inv);
+}
 
 __global__ void xcc_map_kernel(uint32_t* out) {
   uint32_t x;
@@ -73,6 +181,46 @@ extern "C" int fdp_stream_read(const void* src, uint64_t bytes, uint32_t* sink, 
 extern "C" int fdp_empty(unsigned grid, unsigned block, hipStream_t stream) {
   if (grid == 0 || block == 0 || block > 1024) return 1;
   hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(block), 0, stream);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// The attention kernel's memory pattern at a C2-like shape: a [blocks, hkv,
+// 32, 128] bf16 cache (kblk_bytes / khd_bytes: block and head strides, the
+// head stride 8 KB), int32 table [batch, nblk], 8 query heads per KV head;
+// partials [batch * hkv * 8, splits, 128] fp32, statistics [.., splits].
+extern "C" int fdp_paged_read(const int32_t* bt, int nblk, int batch, int hkv, int splits, const void* k, const void* v,
+                              int64_t kblk_bytes, int64_t khd_bytes, float* part, float* mx, float* sm,
+                              hipStream_t stream, void* start, void* stop) {
+  if (bt == nullptr || k == nullptr || v == nullptr || part == nullptr || mx == nullptr || sm == nullptr ||
+      nblk <= 0 || batch <= 0 || hkv <= 0 || splits <= 0 || splits > nblk || khd_bytes != 16 * kUnit16 ||
+      kblk_bytes < hkv * khd_bytes || (kblk_bytes & 15) || ((reinterpret_cast<uintptr_t>(k) |
+      reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(part)) & 15u))
+    return 1;
+  const int64_t grid = static_cast<int64_t>(batch) * hkv * splits;
+  if (grid > 0x7fffffff) return 1;
+  const int per_xcd = grid % 8 == 0 ? static_cast<int>(grid / 8) : 0;
+  if (start || stop)
+    hipExtLaunchKernelGGL(paged_read_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream,
+                          static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), 0, bt, nblk, splits, hkv,
+                          per_xcd, 0, static_cast<const u32x4*>(k), static_cast<const u32x4*>(v), kblk_bytes / 16,
+                          khd_bytes / 16, part, mx, sm);
+  else
+    hipLaunchKernelGGL(paged_read_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, bt, nblk,
+                       splits, hkv, per_xcd, 0, static_cast<const u32x4*>(k), static_cast<const u32x4*>(v),
+                       kblk_bytes / 16, khd_bytes / 16, part, mx, sm);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// The reducer's memory pattern over fdp_paged_read's partials: rows = batch *
+// hkv * 8 output rows of 128 bf16, splits <= 16.
+extern "C" int fdp_reduce_read(const float* part, const float* mx, const float* sm, int rows, int splits, void* out,
+                               hipStream_t stream) {
+  if (part == nullptr || mx == nullptr || sm == nullptr || out == nullptr || rows <= 0 || splits <= 0 ||
+      splits > kMaxSplits)
+    return 1;
+  const int per_xcd = rows % 8 == 0 ? rows / 8 : 0;
+  hipLaunchKernelGGL(reduce_read_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, stream, part, mx, sm, splits,
+                     per_xcd, static_cast<__bf16*>(out));
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

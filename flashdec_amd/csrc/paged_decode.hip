@@ -1169,19 +1169,18 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     for (int s = 0; s < KS; ++s) ar.akf[s] = *reinterpret_cast<const u32x4*>(ak + 32 * s + 8 * g);
     ar.avf = *reinterpret_cast<const VPiece<D>*>(av + (D / 16) * c);
   }
-  int64_t eff_len;
+  // The row length (and slot) are read here and used only after the first
+  // unit's K/V loads have issued (below): a use ahead of those loads would
+  // put its wait, one more round trip, in front of them.
+  int64_t eff_len = 0;
   int32_t slot = -1;
   [[maybe_unused]] int32_t seq_len = 0;
-  if constexpr (BAL) {
-    eff_len = bal_eff;
-  } else if constexpr (PREFIX) {
-    const int64_t cap = p.max_blocks_per_seq * p.block_size;
-    const int64_t plen = lead_ok ? cp.prefix_len[pair / cp.chunks / p.hkv] : 0;
-    eff_len = plen < 0 ? 0 : (plen < cap ? plen : cap);
-  } else {
+  [[maybe_unused]] int64_t plen = 0;
+  if constexpr (PREFIX) {
+    plen = lead_ok ? cp.prefix_len[pair / cp.chunks / p.hkv] : 0;
+  } else if constexpr (!BAL) {
     seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
     slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
-    eff_len = effective_len(p, seq_len, slot);
   }
   const int32_t first = TAIL ? max(p.tb[b], 0) : 0;
   // Long splits (16-token units, several per wave) take the fixed lane
@@ -1205,6 +1204,25 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       load_unit<T, BS, UNIT, kNT, D>(p, kvh, u, up, c, g, dst);
   };
   load(unit, pages, cur);
+  // The loaded length stays in a VGPR until here (the empty asm redefines
+  // it): its move to an SGPR, and the wait for the load it brings, would
+  // otherwise sit at the load, ahead of the K/V loads above.
+  if constexpr (PREFIX) {
+    asm volatile("" : "+v"(plen));
+    plen = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(plen));
+  } else if constexpr (!BAL) {
+    asm volatile("" : "+v"(seq_len), "+v"(slot));
+    seq_len = __builtin_amdgcn_readfirstlane(seq_len);
+    slot = __builtin_amdgcn_readfirstlane(slot);
+  }
+  if constexpr (BAL) {
+    eff_len = bal_eff;
+  } else if constexpr (PREFIX) {
+    const int64_t cap = p.max_blocks_per_seq * p.block_size;
+    eff_len = plen < 0 ? 0 : (plen < cap ? plen : cap);
+  } else {
+    eff_len = effective_len(p, seq_len, slot);
+  }
   // the float64 cos/sin evaluation overlaps the K/V loads just issued
   if constexpr (ROPE && D == 128) rope_operands<T>(p, seq_len, lane, g, qf[0], ar);
 
@@ -1791,7 +1809,12 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p, int 
 // readlane broadcasts them.  Scalar loads would not do: they complete out of
 // order, so each use of one waits for all (lgkmcnt(0)), which turned the
 // per-split statistics into a round trip per split.  Row length and slot,
-// needed only for the final zero-row select, are vector loads too.
+// needed only for the final zero-row select, are vector loads too.  Once the
+// data has landed, one wave's instruction chain is the kernel's time: the
+// splits' maximum and weights are computed across the lanes (a DPP / permlane
+// reduction and one exp per lane), not as a dependent max / exp step per
+// split (C2 call 8.42 -> 8.27 us, shared-prefix C4 12.43 -> 11.88 us, same
+// box).
 constexpr int kReduceChunk = 16;  // splits whose partial rows are in flight at once
 
 // The reducer's own compact arguments: with the full DecodeParams the
@@ -1822,6 +1845,17 @@ enum ReduceMode { kReducePlain = 0, kReduceCascade = 1, kReduceBalanced = 2 };
 
 __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane_idx));
+}
+
+// Maximum over the wave, every lane receiving it: rotations within each
+// 16-lane row (DPP row_ror), then across the rows (permlane swaps).
+__device__ __forceinline__ float dpp_row_ror_max(float x, int y) { return fmaxf(x, __builtin_bit_cast(float, y)); }
+__device__ __forceinline__ float wave_max_f32(float x) {
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+  return column_max(x);
 }
 
 // W waves per (request, query head): wave w merges the w-th quarter of the
@@ -1867,9 +1901,10 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
   // arguments the loads below cover every split and issue without waiting
   // for the row's prefix length; the splits past `valid` are masked.
   int valid = p.splits;
+  [[maybe_unused]] int32_t row_tb = 0;
   if constexpr (MODE == kReduceCascade) {
     if constexpr (PRE) {
-      valid = p.tb[b + vzero] > 0 ? p.splits : p.tail_splits;
+      row_tb = p.tb[b + vzero];  // compared after the partial loads below have issued
     } else {
       splits = __builtin_amdgcn_readfirstlane(p.tb[b + vzero]) > 0 ? p.splits : p.tail_splits;
       valid = splits;
@@ -1915,27 +1950,34 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
       }
       // keep every load above issued before the broadcasts below (they wait)
       __builtin_amdgcn_sched_barrier(0);
-      float m[kReduceChunk], l[kReduceChunk];
-      float cm = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < kReduceChunk; ++j) {
-        const int src = min(c0 + j, n - 1);
-        m[j] = lane_bcast(lm, src);
-        l[j] = lane_bcast(ll, src);
-        cm = c0 + j < n && s64 + c0 + j < valid ? fmaxf(cm, m[j]) : cm;
+      if constexpr (MODE == kReduceCascade && PRE) {
+        // the row's prefix length is used here, not where it was loaded: the
+        // empty asm keeps the compiler from moving the compare (and its
+        // wait) ahead of this chunk's loads
+        asm volatile("" : "+v"(row_tb));
+        valid = row_tb > 0 ? p.splits : p.tail_splits;
       }
-      const float nm = fmaxf(M, cm);
+      // The chunk's statistics, one split per lane: their maximum by a wave
+      // reduction and each split's weight 2^(m - max) by one exp per lane,
+      // not a chain of dependent max and exp steps per split (the same
+      // values, bit for bit: a maximum is exact in any order).
+      const int cl = lane - c0;  // this lane's split within the chunk
+      const bool mine = cl >= 0 && cl < kReduceChunk && cl < n - c0 && s64 + lane < valid;
+      const float nm = fmaxf(M, wave_max_f32(mine ? lm : -INFINITY));
       const float nmu = nm == -INFINITY ? 0.f : nm;
       const float sc = exp2f(M - nmu);
       L *= sc;
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] *= sc;
+      const float wl = exp2f(lm - nmu);
 #pragma unroll
       for (int j = 0; j < kReduceChunk; ++j) {
+        const int src = min(c0 + j, n - 1);
+        const float w = lane_bcast(wl, src);
+        const float lj = lane_bcast(ll, src);
         // masked splits may hold stale or NaN partials: selected away, not weighted by 0
         const bool use = c0 + j < n && s64 + c0 + j < valid;
-        const float w = use ? exp2f(m[j] - nmu) : 0.f;
-        L += use ? w * l[j] : 0.f;
+        L += use ? w * lj : 0.f;
 #pragma unroll
         for (int e = 0; e < E; ++e) o[e] += use ? w * a[j][e] : 0.f;
       }
@@ -1985,10 +2027,15 @@ __global__ __launch_bounds__(64 * W) void split_reduce_kernel(ReduceParams p) {
 // addressing in leading arguments that the command processor preloads into
 // SGPRs (as for decode_mfma_kernel).  Its loads then issue at wave start
 // instead of after a kernel-argument round trip: with the preloaded attention
-// kernel, a C2 call in a graph went from 9.37 to 8.74 us.
+// kernel, a C2 call in a graph went from 9.37 to 8.74 us.  The preload holds
+// 14 SGPRs (56 bytes of arguments): with 64-bit strides the XCD layout's
+// row count fell just outside it, and its fetch held every partial load
+// back by one round trip; with 32-bit strides (the host checks they fit)
+// everything up to xcd_rows is preloaded (C2 8.63 -> 8.40 us per call, one
+// box).
 template <typename T, int D, int W = 1>
 __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* acc, const float* mx, const float* sm,
-                                                                  int64_t as1, int64_t as2, int64_t ss1,
+                                                                  int32_t as1, int32_t as2, int32_t ss1,
                                                                   int32_t splits, int32_t hq, int32_t xcd_rows,
                                                                   ReduceParams p) {
   ReduceParams q = p;
@@ -2004,13 +2051,14 @@ __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* a
 }
 
 // The cascade merge over a packed workspace (as split_reduce_pre_kernel),
-// with the row prefix lengths preloaded too: every split's partial loads
-// issue at wave start, and rows without a prefix mask the prefix splits once
-// their length arrives (before, the length was a round trip ahead of them).
+// with the row prefix lengths' address preloaded too (32-bit strides make
+// room for it in the 14 preloaded SGPRs): every split's partial loads issue
+// without waiting for a prefix length, and rows without a prefix mask the
+// prefix splits once their length arrives.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void split_reduce_cascade_pre_kernel(const float* acc, const float* mx,
-                                                                      const float* sm, int64_t as1, int64_t as2,
-                                                                      int64_t ss1, int32_t splits, int32_t hq,
+                                                                      const float* sm, int32_t as1, int32_t as2,
+                                                                      int32_t ss1, int32_t splits, int32_t hq,
                                                                       const int32_t* tb, ReduceParams p) {
   ReduceParams q = p;
   q.acc = acc;
@@ -2267,10 +2315,15 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
   const dim3 grid(static_cast<unsigned>(a.num_seqs * a.num_q_heads));
   void* e0 = a.timing_events[2];
   void* e1 = a.timing_events[3];
-  if (MODE == kReducePlain && reduce_layout_packed(r)) {
+  // 32-bit strides keep every argument the partials' addresses need inside
+  // the 14 preloaded SGPRs
+  auto fits = [](int64_t x) { return x >= 0 && x <= INT32_MAX; };
+  const bool pre_ok = reduce_layout_packed(r) && fits(r.as1) && fits(r.as2) && fits(r.ss1);
+  if (MODE == kReducePlain && pre_ok) {
     // the partials' addressing leads the argument list (preloaded into SGPRs)
     auto pre = [&](auto kernel, dim3 block) {
-      dispatch(kernel, grid, block, stream, e0, e1, r.acc, r.mx, r.sm, r.as1, r.as2, r.ss1, r.splits, r.hq,
+      dispatch(kernel, grid, block, stream, e0, e1, r.acc, r.mx, r.sm, static_cast<int32_t>(r.as1),
+               static_cast<int32_t>(r.as2), static_cast<int32_t>(r.ss1), r.splits, r.hq,
                xcd_rows && grid.x % 8 == 0 ? static_cast<int32_t>(grid.x / 8) : 0, r);
     };
     if (r.splits > 32) {
@@ -2283,9 +2336,10 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
     } else {
       pre(split_reduce_pre_kernel<T, 128>, dim3(64));
     }
-  } else if (MODE == kReduceCascade && reduce_layout_packed(r) && r.splits <= 32 && a.head_dim == 128) {
-    dispatch(split_reduce_cascade_pre_kernel<T, 128>, grid, dim3(64), stream, e0, e1, r.acc, r.mx, r.sm, r.as1,
-             r.as2, r.ss1, r.splits, r.hq, r.tb, r);
+  } else if (MODE == kReduceCascade && pre_ok && r.splits <= 32 && a.head_dim == 128) {
+    dispatch(split_reduce_cascade_pre_kernel<T, 128>, grid, dim3(64), stream, e0, e1, r.acc, r.mx, r.sm,
+             static_cast<int32_t>(r.as1), static_cast<int32_t>(r.as2), static_cast<int32_t>(r.ss1), r.splits, r.hq,
+             r.tb, r);
   } else if (r.splits > 32) {
     // more than 32 splits: four waves per row share them
     if (a.head_dim == 64)
