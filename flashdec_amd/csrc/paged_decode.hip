@@ -1869,7 +1869,7 @@ __device__ __forceinline__ float wave_max_f32(float x) {
 // written by this call's attention kernel, and a row with nothing to attend
 // (zero length, or a padding slot) has denominator 0 in every split, which
 // selects the zero row below just as the length test does.
-template <typename T, int D, int MODE, int W, bool PRE>
+template <typename T, int D, int MODE, int W, bool PRE, bool OUTP = false>
 __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row = blockIdx.x) {
   static_assert(!PRE || MODE == kReducePlain || MODE == kReduceCascade,
                 "preloaded reducer arguments are for the plain and cascade merges");
@@ -2013,9 +2013,11 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
   }
   const bool has = PRE || (seq_len > 0 && (!p.fuse || slot >= 0));
   const float inv = (has && L > 0.f) ? 1.f / L : 0.f;
-  T* dst = static_cast<T*>(p.out) + b * p.os0 + qh * p.os1;
+  // OUTP: the output is [rows, D] in row order (its pointer preloaded), so
+  // the store needs no output strides from the kernel-argument buffer
+  T* dst = static_cast<T*>(p.out) + (OUTP ? row * D : b * p.os0 + qh * p.os1);
 #pragma unroll
-  for (int e = 0; e < E; ++e) dst[(lane + 64 * e) * p.os2] = from_f32<T>(o[e] * inv);
+  for (int e = 0; e < E; ++e) dst[(lane + 64 * e) * (OUTP ? 1 : p.os2)] = from_f32<T>(o[e] * inv);
 }
 
 template <typename T, int D, int MODE = kReducePlain, int W = 1>
@@ -2032,13 +2034,16 @@ __global__ __launch_bounds__(64 * W) void split_reduce_kernel(ReduceParams p) {
 // row count fell just outside it, and its fetch held every partial load
 // back by one round trip; with 32-bit strides (the host checks they fit)
 // everything up to xcd_rows is preloaded (C2 8.63 -> 8.40 us per call, one
-// box).
-template <typename T, int D, int W = 1>
+// box).  The output pointer fills the last two SGPRs: with an output in row
+// order (OUTP) the kernel reads nothing from the argument buffer, whose fetch
+// otherwise sat ahead of the output stores (C2 8.26 -> 8.15 us, one box).
+template <typename T, int D, int W = 1, bool OUTP = false>
 __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* acc, const float* mx, const float* sm,
                                                                   int32_t as1, int32_t as2, int32_t ss1,
                                                                   int32_t splits, int32_t hq, int32_t xcd_rows,
-                                                                  ReduceParams p) {
+                                                                  void* out, ReduceParams p) {
   ReduceParams q = p;
+  q.out = out;
   q.acc = acc;
   q.mx = mx;
   q.sm = sm;
@@ -2047,7 +2052,7 @@ __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* a
   q.ss1 = ss1;
   q.splits = splits;
   q.hq = hq;
-  reduce_row<T, D, kReducePlain, W, true>(q, xcd_logical_block(blockIdx.x, xcd_rows));
+  reduce_row<T, D, kReducePlain, W, true, OUTP>(q, xcd_logical_block(blockIdx.x, xcd_rows));
 }
 
 // The cascade merge over a packed workspace (as split_reduce_pre_kernel),
@@ -2324,17 +2329,20 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
     auto pre = [&](auto kernel, dim3 block) {
       dispatch(kernel, grid, block, stream, e0, e1, r.acc, r.mx, r.sm, static_cast<int32_t>(r.as1),
                static_cast<int32_t>(r.as2), static_cast<int32_t>(r.ss1), r.splits, r.hq,
-               xcd_rows && grid.x % 8 == 0 ? static_cast<int32_t>(grid.x / 8) : 0, r);
+               xcd_rows && grid.x % 8 == 0 ? static_cast<int32_t>(grid.x / 8) : 0, r.out, r);
     };
+    // output rows in order: [requests, q heads, head_dim] with unit dim stride
+    const bool outp = r.os2 == 1 && r.os1 == a.head_dim && r.os0 == r.hq * r.os1;
     if (r.splits > 32) {
       if (a.head_dim == 64)
-        pre(split_reduce_pre_kernel<T, 64, 4>, dim3(256));
+        outp ? pre(split_reduce_pre_kernel<T, 64, 4, true>, dim3(256)) : pre(split_reduce_pre_kernel<T, 64, 4>, dim3(256));
       else
-        pre(split_reduce_pre_kernel<T, 128, 4>, dim3(256));
+        outp ? pre(split_reduce_pre_kernel<T, 128, 4, true>, dim3(256))
+             : pre(split_reduce_pre_kernel<T, 128, 4>, dim3(256));
     } else if (a.head_dim == 64) {
-      pre(split_reduce_pre_kernel<T, 64>, dim3(64));
+      outp ? pre(split_reduce_pre_kernel<T, 64, 1, true>, dim3(64)) : pre(split_reduce_pre_kernel<T, 64>, dim3(64));
     } else {
-      pre(split_reduce_pre_kernel<T, 128>, dim3(64));
+      outp ? pre(split_reduce_pre_kernel<T, 128, 1, true>, dim3(64)) : pre(split_reduce_pre_kernel<T, 128>, dim3(64));
     }
   } else if (MODE == kReduceCascade && pre_ok && r.splits <= 32 && a.head_dim == 128) {
     dispatch(split_reduce_cascade_pre_kernel<T, 128>, grid, dim3(64), stream, e0, e1, r.acc, r.mx, r.sm,

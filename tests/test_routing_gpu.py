@@ -42,8 +42,33 @@ def test_c2_shape_row_kernel_and_preloaded_reducer(record):
 
     q, k, v, table, sl = make_paged_inputs([2048] * 8, 16, 2, 128, 32, seed=1)
     out = fd.decode(q, k, v, table, sl)
-    assert record.last_launch() == [mfma(unit=32), "fd::split_reduce_pre_kernel<__bf16, 128, 1>"]
+    # an output in row order: the reducer takes its pointer preloaded and no strides
+    assert record.last_launch() == [mfma(unit=32), "fd::split_reduce_pre_kernel<__bf16, 128, 1, true>"]
     assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_output_view_out_of_row_order_takes_the_strided_store(d, record):
+    """A packed split workspace with an output whose rows are not in order (a view with a
+    wider head stride, and a transposed view): the preloaded reducer reads the output
+    strides, and every row lands where the view puts it."""
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    q, k, v, table, sl = make_paged_inputs([2048, 900, 0, 1500], 16, 2, d, 32, seed=4)
+    splits = _lib.paged_decode_plan(4, 16, 2, d, 2048)
+    assert splits > 1
+    ws = (torch.empty((4, 16, splits, d), device="cuda"), torch.empty((4, 16, splits), device="cuda"),
+          torch.empty((4, 16, splits), device="cuda"))
+    expected = _oracle(q, k, v, table, sl)
+    wide = torch.full((4, 16, d + 24), float("nan"), device="cuda", dtype=q.dtype)
+    transposed = torch.full((16, 4, d), float("nan"), device="cuda", dtype=q.dtype).transpose(0, 1)
+    for out in (wide[..., :d], transposed):
+        pd._decode_with_workspace(q, k, v, table, sl, out, 1.0 / math.sqrt(d), 32, splits, ws, k.shape[0])
+        torch.cuda.synchronize()
+        assert record.last_launch()[1] == f"fd::split_reduce_pre_kernel<__bf16, {d}, 1, false>"
+        assert_close_to_oracle(out, expected)
+    assert torch.isnan(wide[..., d:]).all()  # nothing written past the view
 
 
 @pytest.mark.parametrize(("hq", "d", "ncb"), [(16, 128, 1), (64, 128, 2), (40, 64, 2)])
