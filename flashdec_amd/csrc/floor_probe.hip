@@ -63,20 +63,43 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kUnit16 = 512;  // one 32-token block of one KV head: 32 * 128 bf16 = 8 KB = 512 x 16 B
 constexpr int kGroup = 8;     // query heads per KV head (the probe's shape: D 128, so 8 x 32 threads)
 
+// n / d for n < 2^31 by multiply-high and shifts (Granlund and Montgomery
+// 1994, Figure 4.1), as the decode kernel divides its workgroup index; the
+// host computes m and the shifts (magic).
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t m, int s1, int s2) {
+  const uint32_t t = __umulhi(n, m);
+  return (t + ((n - t) >> s1)) >> s2;
+}
+
+void magic(uint32_t d, uint32_t& m, int& s1, int& s2) {
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+  s1 = l < 1 ? l : 1;
+  s2 = l > 1 ? l - 1 : 0;
+}
+
 // grid: batch * hkv * splits workgroups of 256 threads; per_xcd > 0: the
-// i-th workgroup on XCD x is logical workgroup x * per_xcd + i
-__global__ __launch_bounds__(kThreads, 1) void paged_read_kernel(const int32_t* bt, int32_t nblk, int32_t splits,
-                                                                 int32_t hkv, int32_t per_xcd, int32_t pad,
-                                                                 const u32x4* k, const u32x4* v, int64_t kblk16,
-                                                                 int64_t khd16, float* part, float* mx, float* sm) {
+// i-th workgroup on XCD x is logical workgroup x * per_xcd + i.  Every
+// argument the K/V loads need sits in the 14 preloaded SGPRs (56 bytes:
+// the divisions by splits and hkv come as multipliers and shifts, as in the
+// decode kernel); only the partials' pointers, needed at the end, are fetched.
+__global__ __launch_bounds__(kThreads, 1) void paged_read_kernel(const int32_t* bt, const u32x4* k, const u32x4* v,
+                                                                 int32_t kblk16, int32_t khd16, int32_t nblk,
+                                                                 int32_t splits, uint32_t splits_m, uint32_t hkv_m,
+                                                                 int32_t shifts, int32_t hkv_xcd, float* part,
+                                                                 float* mx, float* sm) {
+  const int hkv = hkv_xcd & 0xffff;
+  const int per_xcd = hkv_xcd >> 16;
   const int wg = per_xcd > 0 ? (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3) : blockIdx.x;
-  const int split = wg % splits;
-  const int pair = wg / splits;
-  const int b = pair / hkv;
-  const int h = pair % hkv;
+  const int pair = static_cast<int>(fast_div(wg, splits_m, shifts & 0xff, (shifts >> 8) & 0xff));
+  const int split = wg - pair * splits;
+  const int b = static_cast<int>(fast_div(pair, hkv_m, (shifts >> 16) & 0xff, shifts >> 24));
+  const int h = pair - b * hkv;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int per_split = (nblk + splits - 1) / splits;
+  const int per_split =
+      static_cast<int>(fast_div(nblk + splits - 1, splits_m, shifts & 0xff, (shifts >> 8) & 0xff));
   int vzero = 0;  // keeps the uniform table load on the vector path, as the decode kernel does
   asm volatile("" : "+v"(vzero));
   uint32_t acc = 0;
@@ -84,8 +107,8 @@ __global__ __launch_bounds__(kThreads, 1) void paged_read_kernel(const int32_t* 
     const int bi = split * per_split + u;
     if (bi >= nblk) break;
     const int64_t blk = bt[static_cast<int64_t>(b) * nblk + bi + vzero];
-    const u32x4* kb = k + blk * kblk16 + h * khd16 + lane;
-    const u32x4* vb = v + blk * kblk16 + h * khd16 + lane;
+    const u32x4* kb = k + blk * kblk16 + static_cast<int64_t>(h) * khd16 + lane;
+    const u32x4* vb = v + blk * kblk16 + static_cast<int64_t>(h) * khd16 + lane;
     u32x4 kk[kUnit16 / 64], vv[kUnit16 / 64];
 #pragma unroll
     for (int i = 0; i < kUnit16 / 64; ++i) kk[i] = __builtin_nontemporal_load(kb + 64 * i);
@@ -193,21 +216,30 @@ extern "C" int fdp_paged_read(const int32_t* bt, int nblk, int batch, int hkv, i
                               hipStream_t stream, void* start, void* stop) {
   if (bt == nullptr || k == nullptr || v == nullptr || part == nullptr || mx == nullptr || sm == nullptr ||
       nblk <= 0 || batch <= 0 || hkv <= 0 || splits <= 0 || splits > nblk || khd_bytes != 16 * kUnit16 ||
-      kblk_bytes < hkv * khd_bytes || (kblk_bytes & 15) || ((reinterpret_cast<uintptr_t>(k) |
+      kblk_bytes < hkv * khd_bytes || (kblk_bytes & 15) || kblk_bytes / 16 > 0x7fffffff ||
+      ((reinterpret_cast<uintptr_t>(k) |
       reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(part)) & 15u))
     return 1;
   const int64_t grid = static_cast<int64_t>(batch) * hkv * splits;
-  if (grid > 0x7fffffff) return 1;
+  if (grid > 0x7fffffff || hkv > 0xffff) return 1;
   const int per_xcd = grid % 8 == 0 ? static_cast<int>(grid / 8) : 0;
+  if (per_xcd > 0x7fff) return 1;
+  uint32_t ms = 0, mh = 0;
+  int a1 = 0, a2 = 0, b1 = 0, b2 = 0;
+  magic(static_cast<uint32_t>(splits), ms, a1, a2);
+  magic(static_cast<uint32_t>(hkv), mh, b1, b2);
+  const int32_t shifts = a1 | (a2 << 8) | (b1 << 16) | (b2 << 24);
+  const int32_t hkv_xcd = hkv | (per_xcd << 16);
+  const int32_t kblk16 = static_cast<int32_t>(kblk_bytes / 16), khd16 = static_cast<int32_t>(khd_bytes / 16);
+  const u32x4* k16 = static_cast<const u32x4*>(k);
+  const u32x4* v16 = static_cast<const u32x4*>(v);
   if (start || stop)
     hipExtLaunchKernelGGL(paged_read_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream,
-                          static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), 0, bt, nblk, splits, hkv,
-                          per_xcd, 0, static_cast<const u32x4*>(k), static_cast<const u32x4*>(v), kblk_bytes / 16,
-                          khd_bytes / 16, part, mx, sm);
+                          static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), 0, bt, k16, v16, kblk16,
+                          khd16, nblk, splits, ms, mh, shifts, hkv_xcd, part, mx, sm);
   else
-    hipLaunchKernelGGL(paged_read_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, bt, nblk,
-                       splits, hkv, per_xcd, 0, static_cast<const u32x4*>(k), static_cast<const u32x4*>(v),
-                       kblk_bytes / 16, khd_bytes / 16, part, mx, sm);
+    hipLaunchKernelGGL(paged_read_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, stream, bt, k16, v16,
+                       kblk16, khd16, nblk, splits, ms, mh, shifts, hkv_xcd, part, mx, sm);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -64,6 +64,10 @@ struct DecodeParams {
   int splits;
   int hint_tiles;    // ceil(bound / 32): bound = max_seq_len or the table capacity
   int hint_tps;      // tiles per split
+  // workgroup-index divisions by splits and hkv as multiply-high and shifts
+  // (fast_div; set for the MFMA row kernel only)
+  uint32_t div_splits_m, div_hkv_m;
+  int div_shifts;  // bits 0-7 / 8-15: splits' shifts, 16-23 / 24-31: hkv's
   // cascade tail pass: row b attends tokens [tb[b], seq_len); its partials
   // take workspace splits [0, splits), the prefix pass's come after them
   const int32_t* tb;
@@ -1005,6 +1009,17 @@ __device__ __forceinline__ int xcd_logical_block(int block, int per_xcd) {
   return per_xcd > 0 ? (block & 7) * per_xcd + (block >> 3) : block;
 }
 
+// n / d for n < 2^31 from the divisor's multiplier m and shifts s1, s2
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994, Figure 4.1; the host computes them in
+// fast_div_magic): five scalar instructions instead of the compiler's
+// reciprocal-based sequence of about twenty-five, which sat ahead of the
+// block-table load.
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t m, int s1, int s2) {
+  const uint32_t t = __umulhi(n, m);
+  return (t + ((n - t) >> s1)) >> s2;
+}
+
 // The XCD this wave runs on (hardware register XCC_ID, bits 3:0).
 __device__ __forceinline__ uint32_t xcc_id() {
   uint32_t x;
@@ -1063,9 +1078,11 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   const int c = lane & 15;
   const int g = lane >> 4;
   int nsplit = PREFIX ? cp.prefix_splits : p.splits;
-  int split = block % nsplit;
   // (request, KV head[, head block]), or (group, KV head, chunk)
-  const int pair = block / nsplit;
+  const int pair = PRE && ROLE == Role::kRow
+                       ? static_cast<int>(fast_div(block, p.div_splits_m, p.div_shifts & 0xff, (p.div_shifts >> 8) & 0xff))
+                       : block / nsplit;
+  int split = block - pair * nsplit;
   const int G = p.group;
   // Row role: more than 16 query heads per KV head take ceil(G / (16 NCB))
   // head blocks of NCB 16-column blocks, one per workgroup (each reads the
@@ -1090,6 +1107,12 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     kvh = gk % p.hkv;
     mem = cp.members + static_cast<int64_t>(gk / p.hkv) * cp.max_members;
     b = mem[0];  // the lead: its table row holds the prefix's block ids
+  } else if constexpr (PRE && ROLE == Role::kRow) {
+    // multiply-high divisions (the split was taken the same way above)
+    const int pk = hblocks == 1 ? pair : pair / hblocks;
+    hb = pair - pk * hblocks;
+    b = static_cast<int>(fast_div(pk, p.div_hkv_m, (p.div_shifts >> 16) & 0xff, p.div_shifts >> 24));
+    kvh = pk - b * p.hkv;
   } else {
     const int pk = pair / hblocks;
     hb = pair - pk * hblocks;
@@ -1582,8 +1605,9 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 // buffer instead.
 template <typename T, int BS, int FUSE, bool MERGE, int UNIT, bool NT, int D = 128, int NCB = 1>
 __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
-    const void* bt, int64_t bts0, int64_t bts1, int64_t max_blocks_per_seq, int32_t splits, int32_t hkv,
-    int32_t group, int32_t hint_tps, int32_t bt_i64, int32_t xcd_blocks, DecodeParams p) {
+    const void* bt, int32_t bts0, int32_t bts1, int32_t max_blocks_per_seq, int32_t splits, int32_t hkv,
+    int32_t group, int32_t hint_tps, int32_t xcd_blocks, uint32_t div_splits_m, uint32_t div_hkv_m,
+    int32_t div_shifts, int32_t bt_i64, DecodeParams p) {
   __shared__ DecodeLds<waves_for<UNIT>(), acc_pitch<D>()> lds;
   DecodeParams q = p;
   q.bt = bt;
@@ -1594,6 +1618,9 @@ __global__ __launch_bounds__(64 * waves_for<UNIT>(), 1) void decode_mfma_kernel(
   q.hkv = hkv;
   q.group = group;
   q.hint_tps = hint_tps;
+  q.div_splits_m = div_splits_m;
+  q.div_hkv_m = div_hkv_m;
+  q.div_shifts = div_shifts;
   q.bt_i64 = bt_i64;
   decode_role<T, BS, FUSE, MERGE, UNIT, Role::kRow, NT, D, waves_for<UNIT>(), false, true, NCB>(
       q, CascadeParams{}, xcd_logical_block(blockIdx.x, xcd_blocks), lds);
@@ -2108,6 +2135,10 @@ bool fast_path_ok(const fd_paged_decode_args& a, int64_t group) {
   for (int64_t s : strides)
     if (s % 8 != 0) return false;
   if (!aligned16(a.q) || !aligned16(a.k_cache) || !aligned16(a.v_cache)) return false;
+  // the MFMA kernel takes the block table's strides and width as 32-bit
+  // preloaded arguments
+  for (int64_t t : {a.block_tables_stride[0], a.block_tables_stride[1], a.max_blocks_per_seq})
+    if (t < 0 || t > INT32_MAX) return false;
   // a row's byte offset inside its block (head, token slot, dims) is a
   // 32-bit lane offset in the MFMA kernel's loads
   for (const int64_t* st : {a.k_stride, a.v_stride}) {
@@ -2177,12 +2208,29 @@ int32_t row_xcd_blocks(unsigned grid, int64_t pair_blocks, bool nt) {
   return nt && grid % 8 == 0 && pair_blocks >= kXcdMinPairBlocks ? static_cast<int32_t>(grid / 8) : 0;
 }
 
-// decode_mfma_kernel's arguments: the preloaded block-table fields, then the parameter block
+// Multiplier and shifts (bits 0-7 s1, 8-15 s2) for fast_div by d >= 1:
+// l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, s1 = min(l, 1),
+// s2 = max(l - 1, 0).
+void fast_div_magic(uint32_t d, uint32_t& m, int& shifts) {
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+  shifts = (l < 1 ? l : 1) | ((l > 1 ? l - 1 : 0) << 8);
+}
+
+// decode_mfma_kernel's arguments: the block-table fields and the workgroup
+// index's divisors (all within the 14 preloaded SGPRs: 32-bit table strides,
+// which fast_path_ok checks), then the parameter block
 template <typename K>
 void dispatch_mfma(K kernel, dim3 grid, dim3 block, hipStream_t stream, void* const* ev, const DecodeParams& p,
                    bool nt) {
-  dispatch(kernel, grid, block, stream, ev[0], ev[1], p.bt, p.bts0, p.bts1, p.max_blocks_per_seq, p.splits, p.hkv,
-           p.group, p.hint_tps, p.bt_i64, row_xcd_blocks(grid.x, p.splits * row_head_blocks(p.group), nt), p);
+  uint32_t ms = 0, mh = 0;
+  int ss = 0, sh = 0;
+  fast_div_magic(static_cast<uint32_t>(p.splits), ms, ss);
+  fast_div_magic(static_cast<uint32_t>(p.hkv), mh, sh);
+  dispatch(kernel, grid, block, stream, ev[0], ev[1], p.bt, static_cast<int32_t>(p.bts0), static_cast<int32_t>(p.bts1),
+           static_cast<int32_t>(p.max_blocks_per_seq), p.splits, p.hkv, p.group, p.hint_tps,
+           row_xcd_blocks(grid.x, p.splits * row_head_blocks(p.group), nt), ms, mh, ss | (sh << 16), p.bt_i64, p);
 }
 
 template <typename T, int BS, int UNIT, bool NT>
