@@ -79,7 +79,7 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "c2-floor", "rope", "ragged", "prefix", "prefix-large",
+    p.add_argument("--workload", choices=("decode", "c2-floor", "c2-timeline", "rope", "ragged", "prefix", "prefix-large",
                                           "prefix-sweep", "engine", "engine-prefix", "formats", "vllm"),
                    default="decode",
                    help="decode: the headline C2 call (default); c2-floor: the C2 call beside a bare read of "
@@ -865,6 +865,96 @@ def run_c2_floor(torch, dev, args):
     return out
 
 
+TIMELINE_PHASES = ("wave start", "block-table entry arrived", "K/V loads issued", "K landed, QK done", "softmax done",
+                   "PV issued", "units done", "wave-merge barrier passed", "partials issued", "partials acknowledged")
+
+
+def run_c2_timeline(torch, dev, args):
+    """Per-wave timeline of the C2 attention kernel, from libflashdec_timeline.so.
+
+    That library is the decode library built with -DFD_TIMELINE: lane 0 of
+    every wave of the MFMA row kernel writes s_memrealtime (100 MHz) at ten
+    phase boundaries (TIMELINE_PHASES) into a device array.  For ctx 2048
+    and 1024 on the headline pools, a graph of one call per pool is replayed
+    30 times; after each replay the last call's stamps are read back.  Every
+    stamp is reported relative to the earliest wave start of its call:
+    p10 / median / p90 / max over the 30 calls' waves, and the median time of
+    each phase.  The stamps' own stores and waits perturb the kernel slightly:
+    the graph's per-call time with them is reported beside the figures.
+    """
+    import ctypes
+
+    import numpy as np
+
+    import flashdec_amd as fd
+    from flashdec_amd import _lib
+
+    lib = _lib.load_library()
+    if not hasattr(lib, "fd_timeline_buffer"):
+        raise RuntimeError("c2-timeline needs libflashdec_timeline.so (FLASHDEC_AMD_LIB points elsewhere)")
+    lib.fd_timeline_buffer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)]
+    lib.fd_timeline_buffer.restype = ctypes.c_int
+    ptr, nbytes = ctypes.c_void_p(), ctypes.c_uint64()
+    assert lib.fd_timeline_buffer(ctypes.byref(ptr), ctypes.byref(nbytes)) == 0
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    batch, hq, hkv, d, bs = 8, 16, 2, 128, 32
+    sm_scale = 1.0 / math.sqrt(d)
+    res = {}
+    for ctx in (2048, 1024):
+        pools = build_pools(torch, args.pools, batch, ctx, hq, hkv, d, bs, dev)
+        splits = _lib.paged_decode_plan(batch, hq, hkv, d, ctx)
+        grid = batch * hkv * splits
+        host = np.zeros(grid * 8 * 16, dtype=np.uint64)
+
+        def call(i):
+            q, k, v, table, lens, out = pools[i % len(pools)]
+            fd.paged_decode_attention_into(q, k, v, table, lens, out, sm_scale=sm_scale)
+
+        us_call = graph_p50_us(torch, dev, call, len(pools), samples=60)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            call(0)
+            side.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(len(pools)):
+                    call(i)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        rel = []
+        for _ in range(30):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert hip.hipMemcpy(host.ctypes.data, ptr.value, host.nbytes, 2) == 0  # device to host
+            st = host.reshape(grid, 8, 16)[:, :4, : len(TIMELINE_PHASES)].reshape(grid * 4, -1).astype(np.int64)
+            rel.append((st - st[:, 0].min()) * 10)  # ns
+        rel = np.concatenate(rel)
+        phases = {}
+        for k, name in enumerate(TIMELINE_PHASES):
+            col = rel[:, k]
+            phases[name] = {"p10": float(np.percentile(col, 10)), "median": float(np.median(col)),
+                            "p90": float(np.percentile(col, 90)), "max": float(col.max())}
+        steps = {f"{TIMELINE_PHASES[k]} -> {TIMELINE_PHASES[k + 1]}": float(np.median(rel[:, k + 1] - rel[:, k]))
+                 for k in range(len(TIMELINE_PHASES) - 1)}
+        log(f"[bench] c2-timeline ctx{ctx} ({grid * 4} waves x 30 calls; instrumented call {us_call:.2f} us):")
+        for name, v in phases.items():
+            log(f"[bench]   {name:28s} p10 {v['p10']:6.0f}  median {v['median']:6.0f}  p90 {v['p90']:6.0f}  "
+                f"max {v['max']:6.0f} ns")
+        res[f"ctx{ctx}"] = {"instrumented_us_per_call": round(us_call, 3), "stamps_ns": phases,
+                            "median_phase_ns": steps, "waves": grid * 4, "calls": 30}
+        del pools
+        torch.cuda.empty_cache()
+    c2 = res["ctx2048"]
+    out = common_fields(args, "C2 attention kernel: median wave end after the first wave start (ns)",
+                        c2["stamps_ns"]["partials acknowledged"]["median"], "ns",
+                        c2["instrumented_us_per_call"] * 1e-3, False,
+                        {"workload": "c2-timeline-b8-hq16-hkv2-d128-bs32", "kv_pools": args.pools})
+    out.update(res)
+    return out
+
+
 def run_ragged(torch, dev, args):
     """C4: B32 Hq16 Hkv2 D128 bf16, seq_lens ~ logU[128, 32768] (seed 1701)."""
     return run_decode_variant(torch, dev, args, "ragged-b32-logU128-32768", ragged_lengths(32, 1701), 3, 1701,
@@ -1326,9 +1416,16 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "c2-timeline":
+        # the measurement build of the library, with the per-wave stamps
+        from flashdec_amd import _build
+
+        if not _build.TIMELINE_LIB_PATH.exists():
+            raise RuntimeError(f"{_build.TIMELINE_LIB_PATH} is not built: run __graft_entry__.build()")
+        os.environ["FLASHDEC_AMD_LIB"] = str(_build.TIMELINE_LIB_PATH)
     _lib.load_library()
     if args.workload != "decode":
-        run = {"c2-floor": run_c2_floor, "rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
+        run = {"c2-floor": run_c2_floor, "c2-timeline": run_c2_timeline, "rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
                "prefix-sweep": run_prefix_sweep, "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
                "vllm": run_vllm}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)

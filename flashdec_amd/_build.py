@@ -1,5 +1,8 @@
 """Build ``libflashdec_hip.so`` (the C-ABI library) in-tree with hipcc for gfx950,
-and ``libflashdec_probe.so`` (bench.py's floor probes, ``csrc/floor_probe.hip``).
+``libflashdec_probe.so`` (bench.py's floor probes, ``csrc/floor_probe.hip``) and
+``libflashdec_timeline.so`` (the same library with the decode kernel's per-wave
+timeline stamps compiled in, ``-DFD_TIMELINE``; bench.py's c2-timeline
+workload only).
 
 Each ``csrc/*.hip`` file is compiled separately, then linked into
 ``flashdec_amd/libflashdec_hip.so``.  The RoPE/append file is compiled with
@@ -16,6 +19,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -25,6 +29,9 @@ LIB_PATH = PACKAGE_DIR / "libflashdec_hip.so"
 # measurement probes for bench.py's floor workload (not the decode library)
 PROBE_SOURCE = "floor_probe.hip"
 PROBE_LIB_PATH = PACKAGE_DIR / "libflashdec_probe.so"
+# measurement build of the decode library (per-wave timeline stamps)
+TIMELINE_LIB_PATH = PACKAGE_DIR / "libflashdec_timeline.so"
+TIMELINE_SOURCE = "paged_decode.hip"
 ARCH = "gfx950"
 
 SOURCES = {
@@ -63,19 +70,30 @@ def _hipcc() -> str:
 
 
 def build_library(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source and link the shared library (and the timeline and
+    probe libraries beside it); returns the library's path."""
     hipcc = _hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
-    objects = []
+    objects, jobs = [], []
     for name, extra in SOURCES.items():
         src = CSRC / name
         obj = BUILD_DIR / (src.stem + ".o")
-        cmd = [hipcc, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
-        _run(cmd, verbose)
+        jobs.append([hipcc, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)])
         objects.append(str(obj))
+    # the timeline build differs in the decode kernels' file only
+    tl_obj = BUILD_DIR / "paged_decode_timeline.o"
+    jobs.append([hipcc, *COMMON_FLAGS, *SOURCES[TIMELINE_SOURCE], "-DFD_TIMELINE", "-c", str(CSRC / TIMELINE_SOURCE),
+                 "-o", str(tl_obj)])
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
+        for f in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
+            f.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
+    tl_objects = [str(tl_obj) if Path(o).stem == Path(TIMELINE_SOURCE).stem else o for o in objects]
+    tmp = TIMELINE_LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *tl_objects, "-o", str(tmp)], verbose)
+    os.replace(tmp, TIMELINE_LIB_PATH)
     build_probe_library(verbose)
     return LIB_PATH
 

@@ -33,6 +33,29 @@
 
 namespace fd {
 
+// Per-wave timeline of the MFMA row kernel, in a measurement build only
+// (FD_TIMELINE: libflashdec_timeline.so, read by bench.py's c2-timeline
+// workload; the product library compiles none of it).  Lane 0 of each wave
+// writes s_memrealtime (100 MHz) at the phase boundaries of
+// decode_role / process_unit into slot (workgroup * 8 + wave) * 16 + phase.
+#ifdef FD_TIMELINE
+constexpr bool kTimeline = true;
+constexpr int kTimelineWorkgroups = 8192;
+__device__ uint64_t g_timeline[kTimelineWorkgroups * 8 * 16];
+#else
+constexpr bool kTimeline = false;
+#endif
+
+template <int K>
+__device__ __forceinline__ void timeline_stamp() {
+#ifdef FD_TIMELINE
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < kTimelineWorkgroups) {
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    g_timeline[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 16 + K] = t;
+  }
+#endif
+}
+
 struct DecodeParams {
   const void* q;
   int64_t qs0, qs1, qs2;
@@ -620,7 +643,7 @@ __device__ __forceinline__ void softmax_step(const float (&sc)[VR], float (&pr)[
 // reference's grouped kernels do (flashdec/kernels/paged_decode.py:308-310);
 // the denominator sums them in fp32.  Masking is skipped for units whose
 // tokens are all live (wave-uniform test).
-template <typename T, bool FUSE, int UNIT, int D, int NCB>
+template <typename T, bool FUSE, int UNIT, int D, int NCB, bool TL = false>
 __device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (&qf)[NCB][D / 32],
                                              float scale_log2, int tok0, int first, int last, int app,
                                              const AppendRegs<D>& ar, int c, int g, WaveState<D> (&st)[NCB]) {
@@ -663,6 +686,10 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[cb][4 * mt + r] = sb[r] * scale_log2;
     }
+  if constexpr (TL) {
+    asm volatile("" ::"v"(sc[0][0]), "v"(sc[0][VR - 1]));
+    timeline_stamp<3>();  // K landed, QK done
+  }
   // masked tokens: -inf scores and zero V rows (their memory may hold
   // NaN/Inf, and 0 * NaN is NaN)
   if (__ballot(vmask != kAll)) {
@@ -683,6 +710,10 @@ __device__ __forceinline__ void process_unit(UnitRegs<UNIT, D>& t, const u32x4 (
     softmax_step<VR, D>(sc[cb], pr, st[cb]);
 #pragma unroll
     for (int j = 0; j < VR / 2; ++j) ph[cb][j] = pack2<T>(pr[2 * j], pr[2 * j + 1]);
+  }
+  if constexpr (TL) {
+    asm volatile("" ::"v"(ph[0][0]));
+    timeline_stamp<4>();  // softmax done
   }
   // V^T operands: vt_n holds dim (D/16)*c + n of the lane's tokens
 #pragma unroll
@@ -1073,6 +1104,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
                  "s"(p.max_blocks_per_seq), "s"(p.num_blocks), "s"(p.block_size));
   }
 
+  constexpr bool TL = kTimeline && ROLE == Role::kRow && PRE && !DM;
+  if constexpr (TL) timeline_stamp<0>();  // wave start
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15;
@@ -1154,6 +1187,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   }
   int unit = kUnitsPerTile * guess_begin + wave;
   UnitPages pages = fetch_pages<BS, UNIT, kScalarPages>(p, trow, unit);  // clamped, always in bounds
+  if constexpr (TL) {
+    asm volatile("" ::"s"(pages.a));
+    timeline_stamp<1>();  // block-table entry arrived
+  }
   if constexpr (PREFIX) {
     // the prefix role's member loads needed only preloaded arguments; the
     // table, q and K/V addressing ones come in one batch of kernel-argument
@@ -1227,6 +1264,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       load_unit<T, BS, UNIT, kNT, D>(p, kvh, u, up, c, g, dst);
   };
   load(unit, pages, cur);
+  if constexpr (TL) timeline_stamp<2>();  // first unit's K/V loads issued
   // The loaded length stays in a VGPR until here (the empty asm redefines
   // it): its move to an SGPR, and the wait for the load it brings, would
   // otherwise sit at the load, ahead of the K/V loads above.
@@ -1303,8 +1341,9 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         process_unit_dm<T, (FUSE != 0), D>(now, qf[0], p.scale_log2, unit * UNIT, first, last, app, dar, lane,
                                            kstage + wave * D * kDmRowBytes, st[0]);
       else {
-        process_unit<T, (FUSE != 0), UNIT, D, NCB>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c, g,
-                                                   st);
+        process_unit<T, (FUSE != 0), UNIT, D, NCB, TL>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c,
+                                                       g, st);
+        if constexpr (TL) timeline_stamp<5>();  // unit's PV issued
       }
       unit = next;
       next_pages = after;
@@ -1319,6 +1358,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       while (step(cur, alt)) cur = alt;
     }
   }
+  if constexpr (TL) timeline_stamp<6>();  // all units done
   // merge threads: thread -> (column h, dims [d0, d0 + kDpt)), 16 threads
   // per column (8 dims each at head_dim 128, 4 at 64), so that every merge
   // read has the conflict-free pattern of acc_pitch; threads past the first
@@ -1365,6 +1405,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       }
     }
     __syncthreads();
+    if constexpr (TL) timeline_stamp<7>();  // wave merge barrier passed
 
     // merge the slots
     if constexpr (PREFIX) {
@@ -1434,6 +1475,11 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       }
     }
   }  // column blocks
+  if constexpr (TL) {
+    timeline_stamp<8>();  // partials issued
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    timeline_stamp<9>();  // partials acknowledged
+  }
 
   if constexpr (!MERGE) return;  // the reducer kernel merges
   if (p.splits == 1) return;     // rows went straight to the output
@@ -2554,6 +2600,16 @@ int launch_cascade(const fd_paged_decode_args& a, const DecodeParams& p, const C
 }  // namespace
 
 }  // namespace fd
+
+#ifdef FD_TIMELINE
+// Measurement build only: the device address and size of the timeline slots.
+extern "C" int fd_timeline_buffer(void** ptr, uint64_t* bytes) {
+  if (ptr == nullptr || bytes == nullptr) return FD_E_INVALID;
+  if (hipGetSymbolAddress(ptr, HIP_SYMBOL(fd::g_timeline)) != hipSuccess) return FD_E_LAUNCH;
+  *bytes = sizeof(fd::g_timeline);
+  return FD_OK;
+}
+#endif
 
 using namespace fd;
 
