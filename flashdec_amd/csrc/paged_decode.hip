@@ -1265,6 +1265,23 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   };
   load(unit, pages, cur);
   if constexpr (TL) timeline_stamp<2>();  // first unit's K/V loads issued
+  // The split partial's address for this thread's merge row, computed while
+  // the K/V loads are in flight (the empty asm keeps it here, not at the
+  // stores, where it sat on the kernel's last chain)
+  [[maybe_unused]] float* pre_acc = nullptr;
+  [[maybe_unused]] int64_t pre_so = 0;
+  // (one-unit waves only: with several units per wave the held address
+  // costs the loop registers, C5 step 3.186 -> 3.213 ms)
+  constexpr bool kPreStore = ROLE == Role::kRow && NCB == 1 && !MERGE && UNIT == 32;
+  if constexpr (kPreStore) {
+    constexpr int kDptE = D == 128 ? 8 : 4;
+    const int hE = (threadIdx.x / (D / kDptE)) & 15;
+    const int dE = (threadIdx.x % (D / kDptE)) * kDptE;
+    const int qhE = kvh * G + 16 * hb + hE;
+    pre_acc = p.acc + b * p.as0 + qhE * p.as1 + split * p.as2 + dE * p.as3;
+    pre_so = b * p.ss0 + qhE * p.ss1 + split * p.ss2;
+    asm volatile("" : "+v"(pre_acc), "+v"(pre_so));
+  }
   // The loaded length stays in a VGPR until here (the empty asm redefines
   // it): its move to an SGPR, and the wait for the load it brings, would
   // otherwise sit at the load, ahead of the K/V loads above.
@@ -1444,8 +1461,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     // role's partials follow the tail splits
     if (head_ok) {
       const int ws = PREFIX ? p.splits + split : split;
-      float* a = p.acc + ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3;
-      const int64_t so = ob * p.ss0 + qh * p.ss1 + ws * p.ss2;
+      float* a = kPreStore ? pre_acc : p.acc + ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3;
+      const int64_t so = kPreStore ? pre_so : ob * p.ss0 + qh * p.ss1 + ws * p.ss2;
       if constexpr (MERGE) {
         // device-coherent (sc1) stores, visible to every XCD once acknowledged;
         // the host guarantees unit dim stride and 8-byte alignment here
