@@ -24,7 +24,8 @@ FD_INDEX_I32 = 0
 FD_INDEX_I64 = 1
 ABI_VERSION = 9
 SPLIT_COUNTER_STRIDE = 64  # FD_SPLIT_COUNTER_STRIDE: uint32 words per (request, KV head) counter
-NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024  # FD_NOALLOC_SCRATCH_BYTES: per-GPU scratch of fd_paged_decode_noalloc
+NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024  # FD_NOALLOC_SCRATCH_BYTES: one stream's scratch slot of fd_paged_decode_noalloc
+NOALLOC_STREAM_SLOTS = 4  # FD_NOALLOC_STREAM_SLOTS: slots per GPU (one per stream)
 CASCADE_MAX_CHUNK_ROWS = 32  # FD_CASCADE_MAX_CHUNK_ROWS: the larger chunk_rows of fd_cascade_args
 
 _i64 = ctypes.c_int64

@@ -2865,19 +2865,28 @@ extern "C" int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t str
 
 // ------------------------------------------------ no-allocation entry ----
 // Split partials of fd_paged_decode_noalloc live in this file-scope array:
-// one copy per GPU, held until the process ends.  Host code never passes the
-// array's name to a kernel (on the host it is only a stand-in for the symbol):
-// the device address comes from hipGetSymbolAddress, once per device.
-static __device__ __align__(256) float scratch[FD_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+// one copy per GPU, held until the process ends, cut into
+// FD_NOALLOC_STREAM_SLOTS slots of FD_NOALLOC_SCRATCH_BYTES.  Each of the
+// first FD_NOALLOC_STREAM_SLOTS distinct streams that use it on a device owns
+// one slot for the rest of the process, so calls on different streams never
+// share partials, and the calls of one stream run in its order.  Host code
+// never passes the array's name to a kernel (on the host it is only a
+// stand-in for the symbol): the device address comes from
+// hipGetSymbolAddress, once per device.
+static __device__ __align__(256) float scratch[FD_NOALLOC_STREAM_SLOTS * (FD_NOALLOC_SCRATCH_BYTES / sizeof(float))];
 
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
+// slot owners per device (a stream handle; the null stream is a stream too)
+hipStream_t g_slot_owner[kMaxDevices][FD_NOALLOC_STREAM_SLOTS] = {};
+bool g_slot_used[kMaxDevices][FD_NOALLOC_STREAM_SLOTS] = {};
 
-// Device address of `scratch` on the stream's device (the current device for
-// the null stream); looked up on the first call on that device, with it
-// current.
+// Base of the stream's scratch slot on its device (the current device for
+// the null stream).  The array's address is looked up on the first call on
+// that device, with it current; the stream takes a free slot on its first
+// call.  Host bookkeeping only: nothing here launches or allocates.
 int scratch_address(hipStream_t stream, const char* fn, float** out) {
   int cur = 0;
   hipError_t e = hipGetDevice(&cur);
@@ -2902,7 +2911,21 @@ int scratch_address(hipStream_t stream, const char* fn, float** out) {
       return set_error(FD_E_LAUNCH, "%s: restoring device %d failed: %s", fn, cur, hipGetErrorString(restored));
     g_scratch_ptr[dev] = static_cast<float*>(ptr);
   }
-  *out = g_scratch_ptr[dev];
+  int slot = -1;
+  for (int i = 0; i < FD_NOALLOC_STREAM_SLOTS && slot < 0; ++i)
+    if (g_slot_used[dev][i] && g_slot_owner[dev][i] == stream) slot = i;
+  for (int i = 0; i < FD_NOALLOC_STREAM_SLOTS && slot < 0; ++i)
+    if (!g_slot_used[dev][i]) {
+      g_slot_used[dev][i] = true;
+      g_slot_owner[dev][i] = stream;
+      slot = i;
+    }
+  if (slot < 0)
+    return set_error(FD_E_UNSUPPORTED,
+                     "%s: device %d's %d no-allocation scratch slots are taken by other streams (one per stream, "
+                     "for the life of the process); use fewer streams or fd_paged_decode with a workspace",
+                     fn, dev, FD_NOALLOC_STREAM_SLOTS);
+  *out = g_scratch_ptr[dev] + static_cast<size_t>(slot) * (FD_NOALLOC_SCRATCH_BYTES / sizeof(float));
   return FD_OK;
 }
 }  // namespace

@@ -200,8 +200,10 @@ typedef struct fd_paged_decode_args {
 
 int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
 
-/* bytes of the per-GPU scratch array behind fd_paged_decode_noalloc (8 MiB) */
+/* bytes of one stream's slot of the per-GPU scratch behind
+ * fd_paged_decode_noalloc (8 MiB), and the slots per GPU (32 MiB in all) */
 #define FD_NOALLOC_SCRATCH_BYTES 8388608
+#define FD_NOALLOC_STREAM_SLOTS 4
 
 /*
  * fd_paged_decode without a caller workspace and without any allocation.
@@ -211,29 +213,40 @@ int fd_paged_decode(const fd_paged_decode_args* args, fd_stream_t stream);
  *
  * Same arguments, kernels and results as fd_paged_decode, except that
  * split_acc, split_max, split_sum and split_counters must be NULL: the split
- * partials go to a file-scope device array of FD_NOALLOC_SCRATCH_BYTES per
- * GPU, which each GPU the library runs on holds until the process ends.  A
- * launch with num_splits > 1 needs
+ * partials go to a file-scope device array of FD_NOALLOC_STREAM_SLOTS slots
+ * of FD_NOALLOC_SCRATCH_BYTES per GPU, which each GPU the library runs on
+ * holds until the process ends.  A launch with num_splits > 1 needs
  *   num_seqs * num_q_heads * num_splits * (head_dim + 2) * 4 bytes
- * of it (B8 Hq16 D128: up to 126 splits; B64 Hq16: up to 15); larger launches
- * are rejected with FD_E_INVALID before anything runs.  The splits are
- * merged by the reducer kernel (no in-launch merge).  Nothing in the array
- * needs to start at zero.  Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (two streams, two threads) race and must be
- * serialised by the caller.  The array's address on a device is looked up
- * once (hipGetSymbolAddress) by fd_paged_decode_noalloc_prepare or, failing
- * that, by the first call on the device; no call allocates or frees memory.
+ * of a slot (B8 Hq16 D128: up to 126 splits; B64 Hq16: up to 15); larger
+ * launches are rejected with FD_E_INVALID before anything runs.  The splits
+ * are merged by the reducer kernel (no in-launch merge).  Nothing in the
+ * array needs to start at zero.
+ *
+ * Slots: each of the first FD_NOALLOC_STREAM_SLOTS distinct streams (the NULL
+ * stream counts as one) that calls this function (or
+ * fd_paged_decode_noalloc_prepare) on a GPU owns one slot there for the rest
+ * of the process.  Calls on different streams therefore never share
+ * partials, from any number of host threads, and the calls of one stream
+ * run in its order.  A call from a further stream fails with
+ * FD_E_UNSUPPORTED before anything runs.  A call captured into a hipGraph
+ * keeps the slot of the stream it was captured on: replaying that graph on
+ * another stream while the capturing stream runs no-allocation calls, or
+ * replaying it twice at once, races.  The array's address on a device is
+ * looked up once (hipGetSymbolAddress) by fd_paged_decode_noalloc_prepare
+ * or, failing that, by the first call on the device; no call allocates or
+ * frees memory.
  */
 int fd_paged_decode_noalloc(const fd_paged_decode_args* args, fd_stream_t stream);
 
 /*
  * Set-up of fd_paged_decode_noalloc on the stream's device (the current
  * device for a NULL stream): looks the scratch array's device address up,
- * once per device, with that device current, and launches nothing.  Call it
- * (or make one eager fd_paged_decode_noalloc call) on every device before
- * capturing fd_paged_decode_noalloc into a hipGraph, so that no lookup runs
- * inside the capture.  Allocates nothing; idempotent.  No counterpart in the
- * reference.
+ * once per device, with that device current, takes the stream's scratch slot
+ * (FD_E_UNSUPPORTED when every slot belongs to another stream), and launches
+ * nothing.  Call it (or make one eager fd_paged_decode_noalloc call) on every
+ * device before capturing fd_paged_decode_noalloc into a hipGraph, so that
+ * no lookup runs inside the capture.  Allocates nothing; idempotent.  No
+ * counterpart in the reference.
  */
 int fd_paged_decode_noalloc_prepare(fd_stream_t stream);
 

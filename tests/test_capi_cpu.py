@@ -104,6 +104,7 @@ def test_header_constants_match_binding():
     assert int(consts["FD_DTYPE_F32"]) == _lib.FD_DTYPE_F32
     assert int(consts["FD_INDEX_I64"]) == _lib.FD_INDEX_I64
     assert int(consts["FD_NOALLOC_SCRATCH_BYTES"]) == _lib.NOALLOC_SCRATCH_BYTES
+    assert int(consts["FD_NOALLOC_STREAM_SLOTS"]) == _lib.NOALLOC_STREAM_SLOTS
     assert int(consts["FD_CASCADE_MAX_CHUNK_ROWS"]) == _lib.CASCADE_MAX_CHUNK_ROWS
 
 

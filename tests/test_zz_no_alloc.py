@@ -5,7 +5,9 @@ in the library's per-GPU scratch array instead of a caller workspace, so its
 output must equal fd_paged_decode's bit for bit (and the oracle within the
 attention tolerance).  Two calls in a row, the second smaller, check that a
 call never depends on what the previous one left in the scratch; the largest
-launch the scratch holds runs too.
+launch the scratch holds runs too.  Calls on two streams with no ordering
+between them each use their stream's own scratch slot, and a stream past the
+slots is refused (that test runs last: it leaves every slot taken).
 """
 
 import math
@@ -180,3 +182,59 @@ def test_prepare_needs_no_launch_and_is_idempotent():
     for _ in range(3):
         _lib.paged_decode_noalloc_prepare(stream)
     _lib.paged_decode_noalloc_prepare(0)  # the null stream: the current device
+
+
+def test_two_streams_without_ordering_use_their_own_slots():
+    """Two streams enqueue no-allocation calls back to back with nothing ordering one stream
+    against the other; every output equals fd_paged_decode's on the same inputs, bit for bit,
+    because each stream's partials go to a scratch slot of its own."""
+    from flashdec_amd import _lib
+
+    splits = 16
+    inputs = [make_paged_inputs([2048] * 8, 16, 2, 128, 32, seed=200 + i) for i in range(2)]
+    refs = []
+    for q, k, v, table, lens in inputs:
+        ref = torch.empty_like(q)
+        _lib.paged_decode(_args(q, k, v, table, lens, ref, 32, 2, splits, _workspace(8, 16, splits, 128)),
+                          _lib.current_stream_handle(q.device))
+        refs.append(ref)
+    outs = [[torch.full_like(inputs[i][0], float("nan")) for _ in range(6)] for i in range(2)]
+    torch.cuda.synchronize()
+    streams = (torch.cuda.Stream(), torch.cuda.Stream())
+    for rep in range(6):
+        for i, side in enumerate(streams):
+            q, k, v, table, lens = inputs[i]
+            with torch.cuda.stream(side):
+                _lib.paged_decode_noalloc(_args(q, k, v, table, lens, outs[i][rep], 32, 2, splits),
+                                          _lib.current_stream_handle(q.device))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for rep in range(6):
+            assert torch.equal(outs[i][rep], refs[i]), (i, rep)
+
+
+def test_zz_a_stream_past_the_slots_is_refused_before_anything_runs():
+    """New streams take the free scratch slots; the first stream past them gets the
+    library's error (and its output is untouched), while a stream that owns a slot still runs.
+    Runs last in this file: afterwards every slot of the GPU is taken."""
+    from flashdec_amd import _lib
+
+    q, k, v, table, lens = make_paged_inputs([512, 300], 8, 2, 128, 32, seed=9)
+    owner = _lib.current_stream_handle(q.device)
+    _lib.paged_decode_noalloc_prepare(owner)
+    refused = None
+    for n in range(48):  # more than torch's stream pool: its handles repeat
+        side = torch.cuda.Stream()
+        out = torch.full_like(q, float("nan"))
+        with torch.cuda.stream(side):
+            try:
+                _lib.paged_decode_noalloc(_args(q, k, v, table, lens, out, 32, 2, 4),
+                                          _lib.current_stream_handle(q.device))
+            except RuntimeError as exc:
+                refused = str(exc)
+                torch.cuda.synchronize()
+                assert torch.isnan(out).all()
+                break
+    assert refused is not None and "scratch slots" in refused, refused
+    ref, out = _both(q, k, v, table, lens, 32, 2, 4)  # the owner's slot still serves it
+    assert torch.equal(ref, out)
