@@ -1959,7 +1959,9 @@ __device__ __forceinline__ float wave_max_f32(float x) {
 // written by this call's attention kernel, and a row with nothing to attend
 // (zero length, or a padding slot) has denominator 0 in every split, which
 // selects the zero row below just as the length test does.
-template <typename T, int D, int MODE, int W, bool PRE, bool OUTP = false>
+// FCH > 0: the row has exactly FCH splits (a power of two up to 32) in a
+// contiguous [rows, FCH, D] workspace, read as one chunk.
+template <typename T, int D, int MODE, int W, bool PRE, bool OUTP = false, int FCH = 0>
 __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row = blockIdx.x) {
   static_assert(!PRE || MODE == kReducePlain || MODE == kReduceCascade,
                 "preloaded reducer arguments are for the plain and cascade merges");
@@ -2030,13 +2032,21 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
     const int sj = s64 + min(lane, n - 1);
     const float lm = p.mx[sb + sj * ss2];
     const float ll = p.sm[sb + sj * ss2];
-    for (int c0 = 0; c0 < n; c0 += kReduceChunk) {
-      float a[kReduceChunk][E];
+    constexpr bool FULL = FCH > 0;
+    constexpr int CH = FULL ? FCH : kReduceChunk;
+    for (int c0 = 0; c0 < n; c0 += CH) {
+      float a[CH][E];
 #pragma unroll
-      for (int j = 0; j < kReduceChunk; ++j) {
-        const int s = s64 + min(c0 + j, n - 1);  // past the end: re-read, masked below
+      for (int j = 0; j < CH; ++j) {
+        if constexpr (FULL) {
+          // whole chunks of D-float rows: one base, immediate offsets
 #pragma unroll
-        for (int e = 0; e < E; ++e) a[j][e] = ab[s * p.as2 + (lane + 64 * e) * as3];
+          for (int e = 0; e < E; ++e) a[j][e] = ab[(s64 + c0 + j) * D + lane + 64 * e];
+        } else {
+          const int s = s64 + min(c0 + j, n - 1);  // past the end: re-read, masked below
+#pragma unroll
+          for (int e = 0; e < E; ++e) a[j][e] = ab[s * p.as2 + (lane + 64 * e) * as3];
+        }
       }
       // keep every load above issued before the broadcasts below (they wait)
       __builtin_amdgcn_sched_barrier(0);
@@ -2052,24 +2062,40 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
       // not a chain of dependent max and exp steps per split (the same
       // values, bit for bit: a maximum is exact in any order).
       const int cl = lane - c0;  // this lane's split within the chunk
-      const bool mine = cl >= 0 && cl < kReduceChunk && cl < n - c0 && s64 + lane < valid;
-      const float nm = fmaxf(M, wave_max_f32(mine ? lm : -INFINITY));
+      const bool mine = cl >= 0 && cl < CH && cl < n - c0 && s64 + lane < valid;
+      // the statistics are used only from here on: on the clamped path the
+      // empty asm keeps the compiler from hoisting their uses (and the wait
+      // for them) above the chunk's partial loads
+      float lmv = lm, llv = ll;
+      if constexpr (!FULL) asm volatile("" : "+v"(lmv), "+v"(llv));
+      const float nm = fmaxf(M, wave_max_f32(mine ? lmv : -INFINITY));
       const float nmu = nm == -INFINITY ? 0.f : nm;
       const float sc = exp2f(M - nmu);
       L *= sc;
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] *= sc;
-      const float wl = exp2f(lm - nmu);
+      const float wl = exp2f(lmv - nmu);
 #pragma unroll
-      for (int j = 0; j < kReduceChunk; ++j) {
-        const int src = min(c0 + j, n - 1);
-        const float w = lane_bcast(wl, src);
-        const float lj = lane_bcast(ll, src);
-        // masked splits may hold stale or NaN partials: selected away, not weighted by 0
-        const bool use = c0 + j < n && s64 + c0 + j < valid;
-        L += use ? w * lj : 0.f;
+      for (int j = 0; j < CH; ++j) {
+        const int src = FULL ? c0 + j : min(c0 + j, n - 1);
+        const float lj = lane_bcast(llv, src);
+        const bool use = FULL || (c0 + j < n && s64 + c0 + j < valid);
+        if constexpr (MODE == kReduceCascade) {
+          // masked splits may hold stale or NaN partials: selected away, not weighted by 0
+          const float w = lane_bcast(wl, src);
+          L += use ? w * lj : 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[e] += use ? w * a[j][e] : 0.f;
+          for (int e = 0; e < E; ++e) o[e] += use ? w * a[j][e] : 0.f;
+        } else {
+          // every split below n holds this call's partials and the loads past
+          // n re-read split n - 1, so a zero weight masks them; the sums are
+          // fused multiply-adds on every path (whole chunks, clamped chunks
+          // and the in-launch merge round alike)
+          const float w = use ? lane_bcast(wl, src) : 0.f;
+          L += w * lj;
+#pragma unroll
+          for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
+        }
       }
       M = nm;
     }
@@ -2127,7 +2153,7 @@ __global__ __launch_bounds__(64 * W) void split_reduce_kernel(ReduceParams p) {
 // box).  The output pointer fills the last two SGPRs: with an output in row
 // order (OUTP) the kernel reads nothing from the argument buffer, whose fetch
 // otherwise sat ahead of the output stores (C2 8.26 -> 8.15 us, one box).
-template <typename T, int D, int W = 1, bool OUTP = false>
+template <typename T, int D, int W = 1, bool OUTP = false, int FCH = 0>
 __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* acc, const float* mx, const float* sm,
                                                                   int32_t as1, int32_t as2, int32_t ss1,
                                                                   int32_t splits, int32_t hq, int32_t xcd_rows,
@@ -2142,7 +2168,7 @@ __global__ __launch_bounds__(64 * W) void split_reduce_pre_kernel(const float* a
   q.ss1 = ss1;
   q.splits = splits;
   q.hq = hq;
-  reduce_row<T, D, kReducePlain, W, true, OUTP>(q, xcd_logical_block(blockIdx.x, xcd_rows));
+  reduce_row<T, D, kReducePlain, W, true, OUTP, FCH>(q, xcd_logical_block(blockIdx.x, xcd_rows));
 }
 
 // The cascade merge over a packed workspace (as split_reduce_pre_kernel),
@@ -2450,6 +2476,29 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
       else
         outp ? pre(split_reduce_pre_kernel<T, 128, 4, true>, dim3(256))
              : pre(split_reduce_pre_kernel<T, 128, 4>, dim3(256));
+    } else if (outp && r.as2 == a.head_dim && r.as1 == r.splits * a.head_dim && r.ss1 == r.splits &&
+               (r.splits == 2 || r.splits == 4 || r.splits == 8 || r.splits == 16 || r.splits == 32)) {
+      // contiguous [rows, splits, D] partials with a power-of-two split count
+      // (the library's own workspaces: C2 has 16, its ctx1024 companion 8):
+      // every partial load is an immediate offset from one base, with no
+      // clamp, no per-split address and no select
+      auto full = [&](auto k2, auto k4, auto k8, auto k16, auto k32) {
+        switch (r.splits) {
+          case 2: pre(k2, dim3(64)); break;
+          case 4: pre(k4, dim3(64)); break;
+          case 8: pre(k8, dim3(64)); break;
+          case 16: pre(k16, dim3(64)); break;
+          default: pre(k32, dim3(64)); break;
+        }
+      };
+      if (a.head_dim == 64)
+        full(split_reduce_pre_kernel<T, 64, 1, true, 2>, split_reduce_pre_kernel<T, 64, 1, true, 4>,
+             split_reduce_pre_kernel<T, 64, 1, true, 8>, split_reduce_pre_kernel<T, 64, 1, true, 16>,
+             split_reduce_pre_kernel<T, 64, 1, true, 32>);
+      else
+        full(split_reduce_pre_kernel<T, 128, 1, true, 2>, split_reduce_pre_kernel<T, 128, 1, true, 4>,
+             split_reduce_pre_kernel<T, 128, 1, true, 8>, split_reduce_pre_kernel<T, 128, 1, true, 16>,
+             split_reduce_pre_kernel<T, 128, 1, true, 32>);
     } else if (a.head_dim == 64) {
       outp ? pre(split_reduce_pre_kernel<T, 64, 1, true>, dim3(64)) : pre(split_reduce_pre_kernel<T, 64>, dim3(64));
     } else {

@@ -279,13 +279,13 @@ def test_explicit_splits_reducer_kernel_many_splits(num_splits):
 
 
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("num_splits", [5, 40])
+@pytest.mark.parametrize("num_splits", [5, 8, 16, 40])
 def test_packed_and_strided_workspaces_merge_to_the_same_bits(num_splits, head_dim):
     """The plain merge runs one kernel on a packed [B, Hq, S, D] workspace (addressing
     preloaded, empty rows told by their zero denominators) and another on any other
     workspace strides (reading each row's length and slot).  With NaN in both workspaces
-    beforehand, zero-length rows and a padding slot, the two give the same bits; 40 splits
-    take the four-wave merge."""
+    beforehand, zero-length rows and a padding slot, the two give the same bits; 8 and 16
+    splits take the whole-chunk kernel (immediate-offset loads), 40 the four-wave merge."""
     dtype = torch.bfloat16
     hq, hkv, bs = 16, 2, 32
     lens_after = [0, 1, 37, 300, 1100, 65]

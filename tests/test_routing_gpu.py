@@ -42,8 +42,9 @@ def test_c2_shape_row_kernel_and_preloaded_reducer(record):
 
     q, k, v, table, sl = make_paged_inputs([2048] * 8, 16, 2, 128, 32, seed=1)
     out = fd.decode(q, k, v, table, sl)
-    # an output in row order: the reducer takes its pointer preloaded and no strides
-    assert record.last_launch() == [mfma(unit=32), "fd::split_reduce_pre_kernel<__bf16, 128, 1, true>"]
+    # an output in row order: the reducer takes its pointer preloaded and no strides; the
+    # library's contiguous workspace with 16 splits: immediate-offset partial loads
+    assert record.last_launch() == [mfma(unit=32), "fd::split_reduce_pre_kernel<__bf16, 128, 1, true, 16>"]
     assert_close_to_oracle(out, _oracle(q, k, v, table, sl))
 
 
@@ -66,7 +67,7 @@ def test_output_view_out_of_row_order_takes_the_strided_store(d, record):
     for out in (wide[..., :d], transposed):
         pd._decode_with_workspace(q, k, v, table, sl, out, 1.0 / math.sqrt(d), 32, splits, ws, k.shape[0])
         torch.cuda.synchronize()
-        assert record.last_launch()[1] == f"fd::split_reduce_pre_kernel<__bf16, {d}, 1, false>"
+        assert record.last_launch()[1] == f"fd::split_reduce_pre_kernel<__bf16, {d}, 1, false, 0>"
         assert_close_to_oracle(out, expected)
     assert torch.isnan(wide[..., d:]).all()  # nothing written past the view
 
