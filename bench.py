@@ -24,7 +24,9 @@ Timing:
   graph replays is the cross-check.
 * ``roofline.traffic``: HBM bytes per attention-kernel dispatch from the
   committed PMC summary ``profiles/decode_mfma_b8_ctx2048_traffic.json``
-  (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null.
+  (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null
+  (also for any other shape than the headline one those counters were
+  taken on).
 * ``ctx1024``: the same call at ctx1024 (BASELINE's C2 names both
   contexts), timed the same way on 48 pools of its own.
 * ``cpu_baseline``: the reference's CPU path as fp32 torch-CPU ops in its
@@ -1546,6 +1548,9 @@ def main():
 
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     traffic, traffic_meta = load_traffic()
+    if traffic_meta is not None and traffic_meta.get("algorithmic_bytes_per_call") != nbytes:
+        # the committed counters are for the headline shape only
+        traffic, traffic_meta = None, None
     traffic_src = None if traffic_meta is None else os.path.relpath(TRAFFIC_SUMMARY, ROOT)
     if traffic is not None:
         traffic = int(round(traffic))
