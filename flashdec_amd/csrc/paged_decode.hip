@@ -2036,12 +2036,13 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
     constexpr int CH = FULL ? FCH : kReduceChunk;
     for (int c0 = 0; c0 < n; c0 += CH) {
       float a[CH][E];
+      // whole chunks of D-float rows: one base, constant offsets (immediates)
+      [[maybe_unused]] const float* cbase = ab + (s64 + c0) * D + lane;
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
         if constexpr (FULL) {
-          // whole chunks of D-float rows: one base, immediate offsets
 #pragma unroll
-          for (int e = 0; e < E; ++e) a[j][e] = ab[(s64 + c0 + j) * D + lane + 64 * e];
+          for (int e = 0; e < E; ++e) a[j][e] = cbase[j * D + 64 * e];
         } else {
           const int s = s64 + min(c0 + j, n - 1);  // past the end: re-read, masked below
 #pragma unroll
@@ -2091,7 +2092,11 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
           // n re-read split n - 1, so a zero weight masks them; the sums are
           // fused multiply-adds on every path (whole chunks, clamped chunks
           // and the in-launch merge round alike)
-          const float w = use ? lane_bcast(wl, src) : 0.f;
+          // the broadcast runs on every path: a broadcast under the uniform
+          // test becomes a branch, and the branches let the compiler sink
+          // the chunk's partial loads below the statistics' wait
+          const float wb = lane_bcast(wl, src);
+          const float w = use ? wb : 0.f;
           L += w * lj;
 #pragma unroll
           for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
