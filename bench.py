@@ -81,11 +81,14 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-kernels", type=int, default=0, metavar="N",
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
-    p.add_argument("--workload", choices=("decode", "c2-floor", "c2-timeline", "rope", "ragged", "prefix", "prefix-large",
+    p.add_argument("--workload", choices=("decode", "c2-floor", "c2-timeline", "c4-timeline", "rope", "ragged", "prefix",
+                                          "prefix-large",
                                           "prefix-sweep", "engine", "engine-prefix", "formats", "vllm"),
                    default="decode",
                    help="decode: the headline C2 call (default); c2-floor: the C2 call beside a bare read of "
-                        "its bytes and a dependent empty launch (the floor of a call of that size); rope: C3 fused RoPE + KV append; ragged / "
+                        "its bytes and a dependent empty launch (the floor of a call of that size); c2-timeline / "
+                        "c4-timeline: per-wave phase stamps of the C2 attention kernel / the C4 shared-prefix "
+                        "cascade kernel (measurement build); rope: C3 fused RoPE + KV append; ragged / "
                         "prefix: C4 ragged long-context and shared-prefix decode; prefix-large: 64 requests "
                         "sharing a 16384-token prefix; prefix-sweep: cascade chunk rows x prefix splits at four "
                         "shared-prefix sizes; engine: C5 36-layer step; engine-prefix: 36-layer steps "
@@ -871,6 +874,39 @@ TIMELINE_PHASES = ("wave start", "block-table entry arrived", "K/V loads issued"
                    "PV issued", "units done", "wave-merge barrier passed", "partials issued", "partials acknowledged")
 
 
+def timeline_reader():
+    """(read, clear) for the measurement build's per-wave stamp array: read()
+    copies it to the host as uint64 [workgroups, 8 waves, 16 slots]."""
+    import ctypes
+
+    import numpy as np
+
+    from flashdec_amd import _lib
+
+    lib = _lib.load_library()
+    if not hasattr(lib, "fd_timeline_buffer"):
+        raise RuntimeError("the timeline workloads need libflashdec_timeline.so (FLASHDEC_AMD_LIB points elsewhere)")
+    lib.fd_timeline_buffer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)]
+    lib.fd_timeline_buffer.restype = ctypes.c_int
+    ptr, nbytes = ctypes.c_void_p(), ctypes.c_uint64()
+    assert lib.fd_timeline_buffer(ctypes.byref(ptr), ctypes.byref(nbytes)) == 0
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    hip.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    hip.hipMemset.restype = ctypes.c_int
+    host = np.zeros(nbytes.value // 8, dtype=np.uint64)
+
+    def read():
+        assert hip.hipMemcpy(host.ctypes.data, ptr.value, host.nbytes, 2) == 0  # device to host
+        return host.reshape(-1, 8, 16).copy()
+
+    def clear():
+        assert hip.hipMemset(ptr.value, 0, host.nbytes) == 0
+
+    return read, clear
+
+
 def run_c2_timeline(torch, dev, args):
     """Per-wave timeline of the C2 attention kernel, from libflashdec_timeline.so.
 
@@ -884,23 +920,12 @@ def run_c2_timeline(torch, dev, args):
     each phase.  The stamps' own stores and waits perturb the kernel slightly:
     the graph's per-call time with them is reported beside the figures.
     """
-    import ctypes
-
     import numpy as np
 
     import flashdec_amd as fd
     from flashdec_amd import _lib
 
-    lib = _lib.load_library()
-    if not hasattr(lib, "fd_timeline_buffer"):
-        raise RuntimeError("c2-timeline needs libflashdec_timeline.so (FLASHDEC_AMD_LIB points elsewhere)")
-    lib.fd_timeline_buffer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64)]
-    lib.fd_timeline_buffer.restype = ctypes.c_int
-    ptr, nbytes = ctypes.c_void_p(), ctypes.c_uint64()
-    assert lib.fd_timeline_buffer(ctypes.byref(ptr), ctypes.byref(nbytes)) == 0
-    hip = ctypes.CDLL("libamdhip64.so")
-    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    hip.hipMemcpy.restype = ctypes.c_int
+    read, _ = timeline_reader()
     batch, hq, hkv, d, bs = 8, 16, 2, 128, 32
     sm_scale = 1.0 / math.sqrt(d)
     res = {}
@@ -908,7 +933,6 @@ def run_c2_timeline(torch, dev, args):
         pools = build_pools(torch, args.pools, batch, ctx, hq, hkv, d, bs, dev)
         splits = _lib.paged_decode_plan(batch, hq, hkv, d, ctx)
         grid = batch * hkv * splits
-        host = np.zeros(grid * 8 * 16, dtype=np.uint64)
 
         def call(i):
             q, k, v, table, lens, out = pools[i % len(pools)]
@@ -929,8 +953,7 @@ def run_c2_timeline(torch, dev, args):
         for _ in range(30):
             graph.replay()
             torch.cuda.synchronize()
-            assert hip.hipMemcpy(host.ctypes.data, ptr.value, host.nbytes, 2) == 0  # device to host
-            st = host.reshape(grid, 8, 16)[:, :4, : len(TIMELINE_PHASES)].reshape(grid * 4, -1).astype(np.int64)
+            st = read()[:grid, :4, : len(TIMELINE_PHASES)].reshape(grid * 4, -1).astype(np.int64)
             rel.append((st - st[:, 0].min()) * 10)  # ns
         rel = np.concatenate(rel)
         phases = {}
@@ -953,6 +976,91 @@ def run_c2_timeline(torch, dev, args):
                         c2["stamps_ns"]["partials acknowledged"]["median"], "ns",
                         c2["instrumented_us_per_call"] * 1e-3, False,
                         {"workload": "c2-timeline-b8-hq16-hkv2-d128-bs32", "kv_pools": args.pools})
+    out.update(res)
+    return out
+
+
+def run_c4_timeline(torch, dev, args):
+    """Per-wave timeline of the C4 shared-prefix cascade kernel, from libflashdec_timeline.so.
+
+    The C4 prefix workload's pools (16 requests on one 4096-token prefix,
+    tails U{1..512}, seed 1701, 40 pools) through the cascade call; a graph of
+    one call per pool is replayed 30 times, the stamp array cleared before
+    each replay and read after it (the last call's stamps).  Every wave of the
+    cascade kernel writes the phase stamps of the C2 timeline, the end of each
+    of its 16-token units, and its role.  Reported per role (prefix, tail), in
+    ns after the call's first wave start: p10 / median / p90 / max of every
+    phase and unit end over the 30 calls' waves; the instrumented call's time
+    beside them.
+    """
+    import numpy as np
+
+    from flashdec_amd import cascade
+
+    read, clear = timeline_reader()
+    hq, hkv, d, bs = 16, 2, 128, 32
+    sm_scale = 1.0 / math.sqrt(d)
+    tails = np.random.default_rng(1701).integers(1, 513, size=16)
+    lens = [4096 + int(t) for t in tails]
+    pools = decode_pools(torch, dev, lens, hq, hkv, d, bs, 40, 1701, prefix_blocks=128)
+    groups = [cascade.build_cascade_groups(p[3], p[4], bs, hq, hkv) for p in pools]
+
+    def call(i):
+        q, k, v, table, sl, o = pools[i % len(pools)]
+        cascade.paged_decode_attention_cascade_into(q, k, v, table, sl, o, groups[i % len(pools)], sm_scale=sm_scale)
+
+    us_call = graph_p50_us(torch, dev, call, len(pools), samples=60)
+    prep = cascade_prepared(torch, pools[0], groups[0], sm_scale, bs, hkv)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        call(0)
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(len(pools)):
+                call(i)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    names = TIMELINE_PHASES + tuple(f"unit {u} done" for u in range(4)) + ("unit 4+ done",)
+    per_role = {1: [], 2: []}
+    for _ in range(30):
+        torch.cuda.synchronize()
+        clear()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        st = read()
+        role = st[:, :, 15]
+        live = role > 0
+        t0 = st[:, :, 0][live].astype(np.int64).min()
+        rel = (st[:, :, :15].astype(np.int64) - t0) * 10  # ns
+        rel[st[:, :, :15] == 0] = -1  # phase not reached (units past the wave's last)
+        for r in (1, 2):
+            per_role[r].append(rel[role == r])
+    res = {}
+    for r, label in ((1, "prefix"), (2, "tail")):
+        rel = np.concatenate(per_role[r])
+        phases = {}
+        for k, name in enumerate(names):
+            col = rel[:, k][rel[:, k] >= 0]
+            if col.size == 0:
+                continue
+            phases[name] = {"waves": int(col.size), "p10": float(np.percentile(col, 10)),
+                            "median": float(np.median(col)), "p90": float(np.percentile(col, 90)),
+                            "max": float(col.max())}
+        log(f"[bench] c4-timeline {label} role ({rel.shape[0] // 30} waves x 30 calls; instrumented call "
+            f"{us_call:.2f} us):")
+        for name, v in phases.items():
+            log(f"[bench]   {name:28s} p10 {v['p10']:6.0f}  median {v['median']:6.0f}  p90 {v['p90']:6.0f}  "
+                f"max {v['max']:6.0f} ns  ({v['waves'] // 30} waves)")
+        res[label] = {"waves": rel.shape[0] // 30, "stamps_ns": phases}
+    out = common_fields(args, "C4 shared-prefix cascade kernel: median prefix-role wave end after the first wave "
+                        "start (ns)", res["prefix"]["stamps_ns"]["partials acknowledged"]["median"], "ns",
+                        us_call * 1e-3, False,
+                        {"workload": "c4-timeline-shared-prefix-16x4096+U512", "kv_pools": len(pools),
+                         "tail_splits": prep[0].num_splits, "prefix_splits": prep[1].prefix_splits,
+                         "chunk_rows": prep[1].chunk_rows})
+    out["instrumented_us_per_call"] = round(us_call, 3)
     out.update(res)
     return out
 
@@ -1418,7 +1526,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload == "c2-timeline":
+    if args.workload in ("c2-timeline", "c4-timeline"):
         # the measurement build of the library, with the per-wave stamps
         from flashdec_amd import _build
 
@@ -1427,7 +1535,7 @@ def main():
         os.environ["FLASHDEC_AMD_LIB"] = str(_build.TIMELINE_LIB_PATH)
     _lib.load_library()
     if args.workload != "decode":
-        run = {"c2-floor": run_c2_floor, "c2-timeline": run_c2_timeline, "rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
+        run = {"c2-floor": run_c2_floor, "c2-timeline": run_c2_timeline, "c4-timeline": run_c4_timeline, "rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
                "prefix-sweep": run_prefix_sweep, "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
                "vllm": run_vllm}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)

@@ -33,11 +33,15 @@
 
 namespace fd {
 
-// Per-wave timeline of the MFMA row kernel, in a measurement build only
-// (FD_TIMELINE: libflashdec_timeline.so, read by bench.py's c2-timeline
-// workload; the product library compiles none of it).  Lane 0 of each wave
-// writes s_memrealtime (100 MHz) at the phase boundaries of
-// decode_role / process_unit into slot (workgroup * 8 + wave) * 16 + phase.
+// Per-wave timeline of the MFMA row kernel and the cascade kernel, in a
+// measurement build only (FD_TIMELINE: libflashdec_timeline.so, read by
+// bench.py's c2-timeline and c4-timeline workloads; the product library
+// compiles none of it).  Lane 0 of each wave writes s_memrealtime (100 MHz)
+// at the phase boundaries of decode_role / process_unit into slot
+// (workgroup * 8 + wave) * 16 + phase: phases 0-9 as named at the stamps,
+// 10-14 the end of the wave's units 0-4 (later units in 14), and in the
+// cascade kernel slot 15 the wave's role (1 prefix, 2 tail) instead of a
+// time.
 #ifdef FD_TIMELINE
 constexpr bool kTimeline = true;
 constexpr int kTimelineWorkgroups = 8192;
@@ -46,14 +50,17 @@ __device__ uint64_t g_timeline[kTimelineWorkgroups * 8 * 16];
 constexpr bool kTimeline = false;
 #endif
 
+__device__ __forceinline__ void timeline_put([[maybe_unused]] int k, [[maybe_unused]] bool mark,
+                                             [[maybe_unused]] uint64_t v) {
+#ifdef FD_TIMELINE
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < kTimelineWorkgroups)
+    g_timeline[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 16 + k] = mark ? v : __builtin_amdgcn_s_memrealtime();
+#endif
+}
+
 template <int K>
 __device__ __forceinline__ void timeline_stamp() {
-#ifdef FD_TIMELINE
-  if ((threadIdx.x & 63) == 0 && blockIdx.x < kTimelineWorkgroups) {
-    const uint64_t t = __builtin_amdgcn_s_memrealtime();
-    g_timeline[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 16 + K] = t;
-  }
-#endif
+  timeline_put(K, false, 0);
 }
 
 struct DecodeParams {
@@ -1104,8 +1111,12 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
                  "s"(p.max_blocks_per_seq), "s"(p.num_blocks), "s"(p.block_size));
   }
 
-  constexpr bool TL = kTimeline && ROLE == Role::kRow && PRE && !DM;
-  if constexpr (TL) timeline_stamp<0>();  // wave start
+  constexpr bool TL = kTimeline && ((ROLE == Role::kRow && PRE && !DM) || PREFIX || TAIL);
+  if constexpr (TL) {
+    timeline_stamp<0>();  // wave start
+    if constexpr (PREFIX || TAIL) timeline_put(15, true, PREFIX ? 1 : 2);
+  }
+  [[maybe_unused]] int tl_units = 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15;
@@ -1123,6 +1134,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   const int hblocks =
       ROLE == Role::kRow ? static_cast<int>(static_cast<unsigned>(G + 16 * NCB - 1) / (16u * NCB)) : 1;
   int b, kvh, chunk = 0, hb = 0;
+  [[maybe_unused]] int grp = 0;  // the prefix role's group
   const int32_t* mem = nullptr;
   int64_t bal_eff = 0;
   if constexpr (BAL) {
@@ -1138,7 +1150,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     chunk = pair % cp.chunks;
     const int gk = pair / cp.chunks;
     kvh = gk % p.hkv;
-    mem = cp.members + static_cast<int64_t>(gk / p.hkv) * cp.max_members;
+    grp = gk / p.hkv;
+    mem = cp.members + static_cast<int64_t>(grp) * cp.max_members;
     b = mem[0];  // the lead: its table row holds the prefix's block ids
   } else if constexpr (PRE && ROLE == Role::kRow) {
     // multiply-high divisions (the split was taken the same way above)
@@ -1237,7 +1250,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   [[maybe_unused]] int32_t seq_len = 0;
   [[maybe_unused]] int64_t plen = 0;
   if constexpr (PREFIX) {
-    plen = lead_ok ? cp.prefix_len[pair / cp.chunks / p.hkv] : 0;
+    plen = lead_ok ? cp.prefix_len[grp] : 0;
   } else if constexpr (!BAL) {
     seq_len = load_index(p.sl, b * p.sls, p.sl_i64);
     slot = FUSE ? load_index(p.slot, b * p.slots, p.slot_i64) : -1;
@@ -1360,7 +1373,11 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       else {
         process_unit<T, (FUSE != 0), UNIT, D, NCB, TL>(now, qf, p.scale_log2, unit * UNIT, first, last, app, ar, c,
                                                        g, st);
-        if constexpr (TL) timeline_stamp<5>();  // unit's PV issued
+        if constexpr (TL) {
+          timeline_stamp<5>();  // unit's PV issued
+          timeline_put(10 + min(tl_units, 4), false, 0);  // the wave's unit tl_units done
+          ++tl_units;
+        }
       }
       unit = next;
       next_pages = after;
