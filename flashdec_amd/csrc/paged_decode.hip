@@ -606,6 +606,11 @@ __device__ __forceinline__ float column_sum(float x) { return pair_rows32_sum(pa
 // 7.58 -> 7.51 us per call), for weights that only matter above 2^-126.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// 1 / x on the hardware's v_rcp_f32 (1 ulp), for the softmax denominators of
+// the stored rows: the division's correctly rounded sequence is about ten
+// dependent instructions ahead of every output store.
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
 // Online-softmax step over one unit's scores of a lane (base-2 domain): the
 // probabilities pr, and st updated for them.  The reference's kernels move
 // the running maximum to every new block maximum and rescale acc and l each
@@ -1475,7 +1480,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       }
     }
     if (ROLE == Role::kRow && p.splits == 1) {
-      if (head_ok) store_row<T, kDpt>(p, b, qh, d0, o, L > 0.f ? 1.f / L : 0.f);
+      if (head_ok) store_row<T, kDpt>(p, b, qh, d0, o, L > 0.f ? rcp_fast(L) : 0.f);
       continue;
     }
     // split partial: unnormalised acc, base-2 max, denominator; the prefix
@@ -1599,7 +1604,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
         gx[4 + k] += w * part[j][1][k];
       }
     }
-    const float inv = GLx > 0.f ? 1.f / GLx : 0.f;
+    const float inv = GLx > 0.f ? rcp_fast(GLx) : 0.f;
     T* dst = static_cast<T*>(p.out) + b * p.os0 + qq * p.os1 + dd * p.os2;
     if (p.os2 == 1 && dpt == 8) {
       u32x4 w4;
@@ -1671,7 +1676,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     }
     GM = nm;
   }
-  if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? 1.f / GL : 0.f);
+  if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? rcp_fast(GL) : 0.f);
 }
 
 // FUSE: 0 none, 1 fused append, 2 fused append with RoPE of q and the new K;
@@ -1961,6 +1966,14 @@ __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
 // Maximum over the wave, every lane receiving it: rotations within each
 // 16-lane row (DPP row_ror), then across the rows (permlane swaps).
 __device__ __forceinline__ float dpp_row_ror_max(float x, int y) { return fmaxf(x, __builtin_bit_cast(float, y)); }
+// Maximum within each 16-lane row (every lane of the row receiving it)
+__device__ __forceinline__ float row_max_f32(float x) {
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+  x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+  return x;
+}
 __device__ __forceinline__ float wave_max_f32(float x) {
   x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
   x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
@@ -2090,7 +2103,11 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
       // for them) above the chunk's partial loads
       float lmv = lm, llv = ll;
       if constexpr (!FULL) asm volatile("" : "+v"(lmv), "+v"(llv));
-      const float nm = fmaxf(M, wave_max_f32(mine ? lmv : -INFINITY));
+      // a whole chunk of at most 16 splits sits in lanes 0-15, the first DPP
+      // row: its maximum needs no swaps across rows (the other rows' lanes
+      // hold -inf and are never broadcast from)
+      const float cmx = mine ? lmv : -INFINITY;
+      const float nm = fmaxf(M, FULL && FCH <= 16 ? row_max_f32(cmx) : wave_max_f32(cmx));
       const float nmu = nm == -INFINITY ? 0.f : nm;
       const float sc = exp2_fast(M - nmu);
       L *= sc;
@@ -2154,7 +2171,7 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
     }
   }
   const bool has = PRE || (seq_len > 0 && (!p.fuse || slot >= 0));
-  const float inv = (has && L > 0.f) ? 1.f / L : 0.f;
+  const float inv = (has && L > 0.f) ? rcp_fast(L) : 0.f;
   // OUTP: the output is [rows, D] in row order (its pointer preloaded), so
   // the store needs no output strides from the kernel-argument buffer
   T* dst = static_cast<T*>(p.out) + (OUTP ? row * D : b * p.os0 + qh * p.os1);
