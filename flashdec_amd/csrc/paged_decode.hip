@@ -2013,6 +2013,10 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
   const int lane = threadIdx.x & 63;
   const int wave = W > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
   constexpr int E = D / 64;  // dims per lane
+  // whole chunks at head_dim 128 into a row-order output: lane l holds dims
+  // 2l and 2l + 1 (one 8-byte load per split, one 4-byte store), else dims
+  // l + 64e
+  constexpr bool PAIR = FCH > 0 && OUTP && E == 2 && W == 1;
   // a VGPR zero keeps the uniform row-length / slot loads on the vector path
   int vzero = 0;
   asm volatile("" : "+v"(vzero));
@@ -2071,10 +2075,14 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
     for (int c0 = 0; c0 < n; c0 += CH) {
       float a[CH][E];
       // whole chunks of D-float rows: one base, constant offsets (immediates)
-      [[maybe_unused]] const float* cbase = ab + (s64 + c0) * D + lane;
+      [[maybe_unused]] const float* cbase = ab + (s64 + c0) * D + (PAIR ? 2 * lane : lane);
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        if constexpr (FULL) {
+        if constexpr (PAIR) {
+          const float2 v2 = *reinterpret_cast<const float2*>(cbase + j * D);
+          a[j][0] = v2.x;
+          a[j][1] = v2.y;
+        } else if constexpr (FULL) {
 #pragma unroll
           for (int e = 0; e < E; ++e) a[j][e] = cbase[j * D + 64 * e];
         } else {
@@ -2175,8 +2183,15 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
   // OUTP: the output is [rows, D] in row order (its pointer preloaded), so
   // the store needs no output strides from the kernel-argument buffer
   T* dst = static_cast<T*>(p.out) + (OUTP ? row * D : b * p.os0 + qh * p.os1);
+  if constexpr (PAIR) {
+    struct alignas(4) Two {
+      T x, y;
+    };
+    *reinterpret_cast<Two*>(dst + 2 * lane) = Two{from_f32<T>(o[0] * inv), from_f32<T>(o[1] * inv)};
+  } else {
 #pragma unroll
-  for (int e = 0; e < E; ++e) dst[(lane + 64 * e) * (OUTP ? 1 : p.os2)] = from_f32<T>(o[e] * inv);
+    for (int e = 0; e < E; ++e) dst[(lane + 64 * e) * (OUTP ? 1 : p.os2)] = from_f32<T>(o[e] * inv);
+  }
 }
 
 template <typename T, int D, int MODE = kReducePlain, int W = 1>
@@ -2520,7 +2535,8 @@ int launch_reduce(const fd_paged_decode_args& a, const ReduceParams& r, hipStrea
         outp ? pre(split_reduce_pre_kernel<T, 128, 4, true>, dim3(256))
              : pre(split_reduce_pre_kernel<T, 128, 4>, dim3(256));
     } else if (outp && r.as2 == a.head_dim && r.as1 == r.splits * a.head_dim && r.ss1 == r.splits &&
-               (r.splits == 2 || r.splits == 4 || r.splits == 8 || r.splits == 16 || r.splits == 32)) {
+               (r.splits == 2 || r.splits == 4 || r.splits == 8 || r.splits == 16 || r.splits == 32) &&
+               (reinterpret_cast<uintptr_t>(r.acc) & 7) == 0 && (reinterpret_cast<uintptr_t>(r.out) & 3) == 0) {
       // contiguous [rows, splits, D] partials with a power-of-two split count
       // (the library's own workspaces: C2 has 16, its ctx1024 companion 8):
       // every partial load is an immediate offset from one base, with no
