@@ -72,6 +72,42 @@ def test_output_view_out_of_row_order_takes_the_strided_store(d, record):
     assert torch.isnan(wide[..., d:]).all()  # nothing written past the view
 
 
+def test_misaligned_whole_chunk_views_take_the_general_merge_with_the_same_bits(record):
+    """The whole-chunk reducer at head_dim 128 loads 8 bytes per split and stores 4 bytes per
+    lane.  An output in row order that starts 2 bytes into its buffer, or a workspace that
+    starts 4 bytes into its buffer, takes the general row-order merge instead, and every
+    layout gives the aligned one's bits."""
+    from flashdec_amd import _lib
+    from flashdec_amd import paged_decode as pd
+
+    d = 128
+    q, k, v, table, sl = make_paged_inputs([2048, 900, 0, 1500], 16, 2, d, 32, seed=9)
+    splits = _lib.paged_decode_plan(4, 16, 2, d, 2048)
+    assert splits == 16
+    n_acc, n_st = 4 * 16 * splits * d, 4 * 16 * splits
+
+    def workspace(shift):
+        flat = torch.full((n_acc + 2 * n_st + shift,), float("nan"), device="cuda")
+        acc = flat[shift:shift + n_acc].view(4, 16, splits, d)
+        mx = flat[shift + n_acc:shift + n_acc + n_st].view(4, 16, splits)
+        sm = flat[shift + n_acc + n_st:shift + n_acc + 2 * n_st].view(4, 16, splits)
+        return acc, mx, sm
+
+    outs = {}
+    for name, out_shift, ws_shift in (("aligned", 0, 0), ("output", 1, 0), ("workspace", 0, 1)):
+        buf = torch.full((4 * 16 * d + out_shift,), float("nan"), device="cuda", dtype=q.dtype)
+        out = buf[out_shift:].view(4, 16, d)
+        ws = workspace(ws_shift)
+        pd._decode_with_workspace(q, k, v, table, sl, out, 1.0 / math.sqrt(d), 32, splits, ws, k.shape[0])
+        torch.cuda.synchronize()
+        fch = 16 if name == "aligned" else 0
+        assert record.last_launch()[1] == f"fd::split_reduce_pre_kernel<__bf16, {d}, 1, true, {fch}>", name
+        outs[name] = out.clone()
+    assert_close_to_oracle(outs["aligned"], _oracle(q, k, v, table, sl))
+    for name in ("output", "workspace"):
+        assert torch.equal(outs[name], outs["aligned"]), name
+
+
 @pytest.mark.parametrize(("hq", "d", "ncb"), [(16, 128, 1), (64, 128, 2), (40, 64, 2)])
 @pytest.mark.parametrize("kv_reuse", [False, True])
 def test_long_rows_16_token_units_and_column_blocks(hq, d, ncb, kv_reuse, record):
