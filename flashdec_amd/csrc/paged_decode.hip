@@ -1489,23 +1489,34 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
       qh = kvh * G + hh;
       head_ok = threadIdx.x < 16 * kDimThreads && hh < G;
     }
+    // every slot read issues before the first use: one LDS round trip after
+    // the barrier instead of one per dependent step
+    float mw[kWaves], lw[kWaves];
+    f32x4 aw0[kWaves];
+    [[maybe_unused]] f32x4 aw1[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = lds.m[w][h];
+      lw[w] = lds.l[w][h];
+      aw0[w] = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][kSpread * d0]);
+      if constexpr (kDpt == 8) aw1[w] = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds.m[w][h]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mw[w]);
     const float Mu = M == -INFINITY ? 0.f : M;
     float L = 0.f;
     float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float wt = exp2_fast(lds.m[w][h] - Mu);
-      L += wt * lds.l[w][h];
-      const f32x4 a0 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][kSpread * d0]);
+      const float wt = exp2_fast(mw[w] - Mu);
+      L += wt * lw[w];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] += wt * a0[j];
+      for (int j = 0; j < 4; ++j) o[j] += wt * aw0[w][j];
       if constexpr (kDpt == 8) {
-        const f32x4 a1 = *reinterpret_cast<const f32x4*>(&lds.acc[w][h][d0 + 4]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[4 + j] += wt * a1[j];
+        for (int j = 0; j < 4; ++j) o[4 + j] += wt * aw1[w][j];
       }
     }
     if (ROLE == Role::kRow && p.splits == 1) {
