@@ -1319,7 +1319,10 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
   // The split partial's address for this thread's merge row, computed while
   // the K/V loads are in flight (the empty asm keeps it here, not at the
   // stores, where it sat on the kernel's last chain)
-  [[maybe_unused]] float* pre_acc = nullptr;
+  // element offsets: the stores keep p.acc as their base, so they stay global
+  // stores (a pointer through the empty asm below lost its address space and
+  // stored through flat instructions: C2 7.55 -> 7.53 us with the offsets)
+  [[maybe_unused]] int64_t pre_ao = 0;
   [[maybe_unused]] int64_t pre_so = 0;
   // (one-unit waves only: with several units per wave the held address
   // costs the loop registers, C5 step 3.186 -> 3.213 ms)
@@ -1329,9 +1332,9 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     const int hE = (threadIdx.x / (D / kDptE)) & 15;
     const int dE = (threadIdx.x % (D / kDptE)) * kDptE;
     const int qhE = kvh * G + 16 * hb + hE;
-    pre_acc = p.acc + b * p.as0 + qhE * p.as1 + split * p.as2 + dE * p.as3;
+    pre_ao = b * p.as0 + qhE * p.as1 + split * p.as2 + dE * p.as3;
     pre_so = b * p.ss0 + qhE * p.ss1 + split * p.ss2;
-    asm volatile("" : "+v"(pre_acc), "+v"(pre_so));
+    asm volatile("" : "+v"(pre_ao), "+v"(pre_so));
   }
   // The loaded length stays in a VGPR until here (the empty asm redefines
   // it): its move to an SGPR, and the wait for the load it brings, would
@@ -1527,7 +1530,7 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     // role's partials follow the tail splits
     if (head_ok) {
       const int ws = PREFIX ? p.splits + split : split;
-      float* a = kPreStore ? pre_acc : p.acc + ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3;
+      float* a = p.acc + (kPreStore ? pre_ao : ob * p.as0 + qh * p.as1 + ws * p.as2 + d0 * p.as3);
       const int64_t so = kPreStore ? pre_so : ob * p.ss0 + qh * p.ss1 + ws * p.ss2;
       if constexpr (MERGE) {
         // device-coherent (sc1) stores, visible to every XCD once acknowledged;
