@@ -27,7 +27,7 @@ Timing:
   (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size), or null
   (also for any other shape than the headline one those counters were
   taken on).
-* ``ctx1024``: the same call at ctx1024 (BASELINE's C2 names both
+* ``ctx1024``: the same call at ctx1024 (the C2 config names both
   contexts), timed the same way on 48 pools of its own.
 * ``cpu_baseline``: the reference's CPU path as fp32 torch-CPU ops in its
   per-(sequence, query-head) loop (oracle/torch_loop.py) under
@@ -175,7 +175,7 @@ def cpu_model():
 def cpu_inputs(name):
     """Seeded numpy inputs of a CPU-baseline config (fp32 arrays, sm_scale, out_dtype, algorithmic bytes).
 
-    C1: B4 Hq8 Hkv2 D64 fp32, bs32, L ~ U{1..512} over a 128-block pool whose
+    C1 (the first benchmark config): B4 Hq8 Hkv2 D64 fp32, bs32, L ~ U{1..512} over a 128-block pool whose
     table rows are consecutive slices of a permutation, seed 61.  C2: B8 Hq16 Hkv2 D128, bs32, every
     length 2048, a 640-block pool (1.25x) with permuted tables, bf16 values (N(0,1) rounded to bf16)
     held in fp32 as the reference upcasts them, seed 20260830 + 8 + 2048.  C2-ctx1024: the same at
@@ -1627,7 +1627,7 @@ def main():
     log(f"[bench] attention kernel: mean {kernel_ms * 1e3:.2f} us, median {statistics.median(attn_ms) * 1e3:.2f} us"
         f"; reducer: mean {statistics.mean(red_ms) * 1e3:.2f} us ({n_calls} calls)")
 
-    # BASELINE's C2 names ctx1024 too: the same call on 48 pools at ctx1024,
+    # the C2 config names ctx1024 too: the same call on 48 pools at ctx1024,
     # timed the same way, rides along in the line
     companion = None
     if (batch, ctx) == (8, 2048):
