@@ -38,6 +38,23 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert isinstance(lib.fd_last_error(), bytes)
 
 
+def test_timeline_stamps_exist_in_the_measurement_build_only():
+    """The per-wave timeline stamps (``-DFD_TIMELINE``) are compiled into
+    ``libflashdec_timeline.so`` for bench.py's timeline workloads; the product
+    library exports no stamp buffer, and the measurement build exports the same
+    C ABI beside it."""
+    from flashdec_amd import _build
+
+    if not _lib.LIB_PATH.exists() or not _build.TIMELINE_LIB_PATH.exists():
+        pytest.fail("the libraries are not built; run __graft_entry__.build()")
+    product = ctypes.CDLL(str(_lib.LIB_PATH))
+    timeline = ctypes.CDLL(str(_build.TIMELINE_LIB_PATH))
+    assert not hasattr(product, "fd_timeline_buffer")
+    assert hasattr(timeline, "fd_timeline_buffer")
+    for name in declared_functions():
+        assert hasattr(timeline, name), name
+
+
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _lib.load_library()
     args = _lib.PagedDecodeArgs()
