@@ -611,6 +611,27 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // dependent instructions ahead of every output store.
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// w * l rounded on its own (the empty asm keeps it out of any fused
+// multiply-add): the terms of a merge's denominator
+__device__ __forceinline__ float merge_term(float w, float l) {
+  float t = w * l;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// The sum of 16 terms in the order a DPP row reduction gives its first lane
+// (rotations by 8, 4, 2, 1): ((x0+x8)+(x4+x12)) + ((x2+x10)+(x6+x14)) and the
+// same over the odd terms, then the two.  The in-launch merge sums its
+// per-thread terms this way so that it matches the reducer bit for bit.
+__device__ __forceinline__ float tree_sum16(const float (&x)[16]) {
+  float a[8], b[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = x[i] + x[i + 8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = a[i] + a[i + 4];
+  return (b[0] + b[2]) + (b[1] + b[3]);
+}
+
 // Online-softmax step over one unit's scores of a lane (base-2 domain): the
 // probabilities pr, and st updated for them.  The reference's kernels move
 // the running maximum to every new block maximum and rescale acc and l each
@@ -1635,18 +1656,19 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) cm = j < p.splits ? fmaxf(cm, pm[j]) : cm;
     const float nmu = cm == -INFINITY ? 0.f : cm;
-    float GLx = 0.f;
     float gx[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float tl[kMergeChunk];  // the denominator's terms, summed as the reducer sums them
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) {
       const float w = j < p.splits ? exp2_fast(pm[j] - nmu) : 0.f;
-      GLx += w * pl[j];
+      tl[j] = j < p.splits ? merge_term(w, pl[j]) : 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         gx[k] += w * part[j][0][k];
         gx[4 + k] += w * part[j][1][k];
       }
     }
+    const float GLx = __builtin_fmaf(0.f, 0.f, tree_sum16(tl));
     const float inv = GLx > 0.f ? rcp_fast(GLx) : 0.f;
     T* dst = static_cast<T*>(p.out) + b * p.os0 + qq * p.os1 + dd * p.os2;
     if (p.os2 == 1 && dpt == 8) {
@@ -1704,19 +1726,20 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
     const float nm = fmaxf(GM, cm);
     const float nmu = nm == -INFINITY ? 0.f : nm;
     const float sc = exp2_fast(GM - nmu);
-    GL *= sc;
 #pragma unroll
     for (int j = 0; j < 8; ++j) go[j] *= sc;
+    float tl[kMergeChunk];  // the denominator's terms, summed as the reducer sums them
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) {
       const float w = s0 + j < p.splits ? exp2_fast(pm[j] - nmu) : 0.f;
-      GL += w * pl[j];
+      tl[j] = s0 + j < p.splits ? merge_term(w, pl[j]) : 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         go[2 * k] += w * __builtin_bit_cast(float, static_cast<uint32_t>(raw[j][k]));
         go[2 * k + 1] += w * __builtin_bit_cast(float, static_cast<uint32_t>(raw[j][k] >> 32));
       }
     }
+    GL = __builtin_fmaf(GL, sc, tree_sum16(tl));
     GM = nm;
   }
   if (head_ok) store_row<T>(p, b, qh, d0, go, GL > 0.f ? rcp_fast(GL) : 0.f);
@@ -2009,6 +2032,17 @@ __device__ __forceinline__ float lane_bcast(float x, int lane_idx) {
 // Maximum over the wave, every lane receiving it: rotations within each
 // 16-lane row (DPP row_ror), then across the rows (permlane swaps).
 __device__ __forceinline__ float dpp_row_ror_max(float x, int y) { return fmaxf(x, __builtin_bit_cast(float, y)); }
+// Sum within each 16-lane row; the row's first lane holds it in the order of
+// tree_sum16 (the other lanes hold the same terms in other orders)
+__device__ __forceinline__ float dpp_row_ror_add(float x, int y) { return x + __builtin_bit_cast(float, y); }
+__device__ __forceinline__ float row_sum_f32(float x) {
+  x = dpp_row_ror_add(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+  x = dpp_row_ror_add(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+  x = dpp_row_ror_add(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+  x = dpp_row_ror_add(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+  return x;
+}
+
 // Maximum within each 16-lane row (every lane of the row receiving it)
 __device__ __forceinline__ float row_max_f32(float x) {
   x = dpp_row_ror_max(x, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
@@ -2108,14 +2142,17 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
   const int per = (splits + W - 1) / W;  // this wave's splits: [s_lo, s_hi)
   const int s_lo = wave * per;
   const int s_hi = min(splits, s_lo + per);
-  for (int s64 = s_lo; s64 < s_hi; s64 += 64) {
-    const int n = min(64, s_hi - s64);  // splits of this pass, one per lane
+  // a whole chunk is one pass of one chunk: its loop bounds are compile-time
+  // (split indices are immediates, not additions to a loop counter)
+  constexpr bool kOnePass = FCH > 0;
+  for (int s64 = s_lo; kOnePass ? s64 < 1 : s64 < s_hi; s64 += 64) {
+    const int n = kOnePass ? FCH : min(64, s_hi - s64);  // splits of this pass, one per lane
     const int sj = s64 + min(lane, n - 1);
     const float lm = p.mx[sb + sj * ss2];
     const float ll = p.sm[sb + sj * ss2];
     constexpr bool FULL = FCH > 0;
     constexpr int CH = FULL ? FCH : kReduceChunk;
-    for (int c0 = 0; c0 < n; c0 += CH) {
+    for (int c0 = 0; kOnePass ? c0 < 1 : c0 < n; c0 += CH) {
       float a[CH][E];
       // whole chunks of D-float rows: one base, constant offsets (immediates)
       [[maybe_unused]] const float* cbase = ab + (s64 + c0) * D + (PAIR ? 2 * lane : lane);
@@ -2161,17 +2198,25 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
       const float nm = fmaxf(M, FULL && FCH <= 16 ? row_max_f32(cmx) : wave_max_f32(cmx));
       const float nmu = nm == -INFINITY ? 0.f : nm;
       const float sc = exp2_fast(M - nmu);
-      L *= sc;
+      if constexpr (MODE == kReduceCascade) L *= sc;
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] *= sc;
       const float wl = exp2_fast(lmv - nmu);
+      if constexpr (MODE != kReduceCascade) {
+        // the chunk's denominator: each lane's term w * l, summed over the
+        // chunk's DPP row (two rows for a whole chunk of 32) instead of one
+        // broadcast and fused multiply-add per split
+        const float rs = row_sum_f32(mine ? merge_term(wl, llv) : 0.f);
+        const float lc = CH > 16 ? lane_bcast(rs, c0) + lane_bcast(rs, c0 + 16) : lane_bcast(rs, c0);
+        L = __builtin_fmaf(L, sc, lc);
+      }
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
         const int src = FULL ? c0 + j : min(c0 + j, n - 1);
-        const float lj = lane_bcast(llv, src);
         const bool use = FULL || (c0 + j < n && s64 + c0 + j < valid);
         if constexpr (MODE == kReduceCascade) {
           // masked splits may hold stale or NaN partials: selected away, not weighted by 0
+          const float lj = lane_bcast(llv, src);
           const float w = lane_bcast(wl, src);
           L += use ? w * lj : 0.f;
 #pragma unroll
@@ -2186,7 +2231,6 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
           // the chunk's partial loads below the statistics' wait
           const float wb = lane_bcast(wl, src);
           const float w = use ? wb : 0.f;
-          L += w * lj;
 #pragma unroll
           for (int e = 0; e < E; ++e) o[e] += w * a[j][e];
         }
