@@ -2198,14 +2198,15 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
       const float nm = fmaxf(M, FULL && FCH <= 16 ? row_max_f32(cmx) : wave_max_f32(cmx));
       const float nmu = nm == -INFINITY ? 0.f : nm;
       const float sc = exp2_fast(M - nmu);
-      if constexpr (MODE == kReduceCascade) L *= sc;
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] *= sc;
       const float wl = exp2_fast(lmv - nmu);
-      if constexpr (MODE != kReduceCascade) {
-        // the chunk's denominator: each lane's term w * l, summed over the
-        // chunk's DPP row (two rows for a whole chunk of 32) instead of one
-        // broadcast and fused multiply-add per split
+      {
+        // the chunk's denominator: each lane's term w * l (zero for a lane
+        // outside the chunk or past the row's valid splits, whatever its
+        // slot holds), summed over the chunk's DPP row (two rows for a whole
+        // chunk of 32) instead of one broadcast and fused multiply-add per
+        // split
         const float rs = row_sum_f32(mine ? merge_term(wl, llv) : 0.f);
         const float lc = CH > 16 ? lane_bcast(rs, c0) + lane_bcast(rs, c0 + 16) : lane_bcast(rs, c0);
         L = __builtin_fmaf(L, sc, lc);
@@ -2216,9 +2217,7 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
         const bool use = FULL || (c0 + j < n && s64 + c0 + j < valid);
         if constexpr (MODE == kReduceCascade) {
           // masked splits may hold stale or NaN partials: selected away, not weighted by 0
-          const float lj = lane_bcast(llv, src);
           const float w = lane_bcast(wl, src);
-          L += use ? w * lj : 0.f;
 #pragma unroll
           for (int e = 0; e < E; ++e) o[e] += use ? w * a[j][e] : 0.f;
         } else {
