@@ -612,7 +612,10 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
 // w * l rounded on its own (the empty asm keeps it out of any fused
-// multiply-add): the terms of a merge's denominator
+// multiply-add): the terms of a merge's denominator.  Callers form it
+// unconditionally and select the result: the compiler does not speculate the
+// asm, so under a uniform test it became a branch per term, and the in-launch
+// merge spilled its running sums around each one.
 __device__ __forceinline__ float merge_term(float w, float l) {
   float t = w * l;
   asm volatile("" : "+v"(t));
@@ -1661,7 +1664,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) {
       const float w = j < p.splits ? exp2_fast(pm[j] - nmu) : 0.f;
-      tl[j] = j < p.splits ? merge_term(w, pl[j]) : 0.f;
+      const float t = merge_term(w, pl[j]);
+      tl[j] = j < p.splits ? t : 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         gx[k] += w * part[j][0][k];
@@ -1732,7 +1736,8 @@ __device__ __forceinline__ void decode_role(const DecodeParams& p, const Cascade
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) {
       const float w = s0 + j < p.splits ? exp2_fast(pm[j] - nmu) : 0.f;
-      tl[j] = s0 + j < p.splits ? merge_term(w, pl[j]) : 0.f;
+      const float t = merge_term(w, pl[j]);
+      tl[j] = s0 + j < p.splits ? t : 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         go[2 * k] += w * __builtin_bit_cast(float, static_cast<uint32_t>(raw[j][k]));
@@ -2207,7 +2212,8 @@ __device__ __forceinline__ void reduce_row(const ReduceParams& p, const int row 
         // slot holds), summed over the chunk's DPP row (two rows for a whole
         // chunk of 32) instead of one broadcast and fused multiply-add per
         // split
-        const float rs = row_sum_f32(mine ? merge_term(wl, llv) : 0.f);
+        const float t = merge_term(wl, llv);
+        const float rs = row_sum_f32(mine ? t : 0.f);
         const float lc = CH > 16 ? lane_bcast(rs, c0) + lane_bcast(rs, c0 + 16) : lane_bcast(rs, c0);
         L = __builtin_fmaf(L, sc, lc);
       }
