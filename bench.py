@@ -83,7 +83,8 @@ def parse_args():
                    help="run N eager calls plus a 64 MiB copy (for rocprofv3) and exit")
     p.add_argument("--workload", choices=("decode", "c2-floor", "c2-timeline", "c4-timeline", "rope", "ragged", "prefix",
                                           "prefix-large",
-                                          "prefix-sweep", "engine", "engine-prefix", "formats", "vllm"),
+                                          "prefix-sweep", "engine", "engine-prefix", "formats", "vllm",
+                                          "ref-shapes"),
                    default="decode",
                    help="decode: the headline C2 call (default); c2-floor: the C2 call beside a bare read of "
                         "its bytes and a dependent empty launch (the floor of a call of that size); c2-timeline / "
@@ -94,7 +95,8 @@ def parse_args():
                         "shared-prefix sizes; engine: C5 36-layer step; engine-prefix: 36-layer steps "
                         "of 64 rows sharing a 16384-token prefix; formats: head_dim 64, large groups, MHA, "
                         "dim-major caches and 8-token blocks; vllm: the vLLM hook's launch at B8 ctx1024/2048, "
-                        "block size 16, fused append")
+                        "block size 16, fused append; ref-shapes: the reference's own published benchmark "
+                        "rows (Hq32/Hkv8 grouped decode, small vLLM shapes, the RoPE + append call)")
     p.add_argument("--engine-steps", type=int, default=200, help="timed steps of the engine workload")
     return p.parse_args()
 
@@ -525,8 +527,10 @@ def ragged_lengths(n, seed):
     return [int(round(math.exp(x))) for x in rng.uniform(math.log(128), math.log(32768), size=n)]
 
 
-def decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks=0):
-    """Independent (q, k, v, table, lens, out) sets; the first ``prefix_blocks`` of every row are shared."""
+def decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks=0, dtype=None):
+    """Independent (q, k, v, table, lens, out) sets; the first ``prefix_blocks`` of every row are shared.
+    bf16 unless ``dtype`` names another cache dtype."""
+    dtype = torch.bfloat16 if dtype is None else dtype
     nblk = [(n + bs - 1) // bs for n in lens]
     private = [max(0, b - prefix_blocks) for b in nblk]
     pool_blocks = int(math.ceil((prefix_blocks + sum(private)) * 1.25)) + 1
@@ -535,9 +539,9 @@ def decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, seed, prefix_blocks=
     gen = torch.Generator(device=dev)
     for i in range(n_pools):
         gen.manual_seed(seed + i)
-        k = torch.empty((pool_blocks, hkv, bs, d), device=dev, dtype=torch.bfloat16).normal_(generator=gen)
+        k = torch.empty((pool_blocks, hkv, bs, d), device=dev, dtype=dtype).normal_(generator=gen)
         v = torch.empty_like(k).normal_(generator=gen)
-        q = torch.randn((len(lens), hq, d), device=dev, generator=gen).to(torch.bfloat16)
+        q = torch.randn((len(lens), hq, d), device=dev, generator=gen).to(dtype)
         perm = torch.randperm(pool_blocks, device=dev, generator=gen).to(torch.int32)
         table = torch.full((len(lens), width), -1, device=dev, dtype=torch.int32)
         shared = perm[:prefix_blocks]
@@ -1168,55 +1172,226 @@ def run_formats(torch, dev, args):
     return out
 
 
+def vllm_hook_call(torch, dev, batch, ctx, n_pools, seed, hq=16, hkv=2, d=128, bs=16):
+    """``fn(i)``: the vLLM CUSTOM hook's launch on pool ``i % n_pools`` -- vLLM's 5-D NHD cache
+    ``[blocks, 2, bs, kv_heads, d]``, every row at ``ctx`` tokens with its current token appended in
+    the launch (slot of position ctx - 1), the split count as the hook picks it.  Returns
+    (fn, splits, pools)."""
+    import flashdec_amd  # noqa: F401  (loads the library)
+    from flashdec_amd.paged_decode import _vllm_paged_decode_attention_into
+    from flashdec_amd.vllm_splits import _AUTO_MIN_SPLIT_TOKENS, _select_num_splits
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    pools = []
+    for q, k, v, table, sl, o in decode_pools(torch, dev, [ctx] * batch, hq, hkv, d, bs, n_pools, seed):
+        kv = torch.empty((k.shape[0], 2, bs, hkv, d), device=dev, dtype=k.dtype)
+        kv[:, 0].copy_(k.permute(0, 2, 1, 3))
+        kv[:, 1].copy_(v.permute(0, 2, 1, 3))
+        del k, v
+        pos = sl.long() - 1
+        slots = table.long().gather(1, (pos // bs).unsqueeze(1)).squeeze(1) * bs + pos % bs
+        ak = torch.randn((batch, hkv, d), device=dev).to(kv.dtype)
+        av = torch.randn((batch, hkv, d), device=dev).to(kv.dtype)
+        pools.append((q, ak, av, kv, table, sl, o, slots))
+    splits = _select_num_splits(0, num_reqs=batch, num_kv_heads=hkv, logical_blocks=-(-ctx // bs),
+                                target_programs=cus, auto_min_tokens=_AUTO_MIN_SPLIT_TOKENS, block_size=bs)
+    ws = (torch.empty((batch, hq, splits, d), device=dev), torch.empty((batch, hq, splits), device=dev),
+          torch.empty((batch, hq, splits), device=dev))
+
+    def fn(i):
+        q, ak, av, kv, table, sl, o, slots = pools[i % len(pools)]
+        _vllm_paged_decode_attention_into(q, ak, av, kv, table, sl, o, slots, *ws, num_reqs=batch,
+                                          num_q_heads=hq, num_kv_heads=hkv, head_dim=d, block_size=bs,
+                                          sm_scale=d ** -0.5, num_splits=splits, max_seq_len=ctx)
+
+    return fn, splits, pools
+
+
 def run_vllm(torch, dev, args):
     """The vLLM CUSTOM hook's launch at the reference's published vLLM shapes: B8, Hq16/Hkv2/D128
     bf16, block size 16, vLLM's 5-D NHD cache ``[blocks, 2, 16, kv_heads, 128]``, every row at
     ctx 1024 or 2048 with its current token appended in the launch (slot of position len - 1),
     splits as the hook picks them (power of two nearest one workgroup per CU, >= 128 tokens each).
     8 rotating pools."""
-    import flashdec_amd  # noqa: F401  (loads the library)
-    from flashdec_amd.paged_decode import _vllm_paged_decode_attention_into
-    from flashdec_amd.vllm_splits import _AUTO_MIN_SPLIT_TOKENS, _select_num_splits
-
     hq, hkv, d, bs, batch = 16, 2, 128, 16, 8
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     lines = []
     for ctx in (1024, 2048):
-        lens = [ctx] * batch
-        pools = []
-        for q, k, v, table, sl, o in decode_pools(torch, dev, lens, hq, hkv, d, bs, 8, 41 + ctx):
-            kv = torch.empty((k.shape[0], 2, bs, hkv, d), device=dev, dtype=k.dtype)
-            kv[:, 0].copy_(k.permute(0, 2, 1, 3))
-            kv[:, 1].copy_(v.permute(0, 2, 1, 3))
-            del k, v
-            pos = sl.long() - 1
-            slots = table.long().gather(1, (pos // bs).unsqueeze(1)).squeeze(1) * bs + pos % bs
-            ak = torch.randn((batch, hkv, d), device=dev).to(kv.dtype)
-            av = torch.randn((batch, hkv, d), device=dev).to(kv.dtype)
-            pools.append((q, ak, av, kv, table, sl, o, slots))
-        splits = _select_num_splits(0, num_reqs=batch, num_kv_heads=hkv, logical_blocks=ctx // bs,
-                                    target_programs=cus, auto_min_tokens=_AUTO_MIN_SPLIT_TOKENS, block_size=bs)
-        ws = (torch.empty((batch, hq, splits, d), device=dev), torch.empty((batch, hq, splits), device=dev),
-              torch.empty((batch, hq, splits), device=dev))
-
-        def fn(i, pools=pools, ws=ws, splits=splits, ctx=ctx):
-            q, ak, av, kv, table, sl, o, slots = pools[i % len(pools)]
-            _vllm_paged_decode_attention_into(q, ak, av, kv, table, sl, o, slots, *ws, num_reqs=batch,
-                                              num_q_heads=hq, num_kv_heads=hkv, head_dim=d, block_size=bs,
-                                              sm_scale=d ** -0.5, num_splits=splits, max_seq_len=ctx)
-
+        fn, splits, _ = vllm_hook_call(torch, dev, batch, ctx, 8, 41 + ctx)
         ms = graph_ms_per_call(torch, dev, fn, args.steps)
         algo = batch * ctx * hkv * d * 2 * 2 + 2 * batch * hq * d * 2 + 4 * batch * (ctx // bs) + 4 * batch
         log(f"[bench] vllm B8 ctx{ctx} bs16 fused append: {ms * 1e3:.2f} us/call, splits {splits}, "
             f"{algo / (ms * 1e-3) / 1e9:.1f} GB/s")
         lines.append({"ctx": ctx, "us_per_call": round(ms * 1e3, 2), "num_splits": splits,
                       "algorithmic_bytes": algo, "gb_per_s": round(algo / (ms * 1e-3) / 1e9, 1)})
-        del pools
+        del fn
     out = common_fields(args, "vLLM CUSTOM hook decode us/call, B8 Hq16/Hkv2/D128 bf16 bs16 fused append",
                         lines[1]["us_per_call"], "us", lines[1]["us_per_call"] * 1e-3, False,
                         {"workload": "vllm-hook-b8-bs16-fused-append", "block_size": bs})
     out["cases"] = lines
     return out
+
+
+# The reference's published p50s (ms, one RTX 5070, CUDA events around each eager call) for the
+# rows the ref-shapes workload repeats.  FlashDec's own column of each summary.
+REF_GROUPED_MS = {  # benchmarks/results/flashinfer_paged_decode_baseline_summary.md:24-39, full-length rows
+    (1, 128): {"float16": 0.015616, "bfloat16": 0.016096},
+    (16, 1024): {"float16": 0.176128, "bfloat16": 0.181664},
+    (16, 8192): {"float16": 1.014976, "bfloat16": 1.050496},
+    (64, 4096): {"float16": 2.562368, "bfloat16": 2.606080},
+}
+REF_DEFAULT_MS = {  # benchmarks/results/paged_decode_default_profile_summary.md:16-23, lengths ~ U{L/2..L}
+    (1, 128): {"float16": 0.015328, "bfloat16": 0.038176},
+    (16, 1024): {"float16": 0.155520, "bfloat16": 0.160864},
+    (16, 8192): {"float16": 0.884576, "bfloat16": 0.928064},
+    (64, 4096): {"float16": 1.934560, "bfloat16": 1.961216},
+}
+REF_VLLM_MS = {  # benchmarks/results/vllm_qwen_attention_summary.md:20-24
+    (1, 128): 0.009952, (1, 1024): 0.013792, (4, 1024): 0.017888, (8, 1024): 0.024192, (8, 2048): 0.038528,
+}
+REF_ROPE_APPEND_MS = {  # benchmarks/results/rope_kv_append_backends_summary.md:36-41, fused_cuda column
+    "default": (16, 1024, {"float16": 1.436736, "bfloat16": 1.447424}),
+    "large_batch": (64, 1024, {"float16": 3.419392, "bfloat16": 2.448480}),
+    "long_context": (16, 4096, {"float16": 1.465536, "bfloat16": 1.076192}),
+}
+
+
+def event_p50_ms(torch, fn, warmup=20, repeat=100):
+    """p50 ms of ``fn()`` timed as the reference times its rows: HIP events recorded around each
+    eager call, a synchronisation after each (flashdec/benchmark.py:149-173)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeat):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    return statistics.median(times)
+
+
+def flushed_p50_ms(torch, dev, fn, reps=200, warmup=25):
+    """p50 ms of ``fn()`` timed as the reference times its vLLM rows with Triton's do_bench
+    (benchmarks/run_vllm_attention_microbench.py:230-241; Triton 3.6, not importable here): before
+    each call a large buffer is zeroed so that the call starts with cold caches (Triton clears 256 MB;
+    512 MiB here, more than MI355X's 256 MB Infinity Cache), HIP events record around each call, and
+    the host does not wait between calls, so the launch's host work overlaps the clear."""
+    flush = torch.empty(512 * 2**20 // 4, dtype=torch.int32, device=dev)
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        flush.zero_()
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
+def run_ref_shapes(torch, dev, args):
+    """The reference's own published benchmark rows, repeated on MI355X with this library.
+
+    - grouped decode, Hq32/Hkv8/D128, block size 32, token-major, fp16 and bf16, through
+      ``paged_decode_attention_into`` (library-planned splits): every row at its full length (the
+      FlashInfer-baseline rows) and lengths ~ U{L/2..L} (the default-configuration profile);
+    - the vLLM hook's launch at the small Qwen shapes (B1 ctx128, B1 ctx1024, B4 ctx1024; block 16,
+      fused current-token append) beside the B8 rows;
+    - the whole ``rope_paged_kv_append(..., append_backend="fused_cuda")`` call (Hq32/Hkv8/D128,
+      block 32, base 10000) on a one-layer cache seeded with the row's context, one token per call.
+    Every row is timed with the reference's method for it: events around each eager call with a
+    synchronisation after each, p50 of 100 after 20 warm-ups (``event_p50_us``: the grouped,
+    default-profile and RoPE + append rows), or Triton's do_bench (``flushed_p50_us``: the vLLM
+    rows).  The decode and vLLM rows carry both, and the headline's method beside them (p50 of
+    graph replays over rotating pools that together exceed the 256 MB Infinity Cache where the
+    shape allows)."""
+    import numpy as np
+    import flashdec_amd as fd
+    from flashdec_amd.cache import PagedKVCache
+    from flashdec_amd.rope import rope_paged_kv_append
+
+    hq, hkv, d, bs = 32, 8, 128, 32
+    dtypes = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+    rows = []
+    for kind, table in (("full", REF_GROUPED_MS), ("default", REF_DEFAULT_MS)):
+        for (batch, ctx), ref in table.items():
+            if kind == "full":
+                lens = [ctx] * batch
+            else:
+                rng = np.random.default_rng(1000 + batch + ctx)
+                lens = [int(x) for x in rng.integers(max(1, ctx // 2), ctx + 1, size=batch)]
+            kv_bytes = sum(lens) * hkv * d * 2 * 2
+            n_pools = max(3, min(48, -(-640 * 2**20 // kv_bytes)))
+            algo = kv_bytes + 2 * batch * hq * d * 2 + 4 * batch * (-(-ctx // bs)) + 4 * batch
+            for dname, dt in dtypes.items():
+                pools = decode_pools(torch, dev, lens, hq, hkv, d, bs, n_pools, 77 + batch + ctx, dtype=dt)
+
+                def fn(i, pools=pools):
+                    q, k, v, tab, sl, o = pools[i % len(pools)]
+                    fd.paged_decode_attention_into(q, k, v, tab, sl, o, sm_scale=d ** -0.5)
+
+                counter = iter(range(10**9))
+                ev_ms = event_p50_ms(torch, lambda: fn(next(counter)))
+                fl_ms = flushed_p50_ms(torch, dev, lambda: fn(next(counter)))
+                graph_us = graph_p50_us(torch, dev, fn, n_pools, samples=120, warmup=24)
+                line = {"rows": kind, "batch": batch, "ctx": ctx, "dtype": dname, "pools": n_pools,
+                        "event_p50_us": round(ev_ms * 1e3, 2), "flushed_p50_us": round(fl_ms * 1e3, 2),
+                        "graph_p50_us": round(graph_us, 2),
+                        "algorithmic_bytes": algo, "graph_gb_per_s": round(algo / (graph_us * 1e-6) / 1e9, 1),
+                        "reference_rtx5070_us": round(ref[dname] * 1e3, 2),
+                        "speedup_event": round(ref[dname] * 1e3 / (ev_ms * 1e3), 2)}
+                rows.append(line)
+                log(f"[bench] ref-shapes decode {kind} B{batch} ctx{ctx} {dname}: event p50 {ev_ms * 1e3:.2f} us, "
+                    f"flushed p50 {fl_ms * 1e3:.2f} us, graph p50 {graph_us:.2f} us ({line['graph_gb_per_s']} GB/s); reference "
+                    f"{ref[dname] * 1e3:.2f} us on RTX 5070")
+                del pools, fn
+                torch.cuda.empty_cache()
+    for (batch, ctx), ref in REF_VLLM_MS.items():
+        fn, splits, pools = vllm_hook_call(torch, dev, batch, ctx, 8, 51 + batch + ctx)
+        counter = iter(range(10**9))
+        ev_ms = event_p50_ms(torch, lambda: fn(next(counter)))
+        fl_ms = flushed_p50_ms(torch, dev, lambda: fn(next(counter)))
+        graph_us = graph_p50_us(torch, dev, fn, len(pools), samples=120, warmup=24)
+        rows.append({"rows": "vllm-hook", "batch": batch, "ctx": ctx, "dtype": "bfloat16", "num_splits": splits,
+                     "event_p50_us": round(ev_ms * 1e3, 2), "flushed_p50_us": round(fl_ms * 1e3, 2),
+                     "graph_p50_us": round(graph_us, 2), "reference_rtx5070_us": round(ref * 1e3, 2),
+                     "speedup_flushed": round(ref / fl_ms, 2)})
+        log(f"[bench] ref-shapes vllm hook B{batch} ctx{ctx}: event p50 {ev_ms * 1e3:.2f} us, flushed p50 "
+            f"{fl_ms * 1e3:.2f} us, graph p50 {graph_us:.2f} us; reference {ref * 1e3:.2f} us on RTX 5070 (do_bench)")
+        del fn, pools
+    for name, (batch, ctx, ref) in REF_ROPE_APPEND_MS.items():
+        for dname, dt in dtypes.items():
+            steps = 20 + 100 + 1
+            blocks = batch * (-(-(ctx + steps) // bs)) + 8
+            cache = PagedKVCache(1, hkv, d, bs, blocks, dtype=dt, device=dev)
+            ids = list(range(batch))
+            for r in ids:
+                cache.add_request(r)
+            cache.seed_context(ids, ctx)
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(91 + batch + ctx)
+            q = torch.randn((batch, hq, d), device=dev, generator=gen).to(dt)
+            k = torch.randn((batch, hkv, d), device=dev, generator=gen).to(dt)
+            v = torch.randn((batch, hkv, d), device=dev, generator=gen).to(dt)
+            ev_ms = event_p50_ms(torch, lambda: rope_paged_kv_append(cache, 0, ids, q, k, v,
+                                                                      append_backend="fused_cuda"))
+            rows.append({"rows": "rope-append", "case": name, "batch": batch, "ctx": ctx, "dtype": dname,
+                         "event_p50_us": round(ev_ms * 1e3, 2), "reference_rtx5070_us": round(ref[dname] * 1e3, 2),
+                         "speedup_event": round(ref[dname] / ev_ms, 2)})
+            log(f"[bench] ref-shapes rope_paged_kv_append fused {name} B{batch} ctx{ctx} {dname}: event p50 "
+                f"{ev_ms * 1e3:.2f} us; reference {ref[dname] * 1e3:.2f} us on RTX 5070")
+            del cache
+    head = next(r for r in rows if r["rows"] == "full" and r["batch"] == 16 and r["ctx"] == 8192
+                and r["dtype"] == "bfloat16")
+    out = common_fields(args, "reference benchmark rows on MI355X: grouped decode B16 ctx8192 Hq32/Hkv8/D128 bf16 "
+                        "(us/call, reference timing method)", head["event_p50_us"], "us",
+                        head["event_p50_us"] * 1e-3, False, {"workload": "reference-benchmark-rows"})
+    out["rows"] = rows
+    return out
+
 
 
 def run_engine_prefix(torch, dev, args):
@@ -1537,7 +1712,7 @@ def main():
     if args.workload != "decode":
         run = {"c2-floor": run_c2_floor, "c2-timeline": run_c2_timeline, "c4-timeline": run_c4_timeline, "rope": run_rope, "ragged": run_ragged, "prefix": run_prefix, "prefix-large": run_prefix_large,
                "prefix-sweep": run_prefix_sweep, "engine": run_engine, "engine-prefix": run_engine_prefix, "formats": run_formats,
-               "vllm": run_vllm}[args.workload]
+               "vllm": run_vllm, "ref-shapes": run_ref_shapes}[args.workload]
         print(json.dumps(run(torch, dev, args)), flush=True)
         return
     batch, ctx, hq, hkv, d, bs = args.batch, args.ctx, 16, 2, 128, 32
