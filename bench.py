@@ -1248,6 +1248,9 @@ REF_DEFAULT_MS = {  # benchmarks/results/paged_decode_default_profile_summary.md
 REF_VLLM_MS = {  # benchmarks/results/vllm_qwen_attention_summary.md:20-24
     (1, 128): 0.009952, (1, 1024): 0.013792, (4, 1024): 0.017888, (8, 1024): 0.024192, (8, 2048): 0.038528,
 }
+# benchmarks/results/multi_layer_transaction_summary.md:57: bf16 l2_b16_c1024, fused_cuda append and
+# Triton decode -- the token's wall-clock p50, and its decode's device time per layer
+REF_TOKEN_MS = {"token": 3.407861, "decode_layer": 0.133703}
 REF_ROPE_APPEND_MS = {  # benchmarks/results/rope_kv_append_backends_summary.md:36-41, fused_cuda column
     "default": (16, 1024, {"float16": 1.436736, "bfloat16": 1.447424}),
     "large_batch": (64, 1024, {"float16": 3.419392, "bfloat16": 2.448480}),
@@ -1301,7 +1304,9 @@ def run_ref_shapes(torch, dev, args):
     - the vLLM hook's launch at the small Qwen shapes (B1 ctx128, B1 ctx1024, B4 ctx1024; block 16,
       fused current-token append) beside the B8 rows;
     - the whole ``rope_paged_kv_append(..., append_backend="fused_cuda")`` call (Hq32/Hkv8/D128,
-      block 32, base 10000) on a one-layer cache seeded with the row's context, one token per call.
+      block 32, base 10000) on a one-layer cache seeded with the row's context, one token per call;
+    - the multi-layer transaction token: a 2-layer ``DecodeEngine`` step at B16 ctx1024 (wall-clock
+      p50 per token, synchronised around each).
     Every row is timed with the reference's method for it: events around each eager call with a
     synchronisation after each, p50 of 100 after 20 warm-ups (``event_p50_us``: the grouped,
     default-profile and RoPE + append rows), or Triton's do_bench (``flushed_p50_us``: the vLLM
@@ -1384,6 +1389,52 @@ def run_ref_shapes(torch, dev, args):
             log(f"[bench] ref-shapes rope_paged_kv_append fused {name} B{batch} ctx{ctx} {dname}: event p50 "
                 f"{ev_ms * 1e3:.2f} us; reference {ref[dname] * 1e3:.2f} us on RTX 5070")
             del cache
+    # The multi-layer transaction token (benchmarks/run_multi_layer_engine.py:100-230): a 2-layer
+    # engine, B16 with 1024 tokens of seeded context, Hq32/Hkv8/D128 bf16; one token = begin_step,
+    # step_layer per layer (fused RoPE + append, then decode), commit_step, synchronised before and
+    # after; wall-clock p50 over 100 tokens after 10, and the decode launches' device time per layer
+    # (the library's timing hook) beside it.
+    from flashdec_amd.engine import DecodeEngine
+
+    layers, batch, ctx, warm, steps = 2, 16, 1024, 10, 100
+    cache = PagedKVCache(layers, hkv, d, bs, batch * (-(-(ctx + warm + steps + 1) // bs)) + 8,
+                         dtype=torch.bfloat16, device=dev)
+    engine = DecodeEngine(cache, append_backend="fused_cuda", decode_backend="triton")
+    ids = list(range(batch))
+    for r in ids:
+        engine.add_request(r)
+    engine.admit()
+    cache.seed_context(ids, ctx)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    inputs = [[tuple(torch.randn(shape, device=dev, generator=gen).to(torch.bfloat16)
+                     for shape in ((batch, hq, d), (batch, hkv, d), (batch, hkv, d))) for _ in range(layers)]
+              for _ in range(8)]
+    wall = []
+    for s in range(warm + steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tx = engine.begin_step(ids)
+        for layer in range(layers):
+            engine.step_layer(tx, layer, *inputs[s % len(inputs)][layer])
+        engine.commit_step(tx)
+        torch.cuda.synchronize()
+        wall.append((time.perf_counter() - t0) * 1e3)
+    token_ms = statistics.median(wall[warm:])
+    # the decode launch of one such layer, timed through the library's hook around exactly its kernels
+    tq, tk, tv = inputs[0][0]
+    pool = (tq, cache.k_cache[0], cache.v_cache[0], cache.block_tables(ids).to(dev),
+            cache.seq_lens_tensor(ids).to(dev), torch.empty_like(tq))
+    attn_us, red_us = attention_kernel_us(torch, [prepared_args(pool, d ** -0.5, bs, hkv)], 100)
+    rows.append({"rows": "multi-layer-token", "layers": layers, "batch": batch, "ctx": ctx, "dtype": "bfloat16",
+                 "wall_p50_ms": round(token_ms, 4), "decode_kernels_us_per_layer": round(attn_us + red_us, 2),
+                 "reference_rtx5070_token_ms": REF_TOKEN_MS["token"],
+                 "reference_rtx5070_decode_device_ms_per_layer": REF_TOKEN_MS["decode_layer"],
+                 "speedup_token": round(REF_TOKEN_MS["token"] / token_ms, 2)})
+    log(f"[bench] ref-shapes multi-layer token L{layers} B{batch} ctx{ctx} bf16: wall p50 {token_ms:.3f} ms/token, "
+        f"decode kernels {attn_us + red_us:.1f} us/layer; reference {REF_TOKEN_MS['token']:.3f} ms/token, decode "
+        f"{REF_TOKEN_MS['decode_layer'] * 1e3:.1f} us/layer on RTX 5070")
+    del engine, cache
     head = next(r for r in rows if r["rows"] == "full" and r["batch"] == 16 and r["ctx"] == 8192
                 and r["dtype"] == "bfloat16")
     out = common_fields(args, "reference benchmark rows on MI355X: grouped decode B16 ctx8192 Hq32/Hkv8/D128 bf16 "
