@@ -1321,6 +1321,8 @@ def run_ref_shapes(torch, dev, args):
     hq, hkv, d, bs = 32, 8, 128, 32
     dtypes = {"float16": torch.float16, "bfloat16": torch.bfloat16}
     rows = []
+    probes = load_probes()
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
     for kind, table in (("full", REF_GROUPED_MS), ("default", REF_DEFAULT_MS)):
         for (batch, ctx), ref in table.items():
             if kind == "full":
@@ -1348,6 +1350,23 @@ def run_ref_shapes(torch, dev, args):
                         "algorithmic_bytes": algo, "graph_gb_per_s": round(algo / (graph_us * 1e-6) / 1e9, 1),
                         "reference_rtx5070_us": round(ref[dname] * 1e3, 2),
                         "speedup_event": round(ref[dname] * 1e3 / (ev_ms * 1e3), 2)}
+                if kind == "full" and dname == "bfloat16":
+                    # the ceiling of a read of these bytes on this part: one non-temporal read of a
+                    # buffer of the call's algorithmic bytes (the floor workload's probe), same method
+                    n16 = (algo + 15) // 16 * 16
+                    bufs = [torch.empty(n16, dtype=torch.uint8, device=dev) for _ in range(n_pools)]
+
+                    def rd(i, bufs=bufs, n16=n16):
+                        st = torch.cuda.current_stream(dev).cuda_stream
+                        assert probes.fdp_stream_read(bufs[i % len(bufs)].data_ptr(), n16, sink.data_ptr(), st,
+                                                      None, None) == 0
+
+                    read_us = graph_p50_us(torch, dev, rd, n_pools, samples=120, warmup=24)
+                    line["bare_read_graph_p50_us"] = round(read_us, 2)
+                    line["bare_read_gb_per_s"] = round(algo / (read_us * 1e-6) / 1e9, 1)
+                    log(f"[bench] ref-shapes bare read of B{batch} ctx{ctx}'s {algo} bytes: {read_us:.2f} us "
+                        f"({line['bare_read_gb_per_s']} GB/s)")
+                    del bufs, rd
                 rows.append(line)
                 log(f"[bench] ref-shapes decode {kind} B{batch} ctx{ctx} {dname}: event p50 {ev_ms * 1e3:.2f} us, "
                     f"flushed p50 {fl_ms * 1e3:.2f} us, graph p50 {graph_us:.2f} us ({line['graph_gb_per_s']} GB/s); reference "
