@@ -282,9 +282,12 @@ def paged_decode_attention_cascade_into(
     last = getattr(_LAST_CASCADE, "entry", None)
     if last is not None and isinstance(q, torch.Tensor) and q.is_cuda and isinstance(groups, CascadeGroups):
         stream = _lib.current_stream_handle(q.device)
-        key = _cascade_key(q, k_cache, v_cache, block_tables, seq_lens, out, groups, workspace,
-                           (sm_scale, block_size, num_splits, prefix_splits, kv_reuse, chunk_rows, stream))
-        if last[0] == key:
+        try:
+            key = _cascade_key(q, k_cache, v_cache, block_tables, seq_lens, out, groups, workspace,
+                               (sm_scale, block_size, num_splits, prefix_splits, kv_reuse, chunk_rows, stream))
+        except (AttributeError, TypeError):
+            key = None  # an argument that is not a tensor: the full path raises the reference's message
+        if key is not None and last[0] == key:
             # the previous call's metadata and settings: only data pointers change
             args, cas = last[1]
             args.q = q.data_ptr()

@@ -504,6 +504,40 @@ def test_groups_above_16_fused_append_written_once(num_splits, hq, hkv, head_dim
     assert np.array_equal(bits16(v), bits16(v_expected))
 
 
+def test_stream_handle_is_the_current_stream_on_every_stream_and_under_capture():
+    """The launchers take torch's current stream through its raw-stream query: the same handle as
+    torch.cuda.current_stream(...).cuda_stream on the default stream, on a side stream and under
+    graph capture, and a decode captured there replays as the eager call computes it."""
+    from flashdec_amd import _lib
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    assert _lib.current_stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+    assert _lib.current_stream_handle(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        assert _lib.current_stream_handle(dev) == side.cuda_stream
+    q, k, v, table, lens = make_paged_inputs([300, 37], 16, 2, 128, 32, torch.bfloat16, seed=21)
+    ref = torch.empty_like(q)
+    out = torch.empty_like(q)
+    _fd().paged_decode_attention_into(q, k, v, table, lens, ref)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _fd().paged_decode_attention_into(q, k, v, table, lens, out)  # the side stream's workspace, outside capture
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            assert _lib.current_stream_handle(dev) == side.cuda_stream
+            _fd().paged_decode_attention_into(q, k, v, table, lens, out)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+    assert_close_to_oracle(ref, _oracle(q, k, v, table, lens))
+
+
 def test_repeated_calls_reuse_arguments_but_follow_every_pointer():
     """paged_decode_attention_into keeps the last call's validated arguments when only data pointers change:
     alternating inputs, caller workspaces and fused-append rows of one shape, then another shape, must each
