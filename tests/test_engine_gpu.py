@@ -1,8 +1,8 @@
 """DecodeEngine and PagedKVCache transactions on the HIP path.
 
 Each layer of each step is checked against the oracle: the rotated Q and the
-appended K/V bytes bit for bit, the attention output within the north-star
-tolerance (atol 2e-2, rtol 1e-2 against fp32).  Forged caller views must not
+appended K/V bytes bit for bit, the attention output within the
+attention tolerance (atol 2e-2, rtol 1e-2 against fp32).  Forged caller views must not
 steer a launch, and failures must roll the token back (the reference's
 tests/test_multi_layer_engine.py:332-419, 541-570).
 """

@@ -3,8 +3,8 @@
 Two engines start from identical caches.  One runs ``step_layer`` per layer;
 the other replays a captured :class:`DecodeStepGraph`.  After every step:
 - the appended K/V bytes of both caches must be identical;
-- both engines' outputs must match the oracle within the north-star
-  tolerance.
+- both engines' outputs must match the oracle within atol 2e-2 / rtol 1e-2
+  (against fp32).
 The batch's membership may change between steps as long as its size does.
 The graph is checked with the split reducer kernel, with RoPE + append
 fused into the decode launch, and with the in-launch merge (arrival
